@@ -1,0 +1,128 @@
+/*  pk_gpu.h - C ABI of the MI355X (gfx950) weight-GEMM library libpk_gpu.so.
+ *
+ *  Drop-in for the three weight GEMMs of eschmidbauer/parakeet-unified-en-0.6b-c
+ *  (csrc/blas.h:38-69).  Plain C types and pointers only.  Every function
+ *  returns PK_GPU_OK (0) or a negative pk_gpu_status; pk_gpu_last_error()
+ *  gives a message for the calling thread.  Nothing here falls back to the
+ *  CPU: a missing or non-gfx950 device is an error.
+ *
+ *  Semantics shared by the GEMMs (blas.c:89-99, 759-771, 950-963, 1055-1072):
+ *    C <- beta*C (beta == 0 clears C, beta == 1 leaves it), then, unless
+ *    alpha == 0 (or, for int8, B_scale == 0), C += alpha * A * W, row-major,
+ *    where every C[i][j] is the same sequential fused multiply-add chain over
+ *    k ascending that the reference evaluates, so results are bit-identical.
+ *
+ *  Host-pointer entry points (pk_gpu_gemm_i8, pk_gpu_gemm_i4, pk_gpu_sgemm)
+ *  take host memory, exactly as the reference BLAS does.  A weight operand
+ *  whose host range was registered with pk_gpu_register_weight is read from
+ *  its resident device copy; any other operand is copied in for the call.
+ *  C is copied back before the call returns.  Calls may come from any
+ *  thread; each thread gets its own HIP stream and staging buffers.
+ *
+ *  Device-pointer entry points (*_dev) take device pointers, enqueue on the
+ *  given HIP stream (NULL = HIP's null stream) and return without
+ *  synchronising.
+ */
+#ifndef PK_GPU_H
+#define PK_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    PK_GPU_OK       = 0,
+    PK_GPU_EINVAL   = -1,   /* bad argument (sizes, strides, NULL pointer)  */
+    PK_GPU_ENOTSUP  = -2,   /* form the reference call sites never use       */
+    PK_GPU_ENOMEM   = -3,   /* device or pinned allocation failed            */
+    PK_GPU_EHIP     = -4,   /* HIP runtime or launch error                   */
+    PK_GPU_ENODEV   = -5    /* no gfx950 device                              */
+} pk_gpu_status;
+
+/* Select the device (-1: $PK_GPU_DEVICE or 0) and check it is gfx950.
+ * Idempotent; the GEMM entry points call it on first use. */
+int pk_gpu_init(int device);
+/* Free resident weights and per-thread resources of the calling thread. */
+void pk_gpu_shutdown(void);
+/* Message for the last failing call on this thread ("" if none). */
+const char *pk_gpu_last_error(void);
+
+/* ---- resident weights ------------------------------------------------- */
+
+/* Copy host range [host, host+bytes) to the device once.  Later calls whose
+ * operand lies inside a registered range read the device copy.  The host
+ * bytes must not change while registered (the reference's weights are
+ * read-only mmap'd or load-time buffers, weights.c:294-302, 404-546).
+ * Registering an overlapping range is PK_GPU_EINVAL. */
+int pk_gpu_register_weight(const void *host, size_t bytes);
+int pk_gpu_unregister_weight(const void *host);
+/* Device address of a registered host pointer (or NULL). */
+const void *pk_gpu_device_ptr(const void *host);
+/* Bytes currently resident. */
+size_t pk_gpu_resident_bytes(void);
+
+/* ---- drop-in GEMMs (host pointers) ------------------------------------ */
+
+/* Replaces cblas_sgemm_qb (blas.h:54-62, blas.c:759-771): int8 B [K][ldb]
+ * with one per-tensor scale. */
+int pk_gpu_gemm_i8(int M, int N, int K, float alpha,
+                   const float *A, int lda,
+                   const int8_t *B, float B_scale, int ldb,
+                   float beta, float *C, int ldc);
+
+/* Replaces cblas_sgemm_q4b (blas.h:64-69, blas.c:950-963): packed int4
+ * B [K][ldb bytes] (two's-complement nibbles, low nibble = even column,
+ * extract_weights.py:589-592) with fp32 scales [K][N/32] (blas.c:794, 958).
+ * N must be a multiple of 32 (the format's group size,
+ * extract_weights.py:523) and ldb >= N/2. */
+int pk_gpu_gemm_i4(int M, int N, int K, float alpha,
+                   const float *A, int lda,
+                   const uint8_t *B, const float *scales, int ldb,
+                   float beta, float *C, int ldc);
+
+/* Replaces cblas_sgemm (blas.h:38-43, blas.c:1055-1072) for
+ * transA == transB == CblasNoTrans (111), the only form its callers use
+ * (tensor_ops.c:31-36, 579-590); other forms return PK_GPU_ENOTSUP.
+ * Either A or B may be a registered weight (pointwise conv passes the
+ * weight as A, tensor_ops.c:582-583). */
+int pk_gpu_sgemm(int transA, int transB, int M, int N, int K, float alpha,
+                 const float *A, int lda, const float *B, int ldb,
+                 float beta, float *C, int ldc);
+
+/* ---- device-pointer variants (no copies, no synchronisation) ----------- */
+
+int pk_gpu_gemm_i8_dev(int M, int N, int K, float alpha,
+                       const float *dA, int lda,
+                       const int8_t *dB, float B_scale, int ldb,
+                       float beta, float *dC, int ldc, void *stream);
+int pk_gpu_gemm_i4_dev(int M, int N, int K, float alpha,
+                       const float *dA, int lda,
+                       const uint8_t *dB, const float *dscales, int ldb,
+                       float beta, float *dC, int ldc, void *stream);
+int pk_gpu_sgemm_dev(int M, int N, int K, float alpha,
+                     const float *dA, int lda, const float *dB, int ldb,
+                     float beta, float *dC, int ldc, void *stream);
+
+/* Swish y = x * sigmoid(x) with the reference's polynomial exp
+ * (tensor_ops.c:98-120, 367-389); x may equal y. */
+int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);
+
+/* ---- tuning / introspection ------------------------------------------- */
+
+/* Number of kernel tile configurations, and a description of one:
+ * mfma (32, 16 or 4 = v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32),
+ * MFMA column tiles per wave, waves along M and N per workgroup. */
+int pk_gpu_num_configs(void);
+int pk_gpu_config_info(int index, int *mfma, int *cw, int *wgm, int *wgn);
+/* Index of the configuration the dispatcher picks for a shape. */
+int pk_gpu_pick_config(int M, int N, int K);
+/* Force a configuration for later calls on this thread (-1 = automatic). */
+int pk_gpu_force_config(int index);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PK_GPU_H */

@@ -1,0 +1,184 @@
+"""ctypes view of the CPU oracle and of the compiled reference.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
+by bench.py's cpu_baseline leg, always as the checker or the CPU baseline,
+never as the thing measured on the GPU.
+
+  Oracle      oracle/_build/liboracle.so   (pk_oracle.c, scalar restatement)
+  Reference   oracle/_ref/libpkref.so      (csrc/*.c of the reference, built
+                                            by oracle/Makefile, unmodified;
+                                            x86 AVX2 code path)
+              oracle/_ref/libpkref_portable.so  (same sources, blas.c on its
+                                            portable code path, which matches
+                                            the NEON path)
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "_build", "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libpkref.so")
+REF_PORTABLE_SO = os.path.join(HERE, "_ref", "libpkref_portable.so")
+
+_f = ctypes.c_float
+_i = ctypes.c_int
+_p = ctypes.c_void_p
+_u64 = ctypes.c_uint64
+_sz = ctypes.c_size_t
+
+_oracle = None
+_refs = {}
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+def oracle():
+    """Load oracle/_build/liboracle.so (built by `make -C oracle restatement`)."""
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"oracle library missing: {ORACLE_SO} (run __graft_entry__.build())")
+        lib = ctypes.CDLL(ORACLE_SO)
+        gemm = [_i, _i, _i, _f, _p, _i]
+        lib.pkor_sgemm_nn.argtypes = gemm + [_p, _i, _f, _p, _i]
+        lib.pkor_sgemm_qb.argtypes = gemm + [_p, _f, _i, _f, _p, _i]
+        lib.pkor_sgemm_q4b.argtypes = gemm + [_p, _p, _i, _f, _p, _i]
+        for fn in (lib.pkor_sgemm_nn, lib.pkor_sgemm_qb, lib.pkor_sgemm_q4b):
+            fn.restype = None
+        lib.pkor_dequant_i8.argtypes = [ctypes.c_int8, _f]
+        lib.pkor_dequant_i8.restype = _f
+        lib.pkor_nibble_lo.argtypes = [ctypes.c_uint8]
+        lib.pkor_nibble_lo.restype = _i
+        lib.pkor_nibble_hi.argtypes = [ctypes.c_uint8]
+        lib.pkor_nibble_hi.restype = _i
+        lib.pkor_dequant_i8_matrix.argtypes = [_p, _i, _i, _i, _f, _p]
+        lib.pkor_dequant_i4_matrix.argtypes = [_p, _i, _i, _i, _p, _p]
+        lib.pkor_seed.argtypes = [_u64, ctypes.c_char_p]
+        lib.pkor_seed.restype = _u64
+        lib.pkor_fill_normal.argtypes = [_p, _sz, _f, _f, _u64]
+        lib.pkor_fill_uniform.argtypes = [_p, _sz, _f, _f, _u64]
+        lib.pkor_fill_int8.argtypes = [_p, _sz, _i, _i, _u64]
+        lib.pkor_fill_bytes.argtypes = [_p, _sz, _u64]
+        _oracle = lib
+    return _oracle
+
+
+def have_ref(variant="ref"):
+    return os.path.exists(REF_SO if variant == "ref" else REF_PORTABLE_SO)
+
+
+def ref(variant="ref"):
+    """Load a compiled reference: "ref" = AVX2 build, "portable" = blas.c's
+    portable path."""
+    if variant not in _refs:
+        path = REF_SO if variant == "ref" else REF_PORTABLE_SO
+        if not os.path.exists(path):
+            raise RuntimeError(f"reference build missing: {path}")
+        lib = ctypes.CDLL(path)
+        gemm = [_i, _i, _i, _f, _p, _i]
+        lib.cblas_sgemm.argtypes = [_i, _i, _i] + gemm + [_p, _i, _f, _p, _i]
+        lib.cblas_sgemm_qb.argtypes = gemm + [_p, _f, _i, _f, _p, _i]
+        lib.cblas_sgemm_q4b.argtypes = gemm + [_p, _p, _i, _f, _p, _i]
+        for fn in (lib.cblas_sgemm, lib.cblas_sgemm_qb, lib.cblas_sgemm_q4b):
+            fn.restype = None
+        lib.pk_swish.argtypes = [_p, _i]
+        lib.pk_swish.restype = None
+        lib.pk_pool.restype = _p
+        lib.pk_pool_nthreads.argtypes = [_p]
+        lib.pk_pool_nthreads.restype = _i
+        _refs[variant] = lib
+    return _refs[variant]
+
+
+# ---- seeded data ---------------------------------------------------------
+
+def seed(base, name):
+    return int(oracle().pkor_seed(base, name.encode()))
+
+
+def normal(shape, mean, std, s):
+    out = np.empty(shape, np.float32)
+    oracle().pkor_fill_normal(_ptr(out), out.size, mean, std, s)
+    return out
+
+
+def uniform(shape, lo, hi, s):
+    out = np.empty(shape, np.float32)
+    oracle().pkor_fill_uniform(_ptr(out), out.size, lo, hi, s)
+    return out
+
+
+def int8s(shape, lo, hi, s):
+    out = np.empty(shape, np.int8)
+    oracle().pkor_fill_int8(_ptr(out), out.size, lo, hi, s)
+    return out
+
+
+def bytes_(shape, s):
+    out = np.empty(shape, np.uint8)
+    oracle().pkor_fill_bytes(_ptr(out), out.size, s)
+    return out
+
+
+# ---- GEMM wrappers (row-major numpy arrays; C is updated in place) --------
+
+def _check(A, C, M, N, K):
+    assert A.dtype == np.float32 and C.dtype == np.float32
+    assert A.flags.c_contiguous and C.flags.c_contiguous
+
+
+def sgemm(A, B, C, alpha=1.0, beta=0.0, impl="oracle"):
+    M, K = A.shape
+    N = B.shape[1]
+    _check(A, C, M, N, K)
+    if impl == "oracle":
+        oracle().pkor_sgemm_nn(M, N, K, alpha, _ptr(A), K, _ptr(B), N, beta, _ptr(C), N)
+    else:
+        ref(impl).cblas_sgemm(101, 111, 111, M, N, K, alpha, _ptr(A), K, _ptr(B), N, beta, _ptr(C), N)
+    return C
+
+
+def sgemm_qb(A, Q, scale, C, alpha=1.0, beta=0.0, impl="oracle"):
+    M, K = A.shape
+    N = Q.shape[1]
+    _check(A, C, M, N, K)
+    assert Q.dtype == np.int8
+    fn = oracle().pkor_sgemm_qb if impl == "oracle" else ref(impl).cblas_sgemm_qb
+    fn(M, N, K, alpha, _ptr(A), K, _ptr(Q), scale, N, beta, _ptr(C), N)
+    return C
+
+
+def sgemm_q4b(A, P, scales, C, alpha=1.0, beta=0.0, impl="oracle"):
+    """P: packed int4 [K][N/2] uint8; scales: fp32 [K][N/32]."""
+    M, K = A.shape
+    N = P.shape[1] * 2
+    _check(A, C, M, N, K)
+    assert P.dtype == np.uint8 and scales.dtype == np.float32
+    fn = oracle().pkor_sgemm_q4b if impl == "oracle" else ref(impl).cblas_sgemm_q4b
+    fn(M, N, K, alpha, _ptr(A), K, _ptr(P), _ptr(scales), N // 2, beta, _ptr(C), N)
+    return C
+
+
+def dequant_i4(P, scales):
+    K, half = P.shape
+    N = half * 2
+    out = np.empty((K, N), np.float32)
+    oracle().pkor_dequant_i4_matrix(_ptr(P), K, N, half, _ptr(scales), _ptr(out))
+    return out
+
+
+def dequant_i8(Q, scale):
+    K, N = Q.shape
+    out = np.empty((K, N), np.float32)
+    oracle().pkor_dequant_i8_matrix(_ptr(Q), K, N, N, scale, _ptr(out))
+    return out
+
+
+def ref_swish(x):
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    ref().pk_swish(_ptr(y), y.size)
+    return y

@@ -1,0 +1,57 @@
+// pk_gemm_kernels.h - device-side entry points of the weight-GEMM library.
+//
+// Internal C++ interface between the kernels (pk_gemm_kernels.hip) and the
+// host runtime (pk_gpu_runtime.hip).  All pointers are device pointers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pkgpu {
+
+enum WeightKind { W_F32 = 0, W_I8 = 1, W_I4 = 2 };
+
+// One weight GEMM, C <- beta*C + alpha*A*W, row-major, NoTrans/NoTrans,
+// with W given in one of the on-disk formats (weights.c:240-266):
+//   W_F32: fp32 [K][ldb]
+//   W_I8 : int8 [K][ldb] with one per-tensor scale
+//   W_I4 : packed int4 [K][ldb bytes], two's-complement nibbles, low nibble
+//          = even column, scales fp32 [K][N/32]
+struct GemmProblem {
+    WeightKind kind;
+    int M, N, K;
+    float alpha, beta;
+    const float* A; int lda;
+    const void* B;  int ldb;
+    float scale;              // W_I8
+    const float* scales;      // W_I4
+    float* C; int ldc;
+};
+
+// Kernel tile configuration chosen for a shape (see choose_config).
+struct TileConfig {
+    int mfma;   // 32, 16 or 4: v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32
+    int cw;     // MFMA column tiles per wave
+    int wgm;    // waves along M per workgroup
+    int wgn;    // waves along N per workgroup
+    int kt;     // k per LDS chunk
+    int bm() const { return 64 * wgm; }
+    int bn() const { return mfma * cw * wgn; }
+};
+
+// Pick the tile configuration with the lowest modelled time on 256 CUs.
+TileConfig choose_config(int M, int N, int K);
+// Number of configurations and access by index (for tests and sweeps).
+int num_configs();
+TileConfig config_at(int i);
+
+// Launch the whole GEMM (beta pre-pass semantics, early exits, int8 edge
+// columns) on `stream`.  Returns hipSuccess or the launch error.
+// cfg_index < 0 selects choose_config().
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index);
+
+// Swish y = x * (1 / (1 + exp(-x))) with the reference's polynomial exp
+// (tensor_ops.c:98-120, 381-388), n elements, in place allowed.
+hipError_t launch_swish(const float* x, float* y, long long n, hipStream_t stream);
+
+}  // namespace pkgpu

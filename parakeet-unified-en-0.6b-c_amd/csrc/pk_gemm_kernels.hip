@@ -1,0 +1,600 @@
+// pk_gemm_kernels.hip - CDNA4 (gfx950) kernels for the quantized weight GEMMs.
+//
+// Numerics.  The reference computes every output as a sequential fused
+// multiply-add chain over k ascending, c = fma(fl(alpha*A[i][k]), w[k][j], c),
+// starting from fl(beta*C) (csrc/blas.c:89-99, 187-218, 617-651), with the
+// weight dequantised once per element, w = fl((float)q * s) (blas.c:545-553,
+// 815-840).  The fp32 MFMA instructions with K = 1,
+//     v_mfma_f32_32x32x1_2b_f32, v_mfma_f32_16x16x1_4b_f32,
+//     v_mfma_f32_4x4x1_16b_f32,
+// perform exactly one multiply-add per output element, so issuing them in
+// ascending k on one accumulator reproduces the chain element for element,
+// at the full fp32 matrix-core rate.  Nothing here ever splits k across
+// waves or reorders a chain; that is the invariant every tile shape keeps.
+//
+// Data flow per workgroup (BM x BN output tile, KT-deep chunks of k):
+//   global A (fp32, row-major) --> fl(alpha*a) --> LDS As[k][m]   (k-major)
+//   global W (fp32 | int8 | packed int4 + fp32 scales) --> dequant in
+//        registers --> LDS Bs[k][n] fp32                           (k-major)
+//   per k: one ds_read of 64 rows of A (lane l -> row l) and one broadcast
+//   ds_read of the MFMA's column group of B, then one MFMA per column tile.
+// Chunks are double-buffered: chunk c+1 is fetched into registers while
+// chunk c is multiplied, then written to the other LDS buffer.
+#include "pk_gemm_kernels.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace pkgpu {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+// Kernel arguments (device pointers).  N is the number of columns this
+// launch computes; n_groups is the int4 scale-row length N_full/32
+// (blas.c:958).
+struct KArgs {
+    int M, N, K;
+    float alpha, beta;
+    const float* A; int lda;
+    const void* B;  int ldb;
+    float scale;
+    const float* scales; int n_groups;
+    float* C; int ldc;
+    // Exact byte extents the call may read (buffer-descriptor ranges) and
+    // whether A / B rows allow 16-byte vector loads.
+    uint32_t a_bytes, b_bytes, s_bytes;
+    int vec_a, vec_b;
+};
+
+// Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format).
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             kRsrcWord3);
+}
+
+// Raw buffer loads: an offset at or past the descriptor's range returns 0,
+// so staging needs no bounds predicates and never touches memory outside
+// the caller's operand.
+__device__ inline float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ inline uint32_t ld_u32(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ inline uint32_t ld_u8(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+__device__ inline v4u ld_v4(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+
+// ---- MFMA shapes -----------------------------------------------------------
+// Every shape is used with its blocks stacked along M, so one instruction
+// covers 64 rows x NCOL columns: A lane l carries row l, B lane l carries
+// column l % NCOL.  row()/col() give the output element held by (lane, reg).
+
+template <int MF> struct Mfma;
+
+template <> struct Mfma<32> {
+    static constexpr int NCOL = 32, NACC = 32;
+    using acc_t = v32f;
+    __device__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static int row(int l, int r) {
+        return 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (l >> 5) + (r & 3);
+    }
+    __device__ static int col(int l, int) { return l & 31; }
+};
+
+template <> struct Mfma<16> {
+    static constexpr int NCOL = 16, NACC = 16;
+    using acc_t = v16f;
+    __device__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static int row(int l, int r) { return 16 * (r >> 2) + 4 * (l >> 4) + (r & 3); }
+    __device__ static int col(int l, int) { return l & 15; }
+};
+
+template <> struct Mfma<4> {
+    static constexpr int NCOL = 4, NACC = 4;
+    using acc_t = v4f;
+    __device__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static int row(int l, int r) { return 4 * (l >> 2) + r; }
+    __device__ static int col(int l, int) { return l & 3; }
+};
+
+// ---- weight staging (dequantisation, bit-exact) ---------------------------
+// A "unit" is VB consecutive columns of one row of W, fetched with one
+// vector load when rows are 4/16-byte aligned; "elem" is the scalar form.
+// load_*() only issues loads into raw registers; dequant_*() runs after the
+// current chunk's MFMAs, so the loads' latency overlaps the multiplies, and
+// produces fp32 weights exactly as the reference's pack step does.
+
+template <int WK> struct WStage;
+
+template <> struct WStage<W_F32> {
+    static constexpr int VB = 4;
+    struct Unit { v4u w; };
+    struct Elem { float w; };
+    __device__ static Unit load_unit(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
+                                     __amdgpu_buffer_rsrc_t, int k, int n) {
+        return Unit{ld_v4(rb, ((uint32_t)k * p.ldb + n) * 4u)};
+    }
+    __device__ static void dequant_unit(const KArgs&, const Unit& u, float* out) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = __uint_as_float(u.w[j]);
+    }
+    __device__ static Elem load_elem(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
+                                     __amdgpu_buffer_rsrc_t, int k, int n) {
+        return Elem{ld_f32(rb, ((uint32_t)k * p.ldb + n) * 4u)};
+    }
+    __device__ static float dequant_elem(const KArgs&, const Elem& e, int) { return e.w; }
+};
+
+// blas.c:545-553: fl((float)q * scale)
+template <> struct WStage<W_I8> {
+    static constexpr int VB = 4;
+    struct Unit { uint32_t w; };
+    struct Elem { uint32_t q; };
+    __device__ static Unit load_unit(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
+                                     __amdgpu_buffer_rsrc_t, int k, int n) {
+        return Unit{ld_u32(rb, (uint32_t)k * p.ldb + n)};
+    }
+    __device__ static void dequant_unit(const KArgs& p, const Unit& u, float* out) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = __fmul_rn((float)(int8_t)(u.w >> (8 * j)), p.scale);
+    }
+    __device__ static Elem load_elem(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
+                                     __amdgpu_buffer_rsrc_t, int k, int n) {
+        return Elem{ld_u8(rb, (uint32_t)k * p.ldb + n)};
+    }
+    __device__ static float dequant_elem(const KArgs& p, const Elem& e, int) {
+        return __fmul_rn((float)(int8_t)e.q, p.scale);
+    }
+};
+
+// blas.c:834-840 (portable/NEON decode) and blas.c:794 (scale index): byte j
+// of row k holds column 2j in the low nibble and 2j+1 in the high nibble,
+// both two's complement; scale = scales[k * (N/32) + n/32].
+template <> struct WStage<W_I4> {
+    static constexpr int VB = 8;
+    struct Unit { uint32_t w; float s; };
+    struct Elem { uint32_t b; float s; };
+    __device__ static Unit load_unit(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
+                                     __amdgpu_buffer_rsrc_t rs, int k, int n) {
+        return Unit{ld_u32(rb, (uint32_t)k * p.ldb + (n >> 1)),
+                    ld_f32(rs, ((uint32_t)k * p.n_groups + (n >> 5)) * 4u)};
+    }
+    __device__ static void dequant_unit(const KArgs&, const Unit& u, float* out) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int v = (int)(u.w << (28 - 4 * j)) >> 28;     // sign-extend nibble j
+            out[j] = __fmul_rn((float)v, u.s);
+        }
+    }
+    __device__ static Elem load_elem(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
+                                     __amdgpu_buffer_rsrc_t rs, int k, int n) {
+        return Elem{ld_u8(rb, (uint32_t)k * p.ldb + (n >> 1)),
+                    ld_f32(rs, ((uint32_t)k * p.n_groups + (n >> 5)) * 4u)};
+    }
+    __device__ static float dequant_elem(const KArgs&, const Elem& e, int n) {
+        const int v = (n & 1) ? ((int)(int8_t)e.b >> 4) : ((int)(int8_t)(e.b << 4) >> 4);
+        return __fmul_rn((float)v, e.s);
+    }
+};
+
+// ---- the chain GEMM ---------------------------------------------------------
+
+template <int WK, int MF, int CW, int WGM, int WGN, int KT, bool VEC>
+__global__ __launch_bounds__(64 * WGM * WGN)
+void chain_gemm(KArgs p)
+{
+    using T = Mfma<MF>;
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int BM = 64 * WGM;
+    constexpr int AS = BM + 1;              // padded row of As: conflict-free stores
+    constexpr int WN = T::NCOL * CW;
+    constexpr int BN = WN * WGN;
+    constexpr int A_PER = (BM * KT) / NT;
+    constexpr int B_PER = (BN * KT) / NT;
+    static_assert((BM * KT) % NT == 0 && (BN * KT) % NT == 0, "tile/threads");
+
+    __shared__ float As[2][KT * AS];
+    __shared__ float Bs[2][KT * BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    // Chains start from beta*C exactly as scale_c leaves it (blas.c:89-99).
+    typename T::acc_t acc[CW];
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+#pragma unroll
+        for (int r = 0; r < T::NACC; ++r) {
+            const int row = m0 + wm * 64 + T::row(lane, r);
+            const int col = n0 + wn * WN + c * T::NCOL + T::col(lane, r);
+            float v = 0.0f;
+            if (p.beta != 0.0f && row < p.M && col < p.N) {
+                const float cv = p.C[(size_t)row * p.ldc + col];
+                v = (p.beta == 1.0f) ? cv : __fmul_rn(cv, p.beta);
+            }
+            acc[c][r] = v;
+        }
+    }
+
+    const int nchunks = (p.K + KT - 1) / KT;
+    using WS = WStage<WK>;
+    constexpr int VB = WS::VB;
+    constexpr int A_UNITS = A_PER / 4;
+    constexpr int B_UNITS = B_PER / VB;
+    static_assert(A_PER % 4 == 0 && B_PER % VB == 0 && BN % VB == 0 && KT % 4 == 0, "units");
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.A, p.a_bytes);
+    const __amdgpu_buffer_rsrc_t rsB = make_rsrc(p.B, p.b_bytes);
+    const __amdgpu_buffer_rsrc_t rsS = make_rsrc(WK == W_I4 ? (const void*)p.scales : p.B,
+                                                 WK == W_I4 ? p.s_bytes : 0u);
+    // Raw staging registers: the A words and the undecoded weight words of
+    // the next chunk, in the vector (VEC) or the scalar form.
+    v4u ra4[VEC ? A_UNITS : 1];
+    float ra1[VEC ? 1 : A_PER];
+    typename WS::Unit rbu[VEC ? B_UNITS : 1];
+    typename WS::Elem rbe[VEC ? 1 : B_PER];
+
+    // All loads are unconditional buffer loads (out-of-range -> 0); rows of A
+    // past M and columns of W past N only feed outputs that are never stored,
+    // and k past K is never multiplied (kn below).
+    auto load_chunk = [&](int ch) {
+        const int k0 = ch * KT;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < A_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int row = e / (KT / 4), kq = e % (KT / 4);
+                ra4[i] = ld_v4(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + 4 * kq) * 4u);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_PER; ++i) {
+                const int e = tid + i * NT;
+                const int row = e / KT, kk = e % KT;
+                ra1[i] = ld_f32(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + kk) * 4u);
+            }
+        }
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < B_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int kk = e / (BN / VB), nq = e % (BN / VB);
+                rbu[i] = WS::load_unit(p, rsB, rsS, k0 + kk, n0 + VB * nq);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < B_PER; ++i) {
+                const int e = tid + i * NT;
+                const int kk = e / BN, n = e % BN;
+                rbe[i] = WS::load_elem(p, rsB, rsS, k0 + kk, n0 + n);
+            }
+        }
+    };
+    // fl(alpha*a) and the weight dequantisation happen here, then LDS stores.
+    auto store_chunk = [&](int buf) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < A_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int row = e / (KT / 4), kq = e % (KT / 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    As[buf][(4 * kq + j) * AS + row] = __fmul_rn(p.alpha, __uint_as_float(ra4[i][j]));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_PER; ++i) {
+                const int e = tid + i * NT;
+                As[buf][(e % KT) * AS + e / KT] = __fmul_rn(p.alpha, ra1[i]);
+            }
+        }
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < B_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int kk = e / (BN / VB), nq = e % (BN / VB);
+                float w[VB];
+                WS::dequant_unit(p, rbu[i], w);
+#pragma unroll
+                for (int j = 0; j < VB; ++j) Bs[buf][kk * BN + VB * nq + j] = w[j];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < B_PER; ++i) {
+                const int e = tid + i * NT;
+                Bs[buf][e] = WS::dequant_elem(p, rbe[i], e % BN);   // [kk * BN + n]
+            }
+        }
+    };
+
+    if (nchunks > 0) {
+        load_chunk(0);
+        store_chunk(0);
+    }
+    __syncthreads();
+
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const int buf = ch & 1;
+        if (ch + 1 < nchunks) load_chunk(ch + 1);
+        const float* as = &As[buf][wm * 64 + lane];
+        const float* bs = &Bs[buf][wn * WN + (lane % T::NCOL)];
+        const int kn = min(KT, p.K - ch * KT);
+        if (kn == KT) {
+            // Operands for k+U are read from LDS while k..k+U-1 are multiplied.
+            constexpr int U = 8;
+            float av[2][U], bv[2][U][CW];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                av[0][u] = as[u * AS];
+#pragma unroll
+                for (int c = 0; c < CW; ++c) bv[0][u][c] = bs[u * BN + c * T::NCOL];
+            }
+#pragma unroll
+            for (int k8 = 0; k8 < KT; k8 += U) {
+                const int cur = (k8 / U) & 1;
+                if (k8 + U < KT) {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        av[cur ^ 1][u] = as[(k8 + U + u) * AS];
+#pragma unroll
+                        for (int c = 0; c < CW; ++c)
+                            bv[cur ^ 1][u][c] = bs[(k8 + U + u) * BN + c * T::NCOL];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int c = 0; c < CW; ++c) acc[c] = T::step(av[cur][u], bv[cur][u][c], acc[c]);
+            }
+        } else {
+            for (int kk = 0; kk < kn; ++kk) {
+                const float a = as[kk * AS];
+#pragma unroll
+                for (int c = 0; c < CW; ++c)
+                    acc[c] = T::step(a, bs[kk * BN + c * T::NCOL], acc[c]);
+            }
+        }
+        if (ch + 1 < nchunks) store_chunk(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+#pragma unroll
+        for (int r = 0; r < T::NACC; ++r) {
+            const int row = m0 + wm * 64 + T::row(lane, r);
+            const int col = n0 + wn * WN + c * T::NCOL + T::col(lane, r);
+            if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[c][r];
+        }
+    }
+}
+
+// int8 columns j >= 16*floor(N/16): the compiled reference evaluates
+// blas.c:752 (c += ax*bs*(float)b) as c = fma(fl(A*fl(alpha*bs)), (float)q, c)
+// after hoisting alpha*bs; one thread per output, k ascending.
+__global__ void i8_edge(KArgs p, int n_begin, int n_edge)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)p.M * n_edge) return;
+    const int i = (int)(idx / n_edge);
+    const int j = n_begin + (int)(idx % n_edge);
+    const int8_t* Q = static_cast<const int8_t*>(p.B);
+    float c = 0.0f;
+    if (p.beta != 0.0f) {
+        const float cv = p.C[(size_t)i * p.ldc + j];
+        c = (p.beta == 1.0f) ? cv : __fmul_rn(cv, p.beta);
+    }
+    const float as = __fmul_rn(p.alpha, p.scale);
+    for (int k = 0; k < p.K; ++k) {
+        const float a = __fmul_rn(p.A[(size_t)i * p.lda + k], as);
+        c = __fmaf_rn(a, (float)Q[(size_t)k * p.ldb + j], c);
+    }
+    p.C[(size_t)i * p.ldc + j] = c;
+}
+
+// C <- beta*C alone (alpha == 0, int8 scale == 0, or K == 0): blas.c:89-99.
+__global__ void scale_c(float* C, int M, int N, int ldc, float beta)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)M * N) return;
+    const int i = (int)(idx / N), j = (int)(idx % N);
+    float* c = C + (size_t)i * ldc + j;
+    *c = (beta == 0.0f) ? 0.0f : __fmul_rn(*c, beta);
+}
+
+// Swish as tensor_ops.c:381-388 / 98-120 write it: e = exp(-x) from a
+// 2^k * poly(r) range reduction, s = 1/(1+e), y = x*s.  The reference build
+// contracts r = t - k*ln2 and 1 + poly*2^k into FMAs, which is followed here;
+// its 1/(1+e) is rcpps plus one Newton step, which no GPU can reproduce, so
+// this uses an IEEE division (agreement within a few ulp, tested).
+__global__ void swish(const float* x, float* y, long long n)
+{
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    float t = fminf(fmaxf(-v, -87.0f), 87.0f);
+    const float kf = __builtin_rintf(__fmul_rn(t, 1.44269504088896341f));
+    const int ki = (int)kf;
+    const float r = __fmaf_rn(-kf, 0.69314718055994529f, t);
+    float q = 1.0f / 120.0f;
+    q = __fmaf_rn(q, r, 1.0f / 24.0f);
+    q = __fmaf_rn(q, r, 1.0f / 6.0f);
+    q = __fmaf_rn(q, r, 0.5f);
+    q = __fmaf_rn(q, r, 1.0f);
+    q = __fmaf_rn(q, r, 1.0f);
+    const float p2 = __int_as_float((ki + 127) << 23);
+    const float d = __fmaf_rn(q, p2, 1.0f);
+    const float s = __fdiv_rn(1.0f, d);
+    y[i] = __fmul_rn(s, v);
+}
+
+// ---- configurations and dispatch -------------------------------------------
+
+// KT (k per LDS chunk) is sized so one chunk's MFMA time per wave (KT * cw *
+// cycles) covers the latency of the next chunk's loads.
+const TileConfig kConfigs[] = {
+    {32, 2, 2, 2, 32},    // 128 x 128, wave 64 x 64
+    {32, 1, 2, 2, 32},    // 128 x 64,  wave 64 x 32
+    {16, 2, 1, 4, 32},    //  64 x 128, wave 64 x 32
+    {16, 1, 1, 4, 64},    //  64 x 64,  wave 64 x 16
+    {4, 4, 1, 4, 64},     //  64 x 64,  wave 64 x 16
+    {4, 1, 1, 4, 128},    //  64 x 16,  wave 64 x 4
+};
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+
+template <int WK, bool VEC>
+hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
+{
+    const TileConfig& t = kConfigs[cfg];
+    dim3 grid((a.N + t.bn() - 1) / t.bn(), (a.M + t.bm() - 1) / t.bm());
+    dim3 block(64 * t.wgm * t.wgn);
+    switch (cfg) {
+    case 0: hipLaunchKernelGGL((chain_gemm<WK, 32, 2, 2, 2, 32, VEC>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((chain_gemm<WK, 32, 1, 2, 2, 32, VEC>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((chain_gemm<WK, 16, 2, 1, 4, 32, VEC>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((chain_gemm<WK, 16, 1, 1, 4, 64, VEC>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((chain_gemm<WK, 4, 4, 1, 4, 64, VEC>), grid, block, 0, s, a); break;
+    case 5: hipLaunchKernelGGL((chain_gemm<WK, 4, 1, 1, 4, 128, VEC>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int WK>
+hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
+{
+    return (a.vec_a && a.vec_b) ? launch_chain<WK, true>(cfg, a, s)
+                                : launch_chain<WK, false>(cfg, a, s);
+}
+
+int mfma_cycles(int mf) { return mf == 32 ? 64 : mf == 16 ? 32 : 8; }
+
+}  // namespace
+
+int num_configs() { return kNumConfigs; }
+TileConfig config_at(int i) { return kConfigs[i]; }
+
+// Modelled time: waves are independent k-chains, one MFMA pipe per SIMD
+// (1024 SIMDs on 256 CUs), each k step costs the wave's MFMA cycles or its
+// share of the CU's LDS reads, whichever is larger.
+TileConfig choose_config(int M, int N, int K)
+{
+    int best = 0;
+    double best_t = 1e300;
+    for (int i = 0; i < kNumConfigs; ++i) {
+        const TileConfig& t = kConfigs[i];
+        const double tiles = (double)((M + t.bm() - 1) / t.bm()) * ((N + t.bn() - 1) / t.bn());
+        const double waves = tiles * t.wgm * t.wgn;
+        const double rounds = std::ceil(waves / 1024.0);
+        const double mfma_k = (double)t.cw * mfma_cycles(t.mfma);
+        const double lds_k = 4.0 * (2.0 + 2.0 * t.cw);
+        const double est = rounds * (double)K * std::max(mfma_k, lds_k);
+        if (est < best_t * 0.999) { best_t = est; best = i; }
+    }
+    return kConfigs[best];
+}
+
+static int config_index(const TileConfig& c)
+{
+    for (int i = 0; i < kNumConfigs; ++i)
+        if (kConfigs[i].mfma == c.mfma && kConfigs[i].cw == c.cw &&
+            kConfigs[i].wgm == c.wgm && kConfigs[i].wgn == c.wgn && kConfigs[i].kt == c.kt)
+            return i;
+    return 0;
+}
+
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
+{
+    if (p.M <= 0 || p.N <= 0) return hipSuccess;
+    const bool early = (p.alpha == 0.0f) || (p.kind == W_I8 && p.scale == 0.0f) || p.K <= 0;
+    if (early) {   // blas.c:764-765, 955-956, 1063-1064: only the beta step runs
+        if (p.beta == 1.0f) return hipSuccess;
+        const long long n = (long long)p.M * p.N;
+        hipLaunchKernelGGL(scale_c, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                           p.C, p.M, p.N, p.ldc, p.beta);
+        return hipGetLastError();
+    }
+
+    KArgs a;
+    a.M = p.M; a.N = p.N; a.K = p.K;
+    a.alpha = p.alpha; a.beta = p.beta;
+    a.A = p.A; a.lda = p.lda;
+    a.B = p.B; a.ldb = p.ldb;
+    a.scale = p.scale;
+    a.scales = p.scales; a.n_groups = p.N / 32;
+    a.C = p.C; a.ldc = p.ldc;
+
+    // Exact extents of what the call may read; the kernels address operands
+    // through 32-bit buffer offsets, so each must stay below 2 GiB.
+    const size_t esz = p.kind == W_F32 ? 4 : 1;
+    const size_t b_row = p.kind == W_I4 ? (size_t)p.N / 2 : (size_t)p.N;
+    const size_t a_ext = ((size_t)(p.M - 1) * p.lda + p.K) * 4;
+    const size_t b_ext = ((size_t)(p.K - 1) * p.ldb + b_row) * esz;
+    const size_t s_ext = p.kind == W_I4 ? (size_t)p.K * (p.N / 32) * 4 : 0;
+    const size_t lim = (size_t)1 << 31;
+    if (a_ext >= lim || b_ext >= lim || s_ext >= lim) return hipErrorInvalidValue;
+    a.a_bytes = (uint32_t)a_ext;
+    a.b_bytes = (uint32_t)b_ext;
+    a.s_bytes = (uint32_t)s_ext;
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(p.A), pb = reinterpret_cast<uintptr_t>(p.B);
+    a.vec_a = (p.lda % 4 == 0) && (pa % 16 == 0);
+    a.vec_b = p.kind == W_F32 ? ((p.ldb % 4 == 0) && (pb % 16 == 0))
+                              : ((p.ldb % 4 == 0) && (pb % 4 == 0));
+
+    int n_main = p.N;
+    if (p.kind == W_I8) n_main = (p.N / 16) * 16;     // blas.c:686, 734
+    a.N = n_main;
+
+    const int cfg = (cfg_index >= 0 && cfg_index < kNumConfigs)
+                        ? cfg_index
+                        : config_index(choose_config(p.M, n_main, p.K));
+    hipError_t err = hipSuccess;
+    if (n_main > 0) {
+        switch (p.kind) {
+        case W_F32: err = launch_chain<W_F32>(cfg, a, stream); break;
+        case W_I8:  err = launch_chain<W_I8>(cfg, a, stream); break;
+        case W_I4:  err = launch_chain<W_I4>(cfg, a, stream); break;
+        }
+        if (err != hipSuccess) return err;
+    }
+    if (p.kind == W_I8 && n_main < p.N) {
+        const int n_edge = p.N - n_main;
+        const long long n = (long long)p.M * n_edge;
+        hipLaunchKernelGGL(i8_edge, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                           a, n_main, n_edge);
+        err = hipGetLastError();
+    }
+    return err;
+}
+
+hipError_t launch_swish(const float* x, float* y, long long n, hipStream_t stream)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(swish, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x, y, n);
+    return hipGetLastError();
+}
+
+}  // namespace pkgpu

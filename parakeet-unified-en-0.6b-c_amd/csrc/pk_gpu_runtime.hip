@@ -1,0 +1,461 @@
+// pk_gpu_runtime.hip - host side of libpk_gpu.so: device selection,
+// resident-weight registry, per-thread streams and staging, and the C ABI
+// declared in include/pk_gpu.h.
+//
+// The reference BLAS is called with host pointers from whatever thread runs
+// the encoder (csrc/tensor_ops.c:31-61, 579-590; main.c:167-188 runs one
+// thread per file).  Here each calling thread owns a HIP stream and a set of
+// staging buffers, so concurrent callers never share mutable state except
+// the weight registry, which is guarded by a mutex.
+#include "pk_gpu.h"
+#include "pk_gemm_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+
+using pkgpu::GemmProblem;
+using pkgpu::WeightKind;
+
+namespace {
+
+std::mutex g_mu;                 // guards everything below
+bool g_inited = false;
+int g_device = -1;
+
+struct Resident {
+    size_t bytes;
+    void* dev;
+};
+std::map<uintptr_t, Resident> g_weights;   // host begin -> device copy
+size_t g_resident_bytes = 0;
+
+thread_local std::string t_err;
+thread_local int t_force_cfg = -1;
+
+// Per-thread stream and staging buffers (slot 0: A, 1: B, 2: C, 3: scales).
+struct ThreadCtx {
+    hipStream_t stream = nullptr;
+    void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t cap[4] = {0, 0, 0, 0};
+};
+thread_local ThreadCtx* t_ctx = nullptr;
+
+int fail(int code, const char* fmt, ...)
+{
+    char msg[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+    t_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    return fail(PK_GPU_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int init_locked(int device)
+{
+    if (g_inited) return PK_GPU_OK;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) return fail(PK_GPU_ENODEV, "no HIP device visible");
+    if (device < 0) {
+        const char* env = getenv("PK_GPU_DEVICE");
+        device = env ? atoi(env) : 0;
+    }
+    if (device >= n) return fail(PK_GPU_ENODEV, "device %d out of range (%d visible)", device, n);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(PK_GPU_ENODEV, "device %d is %s; this library is built for gfx950 only",
+                    device, prop.gcnArchName);
+    g_device = device;
+    g_inited = true;
+    return PK_GPU_OK;
+}
+
+int ensure_init()
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    return init_locked(-1);
+}
+
+// The calling thread's context; creates it (and binds the device) on first use.
+int thread_ctx(ThreadCtx** out)
+{
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!t_ctx) {
+        hipError_t e = hipSetDevice(g_device);
+        if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+        ThreadCtx* c = new ThreadCtx;
+        e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete c;
+            return hip_fail(e, "hipStreamCreate");
+        }
+        t_ctx = c;
+    }
+    *out = t_ctx;
+    return PK_GPU_OK;
+}
+
+int staging(ThreadCtx* c, int slot, size_t bytes, void** out)
+{
+    if (bytes == 0) bytes = 4;
+    if (c->cap[slot] < bytes) {
+        if (c->buf[slot]) (void)hipFree(c->buf[slot]);
+        c->buf[slot] = nullptr;
+        c->cap[slot] = 0;
+        size_t want = bytes + bytes / 4;                 // grow with headroom
+        hipError_t e = hipMalloc(&c->buf[slot], want);
+        if (e != hipSuccess) return fail(PK_GPU_ENOMEM, "staging alloc of %zu bytes failed", want);
+        c->cap[slot] = want;
+    }
+    *out = c->buf[slot];
+    return PK_GPU_OK;
+}
+
+// Device copy of [host, host+need) if the whole range lies in one registered
+// weight, else nullptr.
+const void* resident(const void* host, size_t need)
+{
+    if (!host) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    const uintptr_t h = reinterpret_cast<uintptr_t>(host);
+    auto it = g_weights.upper_bound(h);
+    if (it == g_weights.begin()) return nullptr;
+    --it;
+    if (h >= it->first && h + need <= it->first + it->second.bytes)
+        return static_cast<const char*>(it->second.dev) + (h - it->first);
+    return nullptr;
+}
+
+// Operand rows x cols elements of elem bytes with row pitch ld: either its
+// resident copy (keeps pitch ld) or a packed staged copy (pitch cols).
+int operand(ThreadCtx* c, int slot, const void* host, int rows, int cols, int ld, size_t elem,
+            const void** dev, int* dev_ld)
+{
+    const size_t extent = rows > 0 ? ((size_t)(rows - 1) * ld + cols) * elem : 0;
+    if (const void* r = resident(host, extent)) {
+        *dev = r;
+        *dev_ld = ld;
+        return PK_GPU_OK;
+    }
+    void* d = nullptr;
+    int rc = staging(c, slot, (size_t)rows * cols * elem, &d);
+    if (rc) return rc;
+    if (rows > 0 && cols > 0) {
+        hipError_t e = hipMemcpy2DAsync(d, (size_t)cols * elem, host, (size_t)ld * elem,
+                                        (size_t)cols * elem, rows, hipMemcpyHostToDevice,
+                                        c->stream);
+        if (e != hipSuccess) return hip_fail(e, "operand upload");
+    }
+    *dev = d;
+    *dev_ld = cols;
+    return PK_GPU_OK;
+}
+
+int check_gemm(int M, int N, int K, int lda, int ldb_min, int ldb, int ldc)
+{
+    if (M < 0 || N < 0 || K < 0) return fail(PK_GPU_EINVAL, "negative size M=%d N=%d K=%d", M, N, K);
+    if (lda < (K > 1 ? K : 1)) return fail(PK_GPU_EINVAL, "lda=%d < K=%d", lda, K);
+    if (ldb < (ldb_min > 1 ? ldb_min : 1)) return fail(PK_GPU_EINVAL, "ldb=%d < %d", ldb, ldb_min);
+    if (ldc < (N > 1 ? N : 1)) return fail(PK_GPU_EINVAL, "ldc=%d < N=%d", ldc, N);
+    return PK_GPU_OK;
+}
+
+bool does_multiply(const GemmProblem& p)
+{
+    return p.M > 0 && p.N > 0 && p.K > 0 && p.alpha != 0.0f &&
+           !(p.kind == pkgpu::W_I8 && p.scale == 0.0f);
+}
+
+int launch(const GemmProblem& p, hipStream_t s)
+{
+    hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg);
+    if (e == hipErrorInvalidValue)
+        return fail(PK_GPU_EINVAL, "operand extent of %dx%dx%d GEMM exceeds 2 GiB", p.M, p.N, p.K);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return PK_GPU_OK;
+}
+
+// Host-pointer GEMM: stage what is not resident, run, copy C back, wait.
+int host_gemm(GemmProblem p, const float* hA, const void* hB, const float* hScales, float* hC,
+              size_t b_elem, int b_cols)
+{
+    if (p.M == 0 || p.N == 0) return PK_GPU_OK;              // scale_c loops are empty
+    const bool mul = does_multiply(p);
+    if (!mul && p.beta == 1.0f) return PK_GPU_OK;            // C unchanged
+    if (!hC) return fail(PK_GPU_EINVAL, "C is NULL");
+    if (mul && (!hA || !hB)) return fail(PK_GPU_EINVAL, "A or B is NULL");
+    if (mul && p.kind == pkgpu::W_I4 && !hScales) return fail(PK_GPU_EINVAL, "scales is NULL");
+
+    ThreadCtx* c = nullptr;
+    int rc = thread_ctx(&c);
+    if (rc) return rc;
+
+    if (mul) {
+        const void* dA = nullptr;
+        int lda = 0;
+        rc = operand(c, 0, hA, p.M, p.K, p.lda, sizeof(float), &dA, &lda);
+        if (rc) return rc;
+        p.A = static_cast<const float*>(dA);
+        p.lda = lda;
+        const void* dB = nullptr;
+        int ldb = 0;
+        rc = operand(c, 1, hB, p.K, b_cols, p.ldb, b_elem, &dB, &ldb);
+        if (rc) return rc;
+        p.B = dB;
+        p.ldb = ldb;
+        if (p.kind == pkgpu::W_I4) {
+            const void* dS = nullptr;
+            int lds = 0;
+            rc = operand(c, 3, hScales, p.K, p.N / 32, p.N / 32, sizeof(float), &dS, &lds);
+            if (rc) return rc;
+            p.scales = static_cast<const float*>(dS);
+        }
+    }
+    void* dC = nullptr;
+    rc = staging(c, 2, (size_t)p.M * p.N * sizeof(float), &dC);
+    if (rc) return rc;
+    hipError_t e;
+    if (p.beta != 0.0f) {
+        e = hipMemcpy2DAsync(dC, (size_t)p.N * 4, hC, (size_t)p.ldc * 4, (size_t)p.N * 4, p.M,
+                             hipMemcpyHostToDevice, c->stream);
+        if (e != hipSuccess) return hip_fail(e, "C upload");
+    }
+    const int ldc_host = p.ldc;
+    p.C = static_cast<float*>(dC);
+    p.ldc = p.N;
+    rc = launch(p, c->stream);
+    if (rc) return rc;
+    e = hipMemcpy2DAsync(hC, (size_t)ldc_host * 4, dC, (size_t)p.N * 4, (size_t)p.N * 4, p.M,
+                         hipMemcpyDeviceToHost, c->stream);
+    if (e != hipSuccess) return hip_fail(e, "C download");
+    e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(e, "stream synchronize");
+    return PK_GPU_OK;
+}
+
+// Device-pointer calls enqueue on the caller's stream; NULL is HIP's null
+// stream, as in every HIP API.  The calling thread is bound to the device.
+hipStream_t pick_stream(void* stream, int* rc)
+{
+    ThreadCtx* c = nullptr;
+    *rc = thread_ctx(&c);
+    return static_cast<hipStream_t>(stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int pk_gpu_init(int device)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_inited && device >= 0 && device != g_device)
+        return fail(PK_GPU_EINVAL, "already initialised on device %d", g_device);
+    return init_locked(device);
+}
+
+void pk_gpu_shutdown(void)
+{
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        for (auto& kv : g_weights) (void)hipFree(kv.second.dev);
+        g_weights.clear();
+        g_resident_bytes = 0;
+    }
+    if (t_ctx) {
+        (void)hipStreamSynchronize(t_ctx->stream);
+        for (int i = 0; i < 4; ++i)
+            if (t_ctx->buf[i]) (void)hipFree(t_ctx->buf[i]);
+        (void)hipStreamDestroy(t_ctx->stream);
+        delete t_ctx;
+        t_ctx = nullptr;
+    }
+}
+
+const char* pk_gpu_last_error(void) { return t_err.c_str(); }
+
+int pk_gpu_register_weight(const void* host, size_t bytes)
+{
+    if (!host || bytes == 0) return fail(PK_GPU_EINVAL, "register: NULL or empty range");
+    ThreadCtx* c = nullptr;
+    int rc = thread_ctx(&c);
+    if (rc) return rc;
+    const uintptr_t h = reinterpret_cast<uintptr_t>(host);
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_weights.upper_bound(h);
+        if (it != g_weights.end() && it->first < h + bytes)
+            return fail(PK_GPU_EINVAL, "register: range overlaps a registered weight");
+        if (it != g_weights.begin()) {
+            --it;
+            if (it->first + it->second.bytes > h)
+                return fail(PK_GPU_EINVAL, "register: range overlaps a registered weight");
+        }
+    }
+    void* d = nullptr;
+    hipError_t e = hipMalloc(&d, bytes);
+    if (e != hipSuccess) return fail(PK_GPU_ENOMEM, "register: device alloc of %zu bytes failed", bytes);
+    e = hipMemcpy(d, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return hip_fail(e, "register: upload");
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_weights[h] = Resident{bytes, d};
+    g_resident_bytes += bytes;
+    return PK_GPU_OK;
+}
+
+int pk_gpu_unregister_weight(const void* host)
+{
+    void* dev = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_weights.find(reinterpret_cast<uintptr_t>(host));
+        if (it == g_weights.end()) return fail(PK_GPU_EINVAL, "unregister: not registered");
+        dev = it->second.dev;
+        g_resident_bytes -= it->second.bytes;
+        g_weights.erase(it);
+    }
+    // Work already queued on any thread's stream may still read it.
+    (void)hipDeviceSynchronize();
+    (void)hipFree(dev);
+    return PK_GPU_OK;
+}
+
+const void* pk_gpu_device_ptr(const void* host) { return resident(host, 1); }
+
+size_t pk_gpu_resident_bytes(void)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    return g_resident_bytes;
+}
+
+int pk_gpu_gemm_i8(int M, int N, int K, float alpha, const float* A, int lda,
+                   const int8_t* B, float B_scale, int ldb, float beta, float* C, int ldc)
+{
+    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_I8, M, N, K, alpha, beta, nullptr, lda, nullptr, ldb,
+                  B_scale, nullptr, nullptr, ldc};
+    return host_gemm(p, A, B, nullptr, C, 1, N);
+}
+
+int pk_gpu_gemm_i4(int M, int N, int K, float alpha, const float* A, int lda,
+                   const uint8_t* B, const float* scales, int ldb, float beta, float* C, int ldc)
+{
+    if (N % 32 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is not a multiple of 32", N);
+    int rc = check_gemm(M, N, K, lda, N / 2, ldb, ldc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_I4, M, N, K, alpha, beta, nullptr, lda, nullptr, ldb,
+                  0.0f, nullptr, nullptr, ldc};
+    return host_gemm(p, A, B, scales, C, 1, N / 2);
+}
+
+int pk_gpu_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float* A,
+                 int lda, const float* B, int ldb, float beta, float* C, int ldc)
+{
+    if (transA != 111 || transB != 111)
+        return fail(PK_GPU_ENOTSUP, "sgemm: only NoTrans/NoTrans (111/111), got %d/%d", transA,
+                    transB);
+    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_F32, M, N, K, alpha, beta, nullptr, lda, nullptr, ldb,
+                  0.0f, nullptr, nullptr, ldc};
+    return host_gemm(p, A, B, nullptr, C, sizeof(float), N);
+}
+
+int pk_gpu_gemm_i8_dev(int M, int N, int K, float alpha, const float* dA, int lda,
+                       const int8_t* dB, float B_scale, int ldb, float beta, float* dC, int ldc,
+                       void* stream)
+{
+    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
+    if (rc) return rc;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_I8, M, N, K, alpha, beta, dA, lda, dB, ldb, B_scale, nullptr, dC, ldc};
+    return launch(p, s);
+}
+
+int pk_gpu_gemm_i4_dev(int M, int N, int K, float alpha, const float* dA, int lda,
+                       const uint8_t* dB, const float* dscales, int ldb, float beta, float* dC,
+                       int ldc, void* stream)
+{
+    if (N % 32 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is not a multiple of 32", N);
+    int rc = check_gemm(M, N, K, lda, N / 2, ldb, ldc);
+    if (rc) return rc;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_I4, M, N, K, alpha, beta, dA, lda, dB, ldb, 0.0f, dscales, dC, ldc};
+    return launch(p, s);
+}
+
+int pk_gpu_sgemm_dev(int M, int N, int K, float alpha, const float* dA, int lda, const float* dB,
+                     int ldb, float beta, float* dC, int ldc, void* stream)
+{
+    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
+    if (rc) return rc;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_F32, M, N, K, alpha, beta, dA, lda, dB, ldb, 0.0f, nullptr, dC, ldc};
+    return launch(p, s);
+}
+
+int pk_gpu_swish_dev(const float* dx, float* dy, long long n, void* stream)
+{
+    if (n < 0 || (n > 0 && (!dx || !dy))) return fail(PK_GPU_EINVAL, "swish: bad arguments");
+    int rc = 0;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    hipError_t e = pkgpu::launch_swish(dx, dy, n, s);
+    return e == hipSuccess ? PK_GPU_OK : hip_fail(e, "swish launch");
+}
+
+int pk_gpu_num_configs(void) { return pkgpu::num_configs(); }
+
+int pk_gpu_config_info(int index, int* mfma, int* cw, int* wgm, int* wgn)
+{
+    if (index < 0 || index >= pkgpu::num_configs()) return fail(PK_GPU_EINVAL, "no config %d", index);
+    pkgpu::TileConfig t = pkgpu::config_at(index);
+    if (mfma) *mfma = t.mfma;
+    if (cw) *cw = t.cw;
+    if (wgm) *wgm = t.wgm;
+    if (wgn) *wgn = t.wgn;
+    return PK_GPU_OK;
+}
+
+int pk_gpu_pick_config(int M, int N, int K)
+{
+    pkgpu::TileConfig t = pkgpu::choose_config(M, N, K);
+    for (int i = 0; i < pkgpu::num_configs(); ++i) {
+        pkgpu::TileConfig u = pkgpu::config_at(i);
+        if (u.mfma == t.mfma && u.cw == t.cw && u.wgm == t.wgm && u.wgn == t.wgn && u.kt == t.kt)
+            return i;
+    }
+    return 0;
+}
+
+int pk_gpu_force_config(int index)
+{
+    if (index >= pkgpu::num_configs()) return fail(PK_GPU_EINVAL, "no config %d", index);
+    t_force_cfg = index < 0 ? -1 : index;
+    return PK_GPU_OK;
+}
+
+}  // extern "C"

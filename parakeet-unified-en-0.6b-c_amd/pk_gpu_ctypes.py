@@ -1,0 +1,98 @@
+"""ctypes binding of libpk_gpu.so (include/pk_gpu.h) for Python callers.
+
+The library is C; this module only declares argument types and turns error
+codes into exceptions.  Device memory and streams may come from PyTorch
+(tensor.data_ptr(), torch.cuda.current_stream().cuda_stream); host-pointer
+calls take numpy arrays.  Importing this module never falls back to the CPU:
+if the shared library is missing, load() raises.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libpk_gpu.so")
+SHIM_PATH = os.path.join(LIB_DIR, "libpk_gpu_cblas.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "pk_gpu.h")
+
+NOTRANS = 111
+
+_i, _f, _p = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+_ll, _sz = ctypes.c_longlong, ctypes.c_size_t
+
+_PROTOS = {
+    "pk_gpu_init": (_i, [_i]),
+    "pk_gpu_shutdown": (None, []),
+    "pk_gpu_last_error": (ctypes.c_char_p, []),
+    "pk_gpu_register_weight": (_i, [_p, _sz]),
+    "pk_gpu_unregister_weight": (_i, [_p]),
+    "pk_gpu_device_ptr": (_p, [_p]),
+    "pk_gpu_resident_bytes": (_sz, []),
+    "pk_gpu_gemm_i8": (_i, [_i, _i, _i, _f, _p, _i, _p, _f, _i, _f, _p, _i]),
+    "pk_gpu_gemm_i4": (_i, [_i, _i, _i, _f, _p, _i, _p, _p, _i, _f, _p, _i]),
+    "pk_gpu_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
+    "pk_gpu_gemm_i8_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _f, _i, _f, _p, _i, _p]),
+    "pk_gpu_gemm_i4_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _p, _i, _f, _p, _i, _p]),
+    "pk_gpu_sgemm_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i, _p]),
+    "pk_gpu_swish_dev": (_i, [_p, _p, _ll, _p]),
+    "pk_gpu_num_configs": (_i, []),
+    "pk_gpu_config_info": (_i, [_i, _p, _p, _p, _p]),
+    "pk_gpu_pick_config": (_i, [_i, _i, _i]),
+    "pk_gpu_force_config": (_i, [_i]),
+}
+
+STATUS = {0: "OK", -1: "EINVAL", -2: "ENOTSUP", -3: "ENOMEM", -4: "EHIP", -5: "ENODEV"}
+
+
+class PkGpuError(RuntimeError):
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} -> {STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load():
+    """Load libpk_gpu.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} not built; run __graft_entry__.build()")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _PROTOS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(fn_name, rc):
+    if rc != 0:
+        msg = load().pk_gpu_last_error()
+        raise PkGpuError(fn_name, rc, msg.decode() if msg else "")
+    return rc
+
+
+def call(fn_name, *args):
+    """Call an int-returning entry point and raise on a non-zero status."""
+    return check(fn_name, getattr(load(), fn_name)(*args))
+
+
+def configs():
+    lib = load()
+    out = []
+    for i in range(lib.pk_gpu_num_configs()):
+        v = [ctypes.c_int() for _ in range(4)]
+        check("pk_gpu_config_info", lib.pk_gpu_config_info(i, *[ctypes.byref(x) for x in v]))
+        out.append(tuple(x.value for x in v))
+    return out
+
+
+def header_functions(path=HEADER):
+    """Function names declared in include/pk_gpu.h."""
+    import re
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pk_gpu_\w+)\s*\(", text)))

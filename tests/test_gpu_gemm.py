@@ -1,0 +1,287 @@
+"""GPU parity: every GEMM through the C ABI against the CPU oracle, bit for
+bit (the oracle is pinned to the compiled reference in test_oracle.py).
+
+Covers every kernel tile configuration, ragged M/N/K edges, alpha/beta
+variants, the int8 N%16 edge path, the host-pointer drop-in path (strided
+operands, resident and staged weights, weight-as-A pointwise convolution),
+the cblas_* shim, and the shapes of every workload: the int8 fused QKV
+(M=32/33), the int4 FFN pair (M=375), the fp32 FFN (M=500), the nine GEMMs
+of one conformer block (T=416), and the batched-chunk shapes (M=3312) by
+sampled rows (rows are independent, test_oracle.test_row_independence).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+from pkgpu import Dev, bits_equal, describe_mismatch, pk
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x5EED1000
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return Dev()
+
+
+def make(kind, M, N, K, tag, wstd=0.02):
+    A = po.normal((M, K), 0.0, 1.0, po.seed(SEED, f"{tag}.A"))
+    C0 = po.normal((M, N), 0.0, 1.0, po.seed(SEED, f"{tag}.C"))
+    if kind == "i4":
+        W = po.bytes_((K, N // 2), po.seed(SEED, f"{tag}.P"))
+        S = po.uniform((K, N // 32), 0.005, 0.02, po.seed(SEED, f"{tag}.S"))
+        return A, W, S, C0
+    if kind == "i8":
+        return A, po.int8s((K, N), -127, 127, po.seed(SEED, f"{tag}.Q")), 0.01, C0
+    return A, po.normal((K, N), 0.0, wstd, po.seed(SEED, f"{tag}.W")), None, C0
+
+
+def oracle(kind, A, W, extra, C0, alpha=1.0, beta=0.0):
+    C = C0.copy()
+    if kind == "i4":
+        return po.sgemm_q4b(A, W, extra, C, alpha, beta)
+    if kind == "i8":
+        return po.sgemm_qb(A, W, extra, C, alpha, beta)
+    return po.sgemm(A, W, C, alpha, beta)
+
+
+def run(dev, kind, A, W, extra, C0, alpha=1.0, beta=0.0, cfg=-1):
+    if kind == "i4":
+        return dev.gemm(kind, A, W, C0, alpha, beta, scales=extra, cfg=cfg)
+    if kind == "i8":
+        return dev.gemm(kind, A, W, C0, alpha, beta, scale=extra, cfg=cfg)
+    return dev.gemm(kind, A, W, C0, alpha, beta, cfg=cfg)
+
+
+def assert_same(got, want, what):
+    assert bits_equal(got, want), f"{what}: {describe_mismatch(got, want)}"
+
+
+# ---- every tile configuration, ragged shapes --------------------------------
+
+CFG_SHAPES = [(1, 32, 1), (5, 64, 37), (33, 96, 160), (64, 128, 64), (65, 160, 33),
+              (130, 256, 300)]
+
+
+@pytest.mark.parametrize("kind", ["f32", "i8", "i4"])
+@pytest.mark.parametrize("cfg", range(6))
+def test_tile_config_bit_exact(dev, cfg, kind):
+    for (M, N, K) in CFG_SHAPES:
+        A, W, extra, C0 = make(kind, M, N, K, f"cfg.{kind}.{M}.{N}.{K}")
+        got = run(dev, kind, A, W, extra, C0, cfg=cfg)
+        assert_same(got, oracle(kind, A, W, extra, C0), f"cfg{cfg} {kind} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("kind", ["f32", "i8", "i4"])
+def test_alpha_beta_variants(dev, kind):
+    M, N, K = 37, 96, 70
+    A, W, extra, C0 = make(kind, M, N, K, f"ab.{kind}")
+    for alpha, beta in [(0.75, 0.5), (1.0, 1.0), (1.0, -2.0), (0.0, 0.5), (0.0, 0.0), (2.5, 0.0)]:
+        got = run(dev, kind, A, W, extra, C0, alpha, beta)
+        assert_same(got, oracle(kind, A, W, extra, C0, alpha, beta), f"{kind} a={alpha} b={beta}")
+
+
+def test_int8_zero_scale_and_nan_clearing(dev):
+    M, N, K = 9, 64, 20
+    A, Q, _, C0 = make("i8", M, N, K, "nan")
+    C0[1, 3] = np.nan
+    got = run(dev, "i8", A, Q, 0.0, C0, 1.0, 0.5)   # scale 0: beta step only
+    assert_same(got, oracle("i8", A, Q, 0.0, C0, 1.0, 0.5), "scale 0")
+    got = run(dev, "i8", A, Q, 0.01, C0, 1.0, 0.0)  # beta 0 clears NaN
+    assert np.isfinite(got).all()
+    assert_same(got, oracle("i8", A, Q, 0.01, C0), "beta 0")
+
+
+@pytest.mark.parametrize("N", [8, 17, 31, 40, 1000, 3075])
+def test_int8_n_edge_columns(dev, N):
+    """N % 16 != 0 takes blas.c:733-755 for the last columns."""
+    M, K = 6, 129
+    A, Q, _, C0 = make("i8", M, N, K, f"edge.{N}")
+    for alpha, beta in [(1.0, 0.0), (0.75, 0.5)]:
+        got = run(dev, "i8", A, Q, 0.0123, C0, alpha, beta)
+        assert_same(got, oracle("i8", A, Q, 0.0123, C0, alpha, beta), f"int8 N={N}")
+
+
+@pytest.mark.parametrize("N", [8, 17, 408, 375])
+def test_fp32_n_edge_columns(dev, N):
+    M, K = 7, 96
+    A, W, _, C0 = make("f32", M, N, K, f"f32edge.{N}")
+    got = run(dev, "f32", A, W, None, C0, 1.0, 1.0)
+    assert_same(got, oracle("f32", A, W, None, C0, 1.0, 1.0), f"fp32 N={N}")
+
+
+# ---- workload shapes --------------------------------------------------------
+
+def test_int8_fused_qkv_clip(dev):
+    """int8 fused QKV of a 2.56 s clip: M=32 (and the real T'=33), K=1024, N=3072."""
+    for M in (32, 33):
+        A, Q, _, _ = make("i8", M, 3072, 1024, f"qkv.{M}")
+        Z = np.zeros((M, 3072), np.float32)
+        got = run(dev, "i8", A, Q, 0.01, Z)
+        assert_same(got, oracle("i8", A, Q, 0.01, Z), f"QKV M={M}")
+
+
+def test_int4_ffn_pair_30s(dev):
+    """int4 FFN pair at M=375: up (1024->4096), swish, down (4096->1024)."""
+    M = 375
+    A, P1, S1, _ = make("i4", M, 4096, 1024, "ffn.up")
+    _, P2, S2, _ = make("i4", 8, 1024, 4096, "ffn.down")
+    Z1 = np.zeros((M, 4096), np.float32)
+    h = run(dev, "i4", A, P1, S1, Z1)
+    assert_same(h, oracle("i4", A, P1, S1, Z1), "FFN up")
+    Z2 = np.zeros((M, 1024), np.float32)
+    out = run(dev, "i4", h, P2, S2, Z2)
+    assert_same(out, oracle("i4", h, P2, S2, Z2), "FFN down")
+
+
+def test_fp32_ffn_500(dev):
+    M = 500
+    A, W1, _, _ = make("f32", M, 4096, 1024, "f32ffn.up")
+    Z = np.zeros((M, 4096), np.float32)
+    h = run(dev, "f32", A, W1, None, Z)
+    assert_same(h, oracle("f32", A, W1, None, Z), "fp32 up")
+    _, W2, _, _ = make("f32", 4, 1024, 4096, "f32ffn.down")
+    Z2 = np.zeros((M, 1024), np.float32)
+    out = run(dev, "f32", h, W2, None, Z2)
+    assert_same(out, oracle("f32", h, W2, None, Z2), "fp32 down")
+
+
+BLOCK_GEMMS = [  # one conformer block at T=416 (encoder.c:193-198, 312, 360, 419, 455, 473)
+    ("i4", 416, 4096, 1024, "ff1.up"), ("i4", 416, 1024, 4096, "ff1.down"),
+    ("i8", 416, 3072, 1024, "qkv"), ("i8", 831, 1024, 1024, "pos"),
+    ("i8", 416, 1024, 1024, "out"),
+    ("f32", 2048, 416, 1024, "pw1"), ("f32", 1024, 416, 1024, "pw2"),
+    ("i4", 416, 4096, 1024, "ff2.up"), ("i4", 416, 1024, 4096, "ff2.down"),
+]
+
+
+@pytest.mark.parametrize("kind,M,N,K,name", BLOCK_GEMMS)
+def test_conformer_block_gemms(dev, kind, M, N, K, name):
+    A, W, extra, _ = make(kind, M, N, K, f"blk.{name}")
+    Z = np.zeros((M, N), np.float32)
+    assert_same(run(dev, kind, A, W, extra, Z), oracle(kind, A, W, extra, Z), name)
+
+
+@pytest.mark.parametrize("kind,N,K", [("i4", 4096, 1024), ("i4", 1024, 4096), ("i8", 3072, 1024),
+                                      ("f32", 1024, 1024)])
+def test_batched_chunks_sampled_rows(dev, kind, N, K):
+    """M = 3312 (2x408 + 6x416 rows): full GPU GEMM, oracle on sampled rows."""
+    M = 3312
+    A, W, extra, _ = make(kind, M, N, K, f"big.{kind}.{N}")
+    got = run(dev, kind, A, W, extra, np.zeros((M, N), np.float32))
+    rows = sorted({0, 1, 63, 64, 127, 128, 408, 1000, 2047, 2048, 3199, 3247, 3248, 3310, 3311})
+    Ar = np.ascontiguousarray(A[rows])
+    want = oracle(kind, Ar, W, extra, np.zeros((len(rows), N), np.float32))
+    assert_same(got[rows], want, f"M=3312 {kind} rows {rows}")
+    assert np.isfinite(got).all()
+
+
+# ---- host-pointer drop-in path ----------------------------------------------
+
+def _host_call(kind, M, N, K, A, lda, W, extra, C, ldc, alpha, beta):
+    lib = pk.load()
+    if kind == "i4":
+        rc = lib.pk_gpu_gemm_i4(M, N, K, alpha, A.ctypes.data, lda, W.ctypes.data,
+                                extra.ctypes.data, N // 2, beta, C.ctypes.data, ldc)
+    elif kind == "i8":
+        rc = lib.pk_gpu_gemm_i8(M, N, K, alpha, A.ctypes.data, lda, W.ctypes.data, extra, N,
+                                beta, C.ctypes.data, ldc)
+    else:
+        rc = lib.pk_gpu_sgemm(111, 111, M, N, K, alpha, A.ctypes.data, lda, W.ctypes.data, N,
+                              beta, C.ctypes.data, ldc)
+    pk.check("host gemm", rc)
+
+
+@pytest.mark.parametrize("kind", ["f32", "i8", "i4"])
+@pytest.mark.parametrize("resident", [False, True])
+def test_host_pointer_dropin_strided(dev, kind, resident):
+    """pk_gpu_gemm_* on host memory with lda > K and ldc > N, beta != 0;
+    with the weight staged per call or resident after registration."""
+    M, N, K = 45, 96, 130
+    lda, ldc = K + 7, N + 5
+    A, W, extra, C0 = make(kind, M, N, K, f"host.{kind}")
+    Apad = np.zeros((M, lda), np.float32)
+    Apad[:, :K] = A
+    Cpad = np.full((M, ldc), 3.5, np.float32)
+    Cpad[:, :N] = C0
+    regs = []
+    if resident:
+        for arr in ([W, extra] if kind == "i4" else [W]):
+            pk.call("pk_gpu_register_weight", arr.ctypes.data, arr.nbytes)
+            regs.append(arr)
+        assert pk.load().pk_gpu_device_ptr(W.ctypes.data)
+    try:
+        _host_call(kind, M, N, K, Apad, lda, W, extra, Cpad, ldc, 0.75, 0.5)
+    finally:
+        for arr in regs:
+            pk.call("pk_gpu_unregister_weight", arr.ctypes.data)
+    want = oracle(kind, A, W, extra, C0, 0.75, 0.5)
+    assert_same(Cpad[:, :N], want, f"host {kind} resident={resident}")
+    assert np.all(Cpad[:, N:] == 3.5), "columns beyond N were written"
+
+
+def test_pointwise_conv_weight_as_A(dev):
+    """pk_pointwise_conv1d: C[Cout][T] = W[Cout][Cin] * x[Cin][T] (tensor_ops.c:579-590),
+    with the weight registered as the A operand."""
+    Cout, Cin, T = 2048, 1024, 416
+    Wt = po.normal((Cout, Cin), 0.0, 0.02, po.seed(SEED, "pw.W"))
+    x = po.normal((Cin, T), 0.0, 1.0, po.seed(SEED, "pw.x"))
+    out = np.empty((Cout, T), np.float32)
+    pk.call("pk_gpu_register_weight", Wt.ctypes.data, Wt.nbytes)
+    try:
+        pk.call("pk_gpu_sgemm", 111, 111, Cout, T, Cin, 1.0, Wt.ctypes.data, Cin, x.ctypes.data,
+                T, 0.0, out.ctypes.data, T)
+    finally:
+        pk.call("pk_gpu_unregister_weight", Wt.ctypes.data)
+    want = po.sgemm(Wt, x, np.zeros((Cout, T), np.float32))
+    assert_same(out, want, "pointwise conv")
+
+
+def test_cblas_shim_symbols(dev):
+    """The drop-in library's cblas_* entry points (blas.h signatures)."""
+    shim = ctypes.CDLL(pk.SHIM_PATH)
+    f, i, p = ctypes.c_float, ctypes.c_int, ctypes.c_void_p
+    shim.cblas_sgemm.argtypes = [i, i, i, i, i, i, f, p, i, p, i, f, p, i]
+    shim.cblas_sgemm_qb.argtypes = [i, i, i, f, p, i, p, f, i, f, p, i]
+    shim.cblas_sgemm_q4b.argtypes = [i, i, i, f, p, i, p, p, i, f, p, i]
+    M, N, K = 33, 128, 96
+    for kind in ("f32", "i8", "i4"):
+        A, W, extra, C0 = make(kind, M, N, K, f"shim.{kind}")
+        C = C0.copy()
+        if kind == "f32":
+            shim.cblas_sgemm(101, 111, 111, M, N, K, 1.0, A.ctypes.data, K, W.ctypes.data, N,
+                             1.0, C.ctypes.data, N)
+        elif kind == "i8":
+            shim.cblas_sgemm_qb(M, N, K, 1.0, A.ctypes.data, K, W.ctypes.data, extra, N, 1.0,
+                                C.ctypes.data, N)
+        else:
+            shim.cblas_sgemm_q4b(M, N, K, 1.0, A.ctypes.data, K, W.ctypes.data,
+                                 extra.ctypes.data, N // 2, 1.0, C.ctypes.data, N)
+        assert_same(C, oracle(kind, A, W, extra, C0, 1.0, 1.0), f"shim {kind}")
+
+
+# ---- swish ------------------------------------------------------------------
+
+@pytest.mark.skipif(not po.have_ref(), reason="needs oracle/_ref")
+def test_swish_matches_reference_within_tolerance(dev):
+    """tensor_ops.c:367-389.  The reference divides with rcpps plus one Newton
+    step (CPU-model specific), so agreement is bounded, not exact:
+    |gpu - ref| <= 4 ulp(ref) + 1e-37, checked on 1.5M values incl. the
+    clamp range."""
+    n = 375 * 4096
+    x = po.normal((n,), 0.0, 4.0, po.seed(SEED, "swish.x"))
+    x[:16] = [0.0, -0.0, 1e-30, -1e-30, 87.0, -87.0, 88.0, -88.0, 200.0, -200.0,
+              1.0, -1.0, 20.0, -20.0, 3e-8, -3e-8]
+    dx = dev.put(x)
+    dy = dev.torch.empty_like(dx)
+    pk.call("pk_gpu_swish_dev", dx.data_ptr(), dy.data_ptr(), n, dev.stream())
+    dev.sync()
+    got = dy.cpu().numpy()
+    want = po.ref_swish(x)
+    ulp = np.spacing(np.abs(want).astype(np.float32))
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    worst = float(np.max(err / np.maximum(ulp, 1e-45)))
+    assert np.all(err <= 4 * ulp + 1e-37), f"worst {worst:.2f} ulp"

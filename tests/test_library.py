@@ -1,0 +1,87 @@
+"""CPU-side checks of the C-ABI libraries (no GPU needed): they load, export
+every entry point the headers declare, the drop-in shim exports the
+reference's three symbols, and without a gfx950 device every entry point
+fails loudly instead of computing on the CPU."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from pkgpu import ROOT, gpu_available, pk
+
+
+def test_libpk_gpu_exports_every_header_function():
+    lib = pk.load()
+    names = pk.header_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_shim_exports_reference_blas_symbols():
+    """libpk_gpu_cblas.so provides csrc/blas.h:38-69's weight GEMMs."""
+    out = subprocess.run(["nm", "-D", "--defined-only", pk.SHIM_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    defined = set(re.findall(r" T (\w+)", out))
+    assert {"cblas_sgemm", "cblas_sgemm_qb", "cblas_sgemm_q4b"} <= defined
+    # the shim must not carry a CPU GEMM of its own: it only forwards
+    assert not {"cblas_sgemv", "cblas_sgemm_st"} & defined
+    hdr = open(os.path.join(ROOT, "include", "pk_gpu_cblas.h")).read()
+    for sym in ("cblas_sgemm", "cblas_sgemm_qb", "cblas_sgemm_q4b"):
+        assert re.search(rf"\b{sym}\s*\(", hdr), sym
+
+
+def test_library_has_no_cpu_gemm_fallback():
+    """libpk_gpu.so links HIP and does not import the reference BLAS."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", pk.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    assert "cblas_" not in out
+    deps = subprocess.run(["ldd", pk.LIB_PATH], capture_output=True, text=True).stdout
+    assert "libamdhip64" in deps
+
+
+@pytest.mark.skipif(gpu_available(), reason="checks the no-device error path")
+def test_no_device_is_an_error_not_a_fallback():
+    lib = pk.load()
+    assert lib.pk_gpu_init(0) == -5          # PK_GPU_ENODEV
+    assert b"device" in lib.pk_gpu_last_error().lower() or lib.pk_gpu_last_error()
+    A = np.ones((2, 4), np.float32)
+    Q = np.ones((4, 16), np.int8)
+    C = np.full((2, 16), 7.0, np.float32)
+    rc = lib.pk_gpu_gemm_i8(2, 16, 4, 1.0, A.ctypes.data, 4, Q.ctypes.data, 0.5, 16, 0.0,
+                            C.ctypes.data, 16)
+    assert rc == -5
+    assert np.all(C == 7.0)                   # nothing was computed on the host
+
+
+def test_argument_validation_precedes_device_use():
+    lib = pk.load()
+    A = np.ones((2, 4), np.float32)
+    C = np.zeros((2, 64), np.float32)
+    P = np.zeros((4, 24), np.uint8)
+    S = np.ones((4, 2), np.float32)
+    # int4 needs N % 32 == 0 (the format's group size)
+    assert lib.pk_gpu_gemm_i4(2, 48, 4, 1.0, A.ctypes.data, 4, P.ctypes.data, S.ctypes.data,
+                              24, 0.0, C.ctypes.data, 64) == -1
+    assert b"multiple of 32" in lib.pk_gpu_last_error()
+    # transposed forms are not used by the reference call sites
+    assert lib.pk_gpu_sgemm(112, 111, 2, 4, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 4, 0.0,
+                            C.ctypes.data, 64) == -2
+    # strides shorter than a row
+    assert lib.pk_gpu_sgemm(111, 111, 2, 8, 4, 1.0, A.ctypes.data, 3, A.ctypes.data, 8, 0.0,
+                            C.ctypes.data, 64) == -1
+    assert lib.pk_gpu_gemm_i8(-1, 8, 4, 1.0, None, 4, None, 1.0, 8, 0.0, None, 8) == -1
+
+
+def test_tile_configs_are_well_formed():
+    cfgs = pk.configs()
+    assert len(cfgs) >= 3
+    for mf, cw, wgm, wgn in cfgs:
+        assert mf in (4, 16, 32) and cw >= 1 and wgm >= 1 and wgn >= 1
+        assert 64 * wgm * wgn <= 1024
+    lib = pk.load()
+    for shape in [(32, 3072, 1024), (375, 4096, 1024), (375, 1024, 4096), (3312, 4096, 1024)]:
+        assert 0 <= lib.pk_gpu_pick_config(*shape) < len(cfgs)
