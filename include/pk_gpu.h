@@ -113,10 +113,13 @@ int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);
 /* ---- tuning / introspection ------------------------------------------- */
 
 /* Number of kernel tile configurations, and a description of one:
+ * family ('R': rows on MFMA lanes, 'X': columns on lanes with A broadcast),
  * mfma (32, 16 or 4 = v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32),
- * MFMA column tiles per wave, waves along M and N per workgroup. */
+ * independent chains per wave, waves along M and N per workgroup, and k per
+ * LDS chunk.  Any pointer may be NULL. */
 int pk_gpu_num_configs(void);
-int pk_gpu_config_info(int index, int *mfma, int *cw, int *wgm, int *wgn);
+int pk_gpu_config_info(int index, int *family, int *mfma, int *cw, int *wgm, int *wgn,
+                       int *kt);
 /* Index of the configuration the dispatcher picks for a shape. */
 int pk_gpu_pick_config(int M, int N, int K);
 /* Force a configuration for later calls on this thread (-1 = automatic). */

@@ -29,14 +29,19 @@ struct GemmProblem {
 };
 
 // Kernel tile configuration chosen for a shape (see choose_config).
+//   family 'R': rows on MFMA lanes, one MFMA = 64 rows x mfma columns,
+//               cw column tiles (independent chains) per wave;
+//   family 'X': columns on MFMA lanes with A broadcast, one MFMA = mfma rows
+//               x 64 columns, cw row groups (independent chains) per wave.
 struct TileConfig {
+    char family;
     int mfma;   // 32, 16 or 4: v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32
-    int cw;     // MFMA column tiles per wave
+    int cw;     // independent chains (MFMA tiles) per wave
     int wgm;    // waves along M per workgroup
     int wgn;    // waves along N per workgroup
     int kt;     // k per LDS chunk
-    int bm() const { return 64 * wgm; }
-    int bn() const { return mfma * cw * wgn; }
+    int bm() const { return family == 'R' ? 64 * wgm : wgm * cw * mfma; }
+    int bn() const { return family == 'R' ? mfma * cw * wgn : 64 * wgn; }
 };
 
 // Pick the tile configuration with the lowest modelled time on 256 CUs.

@@ -198,7 +198,113 @@ template <> struct WStage<W_I4> {
     }
 };
 
-// ---- the chain GEMM ---------------------------------------------------------
+// ---- tile staging ------------------------------------------------------------
+// Stages one KT-deep chunk: A rows [m0, m0+BM) -> As[k*AS + m] as fl(alpha*a),
+// W columns [n0, n0+BN) -> Bs[k*BN + n] as dequantised fp32.  load() only
+// issues unconditional buffer loads (out-of-range -> 0) into raw registers;
+// store() runs after the current chunk's MFMAs, so the loads' latency
+// overlaps the multiplies.  Rows of A past M and columns of W past N only
+// feed outputs that are never stored, and k past K is never multiplied.
+
+template <int WK, int BM, int BN, int KT, int NT, int AS, bool VEC>
+struct Stager {
+    using WS = WStage<WK>;
+    static constexpr int VB = WS::VB;
+    static constexpr int A_PER = (BM * KT) / NT;
+    static constexpr int B_PER = (BN * KT) / NT;
+    static constexpr int A_UNITS = A_PER / 4;
+    static constexpr int B_UNITS = B_PER / VB;
+    static_assert((BM * KT) % NT == 0 && (BN * KT) % NT == 0, "tile/threads");
+    static_assert(A_PER % 4 == 0 && B_PER % VB == 0 && BN % VB == 0 && KT % 4 == 0, "units");
+
+    __amdgpu_buffer_rsrc_t rsA, rsB, rsS;
+    v4u ra4[VEC ? A_UNITS : 1];
+    float ra1[VEC ? 1 : A_PER];
+    typename WS::Unit rbu[VEC ? B_UNITS : 1];
+    typename WS::Elem rbe[VEC ? 1 : B_PER];
+
+    __device__ explicit Stager(const KArgs& p)
+        : rsA(make_rsrc(p.A, p.a_bytes)),
+          rsB(make_rsrc(p.B, p.b_bytes)),
+          rsS(make_rsrc(WK == W_I4 ? (const void*)p.scales : p.B, WK == W_I4 ? p.s_bytes : 0u)) {}
+
+    __device__ void load(const KArgs& p, int tid, int m0, int n0, int k0) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < A_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int row = e / (KT / 4), kq = e % (KT / 4);   // k fastest: coalesced rows
+                ra4[i] = ld_v4(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + 4 * kq) * 4u);
+            }
+#pragma unroll
+            for (int i = 0; i < B_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int kk = e / (BN / VB), nq = e % (BN / VB);  // n fastest
+                rbu[i] = WS::load_unit(p, rsB, rsS, k0 + kk, n0 + VB * nq);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_PER; ++i) {
+                const int e = tid + i * NT;
+                const int row = e / KT, kk = e % KT;
+                ra1[i] = ld_f32(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + kk) * 4u);
+            }
+#pragma unroll
+            for (int i = 0; i < B_PER; ++i) {
+                const int e = tid + i * NT;
+                const int kk = e / BN, n = e % BN;
+                rbe[i] = WS::load_elem(p, rsB, rsS, k0 + kk, n0 + n);
+            }
+        }
+    }
+
+    // fl(alpha*a) and the weight dequantisation happen here.
+    __device__ void store(const KArgs& p, int tid, float* As, float* Bs) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < A_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int row = e / (KT / 4), kq = e % (KT / 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    As[(4 * kq + j) * AS + row] = __fmul_rn(p.alpha, __uint_as_float(ra4[i][j]));
+            }
+#pragma unroll
+            for (int i = 0; i < B_UNITS; ++i) {
+                const int e = tid + i * NT;
+                const int kk = e / (BN / VB), nq = e % (BN / VB);
+                float w[VB];
+                WS::dequant_unit(p, rbu[i], w);
+#pragma unroll
+                for (int j = 0; j < VB; ++j) Bs[kk * BN + VB * nq + j] = w[j];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_PER; ++i) {
+                const int e = tid + i * NT;
+                As[(e % KT) * AS + e / KT] = __fmul_rn(p.alpha, ra1[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < B_PER; ++i) {
+                const int e = tid + i * NT;
+                Bs[e] = WS::dequant_elem(p, rbe[i], e % BN);        // [kk * BN + n]
+            }
+        }
+    }
+};
+
+// Chains start from beta*C exactly as scale_c leaves it (blas.c:89-99).
+__device__ inline float beta_c(const KArgs& p, int row, int col)
+{
+    if (p.beta == 0.0f || row >= p.M || col >= p.N) return 0.0f;
+    const float cv = p.C[(size_t)row * p.ldc + col];
+    return (p.beta == 1.0f) ? cv : __fmul_rn(cv, p.beta);
+}
+
+// ---- family R: rows on lanes ------------------------------------------------
+// Each MFMA covers 64 rows x NCOL columns (blocks stacked along M): A lane l
+// carries row l, B lane l carries column l % NCOL.  A wave owns CW column
+// tiles (CW independent chains); WGM x WGN waves share the staged tiles.
 
 template <int WK, int MF, int CW, int WGM, int WGN, int KT, bool VEC>
 __global__ __launch_bounds__(64 * WGM * WGN)
@@ -210,9 +316,6 @@ void chain_gemm(KArgs p)
     constexpr int AS = BM + 1;              // padded row of As: conflict-free stores
     constexpr int WN = T::NCOL * CW;
     constexpr int BN = WN * WGN;
-    constexpr int A_PER = (BM * KT) / NT;
-    constexpr int B_PER = (BN * KT) / NT;
-    static_assert((BM * KT) % NT == 0 && (BN * KT) % NT == 0, "tile/threads");
 
     __shared__ float As[2][KT * AS];
     __shared__ float Bs[2][KT * BN];
@@ -223,122 +326,25 @@ void chain_gemm(KArgs p)
     const int wm = wave / WGN, wn = wave % WGN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-    // Chains start from beta*C exactly as scale_c leaves it (blas.c:89-99).
     typename T::acc_t acc[CW];
 #pragma unroll
-    for (int c = 0; c < CW; ++c) {
+    for (int c = 0; c < CW; ++c)
 #pragma unroll
-        for (int r = 0; r < T::NACC; ++r) {
-            const int row = m0 + wm * 64 + T::row(lane, r);
-            const int col = n0 + wn * WN + c * T::NCOL + T::col(lane, r);
-            float v = 0.0f;
-            if (p.beta != 0.0f && row < p.M && col < p.N) {
-                const float cv = p.C[(size_t)row * p.ldc + col];
-                v = (p.beta == 1.0f) ? cv : __fmul_rn(cv, p.beta);
-            }
-            acc[c][r] = v;
-        }
-    }
+        for (int r = 0; r < T::NACC; ++r)
+            acc[c][r] = beta_c(p, m0 + wm * 64 + T::row(lane, r),
+                               n0 + wn * WN + c * T::NCOL + T::col(lane, r));
 
+    Stager<WK, BM, BN, KT, NT, AS, VEC> st(p);
     const int nchunks = (p.K + KT - 1) / KT;
-    using WS = WStage<WK>;
-    constexpr int VB = WS::VB;
-    constexpr int A_UNITS = A_PER / 4;
-    constexpr int B_UNITS = B_PER / VB;
-    static_assert(A_PER % 4 == 0 && B_PER % VB == 0 && BN % VB == 0 && KT % 4 == 0, "units");
-    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(p.A, p.a_bytes);
-    const __amdgpu_buffer_rsrc_t rsB = make_rsrc(p.B, p.b_bytes);
-    const __amdgpu_buffer_rsrc_t rsS = make_rsrc(WK == W_I4 ? (const void*)p.scales : p.B,
-                                                 WK == W_I4 ? p.s_bytes : 0u);
-    // Raw staging registers: the A words and the undecoded weight words of
-    // the next chunk, in the vector (VEC) or the scalar form.
-    v4u ra4[VEC ? A_UNITS : 1];
-    float ra1[VEC ? 1 : A_PER];
-    typename WS::Unit rbu[VEC ? B_UNITS : 1];
-    typename WS::Elem rbe[VEC ? 1 : B_PER];
-
-    // All loads are unconditional buffer loads (out-of-range -> 0); rows of A
-    // past M and columns of W past N only feed outputs that are never stored,
-    // and k past K is never multiplied (kn below).
-    auto load_chunk = [&](int ch) {
-        const int k0 = ch * KT;
-        if constexpr (VEC) {
-#pragma unroll
-            for (int i = 0; i < A_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int row = e / (KT / 4), kq = e % (KT / 4);
-                ra4[i] = ld_v4(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + 4 * kq) * 4u);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < A_PER; ++i) {
-                const int e = tid + i * NT;
-                const int row = e / KT, kk = e % KT;
-                ra1[i] = ld_f32(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + kk) * 4u);
-            }
-        }
-        if constexpr (VEC) {
-#pragma unroll
-            for (int i = 0; i < B_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int kk = e / (BN / VB), nq = e % (BN / VB);
-                rbu[i] = WS::load_unit(p, rsB, rsS, k0 + kk, n0 + VB * nq);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < B_PER; ++i) {
-                const int e = tid + i * NT;
-                const int kk = e / BN, n = e % BN;
-                rbe[i] = WS::load_elem(p, rsB, rsS, k0 + kk, n0 + n);
-            }
-        }
-    };
-    // fl(alpha*a) and the weight dequantisation happen here, then LDS stores.
-    auto store_chunk = [&](int buf) {
-        if constexpr (VEC) {
-#pragma unroll
-            for (int i = 0; i < A_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int row = e / (KT / 4), kq = e % (KT / 4);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    As[buf][(4 * kq + j) * AS + row] = __fmul_rn(p.alpha, __uint_as_float(ra4[i][j]));
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < A_PER; ++i) {
-                const int e = tid + i * NT;
-                As[buf][(e % KT) * AS + e / KT] = __fmul_rn(p.alpha, ra1[i]);
-            }
-        }
-        if constexpr (VEC) {
-#pragma unroll
-            for (int i = 0; i < B_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int kk = e / (BN / VB), nq = e % (BN / VB);
-                float w[VB];
-                WS::dequant_unit(p, rbu[i], w);
-#pragma unroll
-                for (int j = 0; j < VB; ++j) Bs[buf][kk * BN + VB * nq + j] = w[j];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < B_PER; ++i) {
-                const int e = tid + i * NT;
-                Bs[buf][e] = WS::dequant_elem(p, rbe[i], e % BN);   // [kk * BN + n]
-            }
-        }
-    };
-
     if (nchunks > 0) {
-        load_chunk(0);
-        store_chunk(0);
+        st.load(p, tid, m0, n0, 0);
+        st.store(p, tid, As[0], Bs[0]);
     }
     __syncthreads();
 
     for (int ch = 0; ch < nchunks; ++ch) {
         const int buf = ch & 1;
-        if (ch + 1 < nchunks) load_chunk(ch + 1);
+        if (ch + 1 < nchunks) st.load(p, tid, m0, n0, (ch + 1) * KT);
         const float* as = &As[buf][wm * 64 + lane];
         const float* bs = &Bs[buf][wn * WN + (lane % T::NCOL)];
         const int kn = min(KT, p.K - ch * KT);
@@ -377,7 +383,7 @@ void chain_gemm(KArgs p)
                     acc[c] = T::step(a, bs[kk * BN + c * T::NCOL], acc[c]);
             }
         }
-        if (ch + 1 < nchunks) store_chunk(buf ^ 1);
+        if (ch + 1 < nchunks) st.store(p, tid, As[buf ^ 1], Bs[buf ^ 1]);
         __syncthreads();
     }
 
@@ -388,6 +394,170 @@ void chain_gemm(KArgs p)
             const int row = m0 + wm * 64 + T::row(lane, r);
             const int col = n0 + wn * WN + c * T::NCOL + T::col(lane, r);
             if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[c][r];
+        }
+    }
+}
+
+// ---- family X: columns on lanes, A broadcast ---------------------------------
+// Each MFMA covers BS rows x 64 columns (blocks side by side along N): B lane
+// l carries column l, and A comes from one block only (CBSZ broadcast of
+// block ABID to all blocks), so a single A register holds NB = 64/BS
+// consecutive k steps (lane BS*t + i = A[row i][k + t]) and ABID = t picks
+// the step.  A wave owns R row groups (R independent chains) sharing each B
+// register; NWM x NWN waves share the staged tiles.
+
+template <int MF> struct MfmaX;
+
+template <> struct MfmaX<4> {
+    static constexpr int BS = 4, NB = 16, CBSZ = 4, NACC = 4;
+    using acc_t = v4f;
+    template <int T_>
+    __device__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, CBSZ, T_, 0);
+    }
+    __device__ static int row(int, int r) { return r; }
+    __device__ static int col(int l, int) { return l; }
+};
+
+template <> struct MfmaX<16> {
+    static constexpr int BS = 16, NB = 4, CBSZ = 2, NACC = 16;
+    using acc_t = v16f;
+    template <int T_>
+    __device__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, CBSZ, T_, 0);
+    }
+    __device__ static int row(int l, int r) { return 4 * (l >> 4) + (r & 3); }
+    __device__ static int col(int l, int r) { return 16 * (r >> 2) + (l & 15); }
+};
+
+template <> struct MfmaX<32> {
+    static constexpr int BS = 32, NB = 2, CBSZ = 1, NACC = 32;
+    using acc_t = v32f;
+    template <int T_>
+    __device__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, CBSZ, T_, 0);
+    }
+    __device__ static int row(int l, int r) { return 8 * ((r & 15) >> 2) + 4 * (l >> 5) + (r & 3); }
+    __device__ static int col(int l, int r) { return 32 * (r >> 4) + (l & 31); }
+};
+
+// Steps t = T_..NB-1 of one NB-block: MFMA with ABID = t for every row group
+// (ABID is an instruction field, so t must be a compile-time constant).
+template <typename T, int R, int T_>
+__device__ inline void x_steps(const float (&a)[R], const float* b, typename T::acc_t (&acc)[R])
+{
+    if constexpr (T_ < T::NB) {
+#pragma unroll
+        for (int g = 0; g < R; ++g) acc[g] = T::template step<T_>(a[g], b[T_], acc[g]);
+        x_steps<T, R, T_ + 1>(a, b, acc);
+    }
+}
+
+// The first n < NB steps only (partial last chunk).
+template <typename T, int R, int T_>
+__device__ inline void x_steps_n(const float (&a)[R], const float* b, typename T::acc_t (&acc)[R],
+                                 int n)
+{
+    if constexpr (T_ < T::NB) {
+        if (T_ < n) {
+#pragma unroll
+            for (int g = 0; g < R; ++g) acc[g] = T::template step<T_>(a[g], b[T_], acc[g]);
+            x_steps_n<T, R, T_ + 1>(a, b, acc, n);
+        }
+    }
+}
+
+template <int MF> struct XPad;                       // conflict-free A-register reads
+template <> struct XPad<4> { static constexpr int v = 4; };
+template <> struct XPad<16> { static constexpr int v = 16; };
+template <> struct XPad<32> { static constexpr int v = 0; };
+
+template <int WK, int MF, int R, int NWM, int NWN, int KT, bool VEC>
+__global__ __launch_bounds__(64 * NWM * NWN)
+void chain_gemm_x(KArgs p)
+{
+    using T = MfmaX<MF>;
+    constexpr int BS = T::BS, NB = T::NB;
+    constexpr int NT = 64 * NWM * NWN;
+    constexpr int BM = NWM * R * BS;
+    constexpr int BN = NWN * 64;
+    constexpr int AS = BM + XPad<MF>::v;
+    static_assert(KT % NB == 0, "chunk must hold whole A registers");
+
+    __shared__ float As[2][KT * AS];
+    __shared__ float Bs[2][KT * BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / NWN, wn = wave % NWN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int wrow = wm * R * BS;                  // wave's first row within the tile
+
+    typename T::acc_t acc[R];
+#pragma unroll
+    for (int g = 0; g < R; ++g)
+#pragma unroll
+        for (int r = 0; r < T::NACC; ++r)
+            acc[g][r] = beta_c(p, m0 + wrow + g * BS + T::row(lane, r),
+                               n0 + wn * 64 + T::col(lane, r));
+
+    Stager<WK, BM, BN, KT, NT, AS, VEC> st(p);
+    const int nchunks = (p.K + KT - 1) / KT;
+    if (nchunks > 0) {
+        st.load(p, tid, m0, n0, 0);
+        st.store(p, tid, As[0], Bs[0]);
+    }
+    __syncthreads();
+
+    // lane BS*t + i reads A[row i][k + t]
+    const int a_off = (lane / BS) * AS + wrow + (lane % BS);
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const int buf = ch & 1;
+        if (ch + 1 < nchunks) st.load(p, tid, m0, n0, (ch + 1) * KT);
+        const float* as = &As[buf][a_off];
+        const float* bs = &Bs[buf][wn * 64 + lane];
+        const int kn = min(KT, p.K - ch * KT);
+        if (kn == KT) {
+            // NB-blocks of k; the next block's operands are read while the
+            // current block is multiplied.
+            float a[2][R], b[2][NB];
+#pragma unroll
+            for (int g = 0; g < R; ++g) a[0][g] = as[g * BS];
+#pragma unroll
+            for (int t = 0; t < NB; ++t) b[0][t] = bs[t * BN];
+#pragma unroll
+            for (int kb = 0; kb < KT; kb += NB) {
+                const int cur = (kb / NB) & 1;
+                if (kb + NB < KT) {
+#pragma unroll
+                    for (int g = 0; g < R; ++g) a[cur ^ 1][g] = as[(kb + NB) * AS + g * BS];
+#pragma unroll
+                    for (int t = 0; t < NB; ++t) b[cur ^ 1][t] = bs[(kb + NB + t) * BN];
+                }
+                x_steps<T, R, 0>(a[cur], b[cur], acc);
+            }
+        } else {
+            for (int kb = 0; kb < kn; kb += NB) {
+                float a[R], b[NB];
+#pragma unroll
+                for (int g = 0; g < R; ++g) a[g] = as[kb * AS + g * BS];
+#pragma unroll
+                for (int t = 0; t < NB; ++t) b[t] = bs[(kb + t) * BN];
+                x_steps_n<T, R, 0>(a, b, acc, kn - kb);
+            }
+        }
+        if (ch + 1 < nchunks) st.store(p, tid, As[buf ^ 1], Bs[buf ^ 1]);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int g = 0; g < R; ++g) {
+#pragma unroll
+        for (int r = 0; r < T::NACC; ++r) {
+            const int row = m0 + wrow + g * BS + T::row(lane, r);
+            const int col = n0 + wn * 64 + T::col(lane, r);
+            if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[g][r];
         }
     }
 }
@@ -453,16 +623,28 @@ __global__ void swish(const float* x, float* y, long long n)
 
 // ---- configurations and dispatch -------------------------------------------
 
-// KT (k per LDS chunk) is sized so one chunk's MFMA time per wave (KT * cw *
-// cycles) covers the latency of the next chunk's loads.
-const TileConfig kConfigs[] = {
-    {32, 2, 2, 2, 32},    // 128 x 128, wave 64 x 64
-    {32, 1, 2, 2, 32},    // 128 x 64,  wave 64 x 32
-    {16, 2, 1, 4, 32},    //  64 x 128, wave 64 x 32
-    {16, 1, 1, 4, 64},    //  64 x 64,  wave 64 x 16
-    {4, 4, 1, 4, 64},     //  64 x 64,  wave 64 x 16
-    {4, 1, 1, 4, 128},    //  64 x 16,  wave 64 x 4
-};
+// KT (k per LDS chunk) is sized so one chunk's MFMA time per wave covers the
+// latency of the next chunk's loads.
+#define PK_CONFIGS(X)                                                       \
+    X(0, 'R', 32, 2, 2, 2, 32)   /* 128 x 128, wave 64 x 64            */  \
+    X(1, 'R', 32, 1, 2, 2, 32)   /* 128 x 64,  wave 64 x 32            */  \
+    X(2, 'R', 16, 2, 1, 4, 32)   /*  64 x 128, wave 64 x 32            */  \
+    X(3, 'R', 16, 1, 1, 4, 64)   /*  64 x 64,  wave 64 x 16            */  \
+    X(4, 'R', 4, 4, 1, 4, 64)    /*  64 x 64,  wave 64 x 16            */  \
+    X(5, 'R', 4, 1, 1, 4, 128)   /*  64 x 16,  wave 64 x 4             */  \
+    X(6, 'X', 4, 1, 4, 1, 64)    /*  16 x 64,  wave 4 x 64, 1 chain    */  \
+    X(7, 'X', 4, 2, 4, 1, 64)    /*  32 x 64,  wave 8 x 64, 2 chains   */  \
+    X(8, 'X', 4, 4, 4, 1, 64)    /*  64 x 64,  wave 16 x 64, 4 chains  */  \
+    X(9, 'X', 4, 2, 2, 2, 64)    /*  16 x 128, wave 8 x 64, 2 chains   */  \
+    X(10, 'X', 4, 8, 2, 2, 32)   /*  64 x 128, wave 32 x 64, 8 chains  */  \
+    X(11, 'X', 16, 1, 4, 1, 64)  /*  64 x 64,  wave 16 x 64            */  \
+    X(12, 'X', 16, 2, 2, 2, 32)  /*  64 x 128, wave 32 x 64, 2 chains  */  \
+    X(13, 'X', 16, 4, 2, 2, 32)  /* 128 x 128, wave 64 x 64, 4 chains  */  \
+    X(14, 'X', 32, 1, 4, 1, 32)  /* 128 x 64,  wave 32 x 64            */  \
+    X(15, 'X', 32, 2, 2, 2, 32)  /* 128 x 128, wave 64 x 64, 2 chains  */
+
+#define PK_CFG_ENTRY(i, fam, mf, c, wm, wn, kt) {fam, mf, c, wm, wn, kt},
+const TileConfig kConfigs[] = {PK_CONFIGS(PK_CFG_ENTRY)};
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
 template <int WK, bool VEC>
@@ -471,15 +653,18 @@ hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
     const TileConfig& t = kConfigs[cfg];
     dim3 grid((a.N + t.bn() - 1) / t.bn(), (a.M + t.bm() - 1) / t.bm());
     dim3 block(64 * t.wgm * t.wgn);
+#define PK_CFG_CASE(i, fam, mf, c, wm, wn, kt)                                            \
+    case i:                                                                               \
+        if constexpr (fam == 'R')                                                         \
+            hipLaunchKernelGGL((chain_gemm<WK, mf, c, wm, wn, kt, VEC>), grid, block, 0, s, a); \
+        else                                                                              \
+            hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, VEC>), grid, block, 0, s, a); \
+        break;
     switch (cfg) {
-    case 0: hipLaunchKernelGGL((chain_gemm<WK, 32, 2, 2, 2, 32, VEC>), grid, block, 0, s, a); break;
-    case 1: hipLaunchKernelGGL((chain_gemm<WK, 32, 1, 2, 2, 32, VEC>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((chain_gemm<WK, 16, 2, 1, 4, 32, VEC>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((chain_gemm<WK, 16, 1, 1, 4, 64, VEC>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((chain_gemm<WK, 4, 4, 1, 4, 64, VEC>), grid, block, 0, s, a); break;
-    case 5: hipLaunchKernelGGL((chain_gemm<WK, 4, 1, 1, 4, 128, VEC>), grid, block, 0, s, a); break;
+        PK_CONFIGS(PK_CFG_CASE)
     default: return hipErrorInvalidValue;
     }
+#undef PK_CFG_CASE
     return hipGetLastError();
 }
 
@@ -490,37 +675,30 @@ hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
                                 : launch_chain<WK, false>(cfg, a, s);
 }
 
-int mfma_cycles(int mf) { return mf == 32 ? 64 : mf == 16 ? 32 : 8; }
-
 }  // namespace
 
 int num_configs() { return kNumConfigs; }
 TileConfig config_at(int i) { return kConfigs[i]; }
 
-// Modelled time: waves are independent k-chains, one MFMA pipe per SIMD
-// (1024 SIMDs on 256 CUs), each k step costs the wave's MFMA cycles or its
-// share of the CU's LDS reads, whichever is larger.
+// Every output is a chain of K dependent MFMA steps, so the work that can run
+// at once is the number of independent chains (M*N / outputs per MFMA).
+// Measured on MI355X (bench sweep over the encoder's GEMM shapes):
+//   M*N <  600K  -> config 6 (X, 4x4, 1 chain/wave): most waves, shortest tiles
+//   M*N < 1.8M   -> config 7 (X, 4x4, 2 chains/wave)
+//   otherwise    -> config 3 (R, 16x16, 64x64 tiles): MFMA-throughput bound
 TileConfig choose_config(int M, int N, int K)
 {
-    int best = 0;
-    double best_t = 1e300;
-    for (int i = 0; i < kNumConfigs; ++i) {
-        const TileConfig& t = kConfigs[i];
-        const double tiles = (double)((M + t.bm() - 1) / t.bm()) * ((N + t.bn() - 1) / t.bn());
-        const double waves = tiles * t.wgm * t.wgn;
-        const double rounds = std::ceil(waves / 1024.0);
-        const double mfma_k = (double)t.cw * mfma_cycles(t.mfma);
-        const double lds_k = 4.0 * (2.0 + 2.0 * t.cw);
-        const double est = rounds * (double)K * std::max(mfma_k, lds_k);
-        if (est < best_t * 0.999) { best_t = est; best = i; }
-    }
-    return kConfigs[best];
+    (void)K;
+    const double outputs = (double)M * (double)N;
+    if (outputs < 600e3) return kConfigs[6];
+    if (outputs < 1.8e6) return kConfigs[7];
+    return kConfigs[3];
 }
 
 static int config_index(const TileConfig& c)
 {
     for (int i = 0; i < kNumConfigs; ++i)
-        if (kConfigs[i].mfma == c.mfma && kConfigs[i].cw == c.cw &&
+        if (kConfigs[i].family == c.family && kConfigs[i].mfma == c.mfma && kConfigs[i].cw == c.cw &&
             kConfigs[i].wgm == c.wgm && kConfigs[i].wgn == c.wgn && kConfigs[i].kt == c.kt)
             return i;
     return 0;

@@ -429,10 +429,12 @@ int pk_gpu_swish_dev(const float* dx, float* dy, long long n, void* stream)
 
 int pk_gpu_num_configs(void) { return pkgpu::num_configs(); }
 
-int pk_gpu_config_info(int index, int* mfma, int* cw, int* wgm, int* wgn)
+int pk_gpu_config_info(int index, int* family, int* mfma, int* cw, int* wgm, int* wgn, int* kt)
 {
     if (index < 0 || index >= pkgpu::num_configs()) return fail(PK_GPU_EINVAL, "no config %d", index);
     pkgpu::TileConfig t = pkgpu::config_at(index);
+    if (family) *family = t.family;
+    if (kt) *kt = t.kt;
     if (mfma) *mfma = t.mfma;
     if (cw) *cw = t.cw;
     if (wgm) *wgm = t.wgm;
@@ -445,7 +447,8 @@ int pk_gpu_pick_config(int M, int N, int K)
     pkgpu::TileConfig t = pkgpu::choose_config(M, N, K);
     for (int i = 0; i < pkgpu::num_configs(); ++i) {
         pkgpu::TileConfig u = pkgpu::config_at(i);
-        if (u.mfma == t.mfma && u.cw == t.cw && u.wgm == t.wgm && u.wgn == t.wgn && u.kt == t.kt)
+        if (u.family == t.family && u.mfma == t.mfma && u.cw == t.cw && u.wgm == t.wgm &&
+            u.wgn == t.wgn && u.kt == t.kt)
             return i;
     }
     return 0;

@@ -36,7 +36,7 @@ _PROTOS = {
     "pk_gpu_sgemm_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i, _p]),
     "pk_gpu_swish_dev": (_i, [_p, _p, _ll, _p]),
     "pk_gpu_num_configs": (_i, []),
-    "pk_gpu_config_info": (_i, [_i, _p, _p, _p, _p]),
+    "pk_gpu_config_info": (_i, [_i, _p, _p, _p, _p, _p, _p]),
     "pk_gpu_pick_config": (_i, [_i, _i, _i]),
     "pk_gpu_force_config": (_i, [_i]),
 }
@@ -54,11 +54,21 @@ _lib = None
 
 
 def load():
-    """Load libpk_gpu.so (raises if it was not built)."""
+    """Load libpk_gpu.so (raises if it was not built).
+
+    PyTorch ships its own libamdhip64.so with the same SONAME as ROCm's
+    (libamdhip64.so.7).  Importing torch first lets the library's HIP
+    dependency bind to that copy, so the process holds one HIP runtime and
+    torch's device pointers, streams and events are valid here; loading the
+    library first would bring in a second runtime."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} not built; run __graft_entry__.build()")
+        try:
+            import torch  # noqa: F401  (one HIP runtime per process, see above)
+        except ImportError:
+            pass
         lib = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in _PROTOS.items():
             fn = getattr(lib, name)
@@ -84,9 +94,10 @@ def configs():
     lib = load()
     out = []
     for i in range(lib.pk_gpu_num_configs()):
-        v = [ctypes.c_int() for _ in range(4)]
+        v = [ctypes.c_int() for _ in range(6)]
         check("pk_gpu_config_info", lib.pk_gpu_config_info(i, *[ctypes.byref(x) for x in v]))
-        out.append(tuple(x.value for x in v))
+        fam, mf, cw, wgm, wgn, kt = (x.value for x in v)
+        out.append((chr(fam), mf, cw, wgm, wgn, kt))
     return out
 
 

@@ -63,11 +63,11 @@ def assert_same(got, want, what):
 # ---- every tile configuration, ragged shapes --------------------------------
 
 CFG_SHAPES = [(1, 32, 1), (5, 64, 37), (33, 96, 160), (64, 128, 64), (65, 160, 33),
-              (130, 256, 300)]
+              (130, 256, 300), (17, 192, 1030)]
 
 
 @pytest.mark.parametrize("kind", ["f32", "i8", "i4"])
-@pytest.mark.parametrize("cfg", range(6))
+@pytest.mark.parametrize("cfg", range(len(pk.configs())))
 def test_tile_config_bit_exact(dev, cfg, kind):
     for (M, N, K) in CFG_SHAPES:
         A, W, extra, C0 = make(kind, M, N, K, f"cfg.{kind}.{M}.{N}.{K}")
