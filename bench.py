@@ -79,6 +79,18 @@ def cpu_baseline(po, X, P1, S1, P2, S2, budget_s):
             "ms_per_step": round(1000 * el / n, 3)}
 
 
+def copy_calibration():
+    """10 torch device copies of 256 MiB: each reads and writes exactly
+    268,435,456 bytes, which scales the traffic counters."""
+    import torch
+    src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": src.numel() * 4, "copies": 10}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,7 +99,13 @@ def main():
     ap.add_argument("--replicas", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 10 plain 256 MiB device-to-device copies (the reference "
+                         "reading for FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (single-GPU hot path; "
               "multi-GPU sharding is a design note, not built)", file=sys.stderr)

@@ -1,0 +1,419 @@
+/*  ref_encode_main.c - end-to-end driver around the reference engine.
+ *
+ *  TEST INFRASTRUCTURE ONLY.  Built by oracle/Makefile into oracle/_ref/:
+ *    pk_encode_gpu      reference host code, weight GEMMs from the GPU
+ *                       drop-in (libpk_gpu_cblas.so), weights registered
+ *    pk_encode_ref      reference host code, weight GEMMs from blas.c's
+ *                       portable path (the NEON path's arithmetic)
+ *    pk_encode_ref_x86  the reference exactly as its Makefile builds it on
+ *                       x86 (AVX2 weight GEMMs, incl. its int4 unpack)
+ *  All three share every other object (attention GEMMs and sgemv from
+ *  blas.c's AVX2 path, tensor ops, weights.c, decoder.c), so any difference
+ *  in their outputs comes from the weight GEMMs alone.
+ *
+ *  It writes a synthetic mixed int4/int8/fp32 model in the reference's
+ *  on-disk format (weights.bin + weights.json, extract_weights.py:894-935),
+ *  loads it with pk_load_weights (which also builds the fused int8 QKV with
+ *  its requantisation, weights.c:404-487), feeds N(0,1) features straight
+ *  into the conformer blocks (the input of encoder.c:495/514, after
+ *  pre-encode), runs the chunked or full encoder exactly as pk_encoder
+ *  would choose (encoder.c:602-610), then the greedy RNN-T decoder
+ *  (decoder.c:80-132), and prints one JSON line with hashes of the encoder
+ *  output and of the token ids.
+ *
+ *  This translation unit includes the reference's encoder.c so that its
+ *  static encode_blocks / encode_blocks_chunked can be called directly.
+ */
+#define _GNU_SOURCE
+#include "encoder.c"
+
+#include "pk_oracle.h"
+
+#include <stdint.h>
+#include <time.h>
+#include <unistd.h>
+#include <xmmintrin.h>
+
+/* PK_DEBUG=1 prints the SSE control word (FTZ/DAZ, rounding) per stage and
+ * hashes of the decoder inputs and of the first joint logits. */
+static void fpenv(const char *stage)
+{
+    if (getenv("PK_DEBUG")) fprintf(stderr, "mxcsr %-14s %08x\n", stage, _mm_getcsr());
+}
+
+#ifdef PK_GPU_REGISTER
+#include "pk_gpu.h"
+#endif
+
+#define SEED_BASE 0x5EED0004ull   /* workload: full encoder */
+
+/* ---- weights.bin / weights.json writer ----------------------------------- */
+
+typedef struct {
+    FILE *bin, *json;
+    long long off;
+    int n;
+} Writer;
+
+static void w_entry_head(Writer *w, const char *name)
+{
+    fprintf(w->json, "%s\n  \"%s\": {", w->n++ ? "," : "", name);
+}
+
+static void w_f32(Writer *w, const char *name, const float *x, size_t n)
+{
+    w_entry_head(w, name);
+    fprintf(w->json, "\"offset\": %lld, \"numel\": %zu, \"dtype\": \"float32\"}", w->off, n);
+    fwrite(x, 4, n, w->bin);
+    w->off += (long long)n * 4;
+}
+
+static void w_i8(Writer *w, const char *name, const int8_t *q, size_t n, float scale)
+{
+    w_entry_head(w, name);
+    fprintf(w->json, "\"offset\": %lld, \"numel\": %zu, \"dtype\": \"int8\", \"scale\": %.9g}",
+            w->off, n, scale);
+    fwrite(q, 1, n, w->bin);
+    w->off += (long long)n;
+}
+
+static void w_i4(Writer *w, const char *name, const uint8_t *p, size_t nbytes,
+                 const float *s, size_t ns)
+{
+    w_entry_head(w, name);
+    fprintf(w->json, "\"offset\": %lld, \"numel\": %zu, \"dtype\": \"int4\", "
+                     "\"scales_offset\": %lld, \"n_scales\": %zu}",
+            w->off, nbytes, w->off + (long long)nbytes, ns);
+    fwrite(p, 1, nbytes, w->bin);
+    fwrite(s, 4, ns, w->bin);
+    w->off += (long long)nbytes + (long long)ns * 4;
+}
+
+static float *scratch_f;
+static size_t scratch_n;
+static float *fbuf(size_t n)
+{
+    if (n > scratch_n) {
+        free(scratch_f);
+        scratch_f = (float *)malloc(n * sizeof(float));
+        scratch_n = n;
+    }
+    return scratch_f;
+}
+
+static void g_normal(Writer *w, const char *name, size_t n, float std)
+{
+    float *x = fbuf(n);
+    pkor_fill_normal(x, n, 0.0f, std, pkor_seed(SEED_BASE, name));
+    w_f32(w, name, x, n);
+}
+
+static void g_const(Writer *w, const char *name, size_t n, float v)
+{
+    float *x = fbuf(n);
+    for (size_t i = 0; i < n; i++) x[i] = v;
+    w_f32(w, name, x, n);
+}
+
+static void g_int8(Writer *w, const char *name, size_t n, float scale)
+{
+    int8_t *q = (int8_t *)malloc(n);
+    pkor_fill_int8(q, n, -127, 127, pkor_seed(SEED_BASE, name));
+    w_i8(w, name, q, n, scale);
+    free(q);
+}
+
+static void g_int4(Writer *w, const char *name, int K, int N)
+{
+    size_t nb = (size_t)K * N / 2, ns = (size_t)K * (N / 32);
+    uint8_t *p = (uint8_t *)malloc(nb);
+    char sname[256];
+    snprintf(sname, sizeof sname, "%s#scales", name);
+    pkor_fill_bytes(p, nb, pkor_seed(SEED_BASE, name));
+    float *s = fbuf(ns);
+    pkor_fill_uniform(s, ns, 0.005f, 0.02f, pkor_seed(SEED_BASE, sname));
+    w_i4(w, name, p, nb, s, ns);
+    free(p);
+}
+
+/* A mixed-mode model at the statistics of the benchmark workloads:
+ * int4 FF linears, int8 attention and pre-encode projections (Q/K/V with
+ * different scales, so the fused-QKV requantisation runs), fp32 elsewhere. */
+static int write_model(const char *dir)
+{
+    char bin[512], json[512], nm[256];
+    snprintf(bin, sizeof bin, "%s/weights.bin", dir);
+    snprintf(json, sizeof json, "%s/weights.json", dir);
+    Writer w = {fopen(bin, "wb"), fopen(json, "w"), 0, 0};
+    if (!w.bin || !w.json) return -1;
+    fprintf(w.json, "{");
+
+    const char *convs[] = {"0", "2", "3", "5", "6"};
+    const int conv_n[] = {256 * 9, 256 * 9, 256 * 256, 256 * 9, 256 * 256};
+    for (int c = 0; c < 5; c++) {
+        snprintf(nm, sizeof nm, "pre_encode.conv.%s.weight", convs[c]);
+        g_normal(&w, nm, conv_n[c], 0.1f);
+        snprintf(nm, sizeof nm, "pre_encode.conv.%s.bias", convs[c]);
+        g_normal(&w, nm, 256, 0.02f);
+    }
+    g_int8(&w, "pre_encode.out.weight", (size_t)4096 * 1024, 0.01f);
+    g_normal(&w, "pre_encode.out.bias", 1024, 0.02f);
+
+    {   /* sinusoidal relative-position table centred at PK_PE_CENTER */
+        size_t n = (size_t)PK_PE_TABLE_SIZE * PK_D_MODEL;
+        float *pe = fbuf(n);
+        for (int p = 0; p < PK_PE_TABLE_SIZE; p++) {
+            double pos = (double)(PK_PE_CENTER - p);
+            for (int i = 0; i < PK_D_MODEL / 2; i++) {
+                double div = exp(-(2.0 * i) * log(10000.0) / PK_D_MODEL);
+                pe[(size_t)p * PK_D_MODEL + 2 * i] = (float)sin(pos * div);
+                pe[(size_t)p * PK_D_MODEL + 2 * i + 1] = (float)cos(pos * div);
+            }
+        }
+        w_f32(&w, "pos_encoding.pe_table", pe, n);
+    }
+
+    const char *norms[] = {"norm_feed_forward1", "norm_self_att", "norm_conv",
+                           "norm_feed_forward2", "norm_out"};
+    for (int b = 0; b < PK_N_BLOCKS; b++) {
+        for (int k = 0; k < 5; k++) {
+            snprintf(nm, sizeof nm, "layers.%d.%s.weight", b, norms[k]);
+            g_const(&w, nm, 1024, 1.0f);
+            snprintf(nm, sizeof nm, "layers.%d.%s.bias", b, norms[k]);
+            g_const(&w, nm, 1024, 0.0f);
+        }
+        for (int f = 1; f <= 2; f++) {
+            snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear1.weight", b, f);
+            g_int4(&w, nm, 1024, 4096);
+            snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear1.bias", b, f);
+            g_normal(&w, nm, 4096, 0.02f);
+            snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear2.weight", b, f);
+            g_int4(&w, nm, 4096, 1024);
+            snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear2.bias", b, f);
+            g_normal(&w, nm, 1024, 0.02f);
+        }
+        const char *proj[] = {"linear_q", "linear_k", "linear_v", "linear_pos", "linear_out"};
+        const float pscale[] = {0.0100f, 0.0110f, 0.0090f, 0.0100f, 0.0100f};
+        for (int k = 0; k < 5; k++) {
+            snprintf(nm, sizeof nm, "layers.%d.self_attn.%s.weight", b, proj[k]);
+            g_int8(&w, nm, (size_t)1024 * 1024, pscale[k]);
+            if (k != 3) {
+                snprintf(nm, sizeof nm, "layers.%d.self_attn.%s.bias", b, proj[k]);
+                g_normal(&w, nm, 1024, 0.02f);
+            }
+        }
+        snprintf(nm, sizeof nm, "layers.%d.self_attn.pos_bias_u", b);
+        g_normal(&w, nm, 1024, 0.02f);
+        snprintf(nm, sizeof nm, "layers.%d.self_attn.pos_bias_v", b);
+        g_normal(&w, nm, 1024, 0.02f);
+        snprintf(nm, sizeof nm, "layers.%d.conv.pointwise_conv1.weight", b);
+        g_normal(&w, nm, (size_t)2048 * 1024, 0.02f);
+        snprintf(nm, sizeof nm, "layers.%d.conv.pointwise_conv1.bias", b);
+        g_normal(&w, nm, 2048, 0.02f);
+        snprintf(nm, sizeof nm, "layers.%d.conv.depthwise_conv.weight", b);
+        g_normal(&w, nm, (size_t)1024 * 9, 1.0f / 3.0f);
+        snprintf(nm, sizeof nm, "layers.%d.conv.depthwise_conv.bias", b);
+        g_normal(&w, nm, 1024, 0.02f);
+        snprintf(nm, sizeof nm, "layers.%d.conv.pointwise_conv2.weight", b);
+        g_normal(&w, nm, (size_t)1024 * 1024, 0.02f);
+        snprintf(nm, sizeof nm, "layers.%d.conv.pointwise_conv2.bias", b);
+        g_normal(&w, nm, 1024, 0.02f);
+    }
+
+    g_normal(&w, "decoder.prediction.embed.weight", (size_t)1025 * 640, 0.5f);
+    for (int l = 0; l < 2; l++) {
+        snprintf(nm, sizeof nm, "decoder.lstm.%d.W_i", l);
+        g_normal(&w, nm, (size_t)2560 * 640, 0.05f);
+        snprintf(nm, sizeof nm, "decoder.lstm.%d.W_r", l);
+        g_normal(&w, nm, (size_t)2560 * 640, 0.05f);
+        snprintf(nm, sizeof nm, "decoder.lstm.%d.B", l);
+        g_normal(&w, nm, 5120, 0.02f);
+    }
+    g_normal(&w, "joint.enc.weight", (size_t)1024 * 640, 0.05f);
+    g_normal(&w, "joint.enc.bias", 640, 0.02f);
+    g_normal(&w, "joint.pred.weight", (size_t)640 * 640, 0.05f);
+    g_normal(&w, "joint.pred.bias", 640, 0.02f);
+    {   /* output projection [640][1025]; each token's column is centred so the
+         * positive mean of relu(hidden) adds no frame-independent offset and
+         * the argmax follows the encoder frame */
+        float *o = fbuf((size_t)640 * 1025);
+        pkor_fill_normal(o, (size_t)640 * 1025, 0.0f, 0.03f, pkor_seed(SEED_BASE, "joint.out.weight"));
+        for (int v = 0; v < 1025; v++) {
+            double mean = 0.0;
+            for (int j = 0; j < 640; j++) mean += o[(size_t)j * 1025 + v];
+            mean /= 640.0;
+            for (int j = 0; j < 640; j++) o[(size_t)j * 1025 + v] -= (float)mean;
+        }
+        w_f32(&w, "joint.out.weight", o, (size_t)640 * 1025);
+    }
+    {   /* output bias: small noise, blank raised so frames emit 0..10 symbols */
+        float *b = fbuf(1025);
+        pkor_fill_normal(b, 1025, 0.0f, 0.02f, pkor_seed(SEED_BASE, "joint.joint_net.2.bias"));
+        b[PK_BLANK] += 2.0f;
+        w_f32(&w, "joint.joint_net.2.bias", b, 1025);
+    }
+
+    fprintf(w.json, "\n}\n");
+    int bad = ferror(w.bin) || ferror(w.json);
+    fclose(w.bin);
+    fclose(w.json);
+    return bad ? -1 : 0;
+}
+
+#ifdef PK_GPU_REGISTER
+/* What an integration adds after pk_load_weights: make every weight-GEMM
+ * operand resident once (int4 data + scales, int8 data incl. the fused QKV
+ * built at load time, fp32 pointwise-conv weights that enter as A). */
+static int reg(const void *p, size_t bytes)
+{
+    int rc = pk_gpu_register_weight(p, bytes);
+    if (rc) fprintf(stderr, "pk_gpu_register_weight: %s\n", pk_gpu_last_error());
+    return rc;
+}
+
+static int register_weight(const Weight *w, size_t K, size_t N)
+{
+    if (w->bits == 4)
+        return reg(w->data, K * N / 2) || reg(w->scales, K * (N / 32) * sizeof(float));
+    if (w->bits == 8) return reg(w->data, K * N);
+    return reg(w->data, K * N * sizeof(float));
+}
+
+static int register_model(const PkModel *m)
+{
+    int rc = register_weight(&m->enc.pre_encode.out_w, 4096, 1024);
+    for (int b = 0; b < PK_N_BLOCKS && !rc; b++) {
+        const ConformerBlock *k = &m->enc.blocks[b];
+        rc = register_weight(&k->ff1.linear1_w, 1024, 4096) ||
+             register_weight(&k->ff1.linear2_w, 4096, 1024) ||
+             register_weight(&k->ff2.linear1_w, 1024, 4096) ||
+             register_weight(&k->ff2.linear2_w, 4096, 1024) ||
+             register_weight(&k->mha.linear_qkv_w, 1024, 3072) ||
+             register_weight(&k->mha.linear_pos_w, 1024, 1024) ||
+             register_weight(&k->mha.linear_out_w, 1024, 1024) ||
+             reg(k->conv.pw1_w, (size_t)2048 * 1024 * sizeof(float)) ||
+             reg(k->conv.pw2_w, (size_t)1024 * 1024 * sizeof(float));
+    }
+    return rc;
+}
+#endif
+
+static uint64_t fnv1a(const void *p, size_t n)
+{
+    const uint8_t *b = (const uint8_t *)p;
+    uint64_t h = 0xCBF29CE484222325ull;
+    for (size_t i = 0; i < n; i++) { h ^= b[i]; h *= 0x100000001B3ull; }
+    return h;
+}
+
+static double now_s(void)
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec + ts.tv_nsec * 1e-9;
+}
+
+int main(int argc, char **argv)
+{
+    if (argc < 2) {
+        fprintf(stderr, "usage: %s <encoder frames> [workdir]\n", argv[0]);
+        return 2;
+    }
+    const int T = atoi(argv[1]);
+    char dir[512];
+    snprintf(dir, sizeof dir, "%s/pk_encode_XXXXXX", argc > 2 ? argv[2] : "/tmp");
+    if (T <= 0 || !mkdtemp(dir)) {
+        fprintf(stderr, "bad frame count or workdir\n");
+        return 2;
+    }
+    pk_verbose = 0;
+
+    fpenv("start");
+    double t0 = now_s();
+    if (write_model(dir)) { fprintf(stderr, "writing the model failed\n"); return 1; }
+    char bin[600], json[600];
+    snprintf(bin, sizeof bin, "%s/weights.bin", dir);
+    snprintf(json, sizeof json, "%s/weights.json", dir);
+    PkModel m;
+    memset(&m, 0, sizeof m);
+    if (pk_load_weights(&m, bin, json)) { fprintf(stderr, "pk_load_weights failed\n"); return 1; }
+    free(scratch_f);
+    scratch_f = NULL;
+    scratch_n = 0;
+#ifdef PK_GPU_REGISTER
+    if (pk_gpu_init(-1) || register_model(&m)) {
+        fprintf(stderr, "GPU setup failed: %s\n", pk_gpu_last_error());
+        return 1;
+    }
+#endif
+    fpenv("after setup");
+    double t_load = now_s() - t0;
+
+    float *x = (float *)malloc((size_t)T * PK_D_MODEL * sizeof(float));
+    pkor_fill_normal(x, (size_t)T * PK_D_MODEL, 0.0f, 1.0f, pkor_seed(SEED_BASE, "features"));
+
+    pk_pool();                              /* thread pool start-up outside the timing */
+    t0 = now_s();
+    float *enc = x;
+    if (should_chunk(T)) {                  /* encoder.c:602-610 */
+        enc = (float *)calloc((size_t)T * PK_D_MODEL, sizeof(float));
+        encode_blocks_chunked(&m, x, T, enc);
+    } else {
+        encode_blocks(&m, x, T);
+    }
+    double t_enc = now_s() - t0;
+    fpenv("after encoder");
+
+    if (getenv("PK_DEBUG")) {     /* decoder inputs and first joint logits */
+        const DecoderWeights *d = &m.dec;
+        float pred[PK_LSTM_HIDDEN], logits[PK_VOCAB];
+        LSTMState st;
+        memset(&st, 0, sizeof st);
+        pk_decoder_step(&m, PK_BLANK, &st, pred);
+        pk_joint(&m, enc, pred, logits);
+        int best = 0;
+        for (int v = 1; v < PK_VOCAB; v++) if (logits[v] > logits[best]) best = v;
+        fprintf(stderr, "dbg embed %016llx joint_out %016llx joint_enc %016llx lstm0 %016llx "
+                        "pred %016llx logits %016llx best %d blank %.6f top %.6f\n",
+                (unsigned long long)fnv1a(d->embed_w, (size_t)1025 * 640 * 4),
+                (unsigned long long)fnv1a(d->joint_out_w, (size_t)640 * 1025 * 4),
+                (unsigned long long)fnv1a(d->joint_enc_w, (size_t)1024 * 640 * 4),
+                (unsigned long long)fnv1a(d->lstm0_Wi, (size_t)2560 * 640 * 4),
+                (unsigned long long)fnv1a(pred, sizeof pred),
+                (unsigned long long)fnv1a(logits, sizeof logits), best, logits[PK_BLANK],
+                logits[best]);
+    }
+    int *tokens = NULL;
+    t0 = now_s();
+    int n_tok = pk_greedy_decode(&m, enc, T, &tokens);
+    double t_dec = now_s() - t0;
+
+    /* bit test: this unit is built with -ffast-math, where isfinite() folds to 1 */
+    float amax = 0.0f;
+    int finite = 1;
+    for (size_t i = 0; i < (size_t)T * PK_D_MODEL; i++) {
+        uint32_t u;
+        memcpy(&u, &enc[i], 4);
+        if ((u & 0x7f800000u) == 0x7f800000u) finite = 0;
+        else if (fabsf(enc[i]) > amax) amax = fabsf(enc[i]);
+    }
+    printf("{\"frames\": %d, \"chunked\": %d, \"enc_fnv\": \"%016llx\", \"enc_absmax\": %.6g, "
+           "\"finite\": %d, \"n_tokens\": %d, \"tokens_fnv\": \"%016llx\", \"first_tokens\": [",
+           T, should_chunk(T), (unsigned long long)fnv1a(enc, (size_t)T * PK_D_MODEL * 4), amax,
+           finite, n_tok, (unsigned long long)fnv1a(tokens, (size_t)n_tok * sizeof(int)));
+    for (int i = 0; i < n_tok && i < 16; i++) printf("%s%d", i ? ", " : "", tokens[i]);
+    printf("], \"threads\": %d, \"load_s\": %.3f, \"encoder_s\": %.4f, \"decoder_s\": %.4f}\n",
+           pk_pool_nthreads(pk_pool()), t_load, t_enc, t_dec);
+
+    free(tokens);
+    if (enc != x) free(enc);
+    free(x);
+#ifdef PK_GPU_REGISTER
+    pk_gpu_shutdown();
+#endif
+    pk_free_weights(&m);
+    unlink(bin);
+    unlink(json);
+    rmdir(dir);
+    return 0;
+}

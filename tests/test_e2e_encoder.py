@@ -1,0 +1,69 @@
+"""End to end: the reference's own encoder and greedy decoder (encoder.c,
+decoder.c, weights.c, compiled from its sources by oracle/Makefile) with
+the weight GEMMs taken from the GPU drop-in, against the same host code
+with blas.c's portable weight GEMMs.  Both load the same synthetic mixed
+int4/int8/fp32 model through pk_load_weights (fused-QKV requantisation
+included); every other object is shared, so equal encoder-output and
+token hashes mean the GPU GEMMs changed nothing.
+
+The x86 AVX2 build of the reference decodes int4 weights wrongly
+(blas.c:815-833, see test_oracle.test_x86_int4_unpack_defect); its output
+is compared too, to show the effect on a whole encoder.
+
+The reference decoder reads uninitialised memory: pk_lstm_step mallocs its
+gate buffer and fills it with cblas_sgemv(NoTrans, beta = 0)
+(tensor_ops.c:601-605), whose NoTrans branch computes beta * Y
+(blas.c:67).  When the recycled heap block holds NaN or Inf bits the LSTM
+state becomes NaN for good, the -ffast-math ReLU of the joint maps NaN to
+0, and the decoder emits only blanks; which run that happens in depends
+on heap history.  Every driver here therefore runs with glibc's
+MALLOC_PERTURB_ set, which fills fresh allocations with a finite pattern,
+so 0 * Y is 0 as beta = 0 intends and the token ids are reproducible."""
+import json
+import os
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REF = os.path.join(os.path.dirname(HERE), "oracle", "_ref")
+THREADS = str(min(os.cpu_count() or 1, 16))
+
+
+def run(binary, frames, tmp_path):
+    path = os.path.join(REF, binary)
+    if not os.path.exists(path):
+        pytest.skip(f"{binary} not built (oracle/Makefile ref)")
+    env = dict(os.environ, PK_THREADS=THREADS, MALLOC_PERTURB_="192")  # 0x3f3f3f3f fill
+    out = subprocess.run([path, str(frames), str(tmp_path)], capture_output=True, text=True,
+                         env=env, timeout=280)
+    assert out.returncode == 0, out.stderr[-2000:]
+    line = [l for l in out.stdout.splitlines() if l.startswith("{")][-1]
+    print(binary, line, flush=True)
+    return json.loads(line)
+
+
+def test_reference_drivers_cpu(tmp_path):
+    """CPU only: the portable-path and x86 builds run, agree on shape and
+    differ in value (the x86 int4 unpack)."""
+    ref = run("pk_encode_ref", 48, tmp_path)
+    x86 = run("pk_encode_ref_x86", 48, tmp_path)
+    assert ref["finite"] == 1 and x86["finite"] == 1 and ref["frames"] == 48
+    assert ref["enc_fnv"] != x86["enc_fnv"]
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("frames", [300, 900])
+def test_gpu_dropin_matches_reference_bit_for_bit(frames, tmp_path):
+    """300 frames: full-sequence path (M = 300, pos M = 599); 900 frames:
+    chunked path, chunks of 408/416/108 rows (pos 815/831/215)."""
+    gpu = run("pk_encode_gpu", frames, tmp_path)
+    ref = run("pk_encode_ref", frames, tmp_path)
+    assert gpu["finite"] == 1
+    assert gpu["chunked"] == ref["chunked"] == (1 if frames > 500 else 0)
+    assert gpu["enc_fnv"] == ref["enc_fnv"], "encoder outputs differ"
+    assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"]
+    assert gpu["first_tokens"] == ref["first_tokens"]
+    x86 = run("pk_encode_ref_x86", frames, tmp_path)
+    assert x86["enc_fnv"] != ref["enc_fnv"]
