@@ -215,7 +215,7 @@ def main():
         "kernel_us": {"int4_up": round(up_ms * 1e3, 2), "swish": round(sw_ms * 1e3, 2),
                       "int4_down": round(dn_ms * 1e3, 2)},
         "wall_ms_per_step": round(1e3 * wall / K, 4),
-        "roofline": {"bound": "mfma", "kernel": "chain_gemm<int4> (up and down launches)",
+        "roofline": {"bound": "mfma", "kernel": "int4 chain GEMM (up and down launches)",
                      "achieved": round(tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": traffic},

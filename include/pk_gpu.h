@@ -113,10 +113,11 @@ int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);
 /* ---- tuning / introspection ------------------------------------------- */
 
 /* Number of kernel tile configurations, and a description of one:
- * family ('R': rows on MFMA lanes, 'X': columns on lanes with A broadcast),
+ * family ('R': rows on MFMA lanes, 'X': columns on lanes with A broadcast,
+ * 'S': the 'X' tiles plus as many producer waves that stage the operands),
  * mfma (32, 16 or 4 = v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32),
- * independent chains per wave, waves along M and N per workgroup, and k per
- * LDS chunk.  Any pointer may be NULL. */
+ * independent chains per wave, multiplying waves along M and N per
+ * workgroup, and k per LDS chunk.  Any pointer may be NULL. */
 int pk_gpu_num_configs(void);
 int pk_gpu_config_info(int index, int *family, int *mfma, int *cw, int *wgm, int *wgn,
                        int *kt);

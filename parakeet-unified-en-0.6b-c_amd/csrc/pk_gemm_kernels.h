@@ -32,7 +32,9 @@ struct GemmProblem {
 //   family 'R': rows on MFMA lanes, one MFMA = 64 rows x mfma columns,
 //               cw column tiles (independent chains) per wave;
 //   family 'X': columns on MFMA lanes with A broadcast, one MFMA = mfma rows
-//               x 64 columns, cw row groups (independent chains) per wave.
+//               x 64 columns, cw row groups (independent chains) per wave;
+//   family 'S': the 'X' tiles with wgm*wgn additional producer waves that
+//               stage the operands while the others only multiply.
 struct TileConfig {
     char family;
     int mfma;   // 32, 16 or 4: v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32
@@ -42,6 +44,7 @@ struct TileConfig {
     int kt;     // k per LDS chunk
     int bm() const { return family == 'R' ? 64 * wgm : wgm * cw * mfma; }
     int bn() const { return family == 'R' ? mfma * cw * wgn : 64 * wgn; }
+    int threads() const { return (family == 'S' ? 128 : 64) * wgm * wgn; }
 };
 
 // Pick the tile configuration with the lowest modelled time on 256 CUs.

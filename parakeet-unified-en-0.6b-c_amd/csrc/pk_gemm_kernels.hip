@@ -1,566 +1,12 @@
-// pk_gemm_kernels.hip - CDNA4 (gfx950) kernels for the quantized weight GEMMs.
-//
-// Numerics.  The reference computes every output as a sequential fused
-// multiply-add chain over k ascending, c = fma(fl(alpha*A[i][k]), w[k][j], c),
-// starting from fl(beta*C) (csrc/blas.c:89-99, 187-218, 617-651), with the
-// weight dequantised once per element, w = fl((float)q * s) (blas.c:545-553,
-// 815-840).  The fp32 MFMA instructions with K = 1,
-//     v_mfma_f32_32x32x1_2b_f32, v_mfma_f32_16x16x1_4b_f32,
-//     v_mfma_f32_4x4x1_16b_f32,
-// perform exactly one multiply-add per output element, so issuing them in
-// ascending k on one accumulator reproduces the chain element for element,
-// at the full fp32 matrix-core rate.  Nothing here ever splits k across
-// waves or reorders a chain; that is the invariant every tile shape keeps.
-//
-// Data flow per workgroup (BM x BN output tile, KT-deep chunks of k):
-//   global A (fp32, row-major) --> fl(alpha*a) --> LDS As[k][m]   (k-major)
-//   global W (fp32 | int8 | packed int4 + fp32 scales) --> dequant in
-//        registers --> LDS Bs[k][n] fp32                           (k-major)
-//   per k: one ds_read of 64 rows of A (lane l -> row l) and one broadcast
-//   ds_read of the MFMA's column group of B, then one MFMA per column tile.
-// Chunks are double-buffered: chunk c+1 is fetched into registers while
-// chunk c is multiplied, then written to the other LDS buffer.
-#include "pk_gemm_kernels.h"
-
-#include <algorithm>
-#include <cmath>
+// pk_gemm_kernels.hip - dispatch of the weight GEMMs and the small kernels
+// around them (beta-only pass, int8 edge columns, swish).  The tile kernels
+// and their numerics are described in pk_gemm_tiles.h.
+#include "pk_gemm_tiles.h"
 
 namespace pkgpu {
 namespace {
 
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef float v32f __attribute__((ext_vector_type(32)));
-
-// Kernel arguments (device pointers).  N is the number of columns this
-// launch computes; n_groups is the int4 scale-row length N_full/32
-// (blas.c:958).
-struct KArgs {
-    int M, N, K;
-    float alpha, beta;
-    const float* A; int lda;
-    const void* B;  int ldb;
-    float scale;
-    const float* scales; int n_groups;
-    float* C; int ldc;
-    // Exact byte extents the call may read (buffer-descriptor ranges) and
-    // whether A / B rows allow 16-byte vector loads.
-    uint32_t a_bytes, b_bytes, s_bytes;
-    int vec_a, vec_b;
-};
-
-// Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format).
-constexpr int kRsrcWord3 = 0x00020000;
-
-__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             kRsrcWord3);
-}
-
-// Raw buffer loads: an offset at or past the descriptor's range returns 0,
-// so staging needs no bounds predicates and never touches memory outside
-// the caller's operand.
-__device__ inline float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
-}
-__device__ inline uint32_t ld_u32(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
-}
-__device__ inline uint32_t ld_u8(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
-}
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-__device__ inline v4u ld_v4(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-}
-
-// ---- MFMA shapes -----------------------------------------------------------
-// Every shape is used with its blocks stacked along M, so one instruction
-// covers 64 rows x NCOL columns: A lane l carries row l, B lane l carries
-// column l % NCOL.  row()/col() give the output element held by (lane, reg).
-
-template <int MF> struct Mfma;
-
-template <> struct Mfma<32> {
-    static constexpr int NCOL = 32, NACC = 32;
-    using acc_t = v32f;
-    __device__ static acc_t step(float a, float b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
-    }
-    __device__ static int row(int l, int r) {
-        return 32 * (r >> 4) + 8 * ((r & 15) >> 2) + 4 * (l >> 5) + (r & 3);
-    }
-    __device__ static int col(int l, int) { return l & 31; }
-};
-
-template <> struct Mfma<16> {
-    static constexpr int NCOL = 16, NACC = 16;
-    using acc_t = v16f;
-    __device__ static acc_t step(float a, float b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
-    }
-    __device__ static int row(int l, int r) { return 16 * (r >> 2) + 4 * (l >> 4) + (r & 3); }
-    __device__ static int col(int l, int) { return l & 15; }
-};
-
-template <> struct Mfma<4> {
-    static constexpr int NCOL = 4, NACC = 4;
-    using acc_t = v4f;
-    __device__ static acc_t step(float a, float b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
-    }
-    __device__ static int row(int l, int r) { return 4 * (l >> 2) + r; }
-    __device__ static int col(int l, int) { return l & 3; }
-};
-
-// ---- weight staging (dequantisation, bit-exact) ---------------------------
-// A "unit" is VB consecutive columns of one row of W, fetched with one
-// vector load when rows are 4/16-byte aligned; "elem" is the scalar form.
-// load_*() only issues loads into raw registers; dequant_*() runs after the
-// current chunk's MFMAs, so the loads' latency overlaps the multiplies, and
-// produces fp32 weights exactly as the reference's pack step does.
-
-template <int WK> struct WStage;
-
-template <> struct WStage<W_F32> {
-    static constexpr int VB = 4;
-    struct Unit { v4u w; };
-    struct Elem { float w; };
-    __device__ static Unit load_unit(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
-                                     __amdgpu_buffer_rsrc_t, int k, int n) {
-        return Unit{ld_v4(rb, ((uint32_t)k * p.ldb + n) * 4u)};
-    }
-    __device__ static void dequant_unit(const KArgs&, const Unit& u, float* out) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[j] = __uint_as_float(u.w[j]);
-    }
-    __device__ static Elem load_elem(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
-                                     __amdgpu_buffer_rsrc_t, int k, int n) {
-        return Elem{ld_f32(rb, ((uint32_t)k * p.ldb + n) * 4u)};
-    }
-    __device__ static float dequant_elem(const KArgs&, const Elem& e, int) { return e.w; }
-};
-
-// blas.c:545-553: fl((float)q * scale)
-template <> struct WStage<W_I8> {
-    static constexpr int VB = 4;
-    struct Unit { uint32_t w; };
-    struct Elem { uint32_t q; };
-    __device__ static Unit load_unit(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
-                                     __amdgpu_buffer_rsrc_t, int k, int n) {
-        return Unit{ld_u32(rb, (uint32_t)k * p.ldb + n)};
-    }
-    __device__ static void dequant_unit(const KArgs& p, const Unit& u, float* out) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[j] = __fmul_rn((float)(int8_t)(u.w >> (8 * j)), p.scale);
-    }
-    __device__ static Elem load_elem(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
-                                     __amdgpu_buffer_rsrc_t, int k, int n) {
-        return Elem{ld_u8(rb, (uint32_t)k * p.ldb + n)};
-    }
-    __device__ static float dequant_elem(const KArgs& p, const Elem& e, int) {
-        return __fmul_rn((float)(int8_t)e.q, p.scale);
-    }
-};
-
-// blas.c:834-840 (portable/NEON decode) and blas.c:794 (scale index): byte j
-// of row k holds column 2j in the low nibble and 2j+1 in the high nibble,
-// both two's complement; scale = scales[k * (N/32) + n/32].
-template <> struct WStage<W_I4> {
-    static constexpr int VB = 8;
-    struct Unit { uint32_t w; float s; };
-    struct Elem { uint32_t b; float s; };
-    __device__ static Unit load_unit(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
-                                     __amdgpu_buffer_rsrc_t rs, int k, int n) {
-        return Unit{ld_u32(rb, (uint32_t)k * p.ldb + (n >> 1)),
-                    ld_f32(rs, ((uint32_t)k * p.n_groups + (n >> 5)) * 4u)};
-    }
-    __device__ static void dequant_unit(const KArgs&, const Unit& u, float* out) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int v = (int)(u.w << (28 - 4 * j)) >> 28;     // sign-extend nibble j
-            out[j] = __fmul_rn((float)v, u.s);
-        }
-    }
-    __device__ static Elem load_elem(const KArgs& p, __amdgpu_buffer_rsrc_t rb,
-                                     __amdgpu_buffer_rsrc_t rs, int k, int n) {
-        return Elem{ld_u8(rb, (uint32_t)k * p.ldb + (n >> 1)),
-                    ld_f32(rs, ((uint32_t)k * p.n_groups + (n >> 5)) * 4u)};
-    }
-    __device__ static float dequant_elem(const KArgs&, const Elem& e, int n) {
-        const int v = (n & 1) ? ((int)(int8_t)e.b >> 4) : ((int)(int8_t)(e.b << 4) >> 4);
-        return __fmul_rn((float)v, e.s);
-    }
-};
-
-// ---- tile staging ------------------------------------------------------------
-// Stages one KT-deep chunk: A rows [m0, m0+BM) -> As[k*AS + m] as fl(alpha*a),
-// W columns [n0, n0+BN) -> Bs[k*BN + n] as dequantised fp32.  load() only
-// issues unconditional buffer loads (out-of-range -> 0) into raw registers;
-// store() runs after the current chunk's MFMAs, so the loads' latency
-// overlaps the multiplies.  Rows of A past M and columns of W past N only
-// feed outputs that are never stored, and k past K is never multiplied.
-
-template <int WK, int BM, int BN, int KT, int NT, int AS, bool VEC>
-struct Stager {
-    using WS = WStage<WK>;
-    static constexpr int VB = WS::VB;
-    static constexpr int A_PER = (BM * KT) / NT;
-    static constexpr int B_PER = (BN * KT) / NT;
-    static constexpr int A_UNITS = A_PER / 4;
-    static constexpr int B_UNITS = B_PER / VB;
-    static_assert((BM * KT) % NT == 0 && (BN * KT) % NT == 0, "tile/threads");
-    static_assert(A_PER % 4 == 0 && B_PER % VB == 0 && BN % VB == 0 && KT % 4 == 0, "units");
-
-    __amdgpu_buffer_rsrc_t rsA, rsB, rsS;
-    v4u ra4[VEC ? A_UNITS : 1];
-    float ra1[VEC ? 1 : A_PER];
-    typename WS::Unit rbu[VEC ? B_UNITS : 1];
-    typename WS::Elem rbe[VEC ? 1 : B_PER];
-
-    __device__ explicit Stager(const KArgs& p)
-        : rsA(make_rsrc(p.A, p.a_bytes)),
-          rsB(make_rsrc(p.B, p.b_bytes)),
-          rsS(make_rsrc(WK == W_I4 ? (const void*)p.scales : p.B, WK == W_I4 ? p.s_bytes : 0u)) {}
-
-    __device__ void load(const KArgs& p, int tid, int m0, int n0, int k0) {
-        if constexpr (VEC) {
-#pragma unroll
-            for (int i = 0; i < A_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int row = e / (KT / 4), kq = e % (KT / 4);   // k fastest: coalesced rows
-                ra4[i] = ld_v4(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + 4 * kq) * 4u);
-            }
-#pragma unroll
-            for (int i = 0; i < B_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int kk = e / (BN / VB), nq = e % (BN / VB);  // n fastest
-                rbu[i] = WS::load_unit(p, rsB, rsS, k0 + kk, n0 + VB * nq);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < A_PER; ++i) {
-                const int e = tid + i * NT;
-                const int row = e / KT, kk = e % KT;
-                ra1[i] = ld_f32(rsA, ((uint32_t)(m0 + row) * p.lda + k0 + kk) * 4u);
-            }
-#pragma unroll
-            for (int i = 0; i < B_PER; ++i) {
-                const int e = tid + i * NT;
-                const int kk = e / BN, n = e % BN;
-                rbe[i] = WS::load_elem(p, rsB, rsS, k0 + kk, n0 + n);
-            }
-        }
-    }
-
-    // fl(alpha*a) and the weight dequantisation happen here.
-    __device__ void store(const KArgs& p, int tid, float* As, float* Bs) {
-        if constexpr (VEC) {
-#pragma unroll
-            for (int i = 0; i < A_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int row = e / (KT / 4), kq = e % (KT / 4);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    As[(4 * kq + j) * AS + row] = __fmul_rn(p.alpha, __uint_as_float(ra4[i][j]));
-            }
-#pragma unroll
-            for (int i = 0; i < B_UNITS; ++i) {
-                const int e = tid + i * NT;
-                const int kk = e / (BN / VB), nq = e % (BN / VB);
-                float w[VB];
-                WS::dequant_unit(p, rbu[i], w);
-#pragma unroll
-                for (int j = 0; j < VB; ++j) Bs[kk * BN + VB * nq + j] = w[j];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < A_PER; ++i) {
-                const int e = tid + i * NT;
-                As[(e % KT) * AS + e / KT] = __fmul_rn(p.alpha, ra1[i]);
-            }
-#pragma unroll
-            for (int i = 0; i < B_PER; ++i) {
-                const int e = tid + i * NT;
-                Bs[e] = WS::dequant_elem(p, rbe[i], e % BN);        // [kk * BN + n]
-            }
-        }
-    }
-};
-
-// Chains start from beta*C exactly as scale_c leaves it (blas.c:89-99).
-__device__ inline float beta_c(const KArgs& p, int row, int col)
-{
-    if (p.beta == 0.0f || row >= p.M || col >= p.N) return 0.0f;
-    const float cv = p.C[(size_t)row * p.ldc + col];
-    return (p.beta == 1.0f) ? cv : __fmul_rn(cv, p.beta);
-}
-
-// ---- family R: rows on lanes ------------------------------------------------
-// Each MFMA covers 64 rows x NCOL columns (blocks stacked along M): A lane l
-// carries row l, B lane l carries column l % NCOL.  A wave owns CW column
-// tiles (CW independent chains); WGM x WGN waves share the staged tiles.
-
-template <int WK, int MF, int CW, int WGM, int WGN, int KT, bool VEC>
-__global__ __launch_bounds__(64 * WGM * WGN)
-void chain_gemm(KArgs p)
-{
-    using T = Mfma<MF>;
-    constexpr int NT = 64 * WGM * WGN;
-    constexpr int BM = 64 * WGM;
-    constexpr int AS = BM + 1;              // padded row of As: conflict-free stores
-    constexpr int WN = T::NCOL * CW;
-    constexpr int BN = WN * WGN;
-
-    __shared__ float As[2][KT * AS];
-    __shared__ float Bs[2][KT * BN];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-
-    typename T::acc_t acc[CW];
-#pragma unroll
-    for (int c = 0; c < CW; ++c)
-#pragma unroll
-        for (int r = 0; r < T::NACC; ++r)
-            acc[c][r] = beta_c(p, m0 + wm * 64 + T::row(lane, r),
-                               n0 + wn * WN + c * T::NCOL + T::col(lane, r));
-
-    Stager<WK, BM, BN, KT, NT, AS, VEC> st(p);
-    const int nchunks = (p.K + KT - 1) / KT;
-    if (nchunks > 0) {
-        st.load(p, tid, m0, n0, 0);
-        st.store(p, tid, As[0], Bs[0]);
-    }
-    __syncthreads();
-
-    for (int ch = 0; ch < nchunks; ++ch) {
-        const int buf = ch & 1;
-        if (ch + 1 < nchunks) st.load(p, tid, m0, n0, (ch + 1) * KT);
-        const float* as = &As[buf][wm * 64 + lane];
-        const float* bs = &Bs[buf][wn * WN + (lane % T::NCOL)];
-        const int kn = min(KT, p.K - ch * KT);
-        if (kn == KT) {
-            // Operands for k+U are read from LDS while k..k+U-1 are multiplied.
-            constexpr int U = 8;
-            float av[2][U], bv[2][U][CW];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                av[0][u] = as[u * AS];
-#pragma unroll
-                for (int c = 0; c < CW; ++c) bv[0][u][c] = bs[u * BN + c * T::NCOL];
-            }
-#pragma unroll
-            for (int k8 = 0; k8 < KT; k8 += U) {
-                const int cur = (k8 / U) & 1;
-                if (k8 + U < KT) {
-#pragma unroll
-                    for (int u = 0; u < U; ++u) {
-                        av[cur ^ 1][u] = as[(k8 + U + u) * AS];
-#pragma unroll
-                        for (int c = 0; c < CW; ++c)
-                            bv[cur ^ 1][u][c] = bs[(k8 + U + u) * BN + c * T::NCOL];
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u)
-#pragma unroll
-                    for (int c = 0; c < CW; ++c) acc[c] = T::step(av[cur][u], bv[cur][u][c], acc[c]);
-            }
-        } else {
-            for (int kk = 0; kk < kn; ++kk) {
-                const float a = as[kk * AS];
-#pragma unroll
-                for (int c = 0; c < CW; ++c)
-                    acc[c] = T::step(a, bs[kk * BN + c * T::NCOL], acc[c]);
-            }
-        }
-        if (ch + 1 < nchunks) st.store(p, tid, As[buf ^ 1], Bs[buf ^ 1]);
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int c = 0; c < CW; ++c) {
-#pragma unroll
-        for (int r = 0; r < T::NACC; ++r) {
-            const int row = m0 + wm * 64 + T::row(lane, r);
-            const int col = n0 + wn * WN + c * T::NCOL + T::col(lane, r);
-            if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[c][r];
-        }
-    }
-}
-
-// ---- family X: columns on lanes, A broadcast ---------------------------------
-// Each MFMA covers BS rows x 64 columns (blocks side by side along N): B lane
-// l carries column l, and A comes from one block only (CBSZ broadcast of
-// block ABID to all blocks), so a single A register holds NB = 64/BS
-// consecutive k steps (lane BS*t + i = A[row i][k + t]) and ABID = t picks
-// the step.  A wave owns R row groups (R independent chains) sharing each B
-// register; NWM x NWN waves share the staged tiles.
-
-template <int MF> struct MfmaX;
-
-template <> struct MfmaX<4> {
-    static constexpr int BS = 4, NB = 16, CBSZ = 4, NACC = 4;
-    using acc_t = v4f;
-    template <int T_>
-    __device__ static acc_t step(float a, float b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, CBSZ, T_, 0);
-    }
-    __device__ static int row(int, int r) { return r; }
-    __device__ static int col(int l, int) { return l; }
-};
-
-template <> struct MfmaX<16> {
-    static constexpr int BS = 16, NB = 4, CBSZ = 2, NACC = 16;
-    using acc_t = v16f;
-    template <int T_>
-    __device__ static acc_t step(float a, float b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, CBSZ, T_, 0);
-    }
-    __device__ static int row(int l, int r) { return 4 * (l >> 4) + (r & 3); }
-    __device__ static int col(int l, int r) { return 16 * (r >> 2) + (l & 15); }
-};
-
-template <> struct MfmaX<32> {
-    static constexpr int BS = 32, NB = 2, CBSZ = 1, NACC = 32;
-    using acc_t = v32f;
-    template <int T_>
-    __device__ static acc_t step(float a, float b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, CBSZ, T_, 0);
-    }
-    __device__ static int row(int l, int r) { return 8 * ((r & 15) >> 2) + 4 * (l >> 5) + (r & 3); }
-    __device__ static int col(int l, int r) { return 32 * (r >> 4) + (l & 31); }
-};
-
-// Steps t = T_..NB-1 of one NB-block: MFMA with ABID = t for every row group
-// (ABID is an instruction field, so t must be a compile-time constant).
-template <typename T, int R, int T_>
-__device__ inline void x_steps(const float (&a)[R], const float* b, typename T::acc_t (&acc)[R])
-{
-    if constexpr (T_ < T::NB) {
-#pragma unroll
-        for (int g = 0; g < R; ++g) acc[g] = T::template step<T_>(a[g], b[T_], acc[g]);
-        x_steps<T, R, T_ + 1>(a, b, acc);
-    }
-}
-
-// The first n < NB steps only (partial last chunk).
-template <typename T, int R, int T_>
-__device__ inline void x_steps_n(const float (&a)[R], const float* b, typename T::acc_t (&acc)[R],
-                                 int n)
-{
-    if constexpr (T_ < T::NB) {
-        if (T_ < n) {
-#pragma unroll
-            for (int g = 0; g < R; ++g) acc[g] = T::template step<T_>(a[g], b[T_], acc[g]);
-            x_steps_n<T, R, T_ + 1>(a, b, acc, n);
-        }
-    }
-}
-
-template <int MF> struct XPad;                       // conflict-free A-register reads
-template <> struct XPad<4> { static constexpr int v = 4; };
-template <> struct XPad<16> { static constexpr int v = 16; };
-template <> struct XPad<32> { static constexpr int v = 0; };
-
-template <int WK, int MF, int R, int NWM, int NWN, int KT, bool VEC>
-__global__ __launch_bounds__(64 * NWM * NWN)
-void chain_gemm_x(KArgs p)
-{
-    using T = MfmaX<MF>;
-    constexpr int BS = T::BS, NB = T::NB;
-    constexpr int NT = 64 * NWM * NWN;
-    constexpr int BM = NWM * R * BS;
-    constexpr int BN = NWN * 64;
-    constexpr int AS = BM + XPad<MF>::v;
-    static_assert(KT % NB == 0, "chunk must hold whole A registers");
-
-    __shared__ float As[2][KT * AS];
-    __shared__ float Bs[2][KT * BN];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / NWN, wn = wave % NWN;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int wrow = wm * R * BS;                  // wave's first row within the tile
-
-    typename T::acc_t acc[R];
-#pragma unroll
-    for (int g = 0; g < R; ++g)
-#pragma unroll
-        for (int r = 0; r < T::NACC; ++r)
-            acc[g][r] = beta_c(p, m0 + wrow + g * BS + T::row(lane, r),
-                               n0 + wn * 64 + T::col(lane, r));
-
-    Stager<WK, BM, BN, KT, NT, AS, VEC> st(p);
-    const int nchunks = (p.K + KT - 1) / KT;
-    if (nchunks > 0) {
-        st.load(p, tid, m0, n0, 0);
-        st.store(p, tid, As[0], Bs[0]);
-    }
-    __syncthreads();
-
-    // lane BS*t + i reads A[row i][k + t]
-    const int a_off = (lane / BS) * AS + wrow + (lane % BS);
-    for (int ch = 0; ch < nchunks; ++ch) {
-        const int buf = ch & 1;
-        if (ch + 1 < nchunks) st.load(p, tid, m0, n0, (ch + 1) * KT);
-        const float* as = &As[buf][a_off];
-        const float* bs = &Bs[buf][wn * 64 + lane];
-        const int kn = min(KT, p.K - ch * KT);
-        if (kn == KT) {
-            // NB-blocks of k; the next block's operands are read while the
-            // current block is multiplied.
-            float a[2][R], b[2][NB];
-#pragma unroll
-            for (int g = 0; g < R; ++g) a[0][g] = as[g * BS];
-#pragma unroll
-            for (int t = 0; t < NB; ++t) b[0][t] = bs[t * BN];
-#pragma unroll
-            for (int kb = 0; kb < KT; kb += NB) {
-                const int cur = (kb / NB) & 1;
-                if (kb + NB < KT) {
-#pragma unroll
-                    for (int g = 0; g < R; ++g) a[cur ^ 1][g] = as[(kb + NB) * AS + g * BS];
-#pragma unroll
-                    for (int t = 0; t < NB; ++t) b[cur ^ 1][t] = bs[(kb + NB + t) * BN];
-                }
-                x_steps<T, R, 0>(a[cur], b[cur], acc);
-            }
-        } else {
-            for (int kb = 0; kb < kn; kb += NB) {
-                float a[R], b[NB];
-#pragma unroll
-                for (int g = 0; g < R; ++g) a[g] = as[kb * AS + g * BS];
-#pragma unroll
-                for (int t = 0; t < NB; ++t) b[t] = bs[(kb + t) * BN];
-                x_steps_n<T, R, 0>(a, b, acc, kn - kb);
-            }
-        }
-        if (ch + 1 < nchunks) st.store(p, tid, As[buf ^ 1], Bs[buf ^ 1]);
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int g = 0; g < R; ++g) {
-#pragma unroll
-        for (int r = 0; r < T::NACC; ++r) {
-            const int row = m0 + wrow + g * BS + T::row(lane, r);
-            const int col = n0 + wn * 64 + T::col(lane, r);
-            if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[g][r];
-        }
-    }
-}
+using tiles::KArgs;
 
 // int8 columns j >= 16*floor(N/16): the compiled reference evaluates
 // blas.c:752 (c += ax*bs*(float)b) as c = fma(fl(A*fl(alpha*bs)), (float)q, c)
@@ -621,88 +67,35 @@ __global__ void swish(const float* x, float* y, long long n)
     y[i] = __fmul_rn(s, v);
 }
 
-// ---- configurations and dispatch -------------------------------------------
-
-// KT (k per LDS chunk) is sized so one chunk's MFMA time per wave covers the
-// latency of the next chunk's loads.
-#define PK_CONFIGS(X)                                                       \
-    X(0, 'R', 32, 2, 2, 2, 32)   /* 128 x 128, wave 64 x 64            */  \
-    X(1, 'R', 32, 1, 2, 2, 32)   /* 128 x 64,  wave 64 x 32            */  \
-    X(2, 'R', 16, 2, 1, 4, 32)   /*  64 x 128, wave 64 x 32            */  \
-    X(3, 'R', 16, 1, 1, 4, 64)   /*  64 x 64,  wave 64 x 16            */  \
-    X(4, 'R', 4, 4, 1, 4, 64)    /*  64 x 64,  wave 64 x 16            */  \
-    X(5, 'R', 4, 1, 1, 4, 128)   /*  64 x 16,  wave 64 x 4             */  \
-    X(6, 'X', 4, 1, 4, 1, 64)    /*  16 x 64,  wave 4 x 64, 1 chain    */  \
-    X(7, 'X', 4, 2, 4, 1, 64)    /*  32 x 64,  wave 8 x 64, 2 chains   */  \
-    X(8, 'X', 4, 4, 4, 1, 64)    /*  64 x 64,  wave 16 x 64, 4 chains  */  \
-    X(9, 'X', 4, 2, 2, 2, 64)    /*  16 x 128, wave 8 x 64, 2 chains   */  \
-    X(10, 'X', 4, 8, 2, 2, 32)   /*  64 x 128, wave 32 x 64, 8 chains  */  \
-    X(11, 'X', 16, 1, 4, 1, 64)  /*  64 x 64,  wave 16 x 64            */  \
-    X(12, 'X', 16, 2, 2, 2, 32)  /*  64 x 128, wave 32 x 64, 2 chains  */  \
-    X(13, 'X', 16, 4, 2, 2, 32)  /* 128 x 128, wave 64 x 64, 4 chains  */  \
-    X(14, 'X', 32, 1, 4, 1, 32)  /* 128 x 64,  wave 32 x 64            */  \
-    X(15, 'X', 32, 2, 2, 2, 32)  /* 128 x 128, wave 64 x 64, 2 chains  */
-
-#define PK_CFG_ENTRY(i, fam, mf, c, wm, wn, kt) {fam, mf, c, wm, wn, kt},
-const TileConfig kConfigs[] = {PK_CONFIGS(PK_CFG_ENTRY)};
-constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
-
-template <int WK, bool VEC>
-hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
-{
-    const TileConfig& t = kConfigs[cfg];
-    dim3 grid((a.N + t.bn() - 1) / t.bn(), (a.M + t.bm() - 1) / t.bm());
-    dim3 block(64 * t.wgm * t.wgn);
-#define PK_CFG_CASE(i, fam, mf, c, wm, wn, kt)                                            \
-    case i:                                                                               \
-        if constexpr (fam == 'R')                                                         \
-            hipLaunchKernelGGL((chain_gemm<WK, mf, c, wm, wn, kt, VEC>), grid, block, 0, s, a); \
-        else                                                                              \
-            hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, VEC>), grid, block, 0, s, a); \
-        break;
-    switch (cfg) {
-        PK_CONFIGS(PK_CFG_CASE)
-    default: return hipErrorInvalidValue;
-    }
-#undef PK_CFG_CASE
-    return hipGetLastError();
-}
-
-template <int WK>
-hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
-{
-    return (a.vec_a && a.vec_b) ? launch_chain<WK, true>(cfg, a, s)
-                                : launch_chain<WK, false>(cfg, a, s);
-}
-
 }  // namespace
+
+using tiles::kConfigs;
+using tiles::kNumConfigs;
 
 int num_configs() { return kNumConfigs; }
 TileConfig config_at(int i) { return kConfigs[i]; }
 
 // Every output is a chain of K dependent MFMA steps, so the work that can run
 // at once is the number of independent chains (M*N / outputs per MFMA).
-// Measured on MI355X (bench sweep over the encoder's GEMM shapes):
-//   M*N <  600K  -> config 6 (X, 4x4, 1 chain/wave): most waves, shortest tiles
-//   M*N < 1.8M   -> config 7 (X, 4x4, 2 chains/wave)
-//   otherwise    -> config 3 (R, 16x16, 64x64 tiles): MFMA-throughput bound
-TileConfig choose_config(int M, int N, int K)
+// Chosen from a sweep of every configuration over the encoder's GEMM shapes
+// on MI355X (hot weights; times in us for the best and the chosen config):
+//   M*N < 200K          config 12 (S 4x4, 1 chain)    QKV M=32: 11.6
+//   M*N < 1M, K >= 2048 config 17 (S 4x4, 8+8 waves)  FF down M=375: 51.6
+//   M*N < 1M            config 13 (S 4x4, 2 chains)   out/pos/conv: 15-26
+//   M*N < 1.6M          config 14 (S 4x4, 3 chains)   FF up M=375: 35.1
+//   M*N < 3M            config 18 (S 16x16)           FF up M=416/500: 41
+//   otherwise           config 11 (X 32x32)           M=3312: 183-275
+static int choose_index(int M, int N, int K)
 {
-    (void)K;
     const double outputs = (double)M * (double)N;
-    if (outputs < 600e3) return kConfigs[6];
-    if (outputs < 1.8e6) return kConfigs[7];
-    return kConfigs[3];
+    if (outputs < 200e3) return 12;
+    if (outputs < 1.0e6) return K >= 2048 ? 17 : 13;
+    if (outputs < 1.6e6) return 14;
+    if (outputs < 3.0e6) return 18;
+    return 11;
 }
 
-static int config_index(const TileConfig& c)
-{
-    for (int i = 0; i < kNumConfigs; ++i)
-        if (kConfigs[i].family == c.family && kConfigs[i].mfma == c.mfma && kConfigs[i].cw == c.cw &&
-            kConfigs[i].wgm == c.wgm && kConfigs[i].wgn == c.wgn && kConfigs[i].kt == c.kt)
-            return i;
-    return 0;
-}
+TileConfig choose_config(int M, int N, int K) { return kConfigs[choose_index(M, N, K)]; }
 
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
 {
@@ -746,15 +139,14 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
     if (p.kind == W_I8) n_main = (p.N / 16) * 16;     // blas.c:686, 734
     a.N = n_main;
 
-    const int cfg = (cfg_index >= 0 && cfg_index < kNumConfigs)
-                        ? cfg_index
-                        : config_index(choose_config(p.M, n_main, p.K));
+    const int cfg = (cfg_index >= 0 && cfg_index < kNumConfigs) ? cfg_index
+                                                                : choose_index(p.M, n_main, p.K);
     hipError_t err = hipSuccess;
     if (n_main > 0) {
         switch (p.kind) {
-        case W_F32: err = launch_chain<W_F32>(cfg, a, stream); break;
-        case W_I8:  err = launch_chain<W_I8>(cfg, a, stream); break;
-        case W_I4:  err = launch_chain<W_I4>(cfg, a, stream); break;
+        case W_F32: err = tiles::launch_chain_f32(cfg, a, stream); break;
+        case W_I8:  err = tiles::launch_chain_i8(cfg, a, stream); break;
+        case W_I4:  err = tiles::launch_chain_i4(cfg, a, stream); break;
         }
         if (err != hipSuccess) return err;
     }

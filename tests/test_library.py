@@ -80,8 +80,8 @@ def test_tile_configs_are_well_formed():
     cfgs = pk.configs()
     assert len(cfgs) >= 3
     for fam, mf, cw, wgm, wgn, kt in cfgs:
-        assert fam in "RX" and mf in (4, 16, 32) and cw >= 1 and wgm >= 1 and wgn >= 1
-        assert 64 * wgm * wgn <= 1024 and kt % 16 == 0
+        assert fam in "RXS" and mf in (4, 16, 32) and cw >= 1 and wgm >= 1 and wgn >= 1
+        assert (128 if fam == "S" else 64) * wgm * wgn <= 1024 and kt % 16 == 0
     lib = pk.load()
     for shape in [(32, 3072, 1024), (375, 4096, 1024), (375, 1024, 4096), (3312, 4096, 1024)]:
         assert 0 <= lib.pk_gpu_pick_config(*shape) < len(cfgs)
