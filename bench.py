@@ -2,7 +2,8 @@
 
 Workload (one "step"): X fp32 [375, 1024] ~ N(0,1)  ->  int4 GEMM up
 (1024 -> 4096, packed nibbles [1024][2048] with fp32 scales [1024][128])
-->  swish  ->  int4 GEMM down (4096 -> 1024, [4096][512] + [4096][32]),
+with Swish fused into its output store  ->  int4 GEMM down (4096 -> 1024,
+[4096][512] + [4096][32]),
 i.e. the feed-forward of 30 s of audio (375 encoder frames,
 encoder.c:179-217 without the host bias/residual adds), through the C ABI
 of libpk_gpu.so with every input already resident in HBM.  Weight nibbles
@@ -133,12 +134,11 @@ def main():
     lib = pk.load()
 
     def up(i):
+        # up-projection with Swish fused into its output store (encoder.c:193-196)
         p, sc = reps[i % R][0], reps[i % R][1]
-        return lib.pk_gpu_gemm_i4_dev(M, FF, D, 1.0, dX.data_ptr(), D, p.data_ptr(), sc.data_ptr(),
-                                      FF // 2, 0.0, dH.data_ptr(), FF, s)
-
-    def sw():
-        return lib.pk_gpu_swish_dev(dH.data_ptr(), dH.data_ptr(), M * FF, s)
+        return lib.pk_gpu_gemm_i4_ex_dev(M, FF, D, 1.0, dX.data_ptr(), D, p.data_ptr(),
+                                         sc.data_ptr(), FF // 2, 0.0, dH.data_ptr(), FF, None,
+                                         pk.EPI_SWISH, s)
 
     def down(i):
         p, sc = reps[i % R][2], reps[i % R][3]
@@ -146,12 +146,12 @@ def main():
                                       D // 2, 0.0, dO.data_ptr(), D, s)
 
     for i in range(args.warmup):
-        assert up(i) == 0 and sw() == 0 and down(i) == 0, pk.load().pk_gpu_last_error()
+        assert up(i) == 0 and down(i) == 0, pk.load().pk_gpu_last_error()
     torch.cuda.synchronize(dev)
 
     # timed region: K steps; events bracket each GEMM launch on the same stream
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(dev)
@@ -163,10 +163,8 @@ def main():
         e[0].record(stream)
         rc |= up(i)
         e[1].record(stream)
-        rc |= sw()
-        e[2].record(stream)
         rc |= down(i)
-        e[3].record(stream)
+        e[2].record(stream)
     t_end.record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
@@ -176,8 +174,7 @@ def main():
     elapsed_ms = t_start.elapsed_time(t_end)
     ms_per_step = elapsed_ms / K
     up_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
-    sw_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
-    dn_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / K
+    dn_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
 
     flops_up = 2.0 * M * FF * D
     flops_dn = 2.0 * M * D * FF
@@ -212,10 +209,9 @@ def main():
                    "tile_configs": [cfg_up, cfg_dn]},
         "gemm_tflops": round(tflops, 2),
         "gemm_gbps": round(gbytes, 1),
-        "kernel_us": {"int4_up": round(up_ms * 1e3, 2), "swish": round(sw_ms * 1e3, 2),
-                      "int4_down": round(dn_ms * 1e3, 2)},
+        "kernel_us": {"int4_up_swish": round(up_ms * 1e3, 2), "int4_down": round(dn_ms * 1e3, 2)},
         "wall_ms_per_step": round(1e3 * wall / K, 4),
-        "roofline": {"bound": "mfma", "kernel": "int4 chain GEMM (up and down launches)",
+        "roofline": {"bound": "mfma", "kernel": "int4 chain GEMM (up with fused Swish, and down)",
                      "achieved": round(tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": traffic},

@@ -106,6 +106,33 @@ int pk_gpu_sgemm_dev(int M, int N, int K, float alpha,
                      const float *dA, int lda, const float *dB, int ldb,
                      float beta, float *dC, int ldc, void *stream);
 
+/* Fused epilogues (encoder.c:193-216: the feed-forward's bias add, Swish and
+ * 0.5 residual, done on the host after each weight GEMM).  The chain result v
+ * of every output gets, in order:
+ *   bias (length N, device pointer, may be NULL): v = fl(v + bias[j]);
+ *   PK_GPU_EPI_NONE:          C[i][j] = v
+ *   PK_GPU_EPI_SWISH:         C[i][j] = swish(v)   (as pk_gpu_swish_dev)
+ *   PK_GPU_EPI_HALF_RESIDUAL: C[i][j] = C[i][j] + 0.5 * v   (beta must be 0:
+ *                             C holds the residual x on entry)
+ * Bias and residual are exact IEEE operations, so results equal the
+ * reference's GEMM + pk_bias_add (+ x += 0.5 * out) bit for bit; Swish is
+ * the device swish (within a few ulp of the reference's, see
+ * pk_gpu_swish_dev).  No counterpart exists in blas.h: the reference runs
+ * these as separate host loops; these entry points serve GPU-resident
+ * callers that chain the block on the device. */
+#define PK_GPU_EPI_NONE 0
+#define PK_GPU_EPI_SWISH 1
+#define PK_GPU_EPI_HALF_RESIDUAL 2
+int pk_gpu_gemm_i8_ex_dev(int M, int N, int K, float alpha, const float *dA, int lda,
+                          const int8_t *dB, float B_scale, int ldb, float beta, float *dC,
+                          int ldc, const float *dbias, int epilogue, void *stream);
+int pk_gpu_gemm_i4_ex_dev(int M, int N, int K, float alpha, const float *dA, int lda,
+                          const uint8_t *dB, const float *dscales, int ldb, float beta,
+                          float *dC, int ldc, const float *dbias, int epilogue, void *stream);
+int pk_gpu_sgemm_ex_dev(int M, int N, int K, float alpha, const float *dA, int lda,
+                        const float *dB, int ldb, float beta, float *dC, int ldc,
+                        const float *dbias, int epilogue, void *stream);
+
 /* Swish y = x * sigmoid(x) with the reference's polynomial exp
  * (tensor_ops.c:98-120, 367-389); x may equal y. */
 int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);

@@ -11,6 +11,13 @@ namespace pkgpu {
 
 enum WeightKind { W_F32 = 0, W_I8 = 1, W_I4 = 2 };
 
+// Elementwise work fused into the GEMM's output store (encoder.c:193-216):
+//   v = chain result; if bias: v = fl(v + bias[j]); then
+//   EPI_SWISH:         C[i][j] = swish(v)                  (pk_swish)
+//   EPI_HALF_RESIDUAL: C[i][j] = fl(C[i][j] + 0.5 * v)     (macaron residual)
+//   EPI_NONE:          C[i][j] = v
+enum Epilogue { EPI_NONE = 0, EPI_SWISH = 1, EPI_HALF_RESIDUAL = 2 };
+
 // One weight GEMM, C <- beta*C + alpha*A*W, row-major, NoTrans/NoTrans,
 // with W given in one of the on-disk formats (weights.c:240-266):
 //   W_F32: fp32 [K][ldb]
@@ -26,6 +33,8 @@ struct GemmProblem {
     float scale;              // W_I8
     const float* scales;      // W_I4
     float* C; int ldc;
+    const float* bias = nullptr;     // length N, or null
+    Epilogue epi = EPI_NONE;         // EPI_HALF_RESIDUAL requires beta == 0
 };
 
 // Kernel tile configuration chosen for a shape (see choose_config).

@@ -28,43 +28,27 @@ __global__ void i8_edge(KArgs p, int n_begin, int n_edge)
         const float a = __fmul_rn(p.A[(size_t)i * p.lda + k], as);
         c = __fmaf_rn(a, (float)Q[(size_t)k * p.ldb + j], c);
     }
-    p.C[(size_t)i * p.ldc + j] = c;
+    tiles::store_c(p, c, i, j);
 }
 
-// C <- beta*C alone (alpha == 0, int8 scale == 0, or K == 0): blas.c:89-99.
-__global__ void scale_c(float* C, int M, int N, int ldc, float beta)
+// C <- beta*C alone (alpha == 0, int8 scale == 0, or K == 0): blas.c:89-99,
+// followed by the fused epilogue when one is requested.
+__global__ void scale_c(KArgs p)
 {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)M * N) return;
-    const int i = (int)(idx / N), j = (int)(idx % N);
-    float* c = C + (size_t)i * ldc + j;
-    *c = (beta == 0.0f) ? 0.0f : __fmul_rn(*c, beta);
+    if (idx >= (long long)p.M * p.N) return;
+    const int i = (int)(idx / p.N), j = (int)(idx % p.N);
+    float* c = p.C + (size_t)i * p.ldc + j;
+    const float v = (p.beta == 0.0f) ? 0.0f : (p.beta == 1.0f ? *c : __fmul_rn(*c, p.beta));
+    tiles::store_c(p, v, i, j);
 }
 
-// Swish as tensor_ops.c:381-388 / 98-120 write it: e = exp(-x) from a
-// 2^k * poly(r) range reduction, s = 1/(1+e), y = x*s.  The reference build
-// contracts r = t - k*ln2 and 1 + poly*2^k into FMAs, which is followed here;
-// its 1/(1+e) is rcpps plus one Newton step, which no GPU can reproduce, so
-// this uses an IEEE division (agreement within a few ulp, tested).
+// pk_swish over n elements (tensor_ops.c:381-388); x may equal y.
 __global__ void swish(const float* x, float* y, long long n)
 {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float v = x[i];
-    float t = fminf(fmaxf(-v, -87.0f), 87.0f);
-    const float kf = __builtin_rintf(__fmul_rn(t, 1.44269504088896341f));
-    const int ki = (int)kf;
-    const float r = __fmaf_rn(-kf, 0.69314718055994529f, t);
-    float q = 1.0f / 120.0f;
-    q = __fmaf_rn(q, r, 1.0f / 24.0f);
-    q = __fmaf_rn(q, r, 1.0f / 6.0f);
-    q = __fmaf_rn(q, r, 0.5f);
-    q = __fmaf_rn(q, r, 1.0f);
-    q = __fmaf_rn(q, r, 1.0f);
-    const float p2 = __int_as_float((ki + 127) << 23);
-    const float d = __fmaf_rn(q, p2, 1.0f);
-    const float s = __fdiv_rn(1.0f, d);
-    y[i] = __fmul_rn(s, v);
+    y[i] = tiles::swish_f(x[i]);
 }
 
 }  // namespace
@@ -100,16 +84,9 @@ TileConfig choose_config(int M, int N, int K) { return kConfigs[choose_index(M, 
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
 {
     if (p.M <= 0 || p.N <= 0) return hipSuccess;
-    const bool early = (p.alpha == 0.0f) || (p.kind == W_I8 && p.scale == 0.0f) || p.K <= 0;
-    if (early) {   // blas.c:764-765, 955-956, 1063-1064: only the beta step runs
-        if (p.beta == 1.0f) return hipSuccess;
-        const long long n = (long long)p.M * p.N;
-        hipLaunchKernelGGL(scale_c, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                           p.C, p.M, p.N, p.ldc, p.beta);
-        return hipGetLastError();
-    }
+    if (p.epi == EPI_HALF_RESIDUAL && p.beta != 0.0f) return hipErrorInvalidValue;
 
-    KArgs a;
+    KArgs a = {};
     a.M = p.M; a.N = p.N; a.K = p.K;
     a.alpha = p.alpha; a.beta = p.beta;
     a.A = p.A; a.lda = p.lda;
@@ -117,6 +94,16 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
     a.scale = p.scale;
     a.scales = p.scales; a.n_groups = p.N / 32;
     a.C = p.C; a.ldc = p.ldc;
+    a.bias = p.bias; a.epi = p.epi;
+
+    const bool fused = p.bias != nullptr || p.epi != EPI_NONE;
+    const bool early = (p.alpha == 0.0f) || (p.kind == W_I8 && p.scale == 0.0f) || p.K <= 0;
+    if (early) {   // blas.c:764-765, 955-956, 1063-1064: only the beta step runs
+        if (p.beta == 1.0f && !fused) return hipSuccess;
+        const long long n = (long long)p.M * p.N;
+        hipLaunchKernelGGL(scale_c, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
 
     // Exact extents of what the call may read; the kernels address operands
     // through 32-bit buffer offsets, so each must stay below 2 GiB.

@@ -62,6 +62,8 @@ struct KArgs {
     // whether A / B rows allow 16-byte vector loads.
     uint32_t a_bytes, b_bytes, s_bytes;
     int vec_a, vec_b;
+    const float* bias;       // fused epilogue (Epilogue in pk_gemm_kernels.h)
+    int epi;
 };
 
 // Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format).
@@ -370,6 +372,48 @@ __device__ __forceinline__ void run_chunks(F& f, int K, int KT)
     chunk_tail<0, PD>(f, c0, nchunks);
 }
 
+// Swish as tensor_ops.c:381-388 / 98-120 write it: e = exp(-x) from a
+// 2^k * poly(r) range reduction, s = 1/(1+e), y = x*s.  The reference build
+// contracts r = t - k*ln2 and 1 + poly*2^k into FMAs, which is followed here;
+// its 1/(1+e) is rcpps plus one Newton step, which no GPU can reproduce, so
+// this uses an IEEE division (agreement within a few ulp, tested).
+__device__ inline float swish_f(float v)
+{
+    const float t = fminf(fmaxf(-v, -87.0f), 87.0f);
+    const float kf = __builtin_rintf(__fmul_rn(t, 1.44269504088896341f));
+    const int ki = (int)kf;
+    const float r = __fmaf_rn(-kf, 0.69314718055994529f, t);
+    float q = 1.0f / 120.0f;
+    q = __fmaf_rn(q, r, 1.0f / 24.0f);
+    q = __fmaf_rn(q, r, 1.0f / 6.0f);
+    q = __fmaf_rn(q, r, 0.5f);
+    q = __fmaf_rn(q, r, 1.0f);
+    q = __fmaf_rn(q, r, 1.0f);
+    const float p2 = __int_as_float((ki + 127) << 23);
+    const float d = __fmaf_rn(q, p2, 1.0f);
+    const float s = __fdiv_rn(1.0f, d);
+    return __fmul_rn(s, v);
+}
+
+// The fused output step for C[row][col] (row < M, col < N): bias add, then
+// the activation or the half residual (encoder.c:193-216).  0.5 * v is exact,
+// so fl(c + 0.5 * v) equals the reference's fma(out, 0.5, x).
+__device__ inline float epilogue(const KArgs& p, float v, int row, int col)
+{
+    if (p.bias) v = __fadd_rn(v, p.bias[col]);
+    if (p.epi == EPI_SWISH) return swish_f(v);
+    if (p.epi == EPI_HALF_RESIDUAL) return __fmaf_rn(v, 0.5f, p.C[(size_t)row * p.ldc + col]);
+    return v;
+}
+
+// Store one output; the plain store is the common case and stays a single
+// write (the condition is uniform across the launch).
+__device__ inline void store_c(const KArgs& p, float v, int row, int col)
+{
+    float* c = p.C + (size_t)row * p.ldc + col;
+    *c = (p.bias == nullptr && p.epi == EPI_NONE) ? v : epilogue(p, v, row, col);
+}
+
 // Chains start from beta*C exactly as scale_c leaves it (blas.c:89-99).
 __device__ inline float beta_c(const KArgs& p, int row, int col)
 {
@@ -495,7 +539,7 @@ void chain_gemm(KArgs p)
         for (int r = 0; r < T::NACC; ++r) {
             const int row = m0 + wm * 64 + T::row(lane, r);
             const int col = n0 + wn * WN + c * T::NCOL + T::col(lane, r);
-            if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[c][r];
+            if (row < p.M && col < p.N) store_c(p, acc[c][r], row, col);
         }
     }
 }
@@ -678,7 +722,7 @@ void chain_gemm_x(KArgs p)
         for (int r = 0; r < T::NACC; ++r) {
             const int row = m0 + wrow + g * BS + T::row(lane, r);
             const int col = n0 + wn * 64 + T::col(lane, r);
-            if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[g][r];
+            if (row < p.M && col < p.N) store_c(p, acc[g][r], row, col);
         }
     }
 }
@@ -799,7 +843,7 @@ void chain_gemm_xs(KArgs p)
         for (int r = 0; r < T::NACC; ++r) {
             const int row = m0 + wrow + g * BS + T::row(lane, r);
             const int col = n0 + wn * 64 + T::col(lane, r);
-            if (row < p.M && col < p.N) p.C[(size_t)row * p.ldc + col] = acc[g][r];
+            if (row < p.M && col < p.N) store_c(p, acc[g][r], row, col);
         }
     }
 }

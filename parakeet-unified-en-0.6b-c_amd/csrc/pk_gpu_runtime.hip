@@ -381,40 +381,80 @@ int pk_gpu_sgemm(int transA, int transB, int M, int N, int K, float alpha, const
     return host_gemm(p, A, B, nullptr, C, sizeof(float), N);
 }
 
+// Device-pointer entry points; the *_ex forms add the fused epilogue.
+static int check_epilogue(const float* bias, int epi, float beta)
+{
+    if (epi < PK_GPU_EPI_NONE || epi > PK_GPU_EPI_HALF_RESIDUAL)
+        return fail(PK_GPU_EINVAL, "epilogue %d is not one of PK_GPU_EPI_*", epi);
+    if (epi == PK_GPU_EPI_HALF_RESIDUAL && beta != 0.0f)
+        return fail(PK_GPU_EINVAL, "half-residual epilogue needs beta == 0 (C is the residual)");
+    (void)bias;
+    return PK_GPU_OK;
+}
+
+static int dev_gemm(GemmProblem p, const float* dbias, int epi, void* stream)
+{
+    int rc = check_epilogue(dbias, epi, p.beta);
+    if (rc) return rc;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    p.bias = dbias;
+    p.epi = static_cast<pkgpu::Epilogue>(epi);
+    return launch(p, s);
+}
+
+int pk_gpu_gemm_i8_ex_dev(int M, int N, int K, float alpha, const float* dA, int lda,
+                          const int8_t* dB, float B_scale, int ldb, float beta, float* dC, int ldc,
+                          const float* dbias, int epilogue, void* stream)
+{
+    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_I8, M, N, K, alpha, beta, dA, lda, dB, ldb, B_scale, nullptr, dC, ldc};
+    return dev_gemm(p, dbias, epilogue, stream);
+}
+
+int pk_gpu_gemm_i4_ex_dev(int M, int N, int K, float alpha, const float* dA, int lda,
+                          const uint8_t* dB, const float* dscales, int ldb, float beta, float* dC,
+                          int ldc, const float* dbias, int epilogue, void* stream)
+{
+    if (N % 32 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is not a multiple of 32", N);
+    int rc = check_gemm(M, N, K, lda, N / 2, ldb, ldc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_I4, M, N, K, alpha, beta, dA, lda, dB, ldb, 0.0f, dscales, dC, ldc};
+    return dev_gemm(p, dbias, epilogue, stream);
+}
+
+int pk_gpu_sgemm_ex_dev(int M, int N, int K, float alpha, const float* dA, int lda,
+                        const float* dB, int ldb, float beta, float* dC, int ldc,
+                        const float* dbias, int epilogue, void* stream)
+{
+    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_F32, M, N, K, alpha, beta, dA, lda, dB, ldb, 0.0f, nullptr, dC, ldc};
+    return dev_gemm(p, dbias, epilogue, stream);
+}
+
 int pk_gpu_gemm_i8_dev(int M, int N, int K, float alpha, const float* dA, int lda,
                        const int8_t* dB, float B_scale, int ldb, float beta, float* dC, int ldc,
                        void* stream)
 {
-    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
-    if (rc) return rc;
-    hipStream_t s = pick_stream(stream, &rc);
-    if (rc) return rc;
-    GemmProblem p{pkgpu::W_I8, M, N, K, alpha, beta, dA, lda, dB, ldb, B_scale, nullptr, dC, ldc};
-    return launch(p, s);
+    return pk_gpu_gemm_i8_ex_dev(M, N, K, alpha, dA, lda, dB, B_scale, ldb, beta, dC, ldc,
+                                 nullptr, PK_GPU_EPI_NONE, stream);
 }
 
 int pk_gpu_gemm_i4_dev(int M, int N, int K, float alpha, const float* dA, int lda,
                        const uint8_t* dB, const float* dscales, int ldb, float beta, float* dC,
                        int ldc, void* stream)
 {
-    if (N % 32 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is not a multiple of 32", N);
-    int rc = check_gemm(M, N, K, lda, N / 2, ldb, ldc);
-    if (rc) return rc;
-    hipStream_t s = pick_stream(stream, &rc);
-    if (rc) return rc;
-    GemmProblem p{pkgpu::W_I4, M, N, K, alpha, beta, dA, lda, dB, ldb, 0.0f, dscales, dC, ldc};
-    return launch(p, s);
+    return pk_gpu_gemm_i4_ex_dev(M, N, K, alpha, dA, lda, dB, dscales, ldb, beta, dC, ldc,
+                                 nullptr, PK_GPU_EPI_NONE, stream);
 }
 
 int pk_gpu_sgemm_dev(int M, int N, int K, float alpha, const float* dA, int lda, const float* dB,
                      int ldb, float beta, float* dC, int ldc, void* stream)
 {
-    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
-    if (rc) return rc;
-    hipStream_t s = pick_stream(stream, &rc);
-    if (rc) return rc;
-    GemmProblem p{pkgpu::W_F32, M, N, K, alpha, beta, dA, lda, dB, ldb, 0.0f, nullptr, dC, ldc};
-    return launch(p, s);
+    return pk_gpu_sgemm_ex_dev(M, N, K, alpha, dA, lda, dB, ldb, beta, dC, ldc, nullptr,
+                               PK_GPU_EPI_NONE, stream);
 }
 
 int pk_gpu_swish_dev(const float* dx, float* dy, long long n, void* stream)

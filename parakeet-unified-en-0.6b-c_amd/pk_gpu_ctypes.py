@@ -34,12 +34,17 @@ _PROTOS = {
     "pk_gpu_gemm_i8_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _f, _i, _f, _p, _i, _p]),
     "pk_gpu_gemm_i4_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _p, _i, _f, _p, _i, _p]),
     "pk_gpu_sgemm_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i, _p]),
+    "pk_gpu_gemm_i8_ex_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _f, _i, _f, _p, _i, _p, _i, _p]),
+    "pk_gpu_gemm_i4_ex_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _p, _i, _f, _p, _i, _p, _i, _p]),
+    "pk_gpu_sgemm_ex_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i, _p, _i, _p]),
     "pk_gpu_swish_dev": (_i, [_p, _p, _ll, _p]),
     "pk_gpu_num_configs": (_i, []),
     "pk_gpu_config_info": (_i, [_i, _p, _p, _p, _p, _p, _p]),
     "pk_gpu_pick_config": (_i, [_i, _i, _i]),
     "pk_gpu_force_config": (_i, [_i]),
 }
+
+EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL = 0, 1, 2
 
 STATUS = {0: "OK", -1: "EINVAL", -2: "ENOTSUP", -3: "ENOMEM", -4: "EHIP", -5: "ENODEV"}
 

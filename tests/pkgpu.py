@@ -61,28 +61,42 @@ class Dev:
     def sync(self):
         self.torch.cuda.synchronize(self.dev)
 
-    def gemm(self, kind, A, W, C0, alpha=1.0, beta=0.0, scale=None, scales=None, cfg=-1):
-        """Run C = beta*C0 + alpha*A*W through *_dev entry points; returns numpy C."""
+    def gemm(self, kind, A, W, C0, alpha=1.0, beta=0.0, scale=None, scales=None, cfg=-1,
+             bias=None, epi=None):
+        """Run C = beta*C0 + alpha*A*W through the *_dev entry points (the *_ex_dev
+        ones when a bias or an epilogue is given); returns numpy C."""
         M, K = A.shape
         dA, dC = self.put(A), self.put(C0)
+        ex = bias is not None or epi is not None
+        dbias = self.put(bias) if bias is not None else None
+        tail = ((dbias.data_ptr() if dbias is not None else None, epi or 0, self.stream())
+                if ex else (self.stream(),))
         pk.call("pk_gpu_force_config", cfg)
         try:
             if kind == "i4":
                 N = W.shape[1] * 2
                 dW, dS = self.put(W), self.put(scales)
-                pk.call("pk_gpu_gemm_i4_dev", M, N, K, alpha, dA.data_ptr(), K, dW.data_ptr(),
-                        dS.data_ptr(), N // 2, beta, dC.data_ptr(), N, self.stream())
+                pk.call("pk_gpu_gemm_i4_ex_dev" if ex else "pk_gpu_gemm_i4_dev", M, N, K, alpha,
+                        dA.data_ptr(), K, dW.data_ptr(), dS.data_ptr(), N // 2, beta,
+                        dC.data_ptr(), N, *tail)
             elif kind == "i8":
                 N = W.shape[1]
                 dW = self.put(W)
-                pk.call("pk_gpu_gemm_i8_dev", M, N, K, alpha, dA.data_ptr(), K, dW.data_ptr(),
-                        scale, N, beta, dC.data_ptr(), N, self.stream())
+                pk.call("pk_gpu_gemm_i8_ex_dev" if ex else "pk_gpu_gemm_i8_dev", M, N, K, alpha,
+                        dA.data_ptr(), K, dW.data_ptr(), scale, N, beta, dC.data_ptr(), N, *tail)
             else:
                 N = W.shape[1]
                 dW = self.put(W)
-                pk.call("pk_gpu_sgemm_dev", M, N, K, alpha, dA.data_ptr(), K, dW.data_ptr(), N,
-                        beta, dC.data_ptr(), N, self.stream())
+                pk.call("pk_gpu_sgemm_ex_dev" if ex else "pk_gpu_sgemm_dev", M, N, K, alpha,
+                        dA.data_ptr(), K, dW.data_ptr(), N, beta, dC.data_ptr(), N, *tail)
         finally:
             pk.call("pk_gpu_force_config", -1)
         self.sync()
         return dC.cpu().numpy()
+
+    def swish(self, X):
+        """pk_gpu_swish_dev on a copy of X; returns numpy."""
+        dX = self.put(X)
+        pk.call("pk_gpu_swish_dev", dX.data_ptr(), dX.data_ptr(), dX.numel(), self.stream())
+        self.sync()
+        return dX.cpu().numpy()

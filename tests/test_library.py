@@ -85,3 +85,17 @@ def test_tile_configs_are_well_formed():
     lib = pk.load()
     for shape in [(32, 3072, 1024), (375, 4096, 1024), (375, 1024, 4096), (3312, 4096, 1024)]:
         assert 0 <= lib.pk_gpu_pick_config(*shape) < len(cfgs)
+
+
+def test_epilogue_validation_precedes_device_use():
+    lib = pk.load()
+    A = np.ones((2, 4), np.float32)
+    C = np.zeros((2, 16), np.float32)
+    # unknown epilogue
+    assert lib.pk_gpu_sgemm_ex_dev(2, 16, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 16, 0.0,
+                                   C.ctypes.data, 16, None, 7, None) == -1
+    assert b"epilogue" in lib.pk_gpu_last_error()
+    # the half residual reads C as the residual, so beta must be 0
+    assert lib.pk_gpu_sgemm_ex_dev(2, 16, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 16, 1.0,
+                                   C.ctypes.data, 16, None, pk.EPI_HALF_RESIDUAL, None) == -1
+    assert b"beta" in lib.pk_gpu_last_error()
