@@ -27,8 +27,7 @@ import time
 import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path.insert(0, os.path.join(ROOT, "tests"))
-sys.path.insert(0, os.path.join(ROOT, "oracle"))
+PKG = os.path.join(ROOT, "parakeet-unified-en-0.6b-c_amd")
 
 METRIC = "encoder frames/sec + GEMM GB/s & TFLOP/s vs MI355X roofline (int4/int8)"
 M, D, FF = 375, 1024, 4096
@@ -43,17 +42,29 @@ def int4_bytes(K, N):
     return K * N // 2 + 4 * K * (N // 32) + 4 * M * K + 4 * M * N
 
 
-def make_inputs(po):
-    X = po.normal((M, D), 0.0, 1.0, po.seed(SEED, "X"))
-    P1 = po.bytes_((D, FF // 2), po.seed(SEED, "up.P"))
-    S1 = po.uniform((D, FF // 32), 0.005, 0.02, po.seed(SEED, "up.S"))
-    P2 = po.bytes_((FF, D // 2), po.seed(SEED, "down.P"))
-    S2 = po.uniform((FF, D // 32), 0.005, 0.02, po.seed(SEED, "down.S"))
+def rng(tensor):
+    """numpy PCG64 stream of one named tensor of the workload (platform-independent)."""
+    return np.random.Generator(np.random.PCG64([SEED, tensor]))
+
+
+def make_inputs():
+    """Seeded synthetic inputs: X ~ N(0,1); packed int4 bytes uniform 0..255 (each
+    nibble uniform 0..15, decoded signed); scales ~U(0.005, 0.02)."""
+    X = rng(0).standard_normal((M, D)).astype(np.float32)
+    P1 = rng(1).integers(0, 256, (D, FF // 2), dtype=np.uint8)
+    S1 = rng(2).uniform(0.005, 0.02, (D, FF // 32)).astype(np.float32)
+    P2 = rng(3).integers(0, 256, (FF, D // 2), dtype=np.uint8)
+    S2 = rng(4).uniform(0.005, 0.02, (FF, D // 32)).astype(np.float32)
     return X, P1, S1, P2, S2
 
 
-def cpu_baseline(po, X, P1, S1, P2, S2, budget_s):
-    """The reference's CPU path on the same inputs, timed for ~budget_s."""
+def cpu_baseline(X, P1, S1, P2, S2, budget_s):
+    """The reference's CPU path on the same inputs, timed for ~budget_s: its own
+    cblas_sgemm_q4b and pk_swish, compiled from its sources into oracle/_ref."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+    if not po.have_ref():
+        return None
     os.environ["PK_THREADS"] = str(CPU_THREADS)
     ref = po.ref("ref")
     threads = ref.pk_pool_nthreads(ref.pk_pool())
@@ -80,6 +91,15 @@ def cpu_baseline(po, X, P1, S1, P2, S2, budget_s):
             "ms_per_step": round(1000 * el / n, 3)}
 
 
+def load_binding():
+    """The ctypes binding of libpk_gpu.so (raises if the library was not built)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("pk_gpu_ctypes", os.path.join(PKG, "pk_gpu_ctypes.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
 def copy_calibration():
     """10 torch device copies of 256 MiB: each reads and writes exactly
     268,435,456 bytes, which scales the traffic counters."""
@@ -90,6 +110,77 @@ def copy_calibration():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": src.numel() * 4, "copies": 10}), flush=True)
+
+
+def alg_bytes(kind, m, n, k):
+    """Algorithmic bytes of one GEMM call: weights (+ int4 scales) + A + C."""
+    w = {"i4": k * n // 2 + 4 * k * (n // 32), "i8": k * n + 4, "f32": 4 * k * n}[kind]
+    return w + 4 * m * k + 4 * m * n
+
+
+def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20):
+    """One JSON line per GEMM shape ("kind:MxNxK"): resident inputs, weights
+    rotating over enough replicas to exceed the Infinity Cache, average launch
+    time from HIP events around a graph replay of `steps` launches."""
+    import torch
+    pk = load_binding()
+    pk.call("pk_gpu_init", 0)
+    lib = pk.load()
+    dev = torch.device("cuda:0")
+    cur = lambda: torch.cuda.current_stream(dev).cuda_stream   # the capture stream inside a graph
+    g = torch.Generator(device=dev)
+    for spec in specs:
+        kind, dims = spec.split(":")
+        m, n, k = (int(v) for v in dims.lower().split("x"))
+        g.manual_seed(SEED)
+        A = torch.randn((m, k), generator=g, device=dev)
+        C = torch.zeros((m, n), device=dev)
+        wbytes = alg_bytes(kind, m, n, k) - 4 * m * k - 4 * m * n
+        reps = max(2, min(256, -(-min_weight_bytes // wbytes)))
+        if kind == "i4":
+            W = [torch.randint(0, 256, (k, n // 2), dtype=torch.uint8, device=dev, generator=g)
+                 for _ in range(reps)]
+            S = [torch.rand((k, n // 32), device=dev, generator=g) * 0.015 + 0.005 for _ in range(reps)]
+            call = lambda i: lib.pk_gpu_gemm_i4_dev(m, n, k, 1.0, A.data_ptr(), k, W[i % reps].data_ptr(),
+                                                    S[i % reps].data_ptr(), n // 2, 0.0, C.data_ptr(), n,
+                                                    cur())
+        elif kind == "i8":
+            W = [torch.randint(-127, 128, (k, n), dtype=torch.int8, device=dev, generator=g)
+                 for _ in range(reps)]
+            call = lambda i: lib.pk_gpu_gemm_i8_dev(m, n, k, 1.0, A.data_ptr(), k, W[i % reps].data_ptr(),
+                                                    0.01, n, 0.0, C.data_ptr(), n, cur())
+        else:
+            W = [torch.randn((k, n), device=dev, generator=g) * 0.02 for _ in range(reps)]
+            call = lambda i: lib.pk_gpu_sgemm_dev(m, n, k, 1.0, A.data_ptr(), k, W[i % reps].data_ptr(),
+                                                  n, 0.0, C.data_ptr(), n, cur())
+        for i in range(warmup):
+            assert call(i) == 0, lib.pk_gpu_last_error()
+        torch.cuda.synchronize(dev)
+        # The launches are captured into one HIP graph and replayed, so they run
+        # back to back: a host loop of ctypes launches cannot keep a queue of
+        # ~10 us kernels full, and per-launch events would time its gaps.
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                call(i)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        us = e0.elapsed_time(e1) / steps * 1e3
+        del graph
+        tf = 2.0 * m * n * k / us / 1e6
+        gbs = alg_bytes(kind, m, n, k) / us / 1e3
+        print(json.dumps({"gemm": f"{kind} {m}x{n}x{k}", "config": lib.pk_gpu_pick_config(m, n, k),
+                          "avg_us": round(us, 2), "tflops": round(tf, 2), "gbps": round(gbs, 1),
+                          "frac_mfma_fp32": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                          "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_replicas": reps,
+                          "steps": steps}), flush=True)
+        del W, A, C
+        torch.cuda.empty_cache()
 
 
 def main():
@@ -103,9 +194,15 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 256 MiB device-to-device copies (the reference "
                          "reading for FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--gemm", action="append", default=[], metavar="KIND:MxNxK",
+                    help="instead of the FFN pair, time single GEMMs (kind i4, i8 or f32); "
+                         "one JSON line each")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.gemm:
+        gemm_mode(args.gemm, args.steps, args.warmup)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (single-GPU hot path; "
@@ -113,8 +210,7 @@ def main():
         sys.exit(2)
 
     import torch
-    from pkgpu import pk
-    import pyoracle as po
+    pk = load_binding()
 
     pk.call("pk_gpu_init", 0)
     dev = torch.device("cuda:0")
@@ -122,7 +218,7 @@ def main():
     stream = torch.cuda.current_stream(dev)
     s = stream.cuda_stream
 
-    X, P1, S1, P2, S2 = make_inputs(po)
+    X, P1, S1, P2, S2 = make_inputs()
     R = args.replicas
     dX = torch.from_numpy(X).to(dev)
     # rotating weight replicas: R copies of (P1, S1, P2, S2), 5.2 MB each
@@ -216,10 +312,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": traffic},
     }
-    if not args.no_cpu and po.have_ref():
-        out["cpu_baseline"] = cpu_baseline(po, X, P1, S1, P2, S2, args.cpu_seconds)
-    else:
-        out["cpu_baseline"] = None
+    out["cpu_baseline"] = None if args.no_cpu else cpu_baseline(X, P1, S1, P2, S2, args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 

@@ -60,7 +60,7 @@ def main():
     # digests of the seeded benchmark inputs (the bytes both hosts must share)
     sys.path.insert(0, ROOT)
     import bench
-    X, P1, S1, P2, S2 = bench.make_inputs(po)
+    X, P1, S1, P2, S2 = bench.make_inputs()
     dig = {name: hashlib.sha256(a.tobytes()).hexdigest()
            for name, a in (("ffn_X", X), ("ffn_up_P", P1), ("ffn_up_S", S1),
                            ("ffn_down_P", P2), ("ffn_down_S", S2))}

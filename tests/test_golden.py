@@ -47,7 +47,7 @@ def test_bench_inputs_match_committed_digests():
     import sys
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     import bench
-    X, P1, S1, P2, S2 = bench.make_inputs(po)
+    X, P1, S1, P2, S2 = bench.make_inputs()
     want = json.load(open(os.path.join(GOLD, "digests.json")))
     got = {name: hashlib.sha256(a.tobytes()).hexdigest()
            for name, a in (("ffn_X", X), ("ffn_up_P", P1), ("ffn_up_S", S1),
