@@ -511,6 +511,10 @@ void chain_gemm(KArgs p)
                             bv[cur ^ 1][u][cc] = bs[((kb + 1) * U + u) * BN + bcol[cc]];
                     }
                 }
+                // Keep the next block's reads here, a block ahead of their use:
+                // left alone, the scheduler sinks them next to their MFMAs and
+                // the chains wait on LDS latency.
+                __builtin_amdgcn_sched_barrier(0);
                 st.store(raw[(j + 1) % PD], p, tid, as_n, bs_n, kb * PER_BLK, (kb + 1) * PER_BLK);
 #pragma unroll
                 for (int u = 0; u < U; ++u)
@@ -695,6 +699,7 @@ void chain_gemm_x(KArgs p)
 #pragma unroll
                     for (int t = 0; t < NB; ++t) b[cur ^ 1][t] = bs[((kb + 1) * NB + t) * BN];
                 }
+                __builtin_amdgcn_sched_barrier(0);    // next block's reads stay a block ahead
                 st.store(raw[(j + 1) % PD], p, tid, as_n, bs_n, kb * PER_BLK, (kb + 1) * PER_BLK);
                 x_steps<T, R, 0>(a[cur], b[cur], acc);
             }

@@ -76,6 +76,17 @@ def test_tile_config_bit_exact(dev, cfg, kind):
 
 
 @pytest.mark.parametrize("kind", ["f32", "i8", "i4"])
+@pytest.mark.parametrize("cfg", range(len(pk.configs())))
+def test_tile_config_alpha_not_one(dev, cfg, kind):
+    """alpha != 1 stages fl(alpha*a) (its own kernel instantiation); with beta."""
+    for (M, N, K) in [(33, 96, 160), (17, 192, 1030)]:
+        A, W, extra, C0 = make(kind, M, N, K, f"cfga.{kind}.{M}.{N}.{K}")
+        got = run(dev, kind, A, W, extra, C0, alpha=-0.75, beta=0.5, cfg=cfg)
+        want = oracle(kind, A, W, extra, C0, alpha=-0.75, beta=0.5)
+        assert_same(got, want, f"cfg{cfg} {kind} {M}x{N}x{K} alpha=-0.75")
+
+
+@pytest.mark.parametrize("kind", ["f32", "i8", "i4"])
 def test_alpha_beta_variants(dev, kind):
     M, N, K = 37, 96, 70
     A, W, extra, C0 = make(kind, M, N, K, f"ab.{kind}")
