@@ -95,6 +95,14 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
     a.scales = p.scales; a.n_groups = p.N / 32;
     a.C = p.C; a.ldc = p.ldc;
     a.bias = p.bias; a.epi = p.epi;
+    // Keep the larger operand's blocks within one XCD's L2 (tile_origin).
+    {
+        const double a_total = 4.0 * p.M * p.K;
+        const double w_total = p.kind == W_F32 ? 4.0 * p.K * p.N
+                             : p.kind == W_I8  ? 1.0 * p.K * p.N
+                                               : 0.5 * p.K * p.N + 4.0 * p.K * (p.N / 32);
+        a.group_rows = a_total >= w_total;
+    }
 
     const bool fused = p.bias != nullptr || p.epi != EPI_NONE;
     const bool early = (p.alpha == 0.0f) || (p.kind == W_I8 && p.scale == 0.0f) || p.K <= 0;

@@ -64,7 +64,29 @@ struct KArgs {
     int vec_a, vec_b;
     const float* bias;       // fused epilogue (Epilogue in pk_gemm_kernels.h)
     int epi;
+    int group_rows;          // tile order: 1 = an XCD's tiles share rows of A, 0 = columns of W
 };
+
+// MI355X dispatches workgroups to its 8 XCDs round-robin by linear id, and
+// each XCD has its own L2.  Tiles are re-ordered so that each XCD owns one
+// contiguous run of the tile sequence, which walks along a row of tiles
+// (sharing A, group_rows) or down a column (sharing W): an operand block is
+// then fetched into one L2 instead of all eight.  The map from the linear id
+// to the position in the sequence is a bijection for any grid size.
+constexpr int kXcds = 8;
+
+__device__ inline void tile_origin(const KArgs& p, int BM, int BN, int& m0, int& n0)
+{
+    const int nbx = gridDim.x, nby = gridDim.y, total = nbx * nby;
+    const int lin = blockIdx.y * nbx + blockIdx.x;
+    const int xcd = lin % kXcds, local = lin / kXcds;
+    const int base = total / kXcds, extra = total % kXcds;
+    const int t = xcd * base + min(xcd, extra) + local;   // start of this XCD's run + local
+    const int bx = p.group_rows ? t % nbx : t / nby;
+    const int by = p.group_rows ? t / nbx : t % nby;
+    m0 = by * BM;
+    n0 = bx * BN;
+}
 
 // Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format).
 constexpr int kRsrcWord3 = 0x00020000;
@@ -450,7 +472,8 @@ void chain_gemm(KArgs p)
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int m0, n0;
+    tile_origin(p, BM, BN, m0, n0);
 
     typename T::acc_t acc[CW];
 #pragma unroll
@@ -644,7 +667,8 @@ void chain_gemm_x(KArgs p)
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave / NWN, wn = wave % NWN;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int m0, n0;
+    tile_origin(p, BM, BN, m0, n0);
     const int wrow = wm * R * BS;                  // wave's first row within the tile
 
     typename T::acc_t acc[R];
@@ -763,7 +787,8 @@ void chain_gemm_xs(KArgs p)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int m0, n0;
+    tile_origin(p, BM, BN, m0, n0);
 
     if (wave >= NC) {
         // Producer: chunk c's raw operands live in raw[c % PD]; while the

@@ -11,7 +11,8 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libpk_gpu.so")
+# PK_GPU_LIB selects another build of the library (e.g. to compare two builds).
+LIB_PATH = os.environ.get("PK_GPU_LIB") or os.path.join(LIB_DIR, "libpk_gpu.so")
 SHIM_PATH = os.path.join(LIB_DIR, "libpk_gpu_cblas.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "pk_gpu.h")
 
