@@ -186,7 +186,8 @@ int launch(const GemmProblem& p, hipStream_t s)
 {
     hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg);
     if (e == hipErrorInvalidValue)
-        return fail(PK_GPU_EINVAL, "operand extent of %dx%dx%d GEMM exceeds 2 GiB", p.M, p.N, p.K);
+        return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
+                    p.M, p.N, p.K);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return PK_GPU_OK;
 }
@@ -290,6 +291,18 @@ void pk_gpu_shutdown(void)
 
 const char* pk_gpu_last_error(void) { return t_err.c_str(); }
 
+// Caller holds g_mu.
+static bool overlaps_registered(uintptr_t h, size_t bytes)
+{
+    auto it = g_weights.upper_bound(h);
+    if (it != g_weights.end() && it->first < h + bytes) return true;
+    if (it != g_weights.begin()) {
+        --it;
+        if (it->first + it->second.bytes > h) return true;
+    }
+    return false;
+}
+
 int pk_gpu_register_weight(const void* host, size_t bytes)
 {
     if (!host || bytes == 0) return fail(PK_GPU_EINVAL, "register: NULL or empty range");
@@ -299,15 +312,11 @@ int pk_gpu_register_weight(const void* host, size_t bytes)
     const uintptr_t h = reinterpret_cast<uintptr_t>(host);
     {
         std::lock_guard<std::mutex> lk(g_mu);
-        auto it = g_weights.upper_bound(h);
-        if (it != g_weights.end() && it->first < h + bytes)
+        if (overlaps_registered(h, bytes))
             return fail(PK_GPU_EINVAL, "register: range overlaps a registered weight");
-        if (it != g_weights.begin()) {
-            --it;
-            if (it->first + it->second.bytes > h)
-                return fail(PK_GPU_EINVAL, "register: range overlaps a registered weight");
-        }
     }
+    // The upload runs unlocked; the overlap test is repeated before insertion
+    // in case another thread registered an overlapping range meanwhile.
     void* d = nullptr;
     hipError_t e = hipMalloc(&d, bytes);
     if (e != hipSuccess) return fail(PK_GPU_ENOMEM, "register: device alloc of %zu bytes failed", bytes);
@@ -316,10 +325,16 @@ int pk_gpu_register_weight(const void* host, size_t bytes)
         (void)hipFree(d);
         return hip_fail(e, "register: upload");
     }
-    std::lock_guard<std::mutex> lk(g_mu);
-    g_weights[h] = Resident{bytes, d};
-    g_resident_bytes += bytes;
-    return PK_GPU_OK;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!overlaps_registered(h, bytes)) {
+            g_weights[h] = Resident{bytes, d};
+            g_resident_bytes += bytes;
+            return PK_GPU_OK;
+        }
+    }
+    (void)hipFree(d);
+    return fail(PK_GPU_EINVAL, "register: range overlaps a registered weight");
 }
 
 int pk_gpu_unregister_weight(const void* host)
@@ -396,6 +411,11 @@ static int dev_gemm(GemmProblem p, const float* dbias, int epi, void* stream)
 {
     int rc = check_epilogue(dbias, epi, p.beta);
     if (rc) return rc;
+    // A NULL device operand would become a buffer descriptor at address 0.
+    if (p.M > 0 && p.N > 0 && !p.C) return fail(PK_GPU_EINVAL, "C is NULL");
+    if (does_multiply(p) &&
+        (!p.A || !p.B || (p.kind == pkgpu::W_I4 && !p.scales)))
+        return fail(PK_GPU_EINVAL, "A, B or scales is NULL");
     hipStream_t s = pick_stream(stream, &rc);
     if (rc) return rc;
     p.bias = dbias;

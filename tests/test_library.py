@@ -99,3 +99,14 @@ def test_epilogue_validation_precedes_device_use():
     assert lib.pk_gpu_sgemm_ex_dev(2, 16, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 16, 1.0,
                                    C.ctypes.data, 16, None, pk.EPI_HALF_RESIDUAL, None) == -1
     assert b"beta" in lib.pk_gpu_last_error()
+
+
+def test_null_device_operands_are_rejected():
+    """A NULL device pointer must be an error, never a descriptor at address 0."""
+    lib = pk.load()
+    assert lib.pk_gpu_sgemm_dev(4, 16, 8, 1.0, None, 8, None, 16, 0.0, None, 16, None) == -1
+    assert b"NULL" in lib.pk_gpu_last_error()
+    C = np.zeros((4, 32), np.float32)
+    assert lib.pk_gpu_gemm_i4_dev(4, 32, 8, 1.0, C.ctypes.data, 8, C.ctypes.data, None, 16, 0.0,
+                                  C.ctypes.data, 32, None) == -1
+    assert b"NULL" in lib.pk_gpu_last_error()
