@@ -95,13 +95,17 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
     a.scales = p.scales; a.n_groups = p.N / 32;
     a.C = p.C; a.ldc = p.ldc;
     a.bias = p.bias; a.epi = p.epi;
-    // Keep the larger operand's blocks within one XCD's L2 (tile_origin).
-    {
+    // Long-M GEMMs (M*N >= 3M outputs) keep the larger operand's blocks within
+    // one XCD's L2 (tile_origin); measured 1-3% faster there.  For the
+    // shorter shapes that order halves the traffic but costs 1.5-3% in time
+    // (bench A/B, cold weights), so they keep the dispatch order.
+    a.tile_order = tiles::ORDER_DISPATCH;
+    if ((double)p.M * p.N >= 3.0e6) {
         const double a_total = 4.0 * p.M * p.K;
         const double w_total = p.kind == W_F32 ? 4.0 * p.K * p.N
                              : p.kind == W_I8  ? 1.0 * p.K * p.N
                                                : 0.5 * p.K * p.N + 4.0 * p.K * (p.N / 32);
-        a.group_rows = a_total >= w_total;
+        a.tile_order = a_total >= w_total ? tiles::ORDER_ROWS : tiles::ORDER_COLS;
     }
 
     const bool fused = p.bias != nullptr || p.epi != EPI_NONE;

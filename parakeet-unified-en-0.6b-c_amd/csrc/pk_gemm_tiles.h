@@ -64,26 +64,31 @@ struct KArgs {
     int vec_a, vec_b;
     const float* bias;       // fused epilogue (Epilogue in pk_gemm_kernels.h)
     int epi;
-    int group_rows;          // tile order: 1 = an XCD's tiles share rows of A, 0 = columns of W
+    int tile_order;          // TileOrder: which operand an XCD's tiles share
 };
 
 // MI355X dispatches workgroups to its 8 XCDs round-robin by linear id, and
-// each XCD has its own L2.  Tiles are re-ordered so that each XCD owns one
-// contiguous run of the tile sequence, which walks along a row of tiles
-// (sharing A, group_rows) or down a column (sharing W): an operand block is
-// then fetched into one L2 instead of all eight.  The map from the linear id
-// to the position in the sequence is a bijection for any grid size.
+// each XCD has its own L2.  With ORDER_ROWS / ORDER_COLS the tiles are
+// re-ordered so that each XCD owns one contiguous run of the tile sequence,
+// which walks along a row of tiles (sharing A) or down a column (sharing W):
+// a block of that operand is then fetched into one L2 instead of all eight.
+// The map from the linear id to the position in the sequence is a bijection
+// for any grid size.  ORDER_DISPATCH keeps the launch order.
+enum TileOrder { ORDER_DISPATCH = 0, ORDER_ROWS = 1, ORDER_COLS = 2 };
 constexpr int kXcds = 8;
 
 __device__ inline void tile_origin(const KArgs& p, int BM, int BN, int& m0, int& n0)
 {
-    const int nbx = gridDim.x, nby = gridDim.y, total = nbx * nby;
-    const int lin = blockIdx.y * nbx + blockIdx.x;
-    const int xcd = lin % kXcds, local = lin / kXcds;
-    const int base = total / kXcds, extra = total % kXcds;
-    const int t = xcd * base + min(xcd, extra) + local;   // start of this XCD's run + local
-    const int bx = p.group_rows ? t % nbx : t / nby;
-    const int by = p.group_rows ? t / nbx : t % nby;
+    int bx = blockIdx.x, by = blockIdx.y;
+    if (p.tile_order != ORDER_DISPATCH) {
+        const int nbx = gridDim.x, nby = gridDim.y, total = nbx * nby;
+        const int lin = blockIdx.y * nbx + blockIdx.x;
+        const int xcd = lin % kXcds, local = lin / kXcds;
+        const int base = total / kXcds, extra = total % kXcds;
+        const int t = xcd * base + min(xcd, extra) + local;   // start of this XCD's run + local
+        bx = p.tile_order == ORDER_ROWS ? t % nbx : t / nby;
+        by = p.tile_order == ORDER_ROWS ? t / nbx : t % nby;
+    }
     m0 = by * BM;
     n0 = bx * BN;
 }
@@ -396,9 +401,12 @@ __device__ __forceinline__ void run_chunks(F& f, int K, int KT)
 
 // Swish as tensor_ops.c:381-388 / 98-120 write it: e = exp(-x) from a
 // 2^k * poly(r) range reduction, s = 1/(1+e), y = x*s.  The reference build
-// contracts r = t - k*ln2 and 1 + poly*2^k into FMAs, which is followed here;
-// its 1/(1+e) is rcpps plus one Newton step, which no GPU can reproduce, so
-// this uses an IEEE division (agreement within a few ulp, tested).
+// contracts r = t - k*ln2 and 1 + poly*2^k into FMAs, which is followed here.
+// Its 1/(1+e) is rcpps (a CPU-model-specific 12-bit table) plus one Newton
+// step, which no GPU can reproduce bit for bit; here it is v_rcp_f32 (about
+// 1 ulp) plus one Newton step, at least as accurate (agreement with the
+// reference within a few ulp is tested).  d = 1 + e lies in [1, e^87], so
+// 1/d stays normal.
 __device__ inline float swish_f(float v)
 {
     const float t = fminf(fmaxf(-v, -87.0f), 87.0f);
@@ -413,7 +421,8 @@ __device__ inline float swish_f(float v)
     q = __fmaf_rn(q, r, 1.0f);
     const float p2 = __int_as_float((ki + 127) << 23);
     const float d = __fmaf_rn(q, p2, 1.0f);
-    const float s = __fdiv_rn(1.0f, d);
+    float s = __builtin_amdgcn_rcpf(d);
+    s = __fmaf_rn(__fmaf_rn(-d, s, 1.0f), s, s);         // one Newton step
     return __fmul_rn(s, v);
 }
 
