@@ -65,6 +65,34 @@ void pkor_fill_int8(int8_t *out, size_t n, int lo, int hi, uint64_t seed);
 /* Uniform bytes 0..255 (each nibble uniform 0..15). */
 void pkor_fill_bytes(uint8_t *out, size_t n, uint64_t seed);
 
+/* ---- conformer-block operations (pk_oracle_block.c) ------------------- */
+
+/* LayerNorm of `rows` rows of length D (tensor_ops.c:150-185).  x86_rsqrt =
+ * 1 restates the compiled vrsqrtss + Newton step (x86 only, for pinning);
+ * 0 takes the correctly rounded 1/sqrt(var + 1e-5f). */
+void  pkor_layer_norm_rows(const float *x, const float *gamma, const float *beta,
+                           float *out, int rows, int D, int x86_rsqrt);
+/* pk_exp_avx2 (tensor_ops.c:98-120) per element, as the build contracts it. */
+float pkor_exp_poly(float x);
+/* Correctly rounded expf. */
+float pkor_expf_cr(float x);
+/* In-place softmax of `rows` rows of length len (tensor_ops.c:336-357). */
+void  pkor_softmax_rows(float *x, int rows, int len);
+/* One NT dot product as kernel_nt_*x16_avx2 computes it (blas.c:221-249). */
+float pkor_dot8(const float *a, const float *b, int K);
+/* Relative-position attention from the biased QKV rows [T][ldq] (Q | K | V,
+ * D = H*Dh each) and the position projection P [2T-1][ldp] to the
+ * concatenated head outputs out [T][ldo] (encoder.c:300-408). */
+void  pkor_attention_core(const float *qkv, int ldq, const float *P, int ldp,
+                          const float *pos_bias_u, const float *pos_bias_v,
+                          float *out, int ldo, int T, int H, int Dh);
+/* GLU over rows of [va | vb] (2D wide) -> rows of D (encoder.c:453-461). */
+void  pkor_glu_rows(const float *in, float *out, int rows, int D);
+/* Depthwise conv over time, channel-major x [C][T], w [C][K]
+ * (tensor_ops.c:476-548). */
+void  pkor_depthwise_conv1d(const float *x, const float *w, const float *b,
+                            float *out, int C, int T, int K);
+
 #ifdef __cplusplus
 }
 #endif

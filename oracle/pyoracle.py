@@ -63,6 +63,20 @@ def oracle():
         lib.pkor_fill_uniform.argtypes = [_p, _sz, _f, _f, _u64]
         lib.pkor_fill_int8.argtypes = [_p, _sz, _i, _i, _u64]
         lib.pkor_fill_bytes.argtypes = [_p, _sz, _u64]
+        lib.pkor_layer_norm_rows.argtypes = [_p, _p, _p, _p, _i, _i, _i]
+        lib.pkor_exp_poly.argtypes = [_f]
+        lib.pkor_exp_poly.restype = _f
+        lib.pkor_expf_cr.argtypes = [_f]
+        lib.pkor_expf_cr.restype = _f
+        lib.pkor_softmax_rows.argtypes = [_p, _i, _i]
+        lib.pkor_dot8.argtypes = [_p, _p, _i]
+        lib.pkor_dot8.restype = _f
+        lib.pkor_attention_core.argtypes = [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i]
+        lib.pkor_glu_rows.argtypes = [_p, _p, _i, _i]
+        lib.pkor_depthwise_conv1d.argtypes = [_p, _p, _p, _p, _i, _i, _i]
+        for fn in (lib.pkor_layer_norm_rows, lib.pkor_softmax_rows, lib.pkor_attention_core,
+                   lib.pkor_glu_rows, lib.pkor_depthwise_conv1d):
+            fn.restype = None
         _oracle = lib
     return _oracle
 
@@ -90,6 +104,13 @@ def ref(variant="ref"):
         lib.pk_pool.restype = _p
         lib.pk_pool_nthreads.argtypes = [_p]
         lib.pk_pool_nthreads.restype = _i
+        lib.pk_layer_norm_rows.argtypes = [_p, _p, _p, _p, _i, _i]
+        lib.pk_softmax_rows.argtypes = [_p, _i, _i]
+        lib.pk_depthwise_conv1d.argtypes = [_p, _p, _p, _p, _i, _i, _i]
+        lib.cblas_sgemm_st.argtypes = [_i, _i, _i] + gemm + [_p, _i, _f, _p, _i]
+        for fn in (lib.pk_layer_norm_rows, lib.pk_softmax_rows, lib.pk_depthwise_conv1d,
+                   lib.cblas_sgemm_st):
+            fn.restype = None
         _refs[variant] = lib
     return _refs[variant]
 
@@ -182,3 +203,85 @@ def ref_swish(x):
     y = np.ascontiguousarray(x, dtype=np.float32).copy()
     ref().pk_swish(_ptr(y), y.size)
     return y
+
+
+# ---- conformer-block operations (pk_oracle_block.c) ------------------------
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def layer_norm(x, gamma, beta, x86_rsqrt=False):
+    """Oracle LayerNorm of the rows of x (correctly rounded 1/sqrt unless
+    x86_rsqrt, which restates the compiled vrsqrtss form)."""
+    x, gamma, beta = _f32(x), _f32(gamma), _f32(beta)
+    out = np.empty_like(x)
+    oracle().pkor_layer_norm_rows(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(out),
+                                  x.shape[0], x.shape[1], int(x86_rsqrt))
+    return out
+
+
+def ref_layer_norm(x, gamma, beta):
+    x, gamma, beta = _f32(x), _f32(gamma), _f32(beta)
+    out = np.empty_like(x)
+    ref().pk_layer_norm_rows(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(out), x.shape[0], x.shape[1])
+    return out
+
+
+def softmax(x):
+    x = _f32(x).copy()
+    oracle().pkor_softmax_rows(_ptr(x), x.shape[0], x.shape[1])
+    return x
+
+
+def ref_softmax(x):
+    x = _f32(x).copy()
+    ref().pk_softmax_rows(_ptr(x), x.shape[0], x.shape[1])
+    return x
+
+
+def attention_core(qkv, P, pu, pv, H=8, Dh=128):
+    """Oracle relative-position attention: qkv [T][3*H*Dh] (bias added),
+    P [2T-1][H*Dh] -> [T][H*Dh]."""
+    qkv, P, pu, pv = _f32(qkv), _f32(P), _f32(pu), _f32(pv)
+    T = qkv.shape[0]
+    out = np.empty((T, H * Dh), np.float32)
+    oracle().pkor_attention_core(_ptr(qkv), qkv.shape[1], _ptr(P), P.shape[1], _ptr(pu), _ptr(pv),
+                                 _ptr(out), H * Dh, T, H, Dh)
+    return out
+
+
+def glu(x):
+    x = _f32(x)
+    D = x.shape[1] // 2
+    out = np.empty((x.shape[0], D), np.float32)
+    oracle().pkor_glu_rows(_ptr(x), _ptr(out), x.shape[0], D)
+    return out
+
+
+def depthwise(x, w, b):
+    """Oracle depthwise conv, channel-major x [C][T], w [C][K]."""
+    x, w, b = _f32(x), _f32(w), _f32(b)
+    out = np.empty_like(x)
+    oracle().pkor_depthwise_conv1d(_ptr(x), _ptr(w), _ptr(b), _ptr(out), x.shape[0], x.shape[1],
+                                   w.shape[1])
+    return out
+
+
+def ref_depthwise(x, w, b):
+    x, w, b = _f32(x), _f32(w), _f32(b)
+    out = np.empty_like(x)
+    ref().pk_depthwise_conv1d(_ptr(x), _ptr(w), _ptr(b), _ptr(out), x.shape[0], x.shape[1],
+                              w.shape[1])
+    return out
+
+
+def ref_sgemm_st(A, B, transB, C=None):
+    """The reference's single-threaded cblas_sgemm_st, NoTrans x (NoTrans | Trans)."""
+    A, B = _f32(A), _f32(B)
+    M, K = A.shape
+    N = B.shape[0] if transB else B.shape[1]
+    C = np.zeros((M, N), np.float32) if C is None else C
+    ref().cblas_sgemm_st(101, 111, 112 if transB else 111, M, N, K, 1.0, _ptr(A), K, _ptr(B),
+                         B.shape[1], 0.0, _ptr(C), N)
+    return C

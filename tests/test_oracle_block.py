@@ -1,0 +1,187 @@
+"""CPU: the oracle's conformer-block operations (oracle/pk_oracle_block.c)
+pinned against the reference compiled from its own sources
+(oracle/_ref/libpkref.so, the x86 AVX2 build), and against closed forms.
+
+Bit-exact pins: LayerNorm (with the compiled vrsqrtss form restated),
+softmax for row lengths that are multiples of 8, the NT dot products of
+the attention scores, the whole attention core for T % 8 == 0, and the
+depthwise convolution for every T.  Tolerance pins (the reference uses
+CPU-model-specific approximations there): LayerNorm with a correctly
+rounded 1/sqrt, softmax tails, GLU."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+
+needs_ref = pytest.mark.skipif(not po.have_ref(), reason="reference build missing (oracle/Makefile ref)")
+RNG = np.random.default_rng(0x5EEDB10C)
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32),
+                          np.asarray(b, np.float32).view(np.uint32))
+
+
+def ulps(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+def rows(n, d, scale=1.0, shift=0.0):
+    return (RNG.standard_normal((n, d)) * scale + shift).astype(np.float32)
+
+
+@needs_ref
+@pytest.mark.parametrize("D", [1024, 64, 1000])
+def test_layer_norm_x86_form_is_bit_exact(D):
+    x = rows(48, D, 3.0, 0.7)
+    g, b = rows(1, D)[0], rows(1, D)[0]
+    assert bits_equal(po.layer_norm(x, g, b, x86_rsqrt=True), po.ref_layer_norm(x, g, b))
+
+
+@needs_ref
+def test_layer_norm_correctly_rounded_form_within_tolerance():
+    """mode 0 differs from the reference only through 1/sqrt: a few ulp of
+    the normalised value, relative to the row's scale."""
+    x = rows(256, 1024, 2.0, -0.3)
+    g, b = rows(1, 1024)[0], rows(1, 1024)[0]
+    ref, ora = po.ref_layer_norm(x, g, b), po.layer_norm(x, g, b)
+    rel = np.abs(ref - ora) / np.maximum(np.abs(ref), 1.0)
+    assert rel.max() < 1e-6
+    # the sums are shared: rows where 1/sqrt agrees are identical
+    assert np.mean([bits_equal(ref[i], ora[i]) for i in range(256)]) > 0.2
+
+
+def test_layer_norm_closed_form():
+    """Against fp64 LayerNorm: mean/var/affine within fp32 rounding."""
+    x = rows(8, 1024, 5.0, 2.0)
+    g, b = rows(1, 1024)[0], rows(1, 1024)[0]
+    x64 = x.astype(np.float64)
+    m = x64.mean(1, keepdims=True)
+    v = ((x64 - m) ** 2).mean(1, keepdims=True)
+    want = (x64 - m) / np.sqrt(v + 1e-5) * g + b
+    assert np.abs(po.layer_norm(x, g, b) - want).max() < 2e-5
+
+
+@needs_ref
+@pytest.mark.parametrize("T", [416, 408, 104, 8, 832])
+def test_softmax_bit_exact_multiple_of_8(T):
+    s = rows(24, T, 4.0)
+    assert bits_equal(po.softmax(s), po.ref_softmax(s))
+
+
+@needs_ref
+@pytest.mark.parametrize("T", [300, 108, 7, 1, 13])
+def test_softmax_tail_within_tolerance(T):
+    s = rows(24, T, 4.0)
+    a, b = po.softmax(s), po.ref_softmax(s)
+    assert np.abs(a - b).max() <= 4e-7
+    assert np.allclose(a.sum(1), 1.0, atol=1e-5)
+
+
+def test_exp_poly_accuracy():
+    """The reference's polynomial exp: the 5-term Taylor remainder r^6/720 at
+    |r| <= ln2/2 bounds it near 3e-6 relative on [-87, 0] ("~1e-6 relative",
+    tensor_ops.c:7-9); exact at 0."""
+    x = np.linspace(-87.0, 0.0, 20001, dtype=np.float32)
+    got = np.array([po.oracle().pkor_exp_poly(float(v)) for v in x], np.float32)
+    want = np.exp(x.astype(np.float64))
+    assert np.max(np.abs(got - want) / want) < 4e-6
+    assert po.oracle().pkor_exp_poly(0.0) == 1.0
+
+
+@needs_ref
+@pytest.mark.parametrize("K", [128, 64, 8])
+def test_nt_dot_bit_exact(K):
+    """K % 8 == 0 (the head dimension is 128); the scalar tail for other K is
+    compiled differently and is never used by the encoder."""
+    A, B = rows(19, K), rows(37, K)
+    want = po.ref_sgemm_st(A, B, transB=True)
+    got = np.empty_like(want)
+    for i in range(A.shape[0]):
+        a = np.ascontiguousarray(A[i])
+        for j in range(B.shape[0]):
+            b = np.ascontiguousarray(B[j])
+            got[i, j] = po.oracle().pkor_dot8(po._ptr(a), po._ptr(b), K)
+    assert bits_equal(got, want)
+
+
+def relative_shift_padded(bd, T):
+    """encoder.c:230-254 as written: pad a zero column, view the flat buffer
+    from offset T with row stride 2T-1."""
+    L = 2 * T - 1
+    padded = np.zeros((T, 2 * T), np.float32)
+    padded[:, 1:] = bd
+    flat = padded.reshape(-1)
+    return np.array([[flat[T + i * L + j] for j in range(T)] for i in range(T)], np.float32)
+
+
+def test_relative_shift_closed_form():
+    T = 9
+    bd = rows(T, 2 * T - 1)
+    closed = np.array([[bd[i, T - 1 - i + j] for j in range(T)] for i in range(T)], np.float32)
+    assert bits_equal(relative_shift_padded(bd, T), closed)
+
+
+def reference_attention(qkv, P, pu, pv, H=8, Dh=128):
+    """The reference's attention core composed from its compiled exported
+    functions: cblas_sgemm_st (NT for AC/BD, NN for scores x V) and
+    pk_softmax_rows, with the head gather, the relative shift and the score
+    combine of encoder.c:315-406 done in numpy (exact fp32 adds/multiplies)."""
+    T, D = qkv.shape[0], H * Dh
+    scale = np.float32(1.0) / np.sqrt(np.float32(Dh))
+    out = np.empty((T, D), np.float32)
+    scores = np.empty((H, T, T), np.float32)
+    for h in range(H):
+        q = qkv[:, h * Dh:(h + 1) * Dh]
+        k = np.ascontiguousarray(qkv[:, D + h * Dh:D + (h + 1) * Dh])
+        qu = np.ascontiguousarray(q + pu[h * Dh:(h + 1) * Dh])
+        qv = np.ascontiguousarray(q + pv[h * Dh:(h + 1) * Dh])
+        ac = po.ref_sgemm_st(qu, k, transB=True)
+        bd = po.ref_sgemm_st(qv, np.ascontiguousarray(P[:, h * Dh:(h + 1) * Dh]), transB=True)
+        scores[h] = (ac + relative_shift_padded(bd, T)) * scale
+    flat = np.ascontiguousarray(scores.reshape(H * T, T))
+    po.ref().pk_softmax_rows(po._ptr(flat), H * T, T)
+    scores = flat.reshape(H, T, T)
+    for h in range(H):
+        v = np.ascontiguousarray(qkv[:, 2 * D + h * Dh:2 * D + (h + 1) * Dh])
+        out[:, h * Dh:(h + 1) * Dh] = po.ref_sgemm_st(np.ascontiguousarray(scores[h]), v, transB=False)
+    return out
+
+
+def attention_inputs(T, H=8, Dh=128):
+    D = H * Dh
+    qkv = rows(T, 3 * D, 0.5)
+    P = rows(2 * T - 1, D, 0.5)
+    return qkv, P, rows(1, D, 0.1)[0], rows(1, D, 0.1)[0]
+
+
+@needs_ref
+@pytest.mark.parametrize("T", [24, 64])
+def test_attention_core_bit_exact(T):
+    qkv, P, pu, pv = attention_inputs(T)
+    assert bits_equal(po.attention_core(qkv, P, pu, pv), reference_attention(qkv, P, pu, pv))
+
+
+@needs_ref
+def test_attention_core_tail_within_tolerance():
+    qkv, P, pu, pv = attention_inputs(21)
+    a, b = po.attention_core(qkv, P, pu, pv), reference_attention(qkv, P, pu, pv)
+    assert np.abs(a - b).max() / np.abs(b).max() < 1e-6
+
+
+@needs_ref
+@pytest.mark.parametrize("T", [416, 408, 108, 20, 13, 12, 9, 8, 5, 1])
+def test_depthwise_bit_exact(T):
+    x = rows(16, T)
+    w, b = rows(16, 9), rows(1, 16)[0]
+    assert bits_equal(po.depthwise(x, w, b), po.ref_depthwise(x, w, b))
+
+
+def test_glu_closed_form():
+    x = rows(32, 2 * 256, 3.0)
+    va, vb = x[:, :256].astype(np.float64), x[:, 256:].astype(np.float64)
+    want = va / (1.0 + np.exp(-vb))
+    got = po.glu(x)
+    assert np.all(ulps(got, want.astype(np.float32)) <= 2)
