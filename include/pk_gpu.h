@@ -114,6 +114,9 @@ int pk_gpu_sgemm_dev(int M, int N, int K, float alpha,
  *   PK_GPU_EPI_SWISH:         C[i][j] = swish(v)   (as pk_gpu_swish_dev)
  *   PK_GPU_EPI_HALF_RESIDUAL: C[i][j] = C[i][j] + 0.5 * v   (beta must be 0:
  *                             C holds the residual x on entry)
+ *   PK_GPU_EPI_RESIDUAL:      C[i][j] = C[i][j] + v   (beta must be 0; the
+ *                             attention and convolution residuals,
+ *                             encoder.c:410-424, 473-475)
  * Bias and residual are exact IEEE operations, so results equal the
  * reference's GEMM + pk_bias_add (+ x += 0.5 * out) bit for bit; Swish is
  * the device swish (within a few ulp of the reference's, see
@@ -123,6 +126,7 @@ int pk_gpu_sgemm_dev(int M, int N, int K, float alpha,
 #define PK_GPU_EPI_NONE 0
 #define PK_GPU_EPI_SWISH 1
 #define PK_GPU_EPI_HALF_RESIDUAL 2
+#define PK_GPU_EPI_RESIDUAL 3
 int pk_gpu_gemm_i8_ex_dev(int M, int N, int K, float alpha, const float *dA, int lda,
                           const int8_t *dB, float B_scale, int ldb, float beta, float *dC,
                           int ldc, const float *dbias, int epilogue, void *stream);
@@ -136,6 +140,116 @@ int pk_gpu_sgemm_ex_dev(int M, int N, int K, float alpha, const float *dA, int l
 /* Swish y = x * sigmoid(x) with the reference's polynomial exp
  * (tensor_ops.c:98-120, 367-389); x may equal y. */
 int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);
+
+/* ---- conformer-block operations (device pointers, no synchronisation) --
+ * The operations between the weight GEMMs of one FastConformer block, for
+ * callers that keep activations on the device (encoder.c:179-491).  Rows are
+ * time-major.  Results equal the reference's bit for bit where its order of
+ * operations is fixed (noted per function); where the reference uses a
+ * CPU-model-specific approximation (vrsqrtss, vrcpps, glibc's vector expf),
+ * the correctly rounded value is taken instead. */
+
+/* LayerNorm of `rows` rows of D floats (pk_layer_norm_rows,
+ * tensor_ops.c:150-185, 187-211); D % 8 == 0; dout may equal dx.  The sums
+ * are the reference's; 1/sqrt(var + 1e-5) is correctly rounded. */
+int pk_gpu_layer_norm_dev(const float *dx, const float *dgamma, const float *dbeta,
+                          float *dout, int rows, int D, void *stream);
+
+/* Relative-position multi-head attention of one sequence of T rows
+ * (encoder.c:300-408, from the fused QKV output to the concatenated heads):
+ *   qkv  [T][ldq]      Q | K | V, H*128 columns each, bias added
+ *   P    [2T-1][ldp]   linear_pos applied to the T-row positional slice
+ *   pos_bias_u, pos_bias_v  [H*128]
+ *   out  [T][ldo]      head h in columns [128h, 128h+128)
+ * Head dimension 128 (PK_HEAD_DIM), 1 <= T <= 512; ldq, ldp, ldo multiples of
+ * 4 and 16-byte aligned rows.  Bit-identical to the reference when T % 8 == 0
+ * (softmax's scalar tail otherwise uses a correctly rounded expf). */
+int pk_gpu_attention_dev(const float *dqkv, int ldq, const float *dP, int ldp,
+                         const float *dpos_bias_u, const float *dpos_bias_v,
+                         float *dout, int ldo, int T, int H, void *stream);
+
+/* GLU over rows of [va | vb] (2*D wide) into rows of D (encoder.c:453-461):
+ * va * (1 / (1 + exp(-vb))), exp correctly rounded. */
+int pk_gpu_glu_dev(const float *din, float *dout, int rows, int D, void *stream);
+
+/* Depthwise convolution over time with zero padding (pk_depthwise_conv1d,
+ * tensor_ops.c:476-548) on time-major x [T][ldx] (C channels), weights
+ * [C][K] (K odd), bias [C] or NULL, then Swish when swish != 0
+ * (encoder.c:467-469).  The convolution is bit-identical to the compiled
+ * reference for every T; Swish as in the GEMM epilogue. */
+int pk_gpu_depthwise_dev(const float *dx, int ldx, const float *dw, const float *db,
+                         float *dout, int ldo, int T, int C, int K, int swish,
+                         void *stream);
+
+/* ---- device-resident encoder ------------------------------------------
+ * The 24 conformer blocks of the encoder (encode_blocks / encode_blocks_
+ * chunked, encoder.c:179-575) with every activation kept on the device.  In
+ * chunked mode all chunks run as one batch: row-independent work (LayerNorm,
+ * the weight GEMMs and their epilogues, GLU) over all chunks' rows at once,
+ * attention and the depthwise convolution per chunk, the position projection
+ * once per block for the longest chunk (a shorter chunk's positional slice
+ * is a row range of the longest one's).  Weights are uploaded once at
+ * creation; the host copies may be freed afterwards. */
+
+/* One weight matrix as the reference holds it (Weight, parakeet.h:42-57):
+ * bits 32: fp32 [K][N]; 8: int8 [K][N] with one scale; 4: packed int4
+ * [K][N/2] with fp32 scales [K][N/32]. */
+typedef struct {
+    const void  *data;
+    float        scale;
+    const float *scales;
+    int          bits;
+} pk_gpu_weight;
+
+/* One conformer block's parameters (ConformerBlock, parakeet.h), host
+ * pointers.  Shapes with d = 1024, ff = 4096, 8 heads of 128:
+ *   norm_*: [d];  ff*_linear1: [d][ff] + bias [ff];  ff*_linear2: [ff][d] +
+ *   bias [d];  linear_qkv: [d][3d] + bias [3d];  linear_pos: [d][d], no
+ *   bias;  linear_out: [d][d] + bias [d];  pos_bias_u/v: [d];
+ *   conv_pw1: fp32 [2d][d] + bias [2d];  conv_dw: [d][9] + bias [d];
+ *   conv_pw2: fp32 [d][d] + bias [d]. */
+typedef struct {
+    const float *norm_ff1_w, *norm_ff1_b;
+    pk_gpu_weight ff1_linear1_w; const float *ff1_linear1_b;
+    pk_gpu_weight ff1_linear2_w; const float *ff1_linear2_b;
+    const float *norm_sa_w, *norm_sa_b;
+    pk_gpu_weight linear_qkv_w;  const float *linear_qkv_b;
+    pk_gpu_weight linear_pos_w;
+    pk_gpu_weight linear_out_w;  const float *linear_out_b;
+    const float *pos_bias_u, *pos_bias_v;
+    const float *norm_conv_w, *norm_conv_b;
+    const float *conv_pw1_w, *conv_pw1_b;
+    const float *conv_dw_w, *conv_dw_b;
+    const float *conv_pw2_w, *conv_pw2_b;
+    const float *norm_ff2_w, *norm_ff2_b;
+    pk_gpu_weight ff2_linear1_w; const float *ff2_linear1_b;
+    pk_gpu_weight ff2_linear2_w; const float *ff2_linear2_b;
+    const float *norm_out_w, *norm_out_b;
+} pk_gpu_block_weights;
+
+typedef struct pk_gpu_encoder pk_gpu_encoder;
+
+/* Upload n_blocks blocks and the positional-encoding table pe_table
+ * [pe_rows][1024] whose centre row is pe_center (PK_PE_TABLE_SIZE,
+ * PK_PE_CENTER). */
+int pk_gpu_encoder_create(pk_gpu_encoder **enc, const pk_gpu_block_weights *blocks,
+                          int n_blocks, const float *pe_table, int pe_rows, int pe_center);
+/* Run every block over x [T][1024] into out [T][1024] (out may equal x).
+ * chunk_size <= 0: one sequence (encode_blocks, encoder.c:495-512);
+ * otherwise chunks of chunk_size output frames with `overlap` frames of
+ * context on each side (encode_blocks_chunked, encoder.c:514-575; the
+ * reference uses PK_CHUNK_SIZE 400 and PK_CHUNK_OVERLAP 8).  Every chunk
+ * (or the sequence) must be at most 512 frames.  Host pointers; returns when
+ * out is written. */
+int pk_gpu_encoder_run(pk_gpu_encoder *enc, const float *x, int T, int chunk_size,
+                       int overlap, float *out);
+/* The same with device pointers, enqueued on `stream` (NULL: the encoder's
+ * own stream); returns without synchronising. */
+int pk_gpu_encoder_run_dev(pk_gpu_encoder *enc, const float *dx, int T, int chunk_size,
+                           int overlap, float *dout, void *stream);
+/* Device bytes held by the encoder (weights + workspace). */
+size_t pk_gpu_encoder_bytes(const pk_gpu_encoder *enc);
+void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
 
 /* ---- tuning / introspection ------------------------------------------- */
 

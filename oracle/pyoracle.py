@@ -11,6 +11,9 @@ never as the thing measured on the GPU.
               oracle/_ref/libpkref_portable.so  (same sources, blas.c on its
                                             portable code path, which matches
                                             the NEON path)
+              oracle/_ref/libpkref_block.so     (the reference's static
+                                            conformer_block, callable;
+                                            ref_block_harness.c)
 """
 import ctypes
 import os
@@ -21,6 +24,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "_build", "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libpkref.so")
 REF_PORTABLE_SO = os.path.join(HERE, "_ref", "libpkref_portable.so")
+REF_BLOCK_SO = os.path.join(HERE, "_ref", "libpkref_block.so")
 
 _f = ctypes.c_float
 _i = ctypes.c_int
@@ -285,3 +289,30 @@ def ref_sgemm_st(A, B, transB, C=None):
     ref().cblas_sgemm_st(101, 111, 112 if transB else 111, M, N, K, 1.0, _ptr(A), K, _ptr(B),
                          B.shape[1], 0.0, _ptr(C), N)
     return C
+
+
+_ref_block = None
+
+
+def have_ref_block():
+    return os.path.exists(REF_BLOCK_SO)
+
+
+def ref_blocks(blocks, n_blocks, pe_slice, x):
+    """Run the reference's conformer_block n_blocks times on x [T][1024] (in a
+    copy), blocks being a ctypes array of pk_gpu_block_weights."""
+    global _ref_block
+    if _ref_block is None:
+        if not have_ref_block():
+            raise RuntimeError(f"reference block harness missing: {REF_BLOCK_SO}")
+        lib = ctypes.CDLL(REF_BLOCK_SO)
+        lib.pkref_conformer_blocks.argtypes = [_p, _i, _p, _p, _i]
+        lib.pkref_conformer_blocks.restype = _i
+        _ref_block = lib
+    x = _f32(x).copy()
+    pe_slice = _f32(pe_slice)
+    rc = _ref_block.pkref_conformer_blocks(ctypes.cast(blocks, _p), n_blocks, _ptr(pe_slice),
+                                           _ptr(x), x.shape[0])
+    if rc:
+        raise RuntimeError("pkref_conformer_blocks failed")
+    return x

@@ -1,0 +1,50 @@
+// pk_block_kernels.h - device-side entry points of the conformer-block
+// operations (pk_block_kernels.hip).  All pointers are device pointers;
+// activations are time-major rows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace pkgpu {
+
+// Longest chunk the attention kernel takes: its score rows live in LDS.
+// The reference's encoder never attends over more than 500 frames unless
+// chunking is forced off (PK_CHUNK_THRESHOLD, parakeet.h; encoder.c:595-610).
+constexpr int kAttnMaxT = 512;
+constexpr int kAttnSld = 528;          // LDS row stride of the scores (>= kAttnMaxT)
+
+// Relative-position attention of n chunks of T rows each (encoder.c:300-408).
+//   qkv  [rows][ldq]: Q | K | V (H*128 columns each, bias added); chunk z
+//        starts at row chunk_rows[z]
+//   P    [2T-1][ldp]: linear_pos(pe_slice(T)) for this T
+//   out  [rows][ldo]: the concatenated head outputs, chunk z at chunk_rows[z]
+struct AttnArgs {
+    const float* qkv; int ldq;
+    const float* P; int ldp;
+    const float* pos_bias_u;   // [H*128]
+    const float* pos_bias_v;
+    float* out; int ldo;
+    const int* chunk_rows;     // device, n entries (null: one chunk at row 0)
+    int T, H;
+};
+
+// Depthwise convolution over time with optional Swish (tensor_ops.c:476-548,
+// encoder.c:467-469), channel c of chunk z: x[chunk_rows[z] + t][c].
+struct DwArgs {
+    const float* x; int ldx;
+    const float* w;            // [C][K]
+    const float* b;            // [C] or null
+    float* out; int ldo;
+    const int* chunk_rows;     // device, n entries (null: one chunk at row 0)
+    int T, C, K;
+    int swish;
+};
+
+hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const float* beta,
+                             float* out, int ldo, int rows, int D, hipStream_t s);
+hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s);
+hipError_t launch_glu(const float* in, int ldi, float* out, int ldo, int rows, int D, hipStream_t s);
+hipError_t launch_depthwise(const DwArgs& a, int n_chunks, hipStream_t s);
+hipError_t launch_transpose(const float* in, float* out, int R, int C, hipStream_t s);
+
+}  // namespace pkgpu

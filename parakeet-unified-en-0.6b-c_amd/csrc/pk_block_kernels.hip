@@ -1,0 +1,446 @@
+// pk_block_kernels.hip - the conformer-block operations between the weight
+// GEMMs, for the device-resident encoder: LayerNorm, relative-position
+// multi-head attention (scores, relative shift, softmax, scores x V), GLU,
+// and the depthwise convolution with its Swish.
+//
+// Activations are time-major rows of d_model = 1024 floats; several chunks
+// of the chunked encoder (encoder.c:514-575) sit one after another in one
+// buffer, and the per-chunk operations (attention, depthwise convolution)
+// take the chunks' first rows from a small device table.
+//
+// Numerics follow the compiled reference (x86 AVX2 build), operation by
+// operation, with every rounding explicit (__f*_rn, and the library is
+// compiled with -ffp-contract=off so no multiply is fused into an add that
+// the reference rounds separately): where the reference's
+// order of operations is fixed by its source or by how it is compiled, the
+// result is bit-identical (attention for T % 8 == 0, depthwise convolution,
+// the LayerNorm sums).  Where the reference uses CPU-model-specific
+// approximations (vrsqrtss for LayerNorm's 1/sqrt, vrcpps for Swish and GLU,
+// glibc's vector expf for GLU), the value here is the correctly rounded one.
+#include "pk_block_kernels.h"
+#include "pk_gemm_tiles.h"
+
+#include <utility>
+
+namespace pkgpu {
+namespace {
+
+using tiles::v4f;
+
+// ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)) across the 8 lanes of an aligned
+// lane group (pk_hsum_avx2, tensor_ops.c:126-134); every lane of the group
+// gets the sum.  fl(a+b) == fl(b+a), so the xor partners give the same
+// association on every lane.
+__device__ inline float hsum8_lanes(float p)
+{
+    const float a = __fadd_rn(p, __shfl_xor(p, 4));
+    const float b = __fadd_rn(a, __shfl_xor(a, 2));
+    return __fadd_rn(b, __shfl_xor(b, 1));
+}
+
+__device__ inline float hsum8(const float (&p)[8])
+{
+    return __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[4]), __fadd_rn(p[2], p[6])),
+                     __fadd_rn(__fadd_rn(p[1], p[5]), __fadd_rn(p[3], p[7])));
+}
+
+// pk_exp_avx2 (tensor_ops.c:98-120) as the reference build compiles it.
+__device__ inline float exp_poly(float x)
+{
+    x = fminf(fmaxf(x, -87.0f), 87.0f);
+    const float kf = __builtin_rintf(__fmul_rn(x, 1.44269504088896341f));
+    const int ki = (int)kf;
+    const float r = __fmaf_rn(-kf, 0.69314718055994529f, x);
+    float y = 1.0f / 120.0f;
+    y = __fmaf_rn(y, r, 1.0f / 24.0f);
+    y = __fmaf_rn(y, r, 1.0f / 6.0f);
+    y = __fmaf_rn(y, r, 0.5f);
+    y = __fmaf_rn(y, r, 1.0f);
+    y = __fmaf_rn(y, r, 1.0f);
+    return __fmul_rn(y, __int_as_float((ki + 127) << 23));
+}
+
+// Correctly rounded expf (rounding the double-precision exp).
+__device__ inline float exp_cr(float x) { return (float)exp((double)x); }
+
+// ---- LayerNorm (tensor_ops.c:150-185) ---------------------------------------
+// 8 rows per wave, 8 lanes per row; lane l of a row holds the partial sums of
+// elements l, l+8, l+16, ... in order, like one AVX2 lane.
+
+__global__ __launch_bounds__(256) void layer_norm_rows(const float* __restrict__ x, int ldx,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta,
+                                                       float* out, int ldo, int rows, int D)
+{
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+    const int l = lane & 7;
+    const bool live = row < rows;
+    const float* xr = x + (size_t)(live ? row : 0) * ldx;
+    float p = 0.0f;
+    for (int i = l; i < D; i += 8) p = __fadd_rn(p, live ? xr[i] : 0.0f);
+    const float mean = __fdiv_rn(hsum8_lanes(p), (float)D);
+    float q = 0.0f;
+    for (int i = l; i < D; i += 8) {
+        const float d = __fsub_rn(live ? xr[i] : 0.0f, mean);
+        q = __fmaf_rn(d, d, q);
+    }
+    const float var = __fdiv_rn(hsum8_lanes(q), (float)D);
+    // sqrtf and '/' are correctly rounded here (HIP's __fsqrt_rn is the
+    // native, approximate square root unless OCML_BASIC_ROUNDED_OPERATIONS).
+    const float inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
+    if (!live) return;
+    float* o = out + (size_t)row * ldo;
+    for (int i = l; i < D; i += 8)
+        o[i] = __fmaf_rn(__fmul_rn(__fsub_rn(xr[i], mean), inv), gamma[i], beta[i]);
+}
+
+// ---- relative-position attention (encoder.c:300-408) ------------------------
+// One workgroup: 32 query rows of one head of one chunk, 4 waves of 8 rows.
+// Products use v_mfma_f32_4x4x1_16b_f32 with block 0's A broadcast to all 16
+// blocks (CBSZ = 4): one MFMA = 4 rows x 64 columns, lane j holds column j of
+// rows 0..3, and the A register lane 4t + i holds row i at k-step t (ABID =
+// t).  Each MFMA is one fused multiply-add per output.
+//
+// Scores (NT dot products, blas.c:221-249): eight accumulators per output,
+// step k goes to accumulator k % 8, so accumulator l is the chain over
+// k = l, l+8, ... of one AVX2 lane; the eight are reduced as hsum8.
+// AC = Q_u K^T per column tile of keys; BD = Q_v P^T per tile of position
+// rows m, scattered to the score of column j = m - (T-1-i) (the relative
+// shift, encoder.c:230-254).  Softmax per row (tensor_ops.c:336-357), then
+// scores x V as one fma chain per output over j ascending (sgemm NN).
+
+constexpr int kDh = 128;                 // PK_HEAD_DIM
+constexpr int kAttnRows = 32;            // query rows per workgroup
+constexpr int kTileLd = kDh + 4;         // padded LDS row of a key / position / value tile
+constexpr float kScoreScale = 0.0883883461356163f;   // 1/sqrtf(128) = 0x3db504f3
+
+template <int T_>
+__device__ inline v4f mfma_bcast(float a, float b, v4f c)
+{
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, T_, 0);
+}
+
+// acc[g][t % 8] += A_g(step t) * b[t] for the 16 steps of one A register.
+template <int... Ts>
+__device__ inline void score_steps(std::integer_sequence<int, Ts...>, const float (&a)[2],
+                                   const float (&b)[16], v4f (&acc)[2][8])
+{
+    ((acc[0][Ts & 7] = mfma_bcast<Ts>(a[0], b[Ts], acc[0][Ts & 7]),
+      acc[1][Ts & 7] = mfma_bcast<Ts>(a[1], b[Ts], acc[1][Ts & 7])), ...);
+}
+
+// Stage 64 rows [r0, r0 + 64) x 128 columns of a row-major source (row
+// stride ld floats) into the LDS tile; rows outside [0, n) read as 0.
+__device__ inline void stage_tile(float* tile, const float* src, int ld, int r0, int n)
+{
+    for (int v = threadIdx.x; v < 64 * (kDh / 4); v += blockDim.x) {
+        const int r = v / (kDh / 4), c4 = v % (kDh / 4);
+        const int gr = r0 + r;
+        float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (gr >= 0 && gr < n) val = *reinterpret_cast<const float4*>(src + (size_t)gr * ld + 4 * c4);
+        *reinterpret_cast<float4*>(tile + r * kTileLd + 4 * c4) = val;
+    }
+}
+
+// One 4-row x 64-column tile of NT dot products for two row groups of a wave:
+// a[g][kb] holds rows (4g..4g+3) in broadcast layout for k in [16kb, 16kb+16).
+__device__ inline void score_tile(const float* tile, const float (&a)[2][8], float (&out)[2][4])
+{
+    const int lane = threadIdx.x & 63;
+    v4f acc[2][8];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) acc[g][l] = v4f{0.f, 0.f, 0.f, 0.f};
+    const float* trow = tile + lane * kTileLd;
+#pragma unroll
+    for (int kb = 0; kb < kDh / 16; ++kb) {
+        float b[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(trow + kb * 16 + 4 * q);
+            b[4 * q] = v.x; b[4 * q + 1] = v.y; b[4 * q + 2] = v.z; b[4 * q + 3] = v.w;
+        }
+        const float ak[2] = {a[0][kb], a[1][kb]};
+        score_steps(std::make_integer_sequence<int, 16>{}, ak, b, acc);
+    }
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float p[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) p[l] = acc[g][l][i];
+            out[g][i] = hsum8(p);
+        }
+}
+
+// scores x V: acc[g][d] += S[row 4g+i][j0 + t] * V[j0 + t][64d + lane], t < n.
+template <int... Ts>
+__device__ inline void pv_steps(std::integer_sequence<int, Ts...>, const float (&a)[2],
+                                const float* vt, int n, v4f (&acc)[2][2])
+{
+    const int lane = threadIdx.x & 63;
+    (((Ts < n) ? (acc[0][0] = mfma_bcast<Ts>(a[0], vt[Ts * kTileLd + lane], acc[0][0]),
+                  acc[1][0] = mfma_bcast<Ts>(a[1], vt[Ts * kTileLd + lane], acc[1][0]),
+                  acc[0][1] = mfma_bcast<Ts>(a[0], vt[Ts * kTileLd + 64 + lane], acc[0][1]),
+                  acc[1][1] = mfma_bcast<Ts>(a[1], vt[Ts * kTileLd + 64 + lane], acc[1][1]), 0)
+               : 0), ...);
+}
+
+__global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
+{
+    __shared__ float S[kAttnRows * kAttnSld];
+    __shared__ float tile[64 * kTileLd];
+
+    const int T = p.T;
+    const int r0 = blockIdx.x * kAttnRows;
+    const int h = blockIdx.y;
+    const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.z] : 0;   // first row of this chunk
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int D = p.H * kDh;
+    const float* qkv = p.qkv + (size_t)row0 * p.ldq;
+    const float* K = qkv + D + h * kDh;
+    const float* V = qkv + 2 * D + h * kDh;
+    const float* P = p.P + h * kDh;
+
+    // Q_u, Q_v rows of this wave in broadcast layout (encoder.c:319-338).
+    float au[2][8], av[2][8];
+    {
+        const int i = lane & 3, t = lane >> 2;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const int r = r0 + 8 * w + 4 * g + i;
+            const float* q = qkv + (size_t)(r < T ? r : 0) * p.ldq + h * kDh;
+#pragma unroll
+            for (int kb = 0; kb < 8; ++kb) {
+                const int k = 16 * kb + t;
+                const float qv = r < T ? q[k] : 0.0f;
+                au[g][kb] = r < T ? __fadd_rn(qv, p.pos_bias_u[h * kDh + k]) : 0.0f;
+                av[g][kb] = r < T ? __fadd_rn(qv, p.pos_bias_v[h * kDh + k]) : 0.0f;
+            }
+        }
+    }
+
+    // AC: S[row][j] = Q_u[row] . K[j]
+    for (int j0 = 0; j0 < T; j0 += 64) {
+        stage_tile(tile, K, p.ldq, j0, T);
+        __syncthreads();
+        float o[2][4];
+        score_tile(tile, au, o);
+        const int j = j0 + lane;
+        if (j < T)
+#pragma unroll
+            for (int g = 0; g < 2; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) S[(8 * w + 4 * g + i) * kAttnSld + j] = o[g][i];
+        __syncthreads();
+    }
+
+    // BD at the shifted positions: m = T-1-row+j for this block's rows.
+    const int r_hi = min(r0 + kAttnRows, T) - 1;
+    const int L = 2 * T - 1;
+    for (int m0 = T - 1 - r_hi; m0 <= 2 * T - 2 - r0; m0 += 64) {
+        stage_tile(tile, P, p.ldp, m0, L);
+        __syncthreads();
+        float o[2][4];
+        score_tile(tile, av, o);
+        const int m = m0 + lane;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rl = 8 * w + 4 * g + i, r = r0 + rl;
+                const int j = m - (T - 1 - r);
+                if (r < T && j >= 0 && j < T) {
+                    float* s = &S[rl * kAttnSld + j];
+                    *s = __fmul_rn(__fadd_rn(*s, o[g][i]), kScoreScale);
+                }
+            }
+        __syncthreads();
+    }
+
+    // Softmax of each row: 8 lanes per row, lane q owns j = q, q+8, ...
+    {
+        const int rl = 8 * w + (lane >> 3), q = lane & 7, r = r0 + rl;
+        float* s = S + rl * kAttnSld;
+        if (r < T) {
+            float mx = s[0];
+            for (int j = q; j < T; j += 8) mx = fmaxf(mx, s[j]);
+            mx = fmaxf(mx, __shfl_xor(mx, 4));
+            mx = fmaxf(mx, __shfl_xor(mx, 2));
+            mx = fmaxf(mx, __shfl_xor(mx, 1));
+            const int T8 = T & ~7;
+            float part = 0.0f;
+            for (int j = q; j < T8; j += 8) {
+                const float e = exp_poly(__fsub_rn(s[j], mx));
+                s[j] = e;
+                part = __fadd_rn(part, e);
+            }
+            float sum = hsum8_lanes(part);
+            if (T8 < T) {                 // scalar tail, one lane, in order
+                if (q == 0)
+                    for (int j = T8; j < T; ++j) {
+                        const float e = exp_cr(__fsub_rn(s[j], mx));
+                        s[j] = e;
+                        sum = __fadd_rn(sum, e);
+                    }
+                sum = __shfl(sum, lane & ~7);
+            }
+            const float inv = __fdiv_rn(1.0f, sum);
+            for (int j = q; j < T; j += 8) s[j] = __fmul_rn(s[j], inv);
+        } else {
+            for (int j = q; j < T; j += 8) s[j] = 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // out[row][h*128 + d] = sum over j ascending of S[row][j] * V[j][d]
+    v4f acc[2][2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) acc[g][0] = acc[g][1] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int i = lane & 3, t = lane >> 2;
+    for (int j0 = 0; j0 < T; j0 += 64) {
+        stage_tile(tile, V, p.ldq, j0, T);
+        __syncthreads();
+        const int nt = min(64, T - j0);
+        for (int jb = 0; jb < nt; jb += 16) {
+            float a[2];
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const int jj = j0 + jb + t;
+                a[g] = jj < T ? S[(8 * w + 4 * g + i) * kAttnSld + jj] : 0.0f;
+            }
+            pv_steps(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, nt - jb, acc);
+        }
+        __syncthreads();
+    }
+    float* out = p.out + (size_t)row0 * p.ldo + h * kDh;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const int r = r0 + 8 * w + 4 * g + ii;
+            if (r < T) {
+                out[(size_t)r * p.ldo + lane] = acc[g][0][ii];
+                out[(size_t)r * p.ldo + 64 + lane] = acc[g][1][ii];
+            }
+        }
+}
+
+// ---- GLU (encoder.c:453-461) -------------------------------------------------
+// gated[r][d] = va * (1 / (1 + exp(-vb))), va = in[r][d], vb = in[r][D + d].
+__global__ void glu_rows(const float* __restrict__ in, int ldi, float* out, int ldo, int rows, int D)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)rows * D) return;
+    const int r = (int)(idx / D), d = (int)(idx % D);
+    const float va = in[(size_t)r * ldi + d], vb = in[(size_t)r * ldi + D + d];
+    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-vb)));
+    out[(size_t)r * ldo + d] = __fmul_rn(va, s);
+}
+
+// ---- depthwise convolution + Swish (tensor_ops.c:476-548, encoder.c:467-469)
+// Time-major x [rows][C]; each chunk (first row from the table, T rows) is
+// convolved on its own with zero padding at its edges.  Positions in the
+// reference's 8-wide interior take the explicit fma chain over the taps; the
+// others take the compiled form of its scalar loops: taps 0..7 multiplied,
+// out-of-range ones as +0, reduced as hsum8 and added to the bias, then fma
+// for the remaining taps.
+__global__ void depthwise_swish(DwArgs p)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)p.T * p.C) return;
+    const int t = (int)(idx / p.C), c = (int)(idx % p.C);
+    const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.y] : 0;
+    const float* x = p.x + (size_t)row0 * p.ldx + c;
+    const float* wc = p.w + (size_t)c * p.K;
+    const int T = p.T, K = p.K, pad = (K - 1) / 2;
+    const int t_hi = T - pad > pad ? T - pad : pad;
+    const int t_vec = pad + (t_hi - pad) / 8 * 8;
+    float val = p.b ? p.b[c] : 0.0f;
+    if (t >= pad && t < t_vec) {
+        for (int k = 0; k < K; ++k) val = __fmaf_rn(x[(size_t)(t - pad + k) * p.ldx], wc[k], val);
+    } else {
+        const int K8 = K & ~7;
+        for (int k0 = 0; k0 < K8; k0 += 8) {
+            float pr[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const int src = t - pad + k0 + l;
+                pr[l] = (src >= 0 && src < T) ? __fmul_rn(x[(size_t)src * p.ldx], wc[k0 + l]) : 0.0f;
+            }
+            val = __fadd_rn(val, hsum8(pr));
+        }
+        for (int k = K8; k < K; ++k) {
+            const int src = t - pad + k;
+            if (src >= 0 && src < T) val = __fmaf_rn(x[(size_t)src * p.ldx], wc[k], val);
+        }
+    }
+    p.out[(size_t)(row0 + t) * p.ldo + c] = p.swish ? tiles::swish_f(val) : val;
+}
+
+// ---- transpose (weights at upload: [R][C] -> [C][R]) --------------------------
+__global__ void transpose(const float* __restrict__ in, float* out, int R, int C)
+{
+    __shared__ float tl[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    for (int y = threadIdx.y; y < 32; y += blockDim.y) {
+        const int r = r0 + y, c = c0 + threadIdx.x;
+        if (r < R && c < C) tl[y][threadIdx.x] = in[(size_t)r * C + c];
+    }
+    __syncthreads();
+    for (int y = threadIdx.y; y < 32; y += blockDim.y) {
+        const int c = c0 + y, r = r0 + threadIdx.x;
+        if (r < R && c < C) out[(size_t)c * R + r] = tl[threadIdx.x][y];
+    }
+}
+
+}  // namespace
+
+hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const float* beta,
+                             float* out, int ldo, int rows, int D, hipStream_t s)
+{
+    if (rows <= 0) return hipSuccess;
+    const int blocks = (rows + 31) / 32;          // 4 waves x 8 rows
+    hipLaunchKernelGGL(layer_norm_rows, dim3(blocks), dim3(256), 0, s, x, ldx, gamma, beta, out,
+                       ldo, rows, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s)
+{
+    if (a.T <= 0 || n_chunks <= 0) return hipSuccess;
+    if (a.T > kAttnMaxT) return hipErrorInvalidValue;
+    dim3 grid((a.T + kAttnRows - 1) / kAttnRows, a.H, n_chunks);
+    hipLaunchKernelGGL(rel_pos_attention, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_glu(const float* in, int ldi, float* out, int ldo, int rows, int D, hipStream_t s)
+{
+    const long long n = (long long)rows * D;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(glu_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, ldi, out,
+                       ldo, rows, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_depthwise(const DwArgs& a, int n_chunks, hipStream_t s)
+{
+    const long long n = (long long)a.T * a.C;
+    if (n <= 0 || n_chunks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(depthwise_swish, dim3((unsigned)((n + 255) / 256), n_chunks), dim3(256), 0, s,
+                       a);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose(const float* in, float* out, int R, int C, hipStream_t s)
+{
+    if (R <= 0 || C <= 0) return hipSuccess;
+    hipLaunchKernelGGL(transpose, dim3((C + 31) / 32, (R + 31) / 32), dim3(32, 8), 0, s, in, out, R, C);
+    return hipGetLastError();
+}
+
+}  // namespace pkgpu

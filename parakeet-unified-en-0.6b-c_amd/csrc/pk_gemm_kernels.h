@@ -15,8 +15,10 @@ enum WeightKind { W_F32 = 0, W_I8 = 1, W_I4 = 2 };
 //   v = chain result; if bias: v = fl(v + bias[j]); then
 //   EPI_SWISH:         C[i][j] = swish(v)                  (pk_swish)
 //   EPI_HALF_RESIDUAL: C[i][j] = fl(C[i][j] + 0.5 * v)     (macaron residual)
+//   EPI_RESIDUAL:      C[i][j] = fl(C[i][j] + v)           (attention / conv residual,
+//                                                           encoder.c:410-424, 473-475)
 //   EPI_NONE:          C[i][j] = v
-enum Epilogue { EPI_NONE = 0, EPI_SWISH = 1, EPI_HALF_RESIDUAL = 2 };
+enum Epilogue { EPI_NONE = 0, EPI_SWISH = 1, EPI_HALF_RESIDUAL = 2, EPI_RESIDUAL = 3 };
 
 // One weight GEMM, C <- beta*C + alpha*A*W, row-major, NoTrans/NoTrans,
 // with W given in one of the on-disk formats (weights.c:240-266):
@@ -34,7 +36,7 @@ struct GemmProblem {
     const float* scales;      // W_I4
     float* C; int ldc;
     const float* bias = nullptr;     // length N, or null
-    Epilogue epi = EPI_NONE;         // EPI_HALF_RESIDUAL requires beta == 0
+    Epilogue epi = EPI_NONE;         // the residual epilogues require beta == 0
 };
 
 // Kernel tile configuration chosen for a shape (see choose_config).

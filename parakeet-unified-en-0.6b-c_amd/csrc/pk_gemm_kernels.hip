@@ -84,7 +84,8 @@ TileConfig choose_config(int M, int N, int K) { return kConfigs[choose_index(M, 
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
 {
     if (p.M <= 0 || p.N <= 0) return hipSuccess;
-    if (p.epi == EPI_HALF_RESIDUAL && p.beta != 0.0f) return hipErrorInvalidValue;
+    if ((p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL) && p.beta != 0.0f)
+        return hipErrorInvalidValue;
 
     KArgs a = {};
     a.M = p.M; a.N = p.N; a.K = p.K;

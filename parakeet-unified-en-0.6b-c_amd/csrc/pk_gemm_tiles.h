@@ -427,13 +427,15 @@ __device__ inline float swish_f(float v)
 }
 
 // The fused output step for C[row][col] (row < M, col < N): bias add, then
-// the activation or the half residual (encoder.c:193-216).  0.5 * v is exact,
-// so fl(c + 0.5 * v) equals the reference's fma(out, 0.5, x).
+// the activation or the (half) residual (encoder.c:193-216, 410-424,
+// 473-475).  0.5 * v is exact, so fl(c + 0.5 * v) equals the reference's
+// fma(out, 0.5, x).
 __device__ inline float epilogue(const KArgs& p, float v, int row, int col)
 {
     if (p.bias) v = __fadd_rn(v, p.bias[col]);
     if (p.epi == EPI_SWISH) return swish_f(v);
     if (p.epi == EPI_HALF_RESIDUAL) return __fmaf_rn(v, 0.5f, p.C[(size_t)row * p.ldc + col]);
+    if (p.epi == EPI_RESIDUAL) return __fadd_rn(p.C[(size_t)row * p.ldc + col], v);
     return v;
 }
 

@@ -1,0 +1,525 @@
+// pk_gpu_encoder.hip - host side of the device-resident conformer encoder and
+// of the block-operation entry points (include/pk_gpu.h).
+//
+// The reference runs each conformer block as host loops around its BLAS
+// (encoder.c:179-491) and the chunks of a long input one after another
+// (encoder.c:514-575).  Here the whole block stays on the device, every
+// weight GEMM carries its bias / Swish / residual in its output store, and
+// all chunks run as one batch of rows: row-independent work (LayerNorm,
+// the weight GEMMs, GLU) sees M = sum of the chunks' rows, while attention
+// and the depthwise convolution run per chunk, one launch per distinct chunk
+// length.  The position projection (linear_pos of the positional slice)
+// runs once per block for the longest chunk: the slice of a chunk of T rows
+// is pe_table[center-T+1, center+T) (encoder.c:220-228), a row range of the
+// longest chunk's slice, and GEMM rows are independent, so a shorter chunk
+// reads its P rows from the same result.
+#include "pk_block_kernels.h"
+#include "pk_gemm_kernels.h"
+#include "pk_gpu.h"
+#include "pk_gpu_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <map>
+#include <vector>
+
+using pkgpu::Epilogue;
+using pkgpu::GemmProblem;
+using pkgpu::WeightKind;
+
+namespace {
+
+constexpr int kD = 1024;          // PK_D_MODEL
+constexpr int kFF = 4096;         // PK_FF_DIM
+constexpr int kHeads = 8;         // PK_N_HEADS
+constexpr int kConvK = 9;         // PK_CONV_KERNEL
+
+struct DevWeight {
+    WeightKind kind = pkgpu::W_F32;
+    const void* data = nullptr;
+    float scale = 0.0f;
+    const float* scales = nullptr;
+    int K = 0, N = 0;
+};
+
+struct DevBlock {
+    const float *ln_ff1_w, *ln_ff1_b, *ln_sa_w, *ln_sa_b, *ln_conv_w, *ln_conv_b;
+    const float *ln_ff2_w, *ln_ff2_b, *ln_out_w, *ln_out_b;
+    DevWeight ff1_w1, ff1_w2, ff2_w1, ff2_w2, qkv, pos, out, pw1t, pw2t;
+    const float *ff1_b1, *ff1_b2, *ff2_b1, *ff2_b2, *qkv_b, *out_b, *pu, *pv;
+    const float *pw1_b, *dw_w, *dw_b, *pw2_b;
+};
+
+struct Chunk {
+    int in_start, in_len, out_start, out_len, left_ov, row;   // row: first row in the batch
+};
+
+}  // namespace
+
+struct pk_gpu_encoder {
+    std::vector<DevBlock> blocks;
+    std::vector<void*> allocs;          // weights, tables
+    size_t weight_bytes = 0;
+    const float* pe = nullptr;          // [pe_rows][kD]
+    int pe_rows = 0, pe_center = 0;
+    hipStream_t stream = nullptr;
+    // workspace, grown on demand
+    size_t ws_rows = 0, ws_prow = 0;
+    float *x = nullptr, *ln = nullptr, *h = nullptr, *att = nullptr, *P = nullptr;
+    int* rows_tab = nullptr;            // device chunk-row table
+    size_t rows_cap = 0;
+    size_t ws_bytes = 0;
+};
+
+namespace {
+
+using pkgpu::rt::error;
+using pkgpu::rt::hip_error;
+
+int dev_alloc(pk_gpu_encoder* e, size_t bytes, void** out)
+{
+    *out = nullptr;
+    hipError_t r = hipMalloc(out, bytes ? bytes : 4);
+    if (r != hipSuccess) return error(PK_GPU_ENOMEM, "device allocation of %zu bytes failed", bytes);
+    e->allocs.push_back(*out);
+    e->weight_bytes += bytes;
+    return PK_GPU_OK;
+}
+
+int upload(pk_gpu_encoder* e, const void* host, size_t bytes, const char* what, const void** out)
+{
+    if (!host) return error(PK_GPU_EINVAL, "%s is NULL", what);
+    void* d = nullptr;
+    int rc = dev_alloc(e, bytes, &d);
+    if (rc) return rc;
+    hipError_t r = hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, e->stream);
+    if (r != hipSuccess) return hip_error(r, what);
+    *out = d;
+    return PK_GPU_OK;
+}
+
+int upload_f(pk_gpu_encoder* e, const float* host, size_t n, const char* what, const float** out)
+{
+    const void* d = nullptr;
+    int rc = upload(e, host, n * sizeof(float), what, &d);
+    *out = static_cast<const float*>(d);
+    return rc;
+}
+
+int upload_weight(pk_gpu_encoder* e, const pk_gpu_weight& w, int K, int N, const char* what,
+                  DevWeight* out)
+{
+    out->K = K;
+    out->N = N;
+    out->scale = w.scale;
+    switch (w.bits) {
+    case 32:
+        out->kind = pkgpu::W_F32;
+        return upload(e, w.data, (size_t)K * N * 4, what, &out->data);
+    case 8:
+        out->kind = pkgpu::W_I8;
+        return upload(e, w.data, (size_t)K * N, what, &out->data);
+    case 4: {
+        out->kind = pkgpu::W_I4;
+        int rc = upload(e, w.data, (size_t)K * N / 2, what, &out->data);
+        if (rc) return rc;
+        return upload_f(e, w.scales, (size_t)K * (N / 32), what, &out->scales);
+    }
+    default:
+        return error(PK_GPU_EINVAL, "%s: bits = %d (expected 32, 8 or 4)", what, w.bits);
+    }
+}
+
+// A pointwise-convolution weight [Cout][Cin] (the A operand of the
+// reference's sgemm, tensor_ops.c:579-590) stored transposed, [Cin][Cout]:
+// out^T[t][c] = sum_k ln[t][k] * W[c][k] is then an NN GEMM with the weight
+// as B and the time-major activations as A, with the same fma chain per
+// output (the two factors of each product just swap places).
+int upload_pointwise(pk_gpu_encoder* e, const float* host, int Cout, int Cin, const char* what,
+                     DevWeight* out)
+{
+    if (!host) return error(PK_GPU_EINVAL, "%s is NULL", what);
+    const size_t bytes = (size_t)Cout * Cin * 4;
+    void* t = nullptr;
+    int rc = dev_alloc(e, bytes, &t);
+    if (rc) return rc;
+    void* tmp = nullptr;
+    if (hipMalloc(&tmp, bytes) != hipSuccess) return error(PK_GPU_ENOMEM, "%s staging", what);
+    hipError_t r = hipMemcpyAsync(tmp, host, bytes, hipMemcpyHostToDevice, e->stream);
+    if (r == hipSuccess)
+        r = pkgpu::launch_transpose(static_cast<const float*>(tmp), static_cast<float*>(t), Cout, Cin,
+                                    e->stream);
+    if (r == hipSuccess) r = hipStreamSynchronize(e->stream);
+    (void)hipFree(tmp);
+    if (r != hipSuccess) return hip_error(r, what);
+    out->kind = pkgpu::W_F32;
+    out->data = t;
+    out->K = Cin;
+    out->N = Cout;
+    return PK_GPU_OK;
+}
+
+int upload_block(pk_gpu_encoder* e, const pk_gpu_block_weights& b, DevBlock* d)
+{
+    int rc = 0;
+#define UP(field, src, n) if (!rc) rc = upload_f(e, b.src, (n), #src, &d->field)
+    UP(ln_ff1_w, norm_ff1_w, kD); UP(ln_ff1_b, norm_ff1_b, kD);
+    UP(ln_sa_w, norm_sa_w, kD);   UP(ln_sa_b, norm_sa_b, kD);
+    UP(ln_conv_w, norm_conv_w, kD); UP(ln_conv_b, norm_conv_b, kD);
+    UP(ln_ff2_w, norm_ff2_w, kD); UP(ln_ff2_b, norm_ff2_b, kD);
+    UP(ln_out_w, norm_out_w, kD); UP(ln_out_b, norm_out_b, kD);
+    UP(ff1_b1, ff1_linear1_b, kFF); UP(ff1_b2, ff1_linear2_b, kD);
+    UP(ff2_b1, ff2_linear1_b, kFF); UP(ff2_b2, ff2_linear2_b, kD);
+    UP(qkv_b, linear_qkv_b, 3 * kD); UP(out_b, linear_out_b, kD);
+    UP(pu, pos_bias_u, kD); UP(pv, pos_bias_v, kD);
+    UP(pw1_b, conv_pw1_b, 2 * kD); UP(pw2_b, conv_pw2_b, kD);
+    UP(dw_w, conv_dw_w, kD * kConvK); UP(dw_b, conv_dw_b, kD);
+#undef UP
+    if (!rc) rc = upload_weight(e, b.ff1_linear1_w, kD, kFF, "ff1.linear1", &d->ff1_w1);
+    if (!rc) rc = upload_weight(e, b.ff1_linear2_w, kFF, kD, "ff1.linear2", &d->ff1_w2);
+    if (!rc) rc = upload_weight(e, b.ff2_linear1_w, kD, kFF, "ff2.linear1", &d->ff2_w1);
+    if (!rc) rc = upload_weight(e, b.ff2_linear2_w, kFF, kD, "ff2.linear2", &d->ff2_w2);
+    if (!rc) rc = upload_weight(e, b.linear_qkv_w, kD, 3 * kD, "linear_qkv", &d->qkv);
+    if (!rc) rc = upload_weight(e, b.linear_pos_w, kD, kD, "linear_pos", &d->pos);
+    if (!rc) rc = upload_weight(e, b.linear_out_w, kD, kD, "linear_out", &d->out);
+    if (!rc) rc = upload_pointwise(e, b.conv_pw1_w, 2 * kD, kD, "conv.pw1", &d->pw1t);
+    if (!rc) rc = upload_pointwise(e, b.conv_pw2_w, kD, kD, "conv.pw2", &d->pw2t);
+    return rc;
+}
+
+void free_workspace(pk_gpu_encoder* e)
+{
+    for (float* p : {e->x, e->ln, e->h, e->att, e->P})
+        if (p) (void)hipFree(p);
+    if (e->rows_tab) (void)hipFree(e->rows_tab);
+    e->x = e->ln = e->h = e->att = e->P = nullptr;
+    e->rows_tab = nullptr;
+    e->ws_rows = e->ws_prow = e->rows_cap = e->ws_bytes = 0;
+}
+
+// Grows the workspace; the old one may still be read by work queued on `s`.
+int workspace(pk_gpu_encoder* e, size_t rows, size_t prow, size_t n_chunks, hipStream_t s)
+{
+    if (rows <= e->ws_rows && prow <= e->ws_prow && n_chunks <= e->rows_cap) return PK_GPU_OK;
+    hipError_t r = hipStreamSynchronize(s);
+    if (r != hipSuccess) return hip_error(r, "encoder stream");
+    rows = std::max(rows, e->ws_rows);
+    prow = std::max(prow, e->ws_prow);
+    n_chunks = std::max(n_chunks, e->rows_cap);
+    free_workspace(e);
+    const size_t bytes[5] = {rows * kD * 4, rows * kD * 4, rows * kFF * 4, rows * kD * 4,
+                             prow * kD * 4};
+    float** dst[5] = {&e->x, &e->ln, &e->h, &e->att, &e->P};
+    for (int i = 0; i < 5; ++i) {
+        if (hipMalloc(reinterpret_cast<void**>(dst[i]), bytes[i]) != hipSuccess) {
+            free_workspace(e);
+            return error(PK_GPU_ENOMEM, "encoder workspace of %zu bytes failed", bytes[i]);
+        }
+        e->ws_bytes += bytes[i];
+    }
+    if (hipMalloc(reinterpret_cast<void**>(&e->rows_tab), n_chunks * sizeof(int)) != hipSuccess) {
+        free_workspace(e);
+        return error(PK_GPU_ENOMEM, "encoder chunk table failed");
+    }
+    e->ws_rows = rows;
+    e->ws_prow = prow;
+    e->rows_cap = n_chunks;
+    return PK_GPU_OK;
+}
+
+int gemm(const DevWeight& w, const float* A, int M, float* C, const float* bias, Epilogue epi,
+         hipStream_t s)
+{
+    GemmProblem p{};
+    p.kind = w.kind;
+    p.M = M;
+    p.N = w.N;
+    p.K = w.K;
+    p.alpha = 1.0f;
+    p.beta = 0.0f;
+    p.A = A;
+    p.lda = w.K;
+    p.B = w.data;
+    p.ldb = w.kind == pkgpu::W_I4 ? w.N / 2 : w.N;
+    p.scale = w.scale;
+    p.scales = w.scales;
+    p.C = C;
+    p.ldc = w.N;
+    p.bias = bias;
+    p.epi = epi;
+    return pkgpu::rt::gemm(p, s);
+}
+
+int check(hipError_t r, const char* what) { return r == hipSuccess ? PK_GPU_OK : hip_error(r, what); }
+
+// encoder.c:514-575: output frames [c*C, c*C + C), input with `ov` frames of
+// context each side, clipped to [0, T).  chunk_size <= 0: one sequence.
+std::vector<Chunk> plan_chunks(int T, int C, int ov)
+{
+    std::vector<Chunk> v;
+    if (C <= 0) {
+        v.push_back({0, T, 0, T, 0, 0});
+        return v;
+    }
+    const int n = (T + C - 1) / C;
+    int row = 0;
+    for (int ci = 0; ci < n; ++ci) {
+        const int out_start = ci * C, out_end = std::min(out_start + C, T);
+        const int in_start = std::max(out_start - ov, 0), in_end = std::min(out_end + ov, T);
+        v.push_back({in_start, in_end - in_start, out_start, out_end - out_start,
+                     out_start - in_start, row});
+        row += in_end - in_start;
+    }
+    return v;
+}
+
+// One conformer block (encoder.c:479-491) over all chunks' rows.
+int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
+              const std::map<int, std::pair<int, int>>& groups, hipStream_t s)
+{
+    int rc;
+    float *x = e->x, *ln = e->ln, *h = e->h, *att = e->att;
+    auto ffn = [&](const float* g, const float* be, const DevWeight& w1, const float* b1,
+                   const DevWeight& w2, const float* b2) {
+        int r = check(pkgpu::launch_layer_norm(x, kD, g, be, ln, kD, R, kD, s), "layer norm");
+        if (!r) r = gemm(w1, ln, R, h, b1, pkgpu::EPI_SWISH, s);                 // encoder.c:193-196
+        if (!r) r = gemm(w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s);          // encoder.c:198-216
+        return r;
+    };
+    // feed-forward 1 (encoder.c:483)
+    if ((rc = ffn(b.ln_ff1_w, b.ln_ff1_b, b.ff1_w1, b.ff1_b1, b.ff1_w2, b.ff1_b2))) return rc;
+
+    // self-attention (encoder.c:300-424)
+    if ((rc = check(pkgpu::launch_layer_norm(x, kD, b.ln_sa_w, b.ln_sa_b, ln, kD, R, kD, s), "layer norm")))
+        return rc;
+    if ((rc = gemm(b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s))) return rc;
+    const float* pe_slice = e->pe + (size_t)(e->pe_center - Tmax + 1) * kD;
+    if ((rc = gemm(b.pos, pe_slice, 2 * Tmax - 1, e->P, nullptr, pkgpu::EPI_NONE, s))) return rc;
+    for (const auto& g : groups) {
+        const int T = g.first;
+        pkgpu::AttnArgs a{};
+        a.qkv = h; a.ldq = 3 * kD;
+        a.P = e->P + (size_t)(Tmax - T) * kD; a.ldp = kD;
+        a.pos_bias_u = b.pu; a.pos_bias_v = b.pv;
+        a.out = att; a.ldo = kD;
+        a.chunk_rows = e->rows_tab + g.second.first;
+        a.T = T; a.H = kHeads;
+        if ((rc = check(pkgpu::launch_attention(a, g.second.second, s), "attention"))) return rc;
+    }
+    if ((rc = gemm(b.out, att, R, x, b.out_b, pkgpu::EPI_RESIDUAL, s))) return rc;
+
+    // convolution module (encoder.c:430-476), time-major throughout
+    if ((rc = check(pkgpu::launch_layer_norm(x, kD, b.ln_conv_w, b.ln_conv_b, ln, kD, R, kD, s),
+                    "layer norm")))
+        return rc;
+    if ((rc = gemm(b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s))) return rc;
+    if ((rc = check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu"))) return rc;
+    for (const auto& g : groups) {
+        pkgpu::DwArgs d{};
+        d.x = att; d.ldx = kD;
+        d.w = b.dw_w; d.b = b.dw_b;
+        d.out = ln; d.ldo = kD;
+        d.chunk_rows = e->rows_tab + g.second.first;
+        d.T = g.first; d.C = kD; d.K = kConvK; d.swish = 1;
+        if ((rc = check(pkgpu::launch_depthwise(d, g.second.second, s), "depthwise conv"))) return rc;
+    }
+    if ((rc = gemm(b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s))) return rc;
+
+    // feed-forward 2 and the block's output LayerNorm (encoder.c:486-487)
+    if ((rc = ffn(b.ln_ff2_w, b.ln_ff2_b, b.ff2_w1, b.ff2_b1, b.ff2_w2, b.ff2_b2))) return rc;
+    return check(pkgpu::launch_layer_norm(x, kD, b.ln_out_w, b.ln_out_b, x, kD, R, kD, s),
+                 "layer norm");
+}
+
+int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out, hipStream_t s,
+        hipMemcpyKind in_kind, hipMemcpyKind out_kind)
+{
+    if (!e) return error(PK_GPU_EINVAL, "encoder is NULL");
+    if (T <= 0) return error(PK_GPU_EINVAL, "T = %d", T);
+    if (!x || !out) return error(PK_GPU_EINVAL, "x or out is NULL");
+    if (chunk > 0 && ov < 0) return error(PK_GPU_EINVAL, "overlap = %d", ov);
+    const std::vector<Chunk> chunks = plan_chunks(T, chunk, ov);
+    int R = 0, Tmax = 0;
+    for (const Chunk& c : chunks) {
+        R += c.in_len;
+        Tmax = std::max(Tmax, c.in_len);
+    }
+    if (Tmax > pkgpu::kAttnMaxT)
+        return error(PK_GPU_ENOTSUP, "a sequence of %d frames exceeds the %d-frame attention limit "
+                     "(use chunks)", Tmax, pkgpu::kAttnMaxT);
+    if (e->pe_center - Tmax + 1 < 0 || e->pe_center + Tmax > e->pe_rows)
+        return error(PK_GPU_EINVAL, "positional table too small for %d frames", Tmax);
+
+    // chunks grouped by length: table entries [first, first + count) hold their rows
+    std::map<int, std::vector<int>> by_len;
+    for (const Chunk& c : chunks) by_len[c.in_len].push_back(c.row);
+    std::vector<int> table;
+    std::map<int, std::pair<int, int>> groups;
+    for (const auto& g : by_len) {
+        groups[g.first] = {(int)table.size(), (int)g.second.size()};
+        table.insert(table.end(), g.second.begin(), g.second.end());
+    }
+    int rc = workspace(e, (size_t)R, (size_t)(2 * Tmax - 1), table.size(), s);
+    if (rc) return rc;
+    if ((rc = check(hipMemcpyAsync(e->rows_tab, table.data(), table.size() * sizeof(int),
+                                   hipMemcpyHostToDevice, s), "chunk table")))
+        return rc;
+    // every chunk's input rows (encoder.c:552-553)
+    for (const Chunk& c : chunks)
+        if ((rc = check(hipMemcpyAsync(e->x + (size_t)c.row * kD, x + (size_t)c.in_start * kD,
+                                       (size_t)c.in_len * kD * 4, in_kind, s), "input copy")))
+            return rc;
+    for (const DevBlock& b : e->blocks)
+        if ((rc = run_block(e, b, R, Tmax, groups, s))) return rc;
+    // the centre rows of every chunk (encoder.c:567-569)
+    for (const Chunk& c : chunks)
+        if ((rc = check(hipMemcpyAsync(out + (size_t)c.out_start * kD,
+                                       e->x + (size_t)(c.row + c.left_ov) * kD,
+                                       (size_t)c.out_len * kD * 4, out_kind, s), "output copy")))
+            return rc;
+    return PK_GPU_OK;
+}
+
+int dev_stream(void* stream, hipStream_t* s)
+{
+    hipStream_t own = nullptr;
+    int rc = pkgpu::rt::bind(&own);
+    *s = static_cast<hipStream_t>(stream);
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pk_gpu_encoder_create(pk_gpu_encoder** out, const pk_gpu_block_weights* blocks, int n_blocks,
+                          const float* pe_table, int pe_rows, int pe_center)
+{
+    if (!out) return error(PK_GPU_EINVAL, "enc is NULL");
+    *out = nullptr;
+    if (!blocks || n_blocks <= 0) return error(PK_GPU_EINVAL, "no blocks");
+    if (!pe_table || pe_rows <= 0 || pe_center < 0 || pe_center >= pe_rows)
+        return error(PK_GPU_EINVAL, "bad positional table (%d rows, centre %d)", pe_rows, pe_center);
+    int rc = pkgpu::rt::bind(nullptr);
+    if (rc) return rc;
+    pk_gpu_encoder* e = new pk_gpu_encoder;
+    hipError_t r = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+    if (r != hipSuccess) {
+        delete e;
+        return hip_error(r, "hipStreamCreate");
+    }
+    e->blocks.resize(n_blocks);
+    for (int i = 0; i < n_blocks && !rc; ++i) rc = upload_block(e, blocks[i], &e->blocks[i]);
+    if (!rc) rc = upload_f(e, pe_table, (size_t)pe_rows * kD, "pe_table", &e->pe);
+    e->pe_rows = pe_rows;
+    e->pe_center = pe_center;
+    if (!rc) rc = check(hipStreamSynchronize(e->stream), "weight upload");
+    if (rc) {
+        pk_gpu_encoder_destroy(e);
+        return rc;
+    }
+    *out = e;
+    return PK_GPU_OK;
+}
+
+int pk_gpu_encoder_run(pk_gpu_encoder* enc, const float* x, int T, int chunk_size, int overlap,
+                       float* out)
+{
+    int rc = pkgpu::rt::bind(nullptr);
+    if (rc) return rc;
+    // x may equal out: the input is copied into the workspace first
+    rc = run(enc, x, T, chunk_size, overlap, out, enc ? enc->stream : nullptr,
+             hipMemcpyHostToDevice, hipMemcpyDeviceToHost);
+    if (rc) return rc;
+    return check(hipStreamSynchronize(enc->stream), "encoder run");
+}
+
+int pk_gpu_encoder_run_dev(pk_gpu_encoder* enc, const float* dx, int T, int chunk_size, int overlap,
+                           float* dout, void* stream)
+{
+    hipStream_t s = nullptr;
+    int rc = dev_stream(stream, &s);
+    if (rc) return rc;
+    if (!stream && enc) s = enc->stream;
+    return run(enc, dx, T, chunk_size, overlap, dout, s, hipMemcpyDeviceToDevice,
+               hipMemcpyDeviceToDevice);
+}
+
+size_t pk_gpu_encoder_bytes(const pk_gpu_encoder* enc)
+{
+    return enc ? enc->weight_bytes + enc->ws_bytes : 0;
+}
+
+void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
+{
+    if (!enc) return;
+    if (enc->stream) (void)hipStreamSynchronize(enc->stream);
+    free_workspace(enc);
+    for (void* p : enc->allocs) (void)hipFree(p);
+    if (enc->stream) (void)hipStreamDestroy(enc->stream);
+    delete enc;
+}
+
+int pk_gpu_layer_norm_dev(const float* dx, const float* dgamma, const float* dbeta, float* dout,
+                          int rows, int D, void* stream)
+{
+    if (rows < 0 || D <= 0 || D % 8) return error(PK_GPU_EINVAL, "rows = %d, D = %d (D %% 8 == 0)", rows, D);
+    if (rows && (!dx || !dgamma || !dbeta || !dout)) return error(PK_GPU_EINVAL, "NULL operand");
+    hipStream_t s;
+    int rc = dev_stream(stream, &s);
+    if (rc) return rc;
+    return check(pkgpu::launch_layer_norm(dx, D, dgamma, dbeta, dout, D, rows, D, s), "layer norm");
+}
+
+int pk_gpu_attention_dev(const float* dqkv, int ldq, const float* dP, int ldp, const float* dpu,
+                         const float* dpv, float* dout, int ldo, int T, int H, void* stream)
+{
+    if (T < 1 || T > pkgpu::kAttnMaxT) return error(PK_GPU_EINVAL, "T = %d (1..%d)", T, pkgpu::kAttnMaxT);
+    if (H < 1) return error(PK_GPU_EINVAL, "H = %d", H);
+    const int D = 128 * H;
+    if (ldq < 3 * D || ldp < D || ldo < D || ldq % 4 || ldp % 4)
+        return error(PK_GPU_EINVAL, "leading dimensions %d/%d/%d too small or not multiples of 4",
+                     ldq, ldp, ldo);
+    if (!dqkv || !dP || !dpu || !dpv || !dout) return error(PK_GPU_EINVAL, "NULL operand");
+    if ((reinterpret_cast<uintptr_t>(dqkv) | reinterpret_cast<uintptr_t>(dP)) % 16)
+        return error(PK_GPU_EINVAL, "qkv and P must be 16-byte aligned");
+    hipStream_t s;
+    int rc = dev_stream(stream, &s);
+    if (rc) return rc;
+    pkgpu::AttnArgs a{};
+    a.qkv = dqkv; a.ldq = ldq; a.P = dP; a.ldp = ldp;
+    a.pos_bias_u = dpu; a.pos_bias_v = dpv;
+    a.out = dout; a.ldo = ldo;
+    a.chunk_rows = nullptr;
+    a.T = T; a.H = H;
+    return check(pkgpu::launch_attention(a, 1, s), "attention");
+}
+
+int pk_gpu_glu_dev(const float* din, float* dout, int rows, int D, void* stream)
+{
+    if (rows < 0 || D <= 0) return error(PK_GPU_EINVAL, "rows = %d, D = %d", rows, D);
+    if (rows && (!din || !dout)) return error(PK_GPU_EINVAL, "NULL operand");
+    hipStream_t s;
+    int rc = dev_stream(stream, &s);
+    if (rc) return rc;
+    return check(pkgpu::launch_glu(din, 2 * D, dout, D, rows, D, s), "glu");
+}
+
+int pk_gpu_depthwise_dev(const float* dx, int ldx, const float* dw, const float* db, float* dout,
+                         int ldo, int T, int C, int K, int swish, void* stream)
+{
+    if (T < 0 || C <= 0 || K <= 0 || K % 2 == 0 || ldx < C || ldo < C)
+        return error(PK_GPU_EINVAL, "T = %d, C = %d, K = %d, ldx = %d, ldo = %d", T, C, K, ldx, ldo);
+    if (T && (!dx || !dw || !dout)) return error(PK_GPU_EINVAL, "NULL operand");
+    hipStream_t s;
+    int rc = dev_stream(stream, &s);
+    if (rc) return rc;
+    pkgpu::DwArgs d{};
+    d.x = dx; d.ldx = ldx; d.w = dw; d.b = db; d.out = dout; d.ldo = ldo;
+    d.chunk_rows = nullptr;
+    d.T = T; d.C = C; d.K = K; d.swish = swish != 0;
+    return check(pkgpu::launch_depthwise(d, 1, s), "depthwise conv");
+}
+
+}  // extern "C"

@@ -9,6 +9,7 @@
 // the weight registry, which is guarded by a mutex.
 #include "pk_gpu.h"
 #include "pk_gemm_kernels.h"
+#include "pk_gpu_internal.h"
 
 #include <hip/hip_runtime.h>
 
@@ -399,10 +400,10 @@ int pk_gpu_sgemm(int transA, int transB, int M, int N, int K, float alpha, const
 // Device-pointer entry points; the *_ex forms add the fused epilogue.
 static int check_epilogue(const float* bias, int epi, float beta)
 {
-    if (epi < PK_GPU_EPI_NONE || epi > PK_GPU_EPI_HALF_RESIDUAL)
+    if (epi < PK_GPU_EPI_NONE || epi > PK_GPU_EPI_RESIDUAL)
         return fail(PK_GPU_EINVAL, "epilogue %d is not one of PK_GPU_EPI_*", epi);
-    if (epi == PK_GPU_EPI_HALF_RESIDUAL && beta != 0.0f)
-        return fail(PK_GPU_EINVAL, "half-residual epilogue needs beta == 0 (C is the residual)");
+    if ((epi == PK_GPU_EPI_HALF_RESIDUAL || epi == PK_GPU_EPI_RESIDUAL) && beta != 0.0f)
+        return fail(PK_GPU_EINVAL, "residual epilogues need beta == 0 (C is the residual)");
     (void)bias;
     return PK_GPU_OK;
 }
@@ -522,3 +523,34 @@ int pk_gpu_force_config(int index)
 }
 
 }  // extern "C"
+
+// Hooks for the other host translation units (pk_gpu_internal.h).
+namespace pkgpu {
+namespace rt {
+
+int error(int code, const char* fmt, ...)
+{
+    char msg[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+    t_err = msg;
+    return code;
+}
+
+int hip_error(hipError_t e, const char* what) { return hip_fail(e, what); }
+
+int bind(hipStream_t* thread_stream)
+{
+    ThreadCtx* c = nullptr;
+    int rc = thread_ctx(&c);
+    if (rc) return rc;
+    if (thread_stream) *thread_stream = c->stream;
+    return PK_GPU_OK;
+}
+
+int gemm(const GemmProblem& p, hipStream_t s) { return launch(p, s); }
+
+}  // namespace rt
+}  // namespace pkgpu

@@ -43,9 +43,48 @@ _PROTOS = {
     "pk_gpu_config_info": (_i, [_i, _p, _p, _p, _p, _p, _p]),
     "pk_gpu_pick_config": (_i, [_i, _i, _i]),
     "pk_gpu_force_config": (_i, [_i]),
+    "pk_gpu_layer_norm_dev": (_i, [_p, _p, _p, _p, _i, _i, _p]),
+    "pk_gpu_attention_dev": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
+    "pk_gpu_glu_dev": (_i, [_p, _p, _i, _i, _p]),
+    "pk_gpu_depthwise_dev": (_i, [_p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p]),
+    "pk_gpu_encoder_create": (_i, [_p, _p, _i, _p, _i, _i]),
+    "pk_gpu_encoder_run": (_i, [_p, _p, _i, _i, _i, _p]),
+    "pk_gpu_encoder_run_dev": (_i, [_p, _p, _i, _i, _i, _p, _p]),
+    "pk_gpu_encoder_bytes": (_sz, [_p]),
+    "pk_gpu_encoder_destroy": (None, [_p]),
 }
 
-EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL = 0, 1, 2
+EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL, EPI_RESIDUAL = 0, 1, 2, 3
+
+
+class Weight(ctypes.Structure):
+    """pk_gpu_weight (include/pk_gpu.h; the reference's Weight, parakeet.h:42-57)."""
+    _fields_ = [("data", _p), ("scale", _f), ("scales", _p), ("bits", _i)]
+
+
+_BLOCK_FIELDS = [
+    ("norm_ff1_w", _p), ("norm_ff1_b", _p),
+    ("ff1_linear1_w", Weight), ("ff1_linear1_b", _p),
+    ("ff1_linear2_w", Weight), ("ff1_linear2_b", _p),
+    ("norm_sa_w", _p), ("norm_sa_b", _p),
+    ("linear_qkv_w", Weight), ("linear_qkv_b", _p),
+    ("linear_pos_w", Weight),
+    ("linear_out_w", Weight), ("linear_out_b", _p),
+    ("pos_bias_u", _p), ("pos_bias_v", _p),
+    ("norm_conv_w", _p), ("norm_conv_b", _p),
+    ("conv_pw1_w", _p), ("conv_pw1_b", _p),
+    ("conv_dw_w", _p), ("conv_dw_b", _p),
+    ("conv_pw2_w", _p), ("conv_pw2_b", _p),
+    ("norm_ff2_w", _p), ("norm_ff2_b", _p),
+    ("ff2_linear1_w", Weight), ("ff2_linear1_b", _p),
+    ("ff2_linear2_w", Weight), ("ff2_linear2_b", _p),
+    ("norm_out_w", _p), ("norm_out_b", _p),
+]
+
+
+class BlockWeights(ctypes.Structure):
+    """pk_gpu_block_weights (include/pk_gpu.h): one conformer block, host pointers."""
+    _fields_ = _BLOCK_FIELDS
 
 STATUS = {0: "OK", -1: "EINVAL", -2: "ENOTSUP", -3: "ENOMEM", -4: "EHIP", -5: "ENODEV"}
 

@@ -1,0 +1,97 @@
+"""Synthetic conformer-block parameters in the reference's formats, shared by
+the block tests: numpy arrays kept alive together with the ctypes
+pk_gpu_block_weights that points at them.
+
+Statistics follow the workloads: int4 feed-forward weights (nibble codes
+uniform 0..15, decoded signed, scales ~U(0.005, 0.02) per 32 columns), int8
+attention projections (uniform -127..127, per-tensor scale 0.01), fp32
+pointwise convolutions ~N(0, 0.02), depthwise taps ~N(0, 1/9), biases
+~N(0, 0.02), LayerNorm gain 1 + N(0, 0.1) and bias N(0, 0.1).
+
+attn_scale sets the int8 attention projections' scale.  The workloads'
+0.01 (weights of standard deviation ~0.73) makes attention logits of several
+hundred, and the reference itself then amplifies a 1-ulp difference about
+tenfold per block (test_oracle_block.test_reference_sensitivity); 0.0005
+(~0.037, about 1/sqrt(1024), like trained projections) keeps it flat."""
+import ctypes
+
+import numpy as np
+
+from pkgpu import pk
+
+D, FF, H, DH, KCONV = 1024, 4096, 8, 128, 9
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class Block:
+    def __init__(self, seed, qkv_bits=8, attn_scale=0.01):
+        rng = np.random.default_rng(seed)
+        self.keep = []
+        f32 = lambda a: self._keep(np.ascontiguousarray(a, dtype=np.float32))
+        normal = lambda shape, s: f32(rng.standard_normal(shape) * s)
+        w = pk.BlockWeights()
+
+        def i4(K, N):
+            data = self._keep(rng.integers(0, 256, (K, N // 2), dtype=np.uint8))
+            scales = f32(rng.uniform(0.005, 0.02, (K, N // 32)))
+            return pk.Weight(data.ctypes.data, 0.0, scales.ctypes.data, 4)
+
+        def i8(K, N, scale=0.01):
+            data = self._keep(rng.integers(-127, 128, (K, N), dtype=np.int8))
+            return pk.Weight(data.ctypes.data, scale, None, 8)
+
+        def fp(K, N, s=0.02):
+            data = normal((K, N), s)
+            return pk.Weight(data.ctypes.data, 0.0, None, 32)
+
+        def ln():
+            return f32(1.0 + rng.standard_normal(D) * 0.1).ctypes.data, normal(D, 0.1).ctypes.data
+
+        w.norm_ff1_w, w.norm_ff1_b = ln()
+        w.ff1_linear1_w, w.ff1_linear1_b = i4(D, FF), normal(FF, 0.02).ctypes.data
+        w.ff1_linear2_w, w.ff1_linear2_b = i4(FF, D), normal(D, 0.02).ctypes.data
+        w.norm_sa_w, w.norm_sa_b = ln()
+        w.linear_qkv_w = i8(D, 3 * D, attn_scale) if qkv_bits == 8 else fp(D, 3 * D)
+        w.linear_qkv_b = normal(3 * D, 0.02).ctypes.data
+        w.linear_pos_w = i8(D, D, attn_scale)
+        w.linear_out_w, w.linear_out_b = i8(D, D, attn_scale), normal(D, 0.02).ctypes.data
+        w.pos_bias_u, w.pos_bias_v = normal(D, 0.02).ctypes.data, normal(D, 0.02).ctypes.data
+        w.norm_conv_w, w.norm_conv_b = ln()
+        w.conv_pw1_w, w.conv_pw1_b = normal((2 * D, D), 0.02).ctypes.data, normal(2 * D, 0.02).ctypes.data
+        w.conv_dw_w, w.conv_dw_b = normal((D, KCONV), 1.0 / 3.0).ctypes.data, normal(D, 0.02).ctypes.data
+        w.conv_pw2_w, w.conv_pw2_b = normal((D, D), 0.02).ctypes.data, normal(D, 0.02).ctypes.data
+        w.norm_ff2_w, w.norm_ff2_b = ln()
+        w.ff2_linear1_w, w.ff2_linear1_b = i4(D, FF), normal(FF, 0.02).ctypes.data
+        w.ff2_linear2_w, w.ff2_linear2_b = i4(FF, D), normal(D, 0.02).ctypes.data
+        w.norm_out_w, w.norm_out_b = ln()
+        self.w = w
+
+    def _keep(self, a):
+        self.keep.append(a)
+        return a
+
+
+def block_array(blocks):
+    arr = (pk.BlockWeights * len(blocks))()
+    for i, b in enumerate(blocks):
+        arr[i] = b.w
+    return arr
+
+
+def pe_table(rows=9999, center=4999):
+    """Sinusoidal relative-position table, row p holding position center - p
+    (the layout pos_encoding.pe_table has in the reference's weights)."""
+    pos = (center - np.arange(rows, dtype=np.float64))[:, None]
+    div = np.exp(-(2.0 * np.arange(D // 2)) * np.log(10000.0) / D)[None, :]
+    pe = np.empty((rows, D), np.float32)
+    pe[:, 0::2] = np.sin(pos * div)
+    pe[:, 1::2] = np.cos(pos * div)
+    return pe
+
+
+def pe_slice(pe, T, center=4999):
+    """encoder.c:220-228: rows [center - T + 1, center + T)."""
+    return np.ascontiguousarray(pe[center - T + 1:center + T])
