@@ -1,22 +1,31 @@
-"""Benchmark: the GPTQ int4 FastConformer FFN pair on one MI355X.
+"""Benchmark: the 24-block FastConformer encoder on one MI355X.
 
-Workload (one "step"): X fp32 [375, 1024] ~ N(0,1)  ->  int4 GEMM up
-(1024 -> 4096, packed nibbles [1024][2048] with fp32 scales [1024][128])
-with Swish fused into its output store  ->  int4 GEMM down (4096 -> 1024,
-[4096][512] + [4096][32]),
-i.e. the feed-forward of 30 s of audio (375 encoder frames,
-encoder.c:179-217 without the host bias/residual adds), through the C ABI
-of libpk_gpu.so with every input already resident in HBM.  Weight nibbles
-are uniform 0..15 (decoded signed, as the format defines) and scales
-~U(0.005, 0.02); the steps rotate over enough weight replicas (> 256 MB)
-that weights stream from HBM rather than from the 256 MB Infinity Cache.
+Workload (one "step", the default): 256 s of audio = 3200 encoder frames of
+fp32 features ~N(0,1), chunked as the reference chunks long inputs (400
+frames + 8 frames of context each side, encoder.c:514-575: chunks of 408,
+6 x 416 and 408 rows) and run as ONE batch through the device-resident
+encoder of libpk_gpu.so (pk_gpu_encoder_run_dev): every weight GEMM over all
+3312 chunk rows at once (int4 feed-forward, int8 fused QKV / position /
+output projections, fp32 pointwise convolutions), attention and the
+depthwise convolution per chunk, every activation resident in HBM.  The
+model is random-init at the workloads' quantization statistics: int4 nibble
+codes uniform 0..15 (decoded signed) with fp32 scales ~U(0.005, 0.02) per
+(row, 32 columns), int8 codes uniform in [-127, 127] with per-tensor scales
+~0.01, fp32 pointwise convolutions ~N(0, 0.02), biases ~N(0, 0.02).
 
-Prints one JSON line: encoder frames/s through the pair, plus
-  roofline      the int4 GEMM kernel: algorithmic flops / HIP-event time,
-                against the fp32 dense MFMA peak (the instruction it issues)
-  cpu_baseline  the reference's own cblas_sgemm_q4b + pk_swish (compiled
-                from its sources, oracle/_ref/libpkref.so) on a bounded
-                sample of the same workload, PK_THREADS=16 host threads.
+Prints one JSON line: encoder frames/s, plus
+  stages        per-stage device time per step, TFLOP/s and GB/s (HIP events
+                around every launch, inside the timed steps)
+  roofline      the dominant kernel, the int4 feed-forward GEMM at M = 3312:
+                algorithmic flops / its HIP-event time, against the fp32 dense
+                MFMA peak (the instruction it issues)
+  cpu_baseline  the reference's own 24 conformer blocks (compiled from its
+                sources, oracle/_ref/libpkref_block_x86.so) on a bounded
+                sample of the same workload: whole 416-row chunks, PK_THREADS
+                = 16 host threads (the reference's clamp).
+
+Other modes: --ffn times the int4 feed-forward pair at M = 375 (30 s of
+audio); --gemm KIND:MxNxK times single weight GEMMs.
 """
 import argparse
 import json
@@ -183,32 +192,8 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20):
         torch.cuda.empty_cache()
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--replicas", type=int, default=64)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run 10 plain 256 MiB device-to-device copies (the reference "
-                         "reading for FETCH_SIZE / WRITE_SIZE counters) and exit")
-    ap.add_argument("--gemm", action="append", default=[], metavar="KIND:MxNxK",
-                    help="instead of the FFN pair, time single GEMMs (kind i4, i8 or f32); "
-                         "one JSON line each")
-    args = ap.parse_args()
-    if args.copy_calibration:
-        copy_calibration()
-        return
-    if args.gemm:
-        gemm_mode(args.gemm, args.steps, args.warmup)
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU only (single-GPU hot path; "
-              "multi-GPU sharding is a design note, not built)", file=sys.stderr)
-        sys.exit(2)
-
+def ffn_mode(args):
+    """The int4 feed-forward pair at M = 375 (one FFN of 30 s of audio)."""
     import torch
     pk = load_binding()
 
@@ -314,6 +299,251 @@ def main():
     }
     out["cpu_baseline"] = None if args.no_cpu else cpu_baseline(X, P1, S1, P2, S2, args.cpu_seconds)
     print(json.dumps(out), flush=True)
+
+
+
+# ---- the 24-block encoder (workload 4) -----------------------------------
+
+ENC_SEED = 0x5EED0004          # workload 4
+ENC_FRAMES, ENC_CHUNK, ENC_OVERLAP = 3200, 400, 8
+N_BLOCKS = 24
+PE_ROWS, PE_CENTER = 9999, 4999
+
+
+def enc_rng(block, tensor):
+    return np.random.Generator(np.random.PCG64([ENC_SEED, block, tensor]))
+
+
+class EncoderModel:
+    """Random-init parameters of the 24 blocks in the reference's formats
+    (numpy arrays kept alive) and the pk_gpu_block_weights array over them."""
+
+    def __init__(self, pk, n_blocks=N_BLOCKS):
+        self.keep = []
+        self.blocks = (pk.BlockWeights * n_blocks)()
+        for b in range(n_blocks):
+            t = iter(range(64))
+            keep = self.keep.append
+
+            def f32(a):
+                a = np.ascontiguousarray(a, np.float32)
+                keep(a)
+                return a.ctypes.data
+
+            def normal(shape, sd):
+                return f32(enc_rng(b, next(t)).standard_normal(shape) * sd)
+
+            def const(n, v):
+                return f32(np.full(n, v))
+
+            def i4(K, N):
+                p = enc_rng(b, next(t)).integers(0, 256, (K, N // 2), dtype=np.uint8)
+                keep(p)
+                sc = f32(enc_rng(b, next(t)).uniform(0.005, 0.02, (K, N // 32)))
+                return pk.Weight(p.ctypes.data, 0.0, sc, 4)
+
+            def i8(K, N, scale):
+                q = enc_rng(b, next(t)).integers(-127, 128, (K, N), dtype=np.int8)
+                keep(q)
+                return pk.Weight(q.ctypes.data, scale, None, 8)
+
+            w = self.blocks[b]
+            w.norm_ff1_w, w.norm_ff1_b = const(D, 1.0), const(D, 0.0)
+            w.ff1_linear1_w, w.ff1_linear1_b = i4(D, FF), normal(FF, 0.02)
+            w.ff1_linear2_w, w.ff1_linear2_b = i4(FF, D), normal(D, 0.02)
+            w.norm_sa_w, w.norm_sa_b = const(D, 1.0), const(D, 0.0)
+            w.linear_qkv_w, w.linear_qkv_b = i8(D, 3 * D, 0.011), normal(3 * D, 0.02)
+            w.linear_pos_w = i8(D, D, 0.01)
+            w.linear_out_w, w.linear_out_b = i8(D, D, 0.01), normal(D, 0.02)
+            w.pos_bias_u, w.pos_bias_v = normal(D, 0.02), normal(D, 0.02)
+            w.norm_conv_w, w.norm_conv_b = const(D, 1.0), const(D, 0.0)
+            w.conv_pw1_w, w.conv_pw1_b = normal((2 * D, D), 0.02), normal(2 * D, 0.02)
+            w.conv_dw_w, w.conv_dw_b = normal((D, 9), 1.0 / 3.0), normal(D, 0.02)
+            w.conv_pw2_w, w.conv_pw2_b = normal((D, D), 0.02), normal(D, 0.02)
+            w.norm_ff2_w, w.norm_ff2_b = const(D, 1.0), const(D, 0.0)
+            w.ff2_linear1_w, w.ff2_linear1_b = i4(D, FF), normal(FF, 0.02)
+            w.ff2_linear2_w, w.ff2_linear2_b = i4(FF, D), normal(D, 0.02)
+            w.norm_out_w, w.norm_out_b = const(D, 1.0), const(D, 0.0)
+        # sinusoidal relative-position table, row p = position PE_CENTER - p
+        pos = (PE_CENTER - np.arange(PE_ROWS, dtype=np.float64))[:, None]
+        div = np.exp(-(2.0 * np.arange(D // 2)) * np.log(10000.0) / D)[None, :]
+        self.pe = np.empty((PE_ROWS, D), np.float32)
+        self.pe[:, 0::2] = np.sin(pos * div)
+        self.pe[:, 1::2] = np.cos(pos * div)
+
+
+def encoder_features(frames=ENC_FRAMES):
+    return enc_rng(0xFEA7, 0).standard_normal((frames, D)).astype(np.float32)
+
+
+def chunk_rows(T=ENC_FRAMES, C=ENC_CHUNK, ov=ENC_OVERLAP):
+    """Input rows of every chunk (encoder.c:531-553)."""
+    rows = []
+    for ci in range(-(-T // C)):
+        o0, o1 = ci * C, min(ci * C + C, T)
+        rows.append(min(o1 + ov, T) - max(o0 - ov, 0))
+    return rows
+
+
+def encoder_cpu_baseline(model, x, budget_s):
+    """The reference's own conformer blocks (libpkref_block_x86.so: its x86
+    build, weight GEMMs included) on whole 416-row chunks of the workload,
+    as many as fit in ~budget_s; output frames per second."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+    if not po.have_ref_block("x86"):
+        return None
+    os.environ["PK_THREADS"] = str(CPU_THREADS)
+    T = ENC_CHUNK + 2 * ENC_OVERLAP
+    pe_slice = np.ascontiguousarray(model.pe[PE_CENTER - T + 1:PE_CENTER + T])
+    n, t0 = 0, time.perf_counter()
+    while True:
+        i0 = ENC_CHUNK * (n % 6 + 1) - ENC_OVERLAP         # the middle chunks
+        po.ref_blocks(model.blocks, N_BLOCKS, pe_slice, x[i0:i0 + T], variant="x86")
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    threads = po.ref_block_threads("x86")
+    return {"value": round(ENC_CHUNK * n / el, 2), "unit": "frames/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"{n} chunk(s) of 416 rows (400 output frames each) through the 24 reference "
+                      f"conformer blocks (x86 AVX2 build, {threads} threads) in {el:.1f} s",
+            "s_per_chunk": round(el / n, 3)}
+
+
+STAGES = ["gemm_i4", "gemm_i8", "gemm_f32", "attention", "layer_norm", "conv_glu_depthwise",
+          "chunk_copies"]
+
+
+def encoder_mode(args):
+    import ctypes
+    import torch
+    pk = load_binding()
+    lib = pk.load()
+    pk.call("pk_gpu_init", 0)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    s = stream.cuda_stream
+
+    model = EncoderModel(pk)
+    x = encoder_features()
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(model.blocks, ctypes.c_void_p),
+            N_BLOCKS, model.pe.ctypes.data, PE_ROWS, PE_CENTER)
+    dx = torch.from_numpy(x).to(dev)
+    dout = torch.empty_like(dx)
+
+    def step():
+        return lib.pk_gpu_encoder_run_dev(enc, dx.data_ptr(), ENC_FRAMES, ENC_CHUNK, ENC_OVERLAP,
+                                          dout.data_ptr(), s)
+
+    for _ in range(args.warmup):
+        pk.check("pk_gpu_encoder_run_dev", step())
+    torch.cuda.synchronize(dev)
+    pk.call("pk_gpu_encoder_profile", enc, 1)
+    K = args.steps
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    rc = 0
+    for _ in range(K):
+        rc |= step()
+    t_end.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - wall0
+    pk.check("pk_gpu_encoder_run_dev", rc)
+    elapsed_ms = t_start.elapsed_time(t_end)
+
+    stages = {}
+    for i, name in enumerate(STAGES):
+        ms, n, fl, by = ctypes.c_double(), ctypes.c_longlong(), ctypes.c_double(), ctypes.c_double()
+        pk.call("pk_gpu_encoder_profile_read", enc, i, ctypes.byref(ms), ctypes.byref(n),
+                ctypes.byref(fl), ctypes.byref(by))
+        sec = ms.value / 1e3
+        stages[name] = {"ms_per_step": round(ms.value / K, 3), "launches_per_step": n.value // K,
+                        "tflops": round(fl.value / sec / 1e12, 2) if sec and fl.value else None,
+                        "gbps": round(by.value / sec / 1e9, 1) if sec else None}
+        if name == "gemm_i4":
+            i4_flops, i4_sec, i4_launches = fl.value, sec, n.value
+    pk.call("pk_gpu_encoder_profile", enc, 0)
+    rows = chunk_rows()
+    i4_tflops = i4_flops / i4_sec / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "encoder_3200_int4_traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+    out = {
+        "metric": METRIC,
+        "value": round(ENC_FRAMES * K / (elapsed_ms / 1e3), 1),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed_ms / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "24-block mixed int4/int8 FastConformer encoder, 256 s of audio = "
+                               "3200 frames, 8 chunks (408/416 rows) run as one batch, "
+                               f"GEMM M = {sum(rows)}",
+                   "frames": ENC_FRAMES, "chunk": ENC_CHUNK, "overlap": ENC_OVERLAP,
+                   "chunk_rows": rows, "blocks": N_BLOCKS, "d_model": D, "d_ff": FF,
+                   "device_bytes": lib.pk_gpu_encoder_bytes(enc)},
+        "stages": stages,
+        "wall_ms_per_step": round(1e3 * wall / K, 3),
+        "roofline": {"bound": "mfma",
+                     "kernel": f"int4 feed-forward chain GEMM, M = {sum(rows)} "
+                               "(1024->4096 with fused bias + Swish, 4096->1024 with bias + half "
+                               "residual)",
+                     "achieved": round(i4_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(i4_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": traffic, "launches_per_step": i4_launches // K},
+    }
+    out["cpu_baseline"] = None if args.no_cpu else encoder_cpu_baseline(model, x, args.cpu_seconds)
+    lib.pk_gpu_encoder_destroy(enc)
+    print(json.dumps(out), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--replicas", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ffn", action="store_true",
+                    help="time the int4 feed-forward pair at M = 375 instead of the encoder")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 10 plain 256 MiB device-to-device copies (the reference "
+                         "reading for FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--gemm", action="append", default=[], metavar="KIND:MxNxK",
+                    help="instead of the encoder, time single GEMMs (kind i4, i8 or f32); "
+                         "one JSON line each")
+    args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (single-GPU hot path; "
+              "multi-GPU sharding is a design note, not built)", file=sys.stderr)
+        sys.exit(2)
+    if args.gemm:
+        gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup)
+        return
+    if args.ffn:
+        args.steps = args.steps or 200
+        args.warmup = 20 if args.warmup is None else args.warmup
+        ffn_mode(args)
+        return
+    args.steps = args.steps or 20
+    args.warmup = 2 if args.warmup is None else args.warmup
+    encoder_mode(args)
 
 
 if __name__ == "__main__":

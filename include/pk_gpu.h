@@ -149,9 +149,9 @@ int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);
  * CPU-model-specific approximation (vrsqrtss, vrcpps, glibc's vector expf),
  * the correctly rounded value is taken instead. */
 
-/* LayerNorm of `rows` rows of D floats (pk_layer_norm_rows,
- * tensor_ops.c:150-185, 187-211); D % 8 == 0; dout may equal dx.  The sums
- * are the reference's; 1/sqrt(var + 1e-5) is correctly rounded. */
+/* LayerNorm of `rows` rows of D = 1024 floats (pk_layer_norm_rows,
+ * tensor_ops.c:150-185, 187-211; d_model); dout may equal dx.  The sums are
+ * the reference's; 1/sqrt(var + 1e-5) is correctly rounded. */
 int pk_gpu_layer_norm_dev(const float *dx, const float *dgamma, const float *dbeta,
                           float *dout, int rows, int D, void *stream);
 
@@ -243,12 +243,32 @@ int pk_gpu_encoder_create(pk_gpu_encoder **enc, const pk_gpu_block_weights *bloc
  * out is written. */
 int pk_gpu_encoder_run(pk_gpu_encoder *enc, const float *x, int T, int chunk_size,
                        int overlap, float *out);
-/* The same with device pointers, enqueued on `stream` (NULL: the encoder's
- * own stream); returns without synchronising. */
+/* The same with device pointers, enqueued on `stream` (NULL = HIP's null
+ * stream, as for every *_dev entry point); returns without synchronising.
+ * Runs of one encoder share its workspace: do not overlap them. */
 int pk_gpu_encoder_run_dev(pk_gpu_encoder *enc, const float *dx, int T, int chunk_size,
                            int overlap, float *dout, void *stream);
 /* Device bytes held by the encoder (weights + workspace). */
 size_t pk_gpu_encoder_bytes(const pk_gpu_encoder *enc);
+
+/* Per-stage timing of later runs: with enable != 0, every launch of a run is
+ * bracketed by HIP events on its stream (the reference's pk_verbose timers
+ * have no finer granularity); 0 stops and clears.  Stages: */
+#define PK_GPU_STAGE_GEMM_I4    0   /* feed-forward GEMMs (int4)              */
+#define PK_GPU_STAGE_GEMM_I8    1   /* QKV, position, output GEMMs (int8)     */
+#define PK_GPU_STAGE_GEMM_F32   2   /* pointwise-convolution GEMMs (fp32)     */
+#define PK_GPU_STAGE_ATTENTION  3   /* relative-position attention            */
+#define PK_GPU_STAGE_LAYER_NORM 4
+#define PK_GPU_STAGE_CONV       5   /* GLU, depthwise convolution + Swish     */
+#define PK_GPU_STAGE_COPY       6   /* chunk input / output copies            */
+#define PK_GPU_N_STAGES         7
+int pk_gpu_encoder_profile(pk_gpu_encoder *enc, int enable);
+/* Totals of one stage since profiling was enabled: device time in ms,
+ * launches, algorithmic flops (2*M*N*K for the GEMMs and attention's three
+ * products) and algorithmic bytes (operands read once + results written
+ * once).  Waits for the profiled runs to finish.  Any pointer may be NULL. */
+int pk_gpu_encoder_profile_read(pk_gpu_encoder *enc, int stage, double *ms, long long *launches,
+                                double *flops, double *bytes);
 void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
 
 /* ---- tuning / introspection ------------------------------------------- */

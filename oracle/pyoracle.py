@@ -24,7 +24,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "_build", "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libpkref.so")
 REF_PORTABLE_SO = os.path.join(HERE, "_ref", "libpkref_portable.so")
-REF_BLOCK_SO = os.path.join(HERE, "_ref", "libpkref_block.so")
+REF_BLOCK_SO = {"portable": os.path.join(HERE, "_ref", "libpkref_block.so"),
+                "x86": os.path.join(HERE, "_ref", "libpkref_block_x86.so")}
 
 _f = ctypes.c_float
 _i = ctypes.c_int
@@ -291,28 +292,39 @@ def ref_sgemm_st(A, B, transB, C=None):
     return C
 
 
-_ref_block = None
+_ref_block = {}
 
 
-def have_ref_block():
-    return os.path.exists(REF_BLOCK_SO)
+def have_ref_block(variant="portable"):
+    return os.path.exists(REF_BLOCK_SO[variant])
 
 
-def ref_blocks(blocks, n_blocks, pe_slice, x):
+def ref_blocks(blocks, n_blocks, pe_slice, x, variant="portable"):
     """Run the reference's conformer_block n_blocks times on x [T][1024] (in a
-    copy), blocks being a ctypes array of pk_gpu_block_weights."""
-    global _ref_block
-    if _ref_block is None:
-        if not have_ref_block():
-            raise RuntimeError(f"reference block harness missing: {REF_BLOCK_SO}")
-        lib = ctypes.CDLL(REF_BLOCK_SO)
+    copy), blocks being a ctypes array of pk_gpu_block_weights.  variant
+    "portable": weight GEMMs from blas.c's portable path (decodes int4 as the
+    format defines); "x86": the reference's x86 build throughout (its AVX2
+    int4 unpack mis-decodes nibbles; used for timing only)."""
+    if variant not in _ref_block:
+        if not have_ref_block(variant):
+            raise RuntimeError(f"reference block harness missing: {REF_BLOCK_SO[variant]}")
+        lib = ctypes.CDLL(REF_BLOCK_SO[variant])
         lib.pkref_conformer_blocks.argtypes = [_p, _i, _p, _p, _i]
         lib.pkref_conformer_blocks.restype = _i
-        _ref_block = lib
+        _ref_block[variant] = lib
     x = _f32(x).copy()
     pe_slice = _f32(pe_slice)
-    rc = _ref_block.pkref_conformer_blocks(ctypes.cast(blocks, _p), n_blocks, _ptr(pe_slice),
-                                           _ptr(x), x.shape[0])
+    rc = _ref_block[variant].pkref_conformer_blocks(ctypes.cast(blocks, _p), n_blocks,
+                                                    _ptr(pe_slice), _ptr(x), x.shape[0])
     if rc:
         raise RuntimeError("pkref_conformer_blocks failed")
     return x
+
+
+def ref_block_threads(variant="portable"):
+    """Threads of the block harness's own reference thread pool."""
+    lib = _ref_block[variant]          # loaded by a previous ref_blocks call
+    lib.pk_pool.restype = _p
+    lib.pk_pool_nthreads.argtypes = [_p]
+    lib.pk_pool_nthreads.restype = _i
+    return lib.pk_pool_nthreads(lib.pk_pool())

@@ -65,34 +65,45 @@ __device__ inline float exp_cr(float x) { return (float)exp((double)x); }
 
 // ---- LayerNorm (tensor_ops.c:150-185) ---------------------------------------
 // 8 rows per wave, 8 lanes per row; lane l of a row holds the partial sums of
-// elements l, l+8, l+16, ... in order, like one AVX2 lane.
+// elements l, l+8, l+16, ... in order, like one AVX2 lane.  Each lane keeps
+// its NPL = D/8 elements in registers: all its loads are issued at once, the
+// two sequential passes (sum, squared deviations) and the output run from
+// registers.  In place (out == x) is safe: a lane writes only what it read.
 
-__global__ __launch_bounds__(256) void layer_norm_rows(const float* __restrict__ x, int ldx,
-                                                       const float* __restrict__ gamma,
-                                                       const float* __restrict__ beta,
-                                                       float* out, int ldo, int rows, int D)
+template <int NPL>
+__global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta,
+                                                      float* out, int ldo, int rows)
 {
+    constexpr int D = 8 * NPL;
     const int lane = threadIdx.x & 63;
-    const int row = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+    const int row = blockIdx.x * 8 + (lane >> 3);
     const int l = lane & 7;
     const bool live = row < rows;
-    const float* xr = x + (size_t)(live ? row : 0) * ldx;
+    const float* xr = x + (size_t)(live ? row : 0) * ldx + l;
+    float v[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) v[i] = xr[8 * i];
     float p = 0.0f;
-    for (int i = l; i < D; i += 8) p = __fadd_rn(p, live ? xr[i] : 0.0f);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) p = __fadd_rn(p, v[i]);
     const float mean = __fdiv_rn(hsum8_lanes(p), (float)D);
     float q = 0.0f;
-    for (int i = l; i < D; i += 8) {
-        const float d = __fsub_rn(live ? xr[i] : 0.0f, mean);
-        q = __fmaf_rn(d, d, q);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        v[i] = __fsub_rn(v[i], mean);
+        q = __fmaf_rn(v[i], v[i], q);
     }
     const float var = __fdiv_rn(hsum8_lanes(q), (float)D);
     // sqrtf and '/' are correctly rounded here (HIP's __fsqrt_rn is the
     // native, approximate square root unless OCML_BASIC_ROUNDED_OPERATIONS).
     const float inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
     if (!live) return;
-    float* o = out + (size_t)row * ldo;
-    for (int i = l; i < D; i += 8)
-        o[i] = __fmaf_rn(__fmul_rn(__fsub_rn(xr[i], mean), inv), gamma[i], beta[i]);
+    float* o = out + (size_t)row * ldo + l;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+        o[8 * i] = __fmaf_rn(__fmul_rn(v[i], inv), gamma[l + 8 * i], beta[l + 8 * i]);
 }
 
 // ---- relative-position attention (encoder.c:300-408) ------------------------
@@ -130,16 +141,31 @@ __device__ inline void score_steps(std::integer_sequence<int, Ts...>, const floa
       acc[1][Ts & 7] = mfma_bcast<Ts>(a[1], b[Ts], acc[1][Ts & 7])), ...);
 }
 
-// Stage 64 rows [r0, r0 + 64) x 128 columns of a row-major source (row
-// stride ld floats) into the LDS tile; rows outside [0, n) read as 0.
-__device__ inline void stage_tile(float* tile, const float* src, int ld, int r0, int n)
+// A 64-row x 128-column tile of a row-major source (row stride ld floats),
+// rows outside [0, n) read as 0: fetched into registers (8 float4 per thread
+// of the 256) one tile ahead of its use, then written to LDS.
+struct TileRegs {
+    float4 v[8];
+};
+
+__device__ inline void load_tile(TileRegs& t, const float* src, int ld, int r0, int n)
 {
-    for (int v = threadIdx.x; v < 64 * (kDh / 4); v += blockDim.x) {
-        const int r = v / (kDh / 4), c4 = v % (kDh / 4);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int idx = threadIdx.x + 256 * q;
+        const int r = idx >> 5, c4 = idx & 31;
         const int gr = r0 + r;
-        float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (gr >= 0 && gr < n) val = *reinterpret_cast<const float4*>(src + (size_t)gr * ld + 4 * c4);
-        *reinterpret_cast<float4*>(tile + r * kTileLd + 4 * c4) = val;
+        t.v[q] = (gr >= 0 && gr < n) ? *reinterpret_cast<const float4*>(src + (size_t)gr * ld + 4 * c4)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+__device__ inline void store_tile(float* tile, const TileRegs& t)
+{
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int idx = threadIdx.x + 256 * q;
+        *reinterpret_cast<float4*>(tile + (idx >> 5) * kTileLd + 4 * (idx & 31)) = t.v[q];
     }
 }
 
@@ -194,10 +220,24 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
     __shared__ float S[kAttnRows * kAttnSld];
     __shared__ float tile[64 * kTileLd];
 
+    // Workgroups are dispatched to the 8 XCDs round-robin; renumber them so
+    // each XCD runs a contiguous run of (row block, head, chunk) tasks, row
+    // block fastest: the row blocks of one head of one chunk then share one
+    // XCD's L2 for their K, P and V tiles.
     const int T = p.T;
-    const int r0 = blockIdx.x * kAttnRows;
-    const int h = blockIdx.y;
-    const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.z] : 0;   // first row of this chunk
+    int rb, h, z;
+    {
+        const int nrb = gridDim.x, nh = gridDim.y, total = nrb * nh * gridDim.z;
+        const int lin = blockIdx.x + nrb * (blockIdx.y + nh * blockIdx.z);
+        const int xcd = lin % 8, local = lin / 8;
+        const int base = total / 8, extra = total % 8;
+        const int task = xcd * base + min(xcd, extra) + local;
+        rb = task % nrb;
+        h = (task / nrb) % nh;
+        z = task / (nrb * nh);
+    }
+    const int r0 = rb * kAttnRows;
+    const int row0 = p.chunk_rows ? p.chunk_rows[z] : 0;   // first row of this chunk
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int D = p.H * kDh;
     const float* qkv = p.qkv + (size_t)row0 * p.ldq;
@@ -224,9 +264,12 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
     }
 
     // AC: S[row][j] = Q_u[row] . K[j]
+    TileRegs pre;
+    load_tile(pre, K, p.ldq, 0, T);
     for (int j0 = 0; j0 < T; j0 += 64) {
-        stage_tile(tile, K, p.ldq, j0, T);
+        store_tile(tile, pre);
         __syncthreads();
+        if (j0 + 64 < T) load_tile(pre, K, p.ldq, j0 + 64, T);
         float o[2][4];
         score_tile(tile, au, o);
         const int j = j0 + lane;
@@ -241,9 +284,12 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
     // BD at the shifted positions: m = T-1-row+j for this block's rows.
     const int r_hi = min(r0 + kAttnRows, T) - 1;
     const int L = 2 * T - 1;
-    for (int m0 = T - 1 - r_hi; m0 <= 2 * T - 2 - r0; m0 += 64) {
-        stage_tile(tile, P, p.ldp, m0, L);
+    const int m_first = T - 1 - r_hi, m_last = 2 * T - 2 - r0;
+    load_tile(pre, P, p.ldp, m_first, L);
+    for (int m0 = m_first; m0 <= m_last; m0 += 64) {
+        store_tile(tile, pre);
         __syncthreads();
+        if (m0 + 64 <= m_last) load_tile(pre, P, p.ldp, m0 + 64, L);
         float o[2][4];
         score_tile(tile, av, o);
         const int m = m0 + lane;
@@ -260,6 +306,7 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
             }
         __syncthreads();
     }
+    load_tile(pre, V, p.ldq, 0, T);      // the first value tile, during the softmax
 
     // Softmax of each row: 8 lanes per row, lane q owns j = q, q+8, ...
     {
@@ -302,8 +349,9 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
     for (int g = 0; g < 2; ++g) acc[g][0] = acc[g][1] = v4f{0.f, 0.f, 0.f, 0.f};
     const int i = lane & 3, t = lane >> 2;
     for (int j0 = 0; j0 < T; j0 += 64) {
-        stage_tile(tile, V, p.ldq, j0, T);
+        store_tile(tile, pre);
         __syncthreads();
+        if (j0 + 64 < T) load_tile(pre, V, p.ldq, j0 + 64, T);
         const int nt = min(64, T - j0);
         for (int jb = 0; jb < nt; jb += 16) {
             float a[2];
@@ -403,9 +451,9 @@ hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const 
                              float* out, int ldo, int rows, int D, hipStream_t s)
 {
     if (rows <= 0) return hipSuccess;
-    const int blocks = (rows + 31) / 32;          // 4 waves x 8 rows
-    hipLaunchKernelGGL(layer_norm_rows, dim3(blocks), dim3(256), 0, s, x, ldx, gamma, beta, out,
-                       ldo, rows, D);
+    if (D != 1024) return hipErrorInvalidValue;   // d_model (PK_D_MODEL)
+    hipLaunchKernelGGL(layer_norm_rows<128>, dim3((rows + 7) / 8), dim3(64), 0, s, x, ldx, gamma,
+                       beta, out, ldo, rows);
     return hipGetLastError();
 }
 

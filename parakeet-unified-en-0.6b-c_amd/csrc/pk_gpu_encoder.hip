@@ -55,6 +55,13 @@ struct Chunk {
     int in_start, in_len, out_start, out_len, left_ov, row;   // row: first row in the batch
 };
 
+// One profiled launch: events on its stream and its algorithmic work.
+struct ProfRec {
+    int stage;
+    hipEvent_t a, b;
+    double flops, bytes;
+};
+
 }  // namespace
 
 struct pk_gpu_encoder {
@@ -70,6 +77,12 @@ struct pk_gpu_encoder {
     int* rows_tab = nullptr;            // device chunk-row table
     size_t rows_cap = 0;
     size_t ws_bytes = 0;
+    // per-stage timing (pk_gpu_encoder_profile)
+    bool prof = false;
+    std::vector<ProfRec> pending;
+    std::vector<hipEvent_t> event_pool;
+    double ms[PK_GPU_N_STAGES] = {}, flops[PK_GPU_N_STAGES] = {}, bytes[PK_GPU_N_STAGES] = {};
+    long long launches[PK_GPU_N_STAGES] = {};
 };
 
 namespace {
@@ -228,8 +241,8 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t prow, size_t n_chunks, hipS
     return PK_GPU_OK;
 }
 
-int gemm(const DevWeight& w, const float* A, int M, float* C, const float* bias, Epilogue epi,
-         hipStream_t s)
+int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float* bias,
+                Epilogue epi, hipStream_t s)
 {
     GemmProblem p{};
     p.kind = w.kind;
@@ -253,6 +266,65 @@ int gemm(const DevWeight& w, const float* A, int M, float* C, const float* bias,
 
 int check(hipError_t r, const char* what) { return r == hipSuccess ? PK_GPU_OK : hip_error(r, what); }
 
+hipEvent_t take_event(pk_gpu_encoder* e)
+{
+    if (!e->event_pool.empty()) {
+        hipEvent_t ev = e->event_pool.back();
+        e->event_pool.pop_back();
+        return ev;
+    }
+    hipEvent_t ev = nullptr;
+    return hipEventCreate(&ev) == hipSuccess ? ev : nullptr;
+}
+
+// Run launch(), bracketed by events on s when profiling is on.
+template <class F>
+int timed(pk_gpu_encoder* e, int stage, double flops, double bytes, hipStream_t s, F&& launch)
+{
+    if (!e->prof) return launch();
+    hipEvent_t a = take_event(e), b = take_event(e);
+    if (!a || !b) return error(PK_GPU_EHIP, "profiling events");
+    hipEventRecord(a, s);
+    int rc = launch();
+    hipEventRecord(b, s);
+    e->pending.push_back({stage, a, b, flops, bytes});
+    return rc;
+}
+
+// Fold finished events into the totals.
+int collect(pk_gpu_encoder* e)
+{
+    for (const ProfRec& r : e->pending) {
+        hipError_t err = hipEventSynchronize(r.b);
+        if (err != hipSuccess) return hip_error(err, "profiling");
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, r.a, r.b);
+        e->ms[r.stage] += ms;
+        e->flops[r.stage] += r.flops;
+        e->bytes[r.stage] += r.bytes;
+        e->launches[r.stage] += 1;
+        e->event_pool.push_back(r.a);
+        e->event_pool.push_back(r.b);
+    }
+    e->pending.clear();
+    return PK_GPU_OK;
+}
+
+double weight_bytes_of(const DevWeight& w)
+{
+    switch (w.kind) {
+    case pkgpu::W_I4: return 0.5 * w.K * w.N + 4.0 * w.K * (w.N / 32);
+    case pkgpu::W_I8: return 1.0 * w.K * w.N + 4.0;
+    default: return 4.0 * w.K * w.N;
+    }
+}
+
+int stage_of(const DevWeight& w)
+{
+    return w.kind == pkgpu::W_I4 ? PK_GPU_STAGE_GEMM_I4
+         : w.kind == pkgpu::W_I8 ? PK_GPU_STAGE_GEMM_I8 : PK_GPU_STAGE_GEMM_F32;
+}
+
 // encoder.c:514-575: output frames [c*C, c*C + C), input with `ov` frames of
 // context each side, clipped to [0, T).  chunk_size <= 0: one sequence.
 std::vector<Chunk> plan_chunks(int T, int C, int ov)
@@ -274,6 +346,26 @@ std::vector<Chunk> plan_chunks(int T, int C, int ov)
     return v;
 }
 
+// A weight GEMM of the block: M rows of A through w, with its epilogue.
+int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
+         const float* bias, Epilogue epi, hipStream_t s)
+{
+    const double flops = 2.0 * M * w.N * w.K;
+    double bytes = weight_bytes_of(w) + 4.0 * M * w.K + 4.0 * M * w.N;
+    if (bias) bytes += 4.0 * w.N;
+    if (epi == pkgpu::EPI_HALF_RESIDUAL || epi == pkgpu::EPI_RESIDUAL) bytes += 4.0 * M * w.N;
+    return timed(e, stage_of(w), flops, bytes, s,
+                 [&] { return gemm_launch(w, A, M, C, bias, epi, s); });
+}
+
+int layer_norm(pk_gpu_encoder* e, const float* x, const float* g, const float* b, float* out, int R,
+               hipStream_t s)
+{
+    return timed(e, PK_GPU_STAGE_LAYER_NORM, 0.0, 8.0 * R * kD + 8.0 * kD, s, [&] {
+        return check(pkgpu::launch_layer_norm(x, kD, g, b, out, kD, R, kD, s), "layer norm");
+    });
+}
+
 // One conformer block (encoder.c:479-491) over all chunks' rows.
 int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
               const std::map<int, std::pair<int, int>>& groups, hipStream_t s)
@@ -282,22 +374,21 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
     float *x = e->x, *ln = e->ln, *h = e->h, *att = e->att;
     auto ffn = [&](const float* g, const float* be, const DevWeight& w1, const float* b1,
                    const DevWeight& w2, const float* b2) {
-        int r = check(pkgpu::launch_layer_norm(x, kD, g, be, ln, kD, R, kD, s), "layer norm");
-        if (!r) r = gemm(w1, ln, R, h, b1, pkgpu::EPI_SWISH, s);                 // encoder.c:193-196
-        if (!r) r = gemm(w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s);          // encoder.c:198-216
+        int r = layer_norm(e, x, g, be, ln, R, s);
+        if (!r) r = gemm(e, w1, ln, R, h, b1, pkgpu::EPI_SWISH, s);            // encoder.c:193-196
+        if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s);     // encoder.c:198-216
         return r;
     };
     // feed-forward 1 (encoder.c:483)
     if ((rc = ffn(b.ln_ff1_w, b.ln_ff1_b, b.ff1_w1, b.ff1_b1, b.ff1_w2, b.ff1_b2))) return rc;
 
     // self-attention (encoder.c:300-424)
-    if ((rc = check(pkgpu::launch_layer_norm(x, kD, b.ln_sa_w, b.ln_sa_b, ln, kD, R, kD, s), "layer norm")))
-        return rc;
-    if ((rc = gemm(b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s))) return rc;
+    if ((rc = layer_norm(e, x, b.ln_sa_w, b.ln_sa_b, ln, R, s))) return rc;
+    if ((rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s))) return rc;
     const float* pe_slice = e->pe + (size_t)(e->pe_center - Tmax + 1) * kD;
-    if ((rc = gemm(b.pos, pe_slice, 2 * Tmax - 1, e->P, nullptr, pkgpu::EPI_NONE, s))) return rc;
+    if ((rc = gemm(e, b.pos, pe_slice, 2 * Tmax - 1, e->P, nullptr, pkgpu::EPI_NONE, s))) return rc;
     for (const auto& g : groups) {
-        const int T = g.first;
+        const int T = g.first, n = g.second.second;
         pkgpu::AttnArgs a{};
         a.qkv = h; a.ldq = 3 * kD;
         a.P = e->P + (size_t)(Tmax - T) * kD; a.ldp = kD;
@@ -305,16 +396,22 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
         a.out = att; a.ldo = kD;
         a.chunk_rows = e->rows_tab + g.second.first;
         a.T = T; a.H = kHeads;
-        if ((rc = check(pkgpu::launch_attention(a, g.second.second, s), "attention"))) return rc;
+        const double flops = 6.0 * T * T * kD * n;     // Q_u K^T, shifted Q_v P^T, scores x V
+        const double bytes = (4.0 * T * 3 * kD + 4.0 * T * kD) * n + 4.0 * (2 * T - 1) * kD;
+        rc = timed(e, PK_GPU_STAGE_ATTENTION, flops, bytes, s, [&] {
+            return check(pkgpu::launch_attention(a, n, s), "attention");
+        });
+        if (rc) return rc;
     }
-    if ((rc = gemm(b.out, att, R, x, b.out_b, pkgpu::EPI_RESIDUAL, s))) return rc;
+    if ((rc = gemm(e, b.out, att, R, x, b.out_b, pkgpu::EPI_RESIDUAL, s))) return rc;
 
     // convolution module (encoder.c:430-476), time-major throughout
-    if ((rc = check(pkgpu::launch_layer_norm(x, kD, b.ln_conv_w, b.ln_conv_b, ln, kD, R, kD, s),
-                    "layer norm")))
-        return rc;
-    if ((rc = gemm(b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s))) return rc;
-    if ((rc = check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu"))) return rc;
+    if ((rc = layer_norm(e, x, b.ln_conv_w, b.ln_conv_b, ln, R, s))) return rc;
+    if ((rc = gemm(e, b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s))) return rc;
+    rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 12.0 * R * kD, s, [&] {
+        return check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu");
+    });
+    if (rc) return rc;
     for (const auto& g : groups) {
         pkgpu::DwArgs d{};
         d.x = att; d.ldx = kD;
@@ -322,14 +419,17 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
         d.out = ln; d.ldo = kD;
         d.chunk_rows = e->rows_tab + g.second.first;
         d.T = g.first; d.C = kD; d.K = kConvK; d.swish = 1;
-        if ((rc = check(pkgpu::launch_depthwise(d, g.second.second, s), "depthwise conv"))) return rc;
+        const double bytes = 8.0 * g.first * kD * g.second.second;
+        rc = timed(e, PK_GPU_STAGE_CONV, 0.0, bytes, s, [&] {
+            return check(pkgpu::launch_depthwise(d, g.second.second, s), "depthwise conv");
+        });
+        if (rc) return rc;
     }
-    if ((rc = gemm(b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s))) return rc;
+    if ((rc = gemm(e, b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s))) return rc;
 
     // feed-forward 2 and the block's output LayerNorm (encoder.c:486-487)
     if ((rc = ffn(b.ln_ff2_w, b.ln_ff2_b, b.ff2_w1, b.ff2_b1, b.ff2_w2, b.ff2_b2))) return rc;
-    return check(pkgpu::launch_layer_norm(x, kD, b.ln_out_w, b.ln_out_b, x, kD, R, kD, s),
-                 "layer norm");
+    return layer_norm(e, x, b.ln_out_w, b.ln_out_b, x, R, s);
 }
 
 int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out, hipStream_t s,
@@ -366,18 +466,26 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
                                    hipMemcpyHostToDevice, s), "chunk table")))
         return rc;
     // every chunk's input rows (encoder.c:552-553)
-    for (const Chunk& c : chunks)
-        if ((rc = check(hipMemcpyAsync(e->x + (size_t)c.row * kD, x + (size_t)c.in_start * kD,
-                                       (size_t)c.in_len * kD * 4, in_kind, s), "input copy")))
-            return rc;
+    for (const Chunk& c : chunks) {
+        const size_t n = (size_t)c.in_len * kD * 4;
+        rc = timed(e, PK_GPU_STAGE_COPY, 0.0, 2.0 * n, s, [&] {
+            return check(hipMemcpyAsync(e->x + (size_t)c.row * kD, x + (size_t)c.in_start * kD, n,
+                                        in_kind, s), "input copy");
+        });
+        if (rc) return rc;
+    }
     for (const DevBlock& b : e->blocks)
         if ((rc = run_block(e, b, R, Tmax, groups, s))) return rc;
     // the centre rows of every chunk (encoder.c:567-569)
-    for (const Chunk& c : chunks)
-        if ((rc = check(hipMemcpyAsync(out + (size_t)c.out_start * kD,
-                                       e->x + (size_t)(c.row + c.left_ov) * kD,
-                                       (size_t)c.out_len * kD * 4, out_kind, s), "output copy")))
-            return rc;
+    for (const Chunk& c : chunks) {
+        const size_t n = (size_t)c.out_len * kD * 4;
+        rc = timed(e, PK_GPU_STAGE_COPY, 0.0, 2.0 * n, s, [&] {
+            return check(hipMemcpyAsync(out + (size_t)c.out_start * kD,
+                                        e->x + (size_t)(c.row + c.left_ov) * kD, n, out_kind, s),
+                         "output copy");
+        });
+        if (rc) return rc;
+    }
     return PK_GPU_OK;
 }
 
@@ -441,7 +549,6 @@ int pk_gpu_encoder_run_dev(pk_gpu_encoder* enc, const float* dx, int T, int chun
     hipStream_t s = nullptr;
     int rc = dev_stream(stream, &s);
     if (rc) return rc;
-    if (!stream && enc) s = enc->stream;
     return run(enc, dx, T, chunk_size, overlap, dout, s, hipMemcpyDeviceToDevice,
                hipMemcpyDeviceToDevice);
 }
@@ -451,10 +558,39 @@ size_t pk_gpu_encoder_bytes(const pk_gpu_encoder* enc)
     return enc ? enc->weight_bytes + enc->ws_bytes : 0;
 }
 
+int pk_gpu_encoder_profile(pk_gpu_encoder* enc, int enable)
+{
+    if (!enc) return error(PK_GPU_EINVAL, "encoder is NULL");
+    int rc = collect(enc);
+    if (rc) return rc;
+    enc->prof = enable != 0;
+    for (int i = 0; i < PK_GPU_N_STAGES; ++i) {
+        enc->ms[i] = enc->flops[i] = enc->bytes[i] = 0.0;
+        enc->launches[i] = 0;
+    }
+    return PK_GPU_OK;
+}
+
+int pk_gpu_encoder_profile_read(pk_gpu_encoder* enc, int stage, double* ms, long long* launches,
+                                double* flops, double* bytes)
+{
+    if (!enc) return error(PK_GPU_EINVAL, "encoder is NULL");
+    if (stage < 0 || stage >= PK_GPU_N_STAGES) return error(PK_GPU_EINVAL, "stage %d", stage);
+    int rc = collect(enc);
+    if (rc) return rc;
+    if (ms) *ms = enc->ms[stage];
+    if (launches) *launches = enc->launches[stage];
+    if (flops) *flops = enc->flops[stage];
+    if (bytes) *bytes = enc->bytes[stage];
+    return PK_GPU_OK;
+}
+
 void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
 {
     if (!enc) return;
     if (enc->stream) (void)hipStreamSynchronize(enc->stream);
+    (void)collect(enc);
+    for (hipEvent_t ev : enc->event_pool) (void)hipEventDestroy(ev);
     free_workspace(enc);
     for (void* p : enc->allocs) (void)hipFree(p);
     if (enc->stream) (void)hipStreamDestroy(enc->stream);
@@ -464,7 +600,7 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
 int pk_gpu_layer_norm_dev(const float* dx, const float* dgamma, const float* dbeta, float* dout,
                           int rows, int D, void* stream)
 {
-    if (rows < 0 || D <= 0 || D % 8) return error(PK_GPU_EINVAL, "rows = %d, D = %d (D %% 8 == 0)", rows, D);
+    if (rows < 0 || D != kD) return error(PK_GPU_EINVAL, "rows = %d, D = %d (D must be %d)", rows, D, kD);
     if (rows && (!dx || !dgamma || !dbeta || !dout)) return error(PK_GPU_EINVAL, "NULL operand");
     hipStream_t s;
     int rc = dev_stream(stream, &s);

@@ -52,6 +52,8 @@ _PROTOS = {
     "pk_gpu_encoder_run_dev": (_i, [_p, _p, _i, _i, _i, _p, _p]),
     "pk_gpu_encoder_bytes": (_sz, [_p]),
     "pk_gpu_encoder_destroy": (None, [_p]),
+    "pk_gpu_encoder_profile": (_i, [_p, _i]),
+    "pk_gpu_encoder_profile_read": (_i, [_p, _i, _p, _p, _p, _p]),
 }
 
 EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL, EPI_RESIDUAL = 0, 1, 2, 3
