@@ -64,11 +64,13 @@ __device__ inline float exp_poly(float x)
 __device__ inline float exp_cr(float x) { return (float)exp((double)x); }
 
 // ---- LayerNorm (tensor_ops.c:150-185) ---------------------------------------
-// 8 rows per wave, 8 lanes per row; lane l of a row holds the partial sums of
-// elements l, l+8, l+16, ... in order, like one AVX2 lane.  Each lane keeps
-// its NPL = D/8 elements in registers: all its loads are issued at once, the
-// two sequential passes (sum, squared deviations) and the output run from
-// registers.  In place (out == x) is safe: a lane writes only what it read.
+// One wave per 8 rows, 8 lanes per row; lane l of a row holds the partial
+// sums of elements l, l+8, l+16, ... in order, like one AVX2 lane.  The rows
+// come in with 16-byte loads into LDS (padded rows: the strided reads of the
+// 64 lanes hit distinct banks but for 2-way overlaps), each lane keeps its
+// NPL = D/8 elements in registers for the two sequential passes (sum,
+// squared deviations), and the outputs leave through LDS as 16-byte stores.
+// In place (out == x) is safe: every row is read before any is written.
 
 template <int NPL>
 __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
@@ -76,15 +78,23 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
                                                       const float* __restrict__ beta,
                                                       float* out, int ldo, int rows)
 {
-    constexpr int D = 8 * NPL;
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 8 + (lane >> 3);
-    const int l = lane & 7;
-    const bool live = row < rows;
-    const float* xr = x + (size_t)(live ? row : 0) * ldx + l;
+    constexpr int D = 8 * NPL, LD = D + 8, V4 = D / 4;
+    __shared__ float buf[8 * LD];
+    const int lane = threadIdx.x;
+    const int row0 = blockIdx.x * 8;
+    const int nr = min(8, rows - row0);
+    for (int idx = lane; idx < 8 * V4; idx += 64) {
+        const int r = idx / V4, c4 = idx % V4;
+        if (r < nr)
+            *reinterpret_cast<float4*>(buf + r * LD + 4 * c4) =
+                *reinterpret_cast<const float4*>(x + (size_t)(row0 + r) * ldx + 4 * c4);
+    }
+    __syncthreads();
+    const int r = lane >> 3, l = lane & 7;
+    float* br = buf + r * LD + l;
     float v[NPL];
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) v[i] = xr[8 * i];
+    for (int i = 0; i < NPL; ++i) v[i] = br[8 * i];
     float p = 0.0f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) p = __fadd_rn(p, v[i]);
@@ -99,11 +109,16 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
     // sqrtf and '/' are correctly rounded here (HIP's __fsqrt_rn is the
     // native, approximate square root unless OCML_BASIC_ROUNDED_OPERATIONS).
     const float inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
-    if (!live) return;
-    float* o = out + (size_t)row * ldo + l;
 #pragma unroll
     for (int i = 0; i < NPL; ++i)
-        o[8 * i] = __fmaf_rn(__fmul_rn(v[i], inv), gamma[l + 8 * i], beta[l + 8 * i]);
+        br[8 * i] = __fmaf_rn(__fmul_rn(v[i], inv), gamma[l + 8 * i], beta[l + 8 * i]);
+    __syncthreads();
+    for (int idx = lane; idx < 8 * V4; idx += 64) {
+        const int rr = idx / V4, c4 = idx % V4;
+        if (rr < nr)
+            *reinterpret_cast<float4*>(out + (size_t)(row0 + rr) * ldo + 4 * c4) =
+                *reinterpret_cast<const float4*>(buf + rr * LD + 4 * c4);
+    }
 }
 
 // ---- relative-position attention (encoder.c:300-408) ------------------------
