@@ -282,7 +282,8 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
 int pk_gpu_num_configs(void);
 int pk_gpu_config_info(int index, int *family, int *mfma, int *cw, int *wgm, int *wgn,
                        int *kt);
-/* Index of the configuration the dispatcher picks for a shape. */
+/* Index of the configuration the dispatcher picks for a shape with int8 or
+ * int4 weights (fp32 weights take configuration 10 where this returns 11). */
 int pk_gpu_pick_config(int M, int N, int K);
 /* Force a configuration for later calls on this thread (-1 = automatic). */
 int pk_gpu_force_config(int index);

@@ -186,6 +186,8 @@ __device__ inline void store_tile(float* tile, const TileRegs& t)
 
 // One 4-row x 64-column tile of NT dot products for two row groups of a wave:
 // a[g][kb] holds rows (4g..4g+3) in broadcast layout for k in [16kb, 16kb+16).
+// The B fragments of the next 16 k-steps are read from LDS while the current
+// 32 MFMAs issue (the scheduling barrier keeps that order).
 __device__ inline void score_tile(const float* tile, const float (&a)[2][8], float (&out)[2][4])
 {
     const int lane = threadIdx.x & 63;
@@ -195,16 +197,22 @@ __device__ inline void score_tile(const float* tile, const float (&a)[2][8], flo
 #pragma unroll
         for (int l = 0; l < 8; ++l) acc[g][l] = v4f{0.f, 0.f, 0.f, 0.f};
     const float* trow = tile + lane * kTileLd;
-#pragma unroll
-    for (int kb = 0; kb < kDh / 16; ++kb) {
-        float b[16];
+    float b[2][16];
+    auto fetch = [&](float (&dst)[16], int kb) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float4 v = *reinterpret_cast<const float4*>(trow + kb * 16 + 4 * q);
-            b[4 * q] = v.x; b[4 * q + 1] = v.y; b[4 * q + 2] = v.z; b[4 * q + 3] = v.w;
+            dst[4 * q] = v.x; dst[4 * q + 1] = v.y; dst[4 * q + 2] = v.z; dst[4 * q + 3] = v.w;
         }
+    };
+    fetch(b[0], 0);
+#pragma unroll
+    for (int kb = 0; kb < kDh / 16; ++kb) {
+        if (kb + 1 < kDh / 16) fetch(b[(kb + 1) & 1], kb + 1);
+        __builtin_amdgcn_sched_barrier(0);
         const float ak[2] = {a[0][kb], a[1][kb]};
-        score_steps(std::make_integer_sequence<int, 16>{}, ak, b, acc);
+        score_steps(std::make_integer_sequence<int, 16>{}, ak, b[kb & 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int g = 0; g < 2; ++g)
@@ -217,7 +225,22 @@ __device__ inline void score_tile(const float* tile, const float (&a)[2][8], flo
         }
 }
 
-// scores x V: acc[g][d] += S[row 4g+i][j0 + t] * V[j0 + t][64d + lane], t < n.
+// scores x V: acc[g][d] += S[row 4g+i][j0 + t] * V[j0 + t][64d + lane].
+// Full blocks of 16 steps read all 32 value fragments first, then issue the
+// 64 MFMAs; a partial last block steps with a bound.
+template <int... Ts>
+__device__ inline void pv_steps_full(std::integer_sequence<int, Ts...>, const float (&a)[2],
+                                     const float* vt, v4f (&acc)[2][2])
+{
+    const int lane = threadIdx.x & 63;
+    float b0[16], b1[16];
+    ((b0[Ts] = vt[Ts * kTileLd + lane], b1[Ts] = vt[Ts * kTileLd + 64 + lane]), ...);
+    ((acc[0][0] = mfma_bcast<Ts>(a[0], b0[Ts], acc[0][0]),
+      acc[1][0] = mfma_bcast<Ts>(a[1], b0[Ts], acc[1][0]),
+      acc[0][1] = mfma_bcast<Ts>(a[0], b1[Ts], acc[0][1]),
+      acc[1][1] = mfma_bcast<Ts>(a[1], b1[Ts], acc[1][1])), ...);
+}
+
 template <int... Ts>
 __device__ inline void pv_steps(std::integer_sequence<int, Ts...>, const float (&a)[2],
                                 const float* vt, int n, v4f (&acc)[2][2])
@@ -264,16 +287,28 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
     float au[2][8], av[2][8];
     {
         const int i = lane & 3, t = lane >> 2;
+        // every load is unconditional (rows past T read row T-1 and are
+        // zeroed after), so they are all in flight together
+        float qv[2][8], bu[8], bv[8];
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-            const int r = r0 + 8 * w + 4 * g + i;
-            const float* q = qkv + (size_t)(r < T ? r : 0) * p.ldq + h * kDh;
+            const int r = min(r0 + 8 * w + 4 * g + i, T - 1);
+            const float* q = qkv + (size_t)r * p.ldq + h * kDh;
+#pragma unroll
+            for (int kb = 0; kb < 8; ++kb) qv[g][kb] = q[16 * kb + t];
+        }
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            bu[kb] = p.pos_bias_u[h * kDh + 16 * kb + t];
+            bv[kb] = p.pos_bias_v[h * kDh + 16 * kb + t];
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const bool live = r0 + 8 * w + 4 * g + i < T;
 #pragma unroll
             for (int kb = 0; kb < 8; ++kb) {
-                const int k = 16 * kb + t;
-                const float qv = r < T ? q[k] : 0.0f;
-                au[g][kb] = r < T ? __fadd_rn(qv, p.pos_bias_u[h * kDh + k]) : 0.0f;
-                av[g][kb] = r < T ? __fadd_rn(qv, p.pos_bias_v[h * kDh + k]) : 0.0f;
+                au[g][kb] = live ? __fadd_rn(qv[g][kb], bu[kb]) : 0.0f;
+                av[g][kb] = live ? __fadd_rn(qv[g][kb], bv[kb]) : 0.0f;
             }
         }
     }
@@ -307,18 +342,26 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
         if (m0 + 64 <= m_last) load_tile(pre, P, p.ldp, m0 + 64, L);
         float o[2][4];
         score_tile(tile, av, o);
+        // every (row, j) takes exactly one shifted BD value: read the eight
+        // scores first, then write them back combined
         const int m = m0 + lane;
+        float sc[2][4];
+        int at[2][4];
 #pragma unroll
         for (int g = 0; g < 2; ++g)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int rl = 8 * w + 4 * g + i, r = r0 + rl;
                 const int j = m - (T - 1 - r);
-                if (r < T && j >= 0 && j < T) {
-                    float* s = &S[rl * kAttnSld + j];
-                    *s = __fmul_rn(__fadd_rn(*s, o[g][i]), kScoreScale);
-                }
+                const bool ok = r < T && j >= 0 && j < T;
+                at[g][i] = ok ? rl * kAttnSld + j : -1;
+                sc[g][i] = S[ok ? rl * kAttnSld + j : 0];
             }
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (at[g][i] >= 0) S[at[g][i]] = __fmul_rn(__fadd_rn(sc[g][i], o[g][i]), kScoreScale);
         __syncthreads();
     }
     load_tile(pre, V, p.ldq, 0, T);      // the first value tile, during the softmax
@@ -329,12 +372,14 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
         float* s = S + rl * kAttnSld;
         if (r < T) {
             float mx = s[0];
+#pragma unroll 8
             for (int j = q; j < T; j += 8) mx = fmaxf(mx, s[j]);
             mx = fmaxf(mx, __shfl_xor(mx, 4));
             mx = fmaxf(mx, __shfl_xor(mx, 2));
             mx = fmaxf(mx, __shfl_xor(mx, 1));
             const int T8 = T & ~7;
             float part = 0.0f;
+#pragma unroll 8
             for (int j = q; j < T8; j += 8) {
                 const float e = exp_poly(__fsub_rn(s[j], mx));
                 s[j] = e;
@@ -351,6 +396,7 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
                 sum = __shfl(sum, lane & ~7);
             }
             const float inv = __fdiv_rn(1.0f, sum);
+#pragma unroll 8
             for (int j = q; j < T; j += 8) s[j] = __fmul_rn(s[j], inv);
         } else {
             for (int j = q; j < T; j += 8) s[j] = 0.0f;
@@ -375,7 +421,10 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
                 const int jj = j0 + jb + t;
                 a[g] = jj < T ? S[(8 * w + 4 * g + i) * kAttnSld + jj] : 0.0f;
             }
-            pv_steps(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, nt - jb, acc);
+            if (nt - jb >= 16)
+                pv_steps_full(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, acc);
+            else
+                pv_steps(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, nt - jb, acc);
         }
         __syncthreads();
     }

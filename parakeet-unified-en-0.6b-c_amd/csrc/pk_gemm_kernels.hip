@@ -69,14 +69,16 @@ TileConfig config_at(int i) { return kConfigs[i]; }
 //   M*N < 1.6M          config 14 (S 4x4, 3 chains)   FF up M=375: 35.1
 //   M*N < 3M            config 18 (S 16x16)           FF up M=416/500: 41
 //   otherwise           config 11 (X 32x32)           M=3312: 183-275
-static int choose_index(int M, int N, int K)
+//                       fp32 weights: config 10 (X 16x16, 2 chains, 2x2 waves):
+//                       pointwise convs M=3312: 143.7 vs 163.1, 71.9 vs 79.2
+static int choose_index(int M, int N, int K, WeightKind kind = W_I8)
 {
     const double outputs = (double)M * (double)N;
     if (outputs < 200e3) return 12;
     if (outputs < 1.0e6) return K >= 2048 ? 17 : 13;
     if (outputs < 1.6e6) return 14;
     if (outputs < 3.0e6) return 18;
-    return 11;
+    return kind == W_F32 ? 10 : 11;
 }
 
 TileConfig choose_config(int M, int N, int K) { return kConfigs[choose_index(M, N, K)]; }
@@ -140,7 +142,7 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
     a.N = n_main;
 
     const int cfg = (cfg_index >= 0 && cfg_index < kNumConfigs) ? cfg_index
-                                                                : choose_index(p.M, n_main, p.K);
+                                                                : choose_index(p.M, n_main, p.K, p.kind);
     hipError_t err = hipSuccess;
     if (n_main > 0) {
         switch (p.kind) {
