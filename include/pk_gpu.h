@@ -245,7 +245,9 @@ int pk_gpu_encoder_run(pk_gpu_encoder *enc, const float *x, int T, int chunk_siz
                        int overlap, float *out);
 /* The same with device pointers, enqueued on `stream` (NULL = HIP's null
  * stream, as for every *_dev entry point); returns without synchronising.
- * Runs of one encoder share its workspace: do not overlap them. */
+ * Runs of one encoder share its workspace: do not overlap them.  The blocks'
+ * launches are captured in a HIP graph on the first run of each (T,
+ * chunk_size, overlap) and replayed afterwards (not while profiling). */
 int pk_gpu_encoder_run_dev(pk_gpu_encoder *enc, const float *dx, int T, int chunk_size,
                            int overlap, float *dout, void *stream);
 /* Device bytes held by the encoder (weights + workspace). */

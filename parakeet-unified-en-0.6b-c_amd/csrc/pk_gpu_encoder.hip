@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <map>
+#include <tuple>
 #include <vector>
 
 using pkgpu::Epilogue;
@@ -83,6 +84,10 @@ struct pk_gpu_encoder {
     std::vector<hipEvent_t> event_pool;
     double ms[PK_GPU_N_STAGES] = {}, flops[PK_GPU_N_STAGES] = {}, bytes[PK_GPU_N_STAGES] = {};
     long long launches[PK_GPU_N_STAGES] = {};
+    // the 24 blocks' launches captured once per (T, chunk, overlap) and
+    // replayed; their device pointers are the workspace's, so a workspace
+    // change drops them
+    std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
 };
 
 namespace {
@@ -201,8 +206,15 @@ int upload_block(pk_gpu_encoder* e, const pk_gpu_block_weights& b, DevBlock* d)
     return rc;
 }
 
+void drop_graphs(pk_gpu_encoder* e)
+{
+    for (auto& g : e->graphs) (void)hipGraphExecDestroy(g.second);
+    e->graphs.clear();
+}
+
 void free_workspace(pk_gpu_encoder* e)
 {
+    drop_graphs(e);
     for (float* p : {e->x, e->ln, e->h, e->att, e->P})
         if (p) (void)hipFree(p);
     if (e->rows_tab) (void)hipFree(e->rows_tab);
@@ -474,8 +486,31 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
         });
         if (rc) return rc;
     }
-    for (const DevBlock& b : e->blocks)
-        if ((rc = run_block(e, b, R, Tmax, groups, s))) return rc;
+    if (e->prof) {            // eager, with an event pair around every launch
+        for (const DevBlock& b : e->blocks)
+            if ((rc = run_block(e, b, R, Tmax, groups, s))) return rc;
+    } else {
+        // One graph per chunking of the input: captured on the encoder's own
+        // stream (the null stream cannot capture), launched on `s`.
+        const auto key = std::make_tuple(T, chunk, ov);
+        auto it = e->graphs.find(key);
+        if (it == e->graphs.end()) {
+            if ((rc = check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal),
+                            "graph capture")))
+                return rc;
+            for (const DevBlock& b : e->blocks)
+                if ((rc = run_block(e, b, R, Tmax, groups, e->stream))) break;
+            hipGraph_t g = nullptr;
+            const hipError_t end = hipStreamEndCapture(e->stream, &g);
+            if (!rc && end != hipSuccess) rc = hip_error(end, "graph capture");
+            hipGraphExec_t ex = nullptr;
+            if (!rc) rc = check(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "graph instantiate");
+            if (g) (void)hipGraphDestroy(g);
+            if (rc) return rc;
+            it = e->graphs.emplace(key, ex).first;
+        }
+        if ((rc = check(hipGraphLaunch(it->second, s), "graph launch"))) return rc;
+    }
     // the centre rows of every chunk (encoder.c:567-569)
     for (const Chunk& c : chunks) {
         const size_t n = (size_t)c.out_len * kD * 4;

@@ -229,6 +229,26 @@ def test_encoder_dev_entry_and_in_place(dev, enc2):
     assert bits_equal(xi, want)
 
 
+def test_encoder_graph_replays_match_eager(dev, enc2):
+    """Without profiling the blocks run as a HIP graph captured on the first
+    run of a chunking and replayed after; with profiling they launch one by
+    one.  Replays on alternating inputs, with eager runs in between, must each
+    equal the eager result bit for bit."""
+    T = 900
+    xs = [rows(T, 1024), rows(T, 1024)]
+    pk.call("pk_gpu_encoder_profile", enc2.h, 1)
+    want = [enc2.run(x, chunk=400) for x in xs]
+    pk.call("pk_gpu_encoder_profile", enc2.h, 0)
+    for rep in range(4):
+        got = enc2.run(xs[rep % 2], chunk=400)
+        assert bits_equal(got, want[rep % 2]), f"replay {rep}"
+        pk.call("pk_gpu_encoder_profile", enc2.h, 1)
+        assert bits_equal(enc2.run(xs[(rep + 1) % 2], chunk=400), want[(rep + 1) % 2])
+        pk.call("pk_gpu_encoder_profile", enc2.h, 0)
+    ms = ctypes.c_double()
+    pk.call("pk_gpu_encoder_profile_read", enc2.h, 0, ctypes.byref(ms), None, None, None)
+
+
 def test_encoder_rejects_oversized_sequence(dev, enc2):
     x = np.zeros((600, 1024), np.float32)
     out = np.empty_like(x)
