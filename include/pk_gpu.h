@@ -117,6 +117,9 @@ int pk_gpu_sgemm_dev(int M, int N, int K, float alpha,
  *   PK_GPU_EPI_RESIDUAL:      C[i][j] = C[i][j] + v   (beta must be 0; the
  *                             attention and convolution residuals,
  *                             encoder.c:410-424, 473-475)
+ *   PK_GPU_EPI_RELU:          C[i][j] = v > 0 ? v : +0   (pk_relu after the
+ *                             pre-encode's pointwise convolutions,
+ *                             encoder.c:132-150)
  * Bias and residual are exact IEEE operations, so results equal the
  * reference's GEMM + pk_bias_add (+ x += 0.5 * out) bit for bit; Swish is
  * the device swish (within a few ulp of the reference's, see
@@ -127,6 +130,7 @@ int pk_gpu_sgemm_dev(int M, int N, int K, float alpha,
 #define PK_GPU_EPI_SWISH 1
 #define PK_GPU_EPI_HALF_RESIDUAL 2
 #define PK_GPU_EPI_RESIDUAL 3
+#define PK_GPU_EPI_RELU 4
 int pk_gpu_gemm_i8_ex_dev(int M, int N, int K, float alpha, const float *dA, int lda,
                           const int8_t *dB, float B_scale, int ldb, float beta, float *dC,
                           int ldc, const float *dbias, int epilogue, void *stream);
@@ -250,6 +254,36 @@ int pk_gpu_encoder_run(pk_gpu_encoder *enc, const float *x, int T, int chunk_siz
  * chunk_size, overlap) and replayed afterwards (not while profiling). */
 int pk_gpu_encoder_run_dev(pk_gpu_encoder *enc, const float *dx, int T, int chunk_size,
                            int overlap, float *dout, void *stream);
+/* Pre-encode parameters (PreEncodeWeights, parakeet.h), host pointers:
+ * conv0 [256][1][3][3], conv2 depthwise [256][1][3][3], conv3 pointwise
+ * [256][256], conv5 depthwise [256][1][3][3], conv6 pointwise [256][256],
+ * each with a [256] bias; out_w [4096][1024] (int8 or fp32) + out_b [1024]. */
+typedef struct {
+    const float *conv0_w, *conv0_b;
+    const float *conv2_w, *conv2_b;
+    const float *conv3_w, *conv3_b;
+    const float *conv5_w, *conv5_b;
+    const float *conv6_w, *conv6_b;
+    pk_gpu_weight out_w;
+    const float *out_b;
+} pk_gpu_pre_encode_weights;
+
+/* Upload the pre-encode once (replacing an earlier one). */
+int pk_gpu_encoder_set_pre_encode(pk_gpu_encoder *enc, const pk_gpu_pre_encode_weights *w);
+/* Encoder frames T' for n_frames mel frames (three stride-2 stages). */
+int pk_gpu_encoder_frames(int n_frames);
+/* pre_encode_and_scale (encoder.c:103-174, 578-592) on the device: mel
+ * [128][n_frames] (as pk_encoder takes it) to x [T'][1024], bit-identical to
+ * the reference.  Enqueued on `stream`. */
+int pk_gpu_encoder_pre_encode_dev(pk_gpu_encoder *enc, const float *dmel, int n_frames,
+                                  float *dx, void *stream);
+/* pk_encoder (encoder.c:595-624) from mel to encoder output: host mel
+ * [128][n_frames] in, out [T'][1024] (pk_gpu_encoder_frames(n_frames) rows);
+ * chunk_size / overlap as for pk_gpu_encoder_run.  Returns when out is
+ * written. */
+int pk_gpu_encoder_run_mel(pk_gpu_encoder *enc, const float *mel, int n_frames, int chunk_size,
+                           int overlap, float *out);
+
 /* Device bytes held by the encoder (weights + workspace). */
 size_t pk_gpu_encoder_bytes(const pk_gpu_encoder *enc);
 

@@ -328,3 +328,26 @@ def ref_block_threads(variant="portable"):
     lib.pk_pool_nthreads.argtypes = [_p]
     lib.pk_pool_nthreads.restype = _i
     return lib.pk_pool_nthreads(lib.pk_pool())
+
+
+def ref_pre_encode(w, mel, variant="portable"):
+    """The reference's pre_encode_and_scale on mel [128][n_frames] with the
+    ctypes pk_gpu_pre_encode_weights w; returns x [T'][1024]."""
+    if variant not in _ref_block:
+        if not have_ref_block(variant):
+            raise RuntimeError(f"reference block harness missing: {REF_BLOCK_SO[variant]}")
+        lib = ctypes.CDLL(REF_BLOCK_SO[variant])
+        lib.pkref_conformer_blocks.argtypes = [_p, _i, _p, _p, _i]
+        lib.pkref_conformer_blocks.restype = _i
+        _ref_block[variant] = lib
+    lib = _ref_block[variant]
+    lib.pkref_pre_encode.argtypes = [_p, _p, _i, _p]
+    lib.pkref_pre_encode.restype = _i
+    mel = _f32(mel)
+    n = mel.shape[1]
+    tp = (((n - 1) // 2 + 1 - 1) // 2 + 1 - 1) // 2 + 1
+    out = np.empty((tp, 1024), np.float32)
+    got = lib.pkref_pre_encode(ctypes.byref(w), _ptr(mel), n, _ptr(out))
+    if got != tp:
+        raise RuntimeError(f"pkref_pre_encode returned {got}, expected {tp}")
+    return out

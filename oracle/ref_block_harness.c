@@ -66,3 +66,25 @@ int pkref_conformer_blocks(const pk_gpu_block_weights *w, int n_blocks, const fl
     free(ws.buf);
     return 0;
 }
+
+/* pre_encode_and_scale (encoder.c:578-592): mel [128][n_frames] -> out
+ * [T'][1024]; returns T' (or -1). */
+int pkref_pre_encode(const pk_gpu_pre_encode_weights *w, const float *mel, int n_frames, float *out)
+{
+    PkModel *m = (PkModel *)calloc(1, sizeof *m);
+    if (!m) return -1;
+    PreEncodeWeights *p = &m->enc.pre_encode;
+    p->conv0_w = w->conv0_w;  p->conv0_b = w->conv0_b;
+    p->conv2_w = w->conv2_w;  p->conv2_b = w->conv2_b;
+    p->conv3_w = w->conv3_w;  p->conv3_b = w->conv3_b;
+    p->conv5_w = w->conv5_w;  p->conv5_b = w->conv5_b;
+    p->conv6_w = w->conv6_w;  p->conv6_b = w->conv6_b;
+    p->out_w = to_weight(w->out_w);
+    p->out_b = w->out_b;
+    float *x = NULL;
+    int Tp = pre_encode_and_scale(m, mel, n_frames, &x);
+    memcpy(out, x, (size_t)Tp * PK_D_MODEL * sizeof(float));
+    free(x);
+    free(m);
+    return Tp;
+}

@@ -493,6 +493,88 @@ __global__ void depthwise_swish(DwArgs p)
     p.out[(size_t)(row0 + t) * p.ldo + c] = p.swish ? tiles::swish_f(val) : val;
 }
 
+// ---- pre-encode subsampling (encoder.c:103-174) ------------------------------
+// Activations channel-last, [H][W][256].  pk_conv2d (tensor_ops.c:436-475)
+// computes every output as val = bias, then val = fma(x, w, val) over its
+// in-range taps (ic, kh, kw ascending), which the kernels below repeat; the
+// 1x1 convolutions are chain GEMMs started from the bias (fill_rows, beta 1).
+
+constexpr int kSub = 256;          // PK_SUB_CHANNELS
+
+// conv.0: 1 -> 256 channels, 3x3, stride 2, pad 1, over the image whose row
+// t is mel frame t (mel [n_mels][T], encoder.c:110-120), then ReLU.
+__global__ void conv0_relu(const float* __restrict__ mel, int T, int n_mels,
+                           const float* __restrict__ w, const float* __restrict__ b, float* out,
+                           int H1, int W1)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)H1 * W1 * kSub) return;
+    const int c = (int)(idx % kSub);
+    const int pos = (int)(idx / kSub), ow = pos % W1, oh = pos / W1;
+    float v = b[c];
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+        const int ih = 2 * oh - 1 + kh;
+#pragma unroll
+        for (int kw = 0; kw < 3; ++kw) {
+            const int iw = 2 * ow - 1 + kw;
+            if (ih >= 0 && ih < T && iw >= 0 && iw < n_mels)
+                v = __fmaf_rn(mel[(size_t)iw * T + ih], w[c * 9 + kh * 3 + kw], v);
+        }
+    }
+    out[idx] = v > 0.0f ? v : 0.0f;
+}
+
+// Depthwise 3x3, stride 2, pad 1 (conv.2 and conv.5, groups = 256).
+__global__ void dwconv3x3s2(const float* __restrict__ in, int H, int W,
+                            const float* __restrict__ w, const float* __restrict__ b, float* out,
+                            int Ho, int Wo)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)Ho * Wo * kSub) return;
+    const int c = (int)(idx % kSub);
+    const int pos = (int)(idx / kSub), ow = pos % Wo, oh = pos / Wo;
+    float v = b[c];
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+        const int ih = 2 * oh - 1 + kh;
+#pragma unroll
+        for (int kw = 0; kw < 3; ++kw) {
+            const int iw = 2 * ow - 1 + kw;
+            if (ih >= 0 && ih < H && iw >= 0 && iw < W)
+                v = __fmaf_rn(in[((size_t)ih * W + iw) * kSub + c], w[c * 9 + kh * 3 + kw], v);
+        }
+    }
+    out[idx] = v;
+}
+
+// rows x n of C set to bias[0..n): the starting value of a chain that the
+// reference begins at the bias.
+__global__ void fill_rows(float* C, const float* __restrict__ bias, long long rows, int n)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * n) return;
+    C[idx] = bias[idx % n];
+}
+
+// [H][W][256] -> [H][256*W], element (c, w) of row h at c*W + w
+// (encoder.c:152-158).
+__global__ void flatten_rows(const float* __restrict__ in, float* out, int H, int W)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int F = kSub * W;
+    if (idx >= (long long)H * F) return;
+    const int h = (int)(idx / F), r = (int)(idx % F), c = r / W, w = r % W;
+    out[idx] = in[((size_t)h * W + w) * kSub + c];
+}
+
+// x *= s in place (s = sqrtf(d_model) = 32, encoder.c:578-592: exact).
+__global__ void scale_inplace(float* x, long long n, float s)
+{
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < n) x[idx] = __fmul_rn(x[idx], s);
+}
+
 // ---- transpose (weights at upload: [R][C] -> [C][R]) --------------------------
 __global__ void transpose(const float* __restrict__ in, float* out, int R, int C)
 {
@@ -552,6 +634,48 @@ hipError_t launch_transpose(const float* in, float* out, int R, int C, hipStream
 {
     if (R <= 0 || C <= 0) return hipSuccess;
     hipLaunchKernelGGL(transpose, dim3((C + 31) / 32, (R + 31) / 32), dim3(32, 8), 0, s, in, out, R, C);
+    return hipGetLastError();
+}
+
+static unsigned blocks_of(long long n) { return (unsigned)((n + 255) / 256); }
+
+hipError_t launch_conv0_relu(const float* mel, int T, int n_mels, const float* w, const float* b,
+                             float* out, int H1, int W1, hipStream_t s)
+{
+    const long long n = (long long)H1 * W1 * kSub;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(conv0_relu, dim3(blocks_of(n)), dim3(256), 0, s, mel, T, n_mels, w, b, out, H1, W1);
+    return hipGetLastError();
+}
+
+hipError_t launch_dwconv3x3s2(const float* in, int H, int W, const float* w, const float* b,
+                              float* out, int Ho, int Wo, hipStream_t s)
+{
+    const long long n = (long long)Ho * Wo * kSub;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(dwconv3x3s2, dim3(blocks_of(n)), dim3(256), 0, s, in, H, W, w, b, out, Ho, Wo);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_rows(float* C, const float* bias, long long rows, int n, hipStream_t s)
+{
+    if (rows * n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_rows, dim3(blocks_of(rows * n)), dim3(256), 0, s, C, bias, rows, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_flatten_rows(const float* in, float* out, int H, int W, hipStream_t s)
+{
+    const long long n = (long long)H * W * kSub;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(flatten_rows, dim3(blocks_of(n)), dim3(256), 0, s, in, out, H, W);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale(float* x, long long n, float sc, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(scale_inplace, dim3(blocks_of(n)), dim3(256), 0, s, x, n, sc);
     return hipGetLastError();
 }
 

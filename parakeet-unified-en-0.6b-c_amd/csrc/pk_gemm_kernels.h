@@ -17,8 +17,9 @@ enum WeightKind { W_F32 = 0, W_I8 = 1, W_I4 = 2 };
 //   EPI_HALF_RESIDUAL: C[i][j] = fl(C[i][j] + 0.5 * v)     (macaron residual)
 //   EPI_RESIDUAL:      C[i][j] = fl(C[i][j] + v)           (attention / conv residual,
 //                                                           encoder.c:410-424, 473-475)
+//   EPI_RELU:          C[i][j] = v > 0 ? v : +0               (pk_relu, tensor_ops.c:401-415)
 //   EPI_NONE:          C[i][j] = v
-enum Epilogue { EPI_NONE = 0, EPI_SWISH = 1, EPI_HALF_RESIDUAL = 2, EPI_RESIDUAL = 3 };
+enum Epilogue { EPI_NONE = 0, EPI_SWISH = 1, EPI_HALF_RESIDUAL = 2, EPI_RESIDUAL = 3, EPI_RELU = 4 };
 
 // One weight GEMM, C <- beta*C + alpha*A*W, row-major, NoTrans/NoTrans,
 // with W given in one of the on-disk formats (weights.c:240-266):

@@ -436,6 +436,8 @@ __device__ inline float epilogue(const KArgs& p, float v, int row, int col)
     if (p.epi == EPI_SWISH) return swish_f(v);
     if (p.epi == EPI_HALF_RESIDUAL) return __fmaf_rn(v, 0.5f, p.C[(size_t)row * p.ldc + col]);
     if (p.epi == EPI_RESIDUAL) return __fadd_rn(p.C[(size_t)row * p.ldc + col], v);
+    // _mm256_max_ps(v, 0) as pk_relu compiles: v unless v > 0 is false, then +0
+    if (p.epi == EPI_RELU) return v > 0.0f ? v : 0.0f;
     return v;
 }
 

@@ -56,6 +56,19 @@ struct Chunk {
     int in_start, in_len, out_start, out_len, left_ov, row;   // row: first row in the batch
 };
 
+constexpr int kMels = 128;        // PK_N_MELS
+constexpr int kSub = 256;         // PK_SUB_CHANNELS
+
+struct DevPreEncode {
+    bool set = false;
+    const float *w0, *b0, *w2, *b2, *b3, *w5, *b5, *b6, *out_b;
+    DevWeight w3t, w6t, out;
+    std::vector<void*> allocs;
+};
+
+// Output size of a 3x3 stride-2 pad-1 stage (encoder.c:116, 125, 137).
+inline int half_up(int n) { return (n + 2 - 3) / 2 + 1; }
+
 // One profiled launch: events on its stream and its algorithmic work.
 struct ProfRec {
     int stage;
@@ -88,6 +101,10 @@ struct pk_gpu_encoder {
     // replayed; their device pointers are the workspace's, so a workspace
     // change drops them
     std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
+    // pre-encode: weights and two ping-pong buffers, grown on demand
+    DevPreEncode pre;
+    float *pre_a = nullptr, *pre_b = nullptr, *pre_x = nullptr;
+    size_t pre_a_n = 0, pre_b_n = 0, pre_x_n = 0;
 };
 
 namespace {
@@ -524,6 +541,94 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
     return PK_GPU_OK;
 }
 
+// Upload into the pre-encode's own allocations (freed when it is replaced).
+int pre_upload(pk_gpu_encoder* e, const void* host, size_t bytes, const char* what, const void** out)
+{
+    if (!host) return error(PK_GPU_EINVAL, "%s is NULL", what);
+    void* d = nullptr;
+    if (hipMalloc(&d, bytes) != hipSuccess) return error(PK_GPU_ENOMEM, "%s: device allocation", what);
+    e->pre.allocs.push_back(d);
+    hipError_t r = hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, e->stream);
+    if (r != hipSuccess) return hip_error(r, what);
+    *out = d;
+    return PK_GPU_OK;
+}
+
+void free_pre(pk_gpu_encoder* e)
+{
+    for (void* p : e->pre.allocs) (void)hipFree(p);
+    e->pre = DevPreEncode{};
+    for (float* p : {e->pre_a, e->pre_b, e->pre_x})
+        if (p) (void)hipFree(p);
+    e->pre_a = e->pre_b = e->pre_x = nullptr;
+    e->pre_a_n = e->pre_b_n = e->pre_x_n = 0;
+}
+
+int grow(float** buf, size_t* cap, size_t n, hipStream_t s)
+{
+    if (n <= *cap) return PK_GPU_OK;
+    hipError_t r = hipStreamSynchronize(s);
+    if (r != hipSuccess) return hip_error(r, "pre-encode stream");
+    if (*buf) (void)hipFree(*buf);
+    *buf = nullptr;
+    *cap = 0;
+    if (hipMalloc(reinterpret_cast<void**>(buf), n * sizeof(float)) != hipSuccess)
+        return error(PK_GPU_ENOMEM, "pre-encode workspace of %zu floats", n);
+    *cap = n;
+    return PK_GPU_OK;
+}
+
+// pre_encode_and_scale (encoder.c:103-174, 578-592): mel [128][T] to
+// x [T'][1024].  Channel-last throughout; the 1x1 convolutions and the output
+// linear are chain GEMMs (the convolutions started from their bias).
+int pre_encode(pk_gpu_encoder* e, const float* mel, int T, float* x, hipStream_t s)
+{
+    const DevPreEncode& w = e->pre;
+    const int H1 = half_up(T), W1 = half_up(kMels);
+    const int H2 = half_up(H1), W2 = half_up(W1);
+    const int H3 = half_up(H2), W3 = half_up(W2);
+    int rc = grow(&e->pre_a, &e->pre_a_n, (size_t)H1 * W1 * kSub, s);
+    if (!rc) rc = grow(&e->pre_b, &e->pre_b_n, (size_t)H2 * W2 * kSub, s);
+    if (rc) return rc;
+    float *A = e->pre_a, *B = e->pre_b;
+    // conv.0 + ReLU -> A [H1][W1][256]
+    if ((rc = check(pkgpu::launch_conv0_relu(mel, T, kMels, w.w0, w.b0, A, H1, W1, s), "conv.0"))) return rc;
+    // conv.2 (depthwise) -> B; conv.3 (pointwise) + ReLU -> A
+    if ((rc = check(pkgpu::launch_dwconv3x3s2(A, H1, W1, w.w2, w.b2, B, H2, W2, s), "conv.2"))) return rc;
+    if ((rc = check(pkgpu::launch_fill_rows(A, w.b3, (long long)H2 * W2, kSub, s), "conv.3 bias"))) return rc;
+    // Rows are independent, so long inputs run in slabs whose operands stay
+    // under the chain kernels' 2 GiB extent.
+    auto pointwise = [&](const DevWeight& wt, const float* in, float* out, int rows) {
+        const int slab = (1 << 28) / kSub;          // 1 GiB of A per launch
+        for (int r0 = 0; r0 < rows; r0 += slab) {
+            GemmProblem p{};
+            p.kind = pkgpu::W_F32;
+            p.M = std::min(slab, rows - r0); p.N = kSub; p.K = kSub;
+            p.alpha = 1.0f; p.beta = 1.0f;
+            p.A = in + (size_t)r0 * kSub; p.lda = kSub;
+            p.B = wt.data; p.ldb = kSub;
+            p.C = out + (size_t)r0 * kSub; p.ldc = kSub;
+            p.epi = pkgpu::EPI_RELU;
+            const int r = pkgpu::rt::gemm(p, s);
+            if (r) return r;
+        }
+        return (int)PK_GPU_OK;
+    };
+    if ((rc = pointwise(w.w3t, B, A, H2 * W2))) return rc;
+    // conv.5 (depthwise) -> B; conv.6 (pointwise) + ReLU -> A
+    if ((rc = check(pkgpu::launch_dwconv3x3s2(A, H2, W2, w.w5, w.b5, B, H3, W3, s), "conv.5"))) return rc;
+    if ((rc = check(pkgpu::launch_fill_rows(A, w.b6, (long long)H3 * W3, kSub, s), "conv.6 bias"))) return rc;
+    if ((rc = pointwise(w.w6t, B, A, H3 * W3))) return rc;
+    // flatten -> B [T'][256*W3]; out linear + bias -> x; times sqrt(1024)
+    if ((rc = check(pkgpu::launch_flatten_rows(A, B, H3, W3, s), "flatten"))) return rc;
+    const int slab = (1 << 28) / (kSub * W3);        // 1 GiB of A per launch
+    for (int r0 = 0; r0 < H3; r0 += slab)
+        if ((rc = gemm_launch(w.out, B + (size_t)r0 * kSub * W3, std::min(slab, H3 - r0),
+                              x + (size_t)r0 * kD, w.out_b, pkgpu::EPI_NONE, s)))
+            return rc;
+    return check(pkgpu::launch_scale(x, (long long)H3 * kD, 32.0f, s), "scale");
+}
+
 int dev_stream(void* stream, hipStream_t* s)
 {
     hipStream_t own = nullptr;
@@ -627,9 +732,123 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
     (void)collect(enc);
     for (hipEvent_t ev : enc->event_pool) (void)hipEventDestroy(ev);
     free_workspace(enc);
+    free_pre(enc);
     for (void* p : enc->allocs) (void)hipFree(p);
     if (enc->stream) (void)hipStreamDestroy(enc->stream);
     delete enc;
+}
+
+int pk_gpu_encoder_set_pre_encode(pk_gpu_encoder* enc, const pk_gpu_pre_encode_weights* w)
+{
+    if (!enc || !w) return error(PK_GPU_EINVAL, "encoder or weights is NULL");
+    int rc = pkgpu::rt::bind(nullptr);
+    if (rc) return rc;
+    (void)hipStreamSynchronize(enc->stream);
+    free_pre(enc);
+    DevPreEncode& d = enc->pre;
+    const void* v = nullptr;
+    auto up = [&](const float* host, size_t n, const char* what, const float** out) {
+        int r = pre_upload(enc, host, n * sizeof(float), what, &v);
+        *out = static_cast<const float*>(v);
+        return r;
+    };
+    if (!rc) rc = up(w->conv0_w, kSub * 9, "conv0_w", &d.w0);
+    if (!rc) rc = up(w->conv0_b, kSub, "conv0_b", &d.b0);
+    if (!rc) rc = up(w->conv2_w, kSub * 9, "conv2_w", &d.w2);
+    if (!rc) rc = up(w->conv2_b, kSub, "conv2_b", &d.b2);
+    if (!rc) rc = up(w->conv3_b, kSub, "conv3_b", &d.b3);
+    if (!rc) rc = up(w->conv5_w, kSub * 9, "conv5_w", &d.w5);
+    if (!rc) rc = up(w->conv5_b, kSub, "conv5_b", &d.b5);
+    if (!rc) rc = up(w->conv6_b, kSub, "conv6_b", &d.b6);
+    if (!rc) rc = up(w->out_b, kD, "out_b", &d.out_b);
+    // 1x1 convolution weights [Cout][Cin] stored transposed, [Cin][Cout]:
+    // the weight becomes the GEMM's B operand (upload_pointwise).
+    for (int k = 0; k < 2 && !rc; ++k) {
+        const float* host = k ? w->conv6_w : w->conv3_w;
+        DevWeight* dw = k ? &d.w6t : &d.w3t;
+        const float* raw = nullptr;
+        rc = up(host, kSub * kSub, k ? "conv6_w" : "conv3_w", &raw);
+        void* t = nullptr;
+        if (!rc && hipMalloc(&t, kSub * kSub * 4) != hipSuccess) rc = error(PK_GPU_ENOMEM, "pointwise");
+        if (!rc) {
+            d.allocs.push_back(t);
+            rc = check(pkgpu::launch_transpose(raw, static_cast<float*>(t), kSub, kSub, enc->stream),
+                       "transpose");
+            dw->kind = pkgpu::W_F32;
+            dw->data = t;
+            dw->K = dw->N = kSub;
+        }
+    }
+    if (!rc) {
+        const pk_gpu_weight& o = w->out_w;
+        const int K = kSub * 16, N = kD;          // 256 channels x 16 mel bins after three stages
+        d.out.K = K;
+        d.out.N = N;
+        d.out.scale = o.scale;
+        if (o.bits == 8) {
+            d.out.kind = pkgpu::W_I8;
+            rc = pre_upload(enc, o.data, (size_t)K * N, "out_w", &d.out.data);
+        } else if (o.bits == 32) {
+            d.out.kind = pkgpu::W_F32;
+            rc = pre_upload(enc, o.data, (size_t)K * N * 4, "out_w", &d.out.data);
+        } else if (o.bits == 4) {
+            d.out.kind = pkgpu::W_I4;
+            rc = pre_upload(enc, o.data, (size_t)K * N / 2, "out_w", &d.out.data);
+            if (!rc) rc = pre_upload(enc, o.scales, (size_t)K * (N / 32) * 4, "out_w scales", &v);
+            d.out.scales = static_cast<const float*>(v);
+        } else {
+            rc = error(PK_GPU_EINVAL, "out_w: bits = %d", o.bits);
+        }
+    }
+    if (!rc) rc = check(hipStreamSynchronize(enc->stream), "pre-encode upload");
+    if (rc) {
+        free_pre(enc);
+        return rc;
+    }
+    d.set = true;
+    return PK_GPU_OK;
+}
+
+int pk_gpu_encoder_frames(int n_frames)
+{
+    return n_frames > 0 ? half_up(half_up(half_up(n_frames))) : 0;
+}
+
+int pk_gpu_encoder_pre_encode_dev(pk_gpu_encoder* enc, const float* dmel, int n_frames, float* dx,
+                                  void* stream)
+{
+    if (!enc || !dmel || !dx) return error(PK_GPU_EINVAL, "NULL argument");
+    if (!enc->pre.set) return error(PK_GPU_EINVAL, "no pre-encode weights (pk_gpu_encoder_set_pre_encode)");
+    if (n_frames <= 0) return error(PK_GPU_EINVAL, "n_frames = %d", n_frames);
+    hipStream_t s;
+    int rc = dev_stream(stream, &s);
+    if (rc) return rc;
+    return pre_encode(enc, dmel, n_frames, dx, s);
+}
+
+int pk_gpu_encoder_run_mel(pk_gpu_encoder* enc, const float* mel, int n_frames, int chunk_size,
+                           int overlap, float* out)
+{
+    if (!enc || !mel || !out) return error(PK_GPU_EINVAL, "NULL argument");
+    if (!enc->pre.set) return error(PK_GPU_EINVAL, "no pre-encode weights (pk_gpu_encoder_set_pre_encode)");
+    if (n_frames <= 0) return error(PK_GPU_EINVAL, "n_frames = %d", n_frames);
+    int rc = pkgpu::rt::bind(nullptr);
+    if (rc) return rc;
+    hipStream_t s = enc->stream;
+    const int Tp = pk_gpu_encoder_frames(n_frames);
+    if ((rc = grow(&enc->pre_x, &enc->pre_x_n, (size_t)Tp * kD, s))) return rc;
+    float* dmel = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&dmel), (size_t)kMels * n_frames * 4) != hipSuccess)
+        return error(PK_GPU_ENOMEM, "mel buffer");
+    rc = check(hipMemcpyAsync(dmel, mel, (size_t)kMels * n_frames * 4, hipMemcpyHostToDevice, s),
+               "mel upload");
+    if (!rc) rc = pre_encode(enc, dmel, n_frames, enc->pre_x, s);
+    if (!rc) rc = run(enc, enc->pre_x, Tp, chunk_size, overlap, out, s, hipMemcpyDeviceToDevice,
+                      hipMemcpyDeviceToHost);
+    if (!rc) rc = check(hipStreamSynchronize(s), "encoder run");
+    else (void)hipStreamSynchronize(s);
+    (void)hipFree(dmel);
+    return rc;
 }
 
 int pk_gpu_layer_norm_dev(const float* dx, const float* dgamma, const float* dbeta, float* dout,

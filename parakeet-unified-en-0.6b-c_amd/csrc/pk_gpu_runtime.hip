@@ -400,7 +400,7 @@ int pk_gpu_sgemm(int transA, int transB, int M, int N, int K, float alpha, const
 // Device-pointer entry points; the *_ex forms add the fused epilogue.
 static int check_epilogue(const float* bias, int epi, float beta)
 {
-    if (epi < PK_GPU_EPI_NONE || epi > PK_GPU_EPI_RESIDUAL)
+    if (epi < PK_GPU_EPI_NONE || epi > PK_GPU_EPI_RELU)
         return fail(PK_GPU_EINVAL, "epilogue %d is not one of PK_GPU_EPI_*", epi);
     if ((epi == PK_GPU_EPI_HALF_RESIDUAL || epi == PK_GPU_EPI_RESIDUAL) && beta != 0.0f)
         return fail(PK_GPU_EINVAL, "residual epilogues need beta == 0 (C is the residual)");

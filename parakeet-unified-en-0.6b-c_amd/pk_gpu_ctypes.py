@@ -53,6 +53,10 @@ _PROTOS = {
     "pk_gpu_encoder_bytes": (_sz, [_p]),
     "pk_gpu_encoder_destroy": (None, [_p]),
     "pk_gpu_encoder_profile": (_i, [_p, _i]),
+    "pk_gpu_encoder_set_pre_encode": (_i, [_p, _p]),
+    "pk_gpu_encoder_frames": (_i, [_i]),
+    "pk_gpu_encoder_pre_encode_dev": (_i, [_p, _p, _i, _p, _p]),
+    "pk_gpu_encoder_run_mel": (_i, [_p, _p, _i, _i, _i, _p]),
     "pk_gpu_encoder_profile_read": (_i, [_p, _i, _p, _p, _p, _p]),
 }
 
@@ -87,6 +91,13 @@ _BLOCK_FIELDS = [
 class BlockWeights(ctypes.Structure):
     """pk_gpu_block_weights (include/pk_gpu.h): one conformer block, host pointers."""
     _fields_ = _BLOCK_FIELDS
+
+
+class PreEncodeWeights(ctypes.Structure):
+    """pk_gpu_pre_encode_weights (include/pk_gpu.h; PreEncodeWeights, parakeet.h)."""
+    _fields_ = [("conv0_w", _p), ("conv0_b", _p), ("conv2_w", _p), ("conv2_b", _p),
+                ("conv3_w", _p), ("conv3_b", _p), ("conv5_w", _p), ("conv5_b", _p),
+                ("conv6_w", _p), ("conv6_b", _p), ("out_w", Weight), ("out_b", _p)]
 
 STATUS = {0: "OK", -1: "EINVAL", -2: "ENOTSUP", -3: "ENOMEM", -4: "EHIP", -5: "ENODEV"}
 

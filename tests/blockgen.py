@@ -95,3 +95,34 @@ def pe_table(rows=9999, center=4999):
 def pe_slice(pe, T, center=4999):
     """encoder.c:220-228: rows [center - T + 1, center + T)."""
     return np.ascontiguousarray(pe[center - T + 1:center + T])
+
+
+class PreEncode:
+    """pre_encode parameters (PreEncodeWeights, parakeet.h): 3x3 convolutions
+    ~N(0, 0.1) (pointwise ~N(0, 1/16)), biases ~N(0, 0.02), int8 out_w codes
+    uniform in [-127, 127] with scale 0.01 / 64 (or fp32 ~N(0, 0.02))."""
+
+    def __init__(self, seed, out_bits=8):
+        rng = np.random.default_rng(seed)
+        self.keep = []
+
+        def f32(a):
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            self.keep.append(a)
+            return a.ctypes.data
+
+        normal = lambda shape, sd: f32(rng.standard_normal(shape) * sd)
+        w = pk.PreEncodeWeights()
+        w.conv0_w, w.conv0_b = normal((256, 9), 0.3), normal(256, 0.02)
+        w.conv2_w, w.conv2_b = normal((256, 9), 0.3), normal(256, 0.02)
+        w.conv3_w, w.conv3_b = normal((256, 256), 1.0 / 16), normal(256, 0.02)
+        w.conv5_w, w.conv5_b = normal((256, 9), 0.3), normal(256, 0.02)
+        w.conv6_w, w.conv6_b = normal((256, 256), 1.0 / 16), normal(256, 0.02)
+        if out_bits == 8:
+            q = rng.integers(-127, 128, (4096, 1024), dtype=np.int8)
+            self.keep.append(q)
+            w.out_w = pk.Weight(q.ctypes.data, 0.01 / 64, None, 8)
+        else:
+            w.out_w = pk.Weight(normal((4096, 1024), 0.02), 0.0, None, 32)
+        w.out_b = normal(1024, 0.02)
+        self.w = w

@@ -254,3 +254,41 @@ def test_encoder_rejects_oversized_sequence(dev, enc2):
     out = np.empty_like(x)
     rc = pk.load().pk_gpu_encoder_run(enc2.h, x.ctypes.data, 600, 0, 8, out.ctypes.data)
     assert rc == -2                               # PK_GPU_ENOTSUP: chunk it
+
+
+@pytest.mark.skipif(not po.have_ref_block(), reason="reference block harness missing")
+@pytest.mark.parametrize("out_bits", [8, 32])
+def test_pre_encode_bit_exact(dev, enc2, out_bits):
+    """pre_encode_and_scale: 3x3 convolutions, depthwise and pointwise
+    convolutions (chains started from the bias), ReLUs, flatten, the output
+    linear and the sqrt(d_model) scale, bit-identical to the reference for
+    odd and even frame counts."""
+    pre = bg.PreEncode(0xB10CE + out_bits, out_bits)
+    pk.call("pk_gpu_encoder_set_pre_encode", enc2.h, ctypes.byref(pre.w))
+    lib = pk.load()
+    for n in (1, 8, 33, 100, 801, 2400):
+        mel = rows(128, n, 2.0)
+        want = po.ref_pre_encode(pre.w, mel)
+        tp = lib.pk_gpu_encoder_frames(n)
+        assert tp == want.shape[0]
+        dmel = dev.put(mel)
+        dx = dev.torch.full((tp, 1024), float("nan"), device=dev.dev)
+        pk.call("pk_gpu_encoder_pre_encode_dev", enc2.h, dmel.data_ptr(), n, dx.data_ptr(),
+                dev.stream())
+        got = dx.cpu().numpy()
+        assert bits_equal(got, want), f"n_frames={n}: " + describe_mismatch(got, want)
+
+
+@pytest.mark.skipif(not po.have_ref_block(), reason="reference block harness missing")
+def test_run_mel_equals_pre_encode_then_blocks(dev, enc2):
+    """pk_gpu_encoder_run_mel = pre-encode on the device, then the blocks
+    (chunked), against the same two steps through their own entry points."""
+    pre = bg.PreEncode(0xB10CF)
+    pk.call("pk_gpu_encoder_set_pre_encode", enc2.h, ctypes.byref(pre.w))
+    n = 4100                                        # T' = 513 -> two chunks
+    mel = rows(128, n, 2.0)
+    tp = pk.load().pk_gpu_encoder_frames(n)
+    out = np.empty((tp, 1024), np.float32)
+    pk.call("pk_gpu_encoder_run_mel", enc2.h, mel.ctypes.data, n, 400, 8, out.ctypes.data)
+    x = po.ref_pre_encode(pre.w, mel)
+    assert bits_equal(out, enc2.run(x, chunk=400))
