@@ -341,9 +341,14 @@ static int create_encoder(const PkModel *m, pk_gpu_encoder **enc)
         w->ff2_linear2_w = gw(b->ff2.linear2_w);  w->ff2_linear2_b = b->ff2.linear2_b;
         w->norm_out_w = b->norm_out_w;  w->norm_out_b = b->norm_out_b;
     }
+    const PreEncodeWeights *p = &m->enc.pre_encode;
+    pk_gpu_pre_encode_weights pw = {p->conv0_w, p->conv0_b, p->conv2_w, p->conv2_b,
+                                    p->conv3_w, p->conv3_b, p->conv5_w, p->conv5_b,
+                                    p->conv6_w, p->conv6_b, gw(p->out_w), p->out_b};
     int rc = pk_gpu_init(-1);
     if (!rc) rc = pk_gpu_encoder_create(enc, bw, PK_N_BLOCKS, m->enc.pe_table, PK_PE_TABLE_SIZE,
                                         PK_PE_CENTER);
+    if (!rc) rc = pk_gpu_encoder_set_pre_encode(*enc, &pw);
     if (rc) fprintf(stderr, "pk_gpu_encoder_create: %s\n", pk_gpu_last_error());
     return rc;
 }
@@ -404,8 +409,19 @@ int main(int argc, char **argv)
     fpenv("after setup");
     double t_load = now_s() - t0;
 
-    float *x = (float *)malloc((size_t)T * PK_D_MODEL * sizeof(float));
-    pkor_fill_normal(x, (size_t)T * PK_D_MODEL, 0.0f, 1.0f, pkor_seed(SEED_BASE, "features"));
+    /* PK_FROM_MEL=1: start from a mel spectrogram [128][8T] (~N(0,1)) and run
+     * pk_encoder (encoder.c:595-611: pre-encode included); otherwise feed
+     * N(0,1) features [T][1024] straight into the blocks. */
+    const int from_mel = getenv("PK_FROM_MEL") && atoi(getenv("PK_FROM_MEL"));
+    const int n_mel = 8 * T;
+    float *x = NULL, *mel = NULL;
+    if (from_mel) {
+        mel = (float *)malloc((size_t)PK_N_MELS * n_mel * sizeof(float));
+        pkor_fill_normal(mel, (size_t)PK_N_MELS * n_mel, 0.0f, 1.0f, pkor_seed(SEED_BASE, "mel"));
+    } else {
+        x = (float *)malloc((size_t)T * PK_D_MODEL * sizeof(float));
+        pkor_fill_normal(x, (size_t)T * PK_D_MODEL, 0.0f, 1.0f, pkor_seed(SEED_BASE, "features"));
+    }
 
     pk_pool();                              /* thread pool start-up outside the timing */
     double t_first = 0.0;
@@ -413,22 +429,25 @@ int main(int argc, char **argv)
     /* one untimed run first: workspace allocation and first kernel loads */
     float *enc = (float *)calloc((size_t)T * PK_D_MODEL, sizeof(float));
     const int chunk = should_chunk(T) ? PK_CHUNK_SIZE : 0;   /* encoder.c:602-610 */
-    t0 = now_s();
-    if (pk_gpu_encoder_run(genc, x, T, chunk, PK_CHUNK_OVERLAP, enc)) {
-        fprintf(stderr, "pk_gpu_encoder_run: %s\n", pk_gpu_last_error());
-        return 1;
-    }
-    t_first = now_s() - t0;
-    t0 = now_s();
-    if (pk_gpu_encoder_run(genc, x, T, chunk, PK_CHUNK_OVERLAP, enc)) {
-        fprintf(stderr, "pk_gpu_encoder_run: %s\n", pk_gpu_last_error());
-        return 1;
+    for (int pass = 0; pass < 2; pass++) {
+        t0 = now_s();
+        int rc = from_mel ? pk_gpu_encoder_run_mel(genc, mel, n_mel, chunk, PK_CHUNK_OVERLAP, enc)
+                          : pk_gpu_encoder_run(genc, x, T, chunk, PK_CHUNK_OVERLAP, enc);
+        if (rc) {
+            fprintf(stderr, "pk_gpu_encoder_run: %s\n", pk_gpu_last_error());
+            return 1;
+        }
+        if (pass == 0) t_first = now_s() - t0;
     }
     double t_enc = now_s() - t0;
 #else
     t0 = now_s();
     float *enc = x;
-    if (should_chunk(T)) {                  /* encoder.c:602-610 */
+    if (from_mel) {
+        int out_len = 0;
+        pk_encoder(&m, mel, n_mel, &enc, &out_len);
+        if (out_len != T) { fprintf(stderr, "pk_encoder gave %d frames\n", out_len); return 1; }
+    } else if (should_chunk(T)) {           /* encoder.c:602-610 */
         enc = (float *)calloc((size_t)T * PK_D_MODEL, sizeof(float));
         encode_blocks_chunked(&m, x, T, enc);
     } else {
@@ -483,9 +502,9 @@ int main(int argc, char **argv)
         if ((u & 0x7f800000u) == 0x7f800000u) finite = 0;
         else if (fabsf(enc[i]) > amax) amax = fabsf(enc[i]);
     }
-    printf("{\"frames\": %d, \"chunked\": %d, \"enc_fnv\": \"%016llx\", \"enc_absmax\": %.6g, "
+    printf("{\"frames\": %d, \"from_mel\": %d, \"chunked\": %d, \"enc_fnv\": \"%016llx\", \"enc_absmax\": %.6g, "
            "\"finite\": %d, \"n_tokens\": %d, \"tokens_fnv\": \"%016llx\", \"first_tokens\": [",
-           T, should_chunk(T), (unsigned long long)fnv1a(enc, (size_t)T * PK_D_MODEL * 4), amax,
+           T, from_mel, should_chunk(T), (unsigned long long)fnv1a(enc, (size_t)T * PK_D_MODEL * 4), amax,
            finite, n_tok, (unsigned long long)fnv1a(tokens, (size_t)n_tok * sizeof(int)));
     for (int i = 0; i < n_tok && i < 16; i++) printf("%s%d", i ? ", " : "", tokens[i]);
     printf("], \"threads\": %d, \"load_s\": %.3f, \"encoder_s\": %.4f, \"encoder_first_s\": %.4f, "
@@ -495,6 +514,7 @@ int main(int argc, char **argv)
     free(tokens);
     if (enc != x) free(enc);
     free(x);
+    free(mel);
 #ifdef PK_GPU_REGISTER
     pk_gpu_shutdown();
 #endif

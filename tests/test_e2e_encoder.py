@@ -30,7 +30,7 @@ REF = os.path.join(os.path.dirname(HERE), "oracle", "_ref")
 THREADS = str(min(os.cpu_count() or 1, 16))
 
 
-def run(binary, frames, tmp_path, dump=None, attn_gain=None):
+def run(binary, frames, tmp_path, dump=None, attn_gain=None, from_mel=False):
     path = os.path.join(REF, binary)
     if not os.path.exists(path):
         pytest.skip(f"{binary} not built (oracle/Makefile ref)")
@@ -39,6 +39,8 @@ def run(binary, frames, tmp_path, dump=None, attn_gain=None):
         env["PK_DUMP_ENC"] = str(dump)
     if attn_gain is not None:
         env["PK_SYNTH_ATTN_GAIN"] = str(attn_gain)
+    if from_mel:
+        env["PK_FROM_MEL"] = "1"
     out = subprocess.run([path, str(frames), str(tmp_path)], capture_output=True, text=True,
                          env=env, timeout=400)
     assert out.returncode == 0, out.stderr[-2000:]
@@ -80,14 +82,16 @@ def test_gpu_dropin_matches_reference_bit_for_bit(frames, tmp_path):
         assert x86["enc_fnv"] != ref["enc_fnv"]
 
 
-def resident_vs_reference(frames, tmp_path, attn_gain):
+def resident_vs_reference(frames, tmp_path, attn_gain, from_mel=False):
     import numpy as np
-    gres = run("pk_encode_gpures", frames, tmp_path, dump=tmp_path / "gpures.f32", attn_gain=attn_gain)
-    ref = run("pk_encode_ref", frames, tmp_path, dump=tmp_path / "ref.f32", attn_gain=attn_gain)
+    gres = run("pk_encode_gpures", frames, tmp_path, dump=tmp_path / "gpures.f32", attn_gain=attn_gain,
+               from_mel=from_mel)
+    ref = run("pk_encode_ref", frames, tmp_path, dump=tmp_path / "ref.f32", attn_gain=attn_gain,
+              from_mel=from_mel)
     a = np.fromfile(tmp_path / "gpures.f32", dtype=np.float32).reshape(frames, 1024)
     b = np.fromfile(tmp_path / "ref.f32", dtype=np.float32).reshape(frames, 1024)
     dev = float(np.abs(a - b).max() / np.abs(b).max())
-    print(json.dumps({"frames": frames, "attn_gain": attn_gain, "threads": THREADS,
+    print(json.dumps({"frames": frames, "from_mel": from_mel, "attn_gain": attn_gain, "threads": THREADS,
                       "max_rel_deviation": dev, "identical_fraction": float(np.mean(a == b)),
                       "tokens_gpu_resident": gres["n_tokens"], "tokens_reference": ref["n_tokens"],
                       "tokens_equal": gres["tokens_fnv"] == ref["tokens_fnv"],
@@ -134,3 +138,16 @@ def test_gpu_resident_encoder_workload_stats(tmp_path):
     a = np.fromfile(tmp_path / "gpures.f32", dtype=np.float32)
     b = np.fromfile(tmp_path / "ref.f32", dtype=np.float32)
     assert 0.5 < np.abs(a).max() / np.abs(b).max() < 2.0
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("frames", [300, 900])
+def test_gpu_resident_encoder_from_mel(frames, tmp_path):
+    """pk_encoder from a mel spectrogram ([128][8 x frames] ~N(0,1)): the
+    reference's pre-encode + blocks on the CPU, against
+    pk_gpu_encoder_run_mel (pre-encode on the device, bit-identical, then the
+    resident blocks), trained-like attention weights; token ids equal."""
+    gres, ref, dev = resident_vs_reference(frames, tmp_path, 0.05, from_mel=True)
+    assert dev <= 1e-3
+    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"]
