@@ -83,11 +83,17 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
     const int lane = threadIdx.x;
     const int row0 = blockIdx.x * 8;
     const int nr = min(8, rows - row0);
-    for (int idx = lane; idx < 8 * V4; idx += 64) {
-        const int r = idx / V4, c4 = idx % V4;
-        if (r < nr)
-            *reinterpret_cast<float4*>(buf + r * LD + 4 * c4) =
-                *reinterpret_cast<const float4*>(x + (size_t)(row0 + r) * ldx + 4 * c4);
+    // all 32 loads of a lane in flight at once (rows past the end read row 0)
+    float4 in[8 * V4 / 64];
+#pragma unroll
+    for (int q = 0; q < 8 * V4 / 64; ++q) {
+        const int idx = lane + 64 * q, r = idx / V4, c4 = idx % V4;
+        in[q] = *reinterpret_cast<const float4*>(x + (size_t)(r < nr ? row0 + r : row0) * ldx + 4 * c4);
+    }
+#pragma unroll
+    for (int q = 0; q < 8 * V4 / 64; ++q) {
+        const int idx = lane + 64 * q;
+        *reinterpret_cast<float4*>(buf + (idx / V4) * LD + 4 * (idx % V4)) = in[q];
     }
     __syncthreads();
     const int r = lane >> 3, l = lane & 7;
@@ -113,8 +119,9 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
     for (int i = 0; i < NPL; ++i)
         br[8 * i] = __fmaf_rn(__fmul_rn(v[i], inv), gamma[l + 8 * i], beta[l + 8 * i]);
     __syncthreads();
-    for (int idx = lane; idx < 8 * V4; idx += 64) {
-        const int rr = idx / V4, c4 = idx % V4;
+#pragma unroll
+    for (int q = 0; q < 8 * V4 / 64; ++q) {
+        const int idx = lane + 64 * q, rr = idx / V4, c4 = idx % V4;
         if (rr < nr)
             *reinterpret_cast<float4*>(out + (size_t)(row0 + rr) * ldo + 4 * c4) =
                 *reinterpret_cast<const float4*>(buf + rr * LD + 4 * c4);
@@ -460,6 +467,9 @@ __global__ void glu_rows(const float* __restrict__ in, int ldi, float* out, int 
 // others take the compiled form of its scalar loops: taps 0..7 multiplied,
 // out-of-range ones as +0, reduced as hsum8 and added to the bias, then fma
 // for the remaining taps.
+// KK = 9 (PK_CONV_KERNEL) fixes the tap count at compile time so every load
+// of an output is issued before its chain; KK = 0 takes p.K at run time.
+template <int KK>
 __global__ void depthwise_swish(DwArgs p)
 {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -467,13 +477,25 @@ __global__ void depthwise_swish(DwArgs p)
     const int t = (int)(idx / p.C), c = (int)(idx % p.C);
     const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.y] : 0;
     const float* x = p.x + (size_t)row0 * p.ldx + c;
-    const float* wc = p.w + (size_t)c * p.K;
-    const int T = p.T, K = p.K, pad = (K - 1) / 2;
+    const int K = KK ? KK : p.K;
+    const float* wc = p.w + (size_t)c * K;
+    const int T = p.T, pad = (K - 1) / 2;
     const int t_hi = T - pad > pad ? T - pad : pad;
     const int t_vec = pad + (t_hi - pad) / 8 * 8;
     float val = p.b ? p.b[c] : 0.0f;
     if (t >= pad && t < t_vec) {
-        for (int k = 0; k < K; ++k) val = __fmaf_rn(x[(size_t)(t - pad + k) * p.ldx], wc[k], val);
+        if constexpr (KK > 0) {
+            float xv[KK], wv[KK];
+#pragma unroll
+            for (int k = 0; k < KK; ++k) {
+                xv[k] = x[(size_t)(t - pad + k) * p.ldx];
+                wv[k] = wc[k];
+            }
+#pragma unroll
+            for (int k = 0; k < KK; ++k) val = __fmaf_rn(xv[k], wv[k], val);
+        } else {
+            for (int k = 0; k < K; ++k) val = __fmaf_rn(x[(size_t)(t - pad + k) * p.ldx], wc[k], val);
+        }
     } else {
         const int K8 = K & ~7;
         for (int k0 = 0; k0 < K8; k0 += 8) {
@@ -511,17 +533,21 @@ __global__ void conv0_relu(const float* __restrict__ mel, int T, int n_mels,
     if (idx >= (long long)H1 * W1 * kSub) return;
     const int c = (int)(idx % kSub);
     const int pos = (int)(idx / kSub), ow = pos % W1, oh = pos / W1;
+    // every tap loaded first (out-of-range ones from a clamped address and
+    // skipped), then the chain over the in-range taps in order
+    float xv[9], wv[9];
+    bool ok[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const int ih = 2 * oh - 1 + k / 3, iw = 2 * ow - 1 + k % 3;
+        ok[k] = ih >= 0 && ih < T && iw >= 0 && iw < n_mels;
+        xv[k] = mel[(size_t)min(max(iw, 0), n_mels - 1) * T + min(max(ih, 0), T - 1)];
+        wv[k] = w[c * 9 + k];
+    }
     float v = b[c];
 #pragma unroll
-    for (int kh = 0; kh < 3; ++kh) {
-        const int ih = 2 * oh - 1 + kh;
-#pragma unroll
-        for (int kw = 0; kw < 3; ++kw) {
-            const int iw = 2 * ow - 1 + kw;
-            if (ih >= 0 && ih < T && iw >= 0 && iw < n_mels)
-                v = __fmaf_rn(mel[(size_t)iw * T + ih], w[c * 9 + kh * 3 + kw], v);
-        }
-    }
+    for (int k = 0; k < 9; ++k)
+        if (ok[k]) v = __fmaf_rn(xv[k], wv[k], v);
     out[idx] = v > 0.0f ? v : 0.0f;
 }
 
@@ -534,17 +560,19 @@ __global__ void dwconv3x3s2(const float* __restrict__ in, int H, int W,
     if (idx >= (long long)Ho * Wo * kSub) return;
     const int c = (int)(idx % kSub);
     const int pos = (int)(idx / kSub), ow = pos % Wo, oh = pos / Wo;
+    float xv[9], wv[9];
+    bool ok[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const int ih = 2 * oh - 1 + k / 3, iw = 2 * ow - 1 + k % 3;
+        ok[k] = ih >= 0 && ih < H && iw >= 0 && iw < W;
+        xv[k] = in[((size_t)min(max(ih, 0), H - 1) * W + min(max(iw, 0), W - 1)) * kSub + c];
+        wv[k] = w[c * 9 + k];
+    }
     float v = b[c];
 #pragma unroll
-    for (int kh = 0; kh < 3; ++kh) {
-        const int ih = 2 * oh - 1 + kh;
-#pragma unroll
-        for (int kw = 0; kw < 3; ++kw) {
-            const int iw = 2 * ow - 1 + kw;
-            if (ih >= 0 && ih < H && iw >= 0 && iw < W)
-                v = __fmaf_rn(in[((size_t)ih * W + iw) * kSub + c], w[c * 9 + kh * 3 + kw], v);
-        }
-    }
+    for (int k = 0; k < 9; ++k)
+        if (ok[k]) v = __fmaf_rn(xv[k], wv[k], v);
     out[idx] = v;
 }
 
@@ -625,8 +653,11 @@ hipError_t launch_depthwise(const DwArgs& a, int n_chunks, hipStream_t s)
 {
     const long long n = (long long)a.T * a.C;
     if (n <= 0 || n_chunks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(depthwise_swish, dim3((unsigned)((n + 255) / 256), n_chunks), dim3(256), 0, s,
-                       a);
+    const dim3 grid((unsigned)((n + 255) / 256), n_chunks);
+    if (a.K == 9)
+        hipLaunchKernelGGL(depthwise_swish<9>, grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(depthwise_swish<0>, grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
