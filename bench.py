@@ -185,7 +185,9 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20):
         del graph
         tf = 2.0 * m * n * k / us / 1e6
         gbs = alg_bytes(kind, m, n, k) / us / 1e3
-        print(json.dumps({"gemm": f"{kind} {m}x{n}x{k}", "config": lib.pk_gpu_pick_config(m, n, k),
+        bits = {"i4": 4, "i8": 8}.get(kind, 32)
+        print(json.dumps({"gemm": f"{kind} {m}x{n}x{k}",
+                          "config": lib.pk_gpu_pick_config_bits(m, n, k, bits),
                           "avg_us": round(us, 2), "tflops": round(tf, 2), "gbps": round(gbs, 1),
                           "frac_mfma_fp32": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_replicas": reps,
@@ -266,8 +268,8 @@ def ffn_mode(args):
     gbytes = (int4_bytes(D, FF) + int4_bytes(FF, D)) / gemm_s / 1e9
     frames_per_s = M * K / (elapsed_ms / 1e3)
 
-    cfg_up = lib.pk_gpu_pick_config(M, FF, D)
-    cfg_dn = lib.pk_gpu_pick_config(M, D, FF)
+    cfg_up = lib.pk_gpu_pick_config_bits(M, FF, D, 4)
+    cfg_dn = lib.pk_gpu_pick_config_bits(M, D, FF, 4)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "int4_ffn_pair_m375_traffic.json")
     if os.path.exists(tpath):

@@ -311,16 +311,19 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
 
 /* Number of kernel tile configurations, and a description of one:
  * family ('R': rows on MFMA lanes, 'X': columns on lanes with A broadcast,
- * 'S': the 'X' tiles plus as many producer waves that stage the operands),
+ * 'S': the 'X' tiles plus as many producer waves that stage the operands,
+ * 'Y': the 'X' tiles with two LDS chunks in flight instead of four),
  * mfma (32, 16 or 4 = v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32),
  * independent chains per wave, multiplying waves along M and N per
  * workgroup, and k per LDS chunk.  Any pointer may be NULL. */
 int pk_gpu_num_configs(void);
 int pk_gpu_config_info(int index, int *family, int *mfma, int *cw, int *wgm, int *wgn,
                        int *kt);
-/* Index of the configuration the dispatcher picks for a shape with int8 or
- * int4 weights (fp32 weights take configuration 10 where this returns 11). */
+/* Index of the configuration the dispatcher picks for a shape with int8
+ * weights, and for weights of `bits` = 4, 8 or 32 (fp32) bits (-1 for any
+ * other value). */
 int pk_gpu_pick_config(int M, int N, int K);
+int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
 /* Force a configuration for later calls on this thread (-1 = automatic). */
 int pk_gpu_force_config(int index);
 

@@ -11,12 +11,22 @@ namespace pkgpu {
 // The reference's encoder never attends over more than 500 frames unless
 // chunking is forced off (PK_CHUNK_THRESHOLD, parakeet.h; encoder.c:595-610).
 constexpr int kAttnMaxT = 512;
-constexpr int kAttnSld = 528;          // LDS row stride of the scores (>= kAttnMaxT)
+constexpr int kAttnRows = 32;          // query rows per workgroup
+// LDS row stride of a workgroup's score rows for chunks of T rows, and the
+// workgroup's LDS: the score rows plus one staging tile of 64 x 68 floats.
+// At T = 416 two workgroups fit in a CU's 160 KiB.
+__host__ __device__ constexpr int attn_sld(int T) { return ((T + 15) & ~15) + 16; }
+__host__ __device__ constexpr unsigned attn_lds_bytes(int T)
+{
+    return 4u * (unsigned)(kAttnRows * attn_sld(T) + 64 * 68);
+}
 
-// Relative-position attention of n chunks of T rows each (encoder.c:300-408).
+// Relative-position attention of n chunks (encoder.c:300-408); chunk z has
+// chunk_T[z] <= T rows (all T when chunk_T is null).
 //   qkv  [rows][ldq]: Q | K | V (H*128 columns each, bias added); chunk z
 //        starts at row chunk_rows[z]
-//   P    [2T-1][ldp]: linear_pos(pe_slice(T)) for this T
+//   P    [2T-1][ldp]: linear_pos(pe_slice(T)); a chunk of Tz rows uses its
+//        rows [T - Tz, T + Tz - 1), which are linear_pos(pe_slice(Tz))
 //   out  [rows][ldo]: the concatenated head outputs, chunk z at chunk_rows[z]
 struct AttnArgs {
     const float* qkv; int ldq;
@@ -25,6 +35,7 @@ struct AttnArgs {
     const float* pos_bias_v;
     float* out; int ldo;
     const int* chunk_rows;     // device, n entries (null: one chunk at row 0)
+    const int* chunk_T;        // device, n entries, each in [1, T] (null: all T)
     int T, H;
 };
 

@@ -144,8 +144,7 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
 // scores x V as one fma chain per output over j ascending (sgemm NN).
 
 constexpr int kDh = 128;                 // PK_HEAD_DIM
-constexpr int kAttnRows = 32;            // query rows per workgroup
-constexpr int kTileLd = kDh + 4;         // padded LDS row of a key / position / value tile
+constexpr int kTileLd = kDh + 4;         // padded LDS row of a value tile
 constexpr float kScoreScale = 0.0883883461356163f;   // 1/sqrtf(128) = 0x3db504f3
 
 template <int T_>
@@ -163,47 +162,72 @@ __device__ inline void score_steps(std::integer_sequence<int, Ts...>, const floa
       acc[1][Ts & 7] = mfma_bcast<Ts>(a[1], b[Ts], acc[1][Ts & 7])), ...);
 }
 
-// A 64-row x 128-column tile of a row-major source (row stride ld floats),
-// rows outside [0, n) read as 0: fetched into registers (8 float4 per thread
-// of the 256) one tile ahead of its use, then written to LDS.
+// Tiles staged through LDS, fetched into registers (4 float4 per thread of
+// the 256) one tile ahead of their use; source rows outside [0, n) read as 0.
+//   half tile:  64 rows x 64 columns (from column c0) of keys or positions,
+//               LDS row stride kHalfLd
+//   value tile: 32 rows x 128 columns of values, LDS row stride kTileLd
+constexpr int kHalfLd = 64 + 4;
+constexpr int kTileFloats = 64 * kHalfLd;          // >= 32 * kTileLd
+static_assert(32 * kTileLd <= kTileFloats, "one LDS buffer holds either tile");
+
 struct TileRegs {
-    float4 v[8];
+    float4 v[4];
 };
 
-__device__ inline void load_tile(TileRegs& t, const float* src, int ld, int r0, int n)
+__device__ inline void load_half(TileRegs& t, const float* src, int ld, int r0, int n, int c0)
 {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4; ++q) {
         const int idx = threadIdx.x + 256 * q;
-        const int r = idx >> 5, c4 = idx & 31;
-        const int gr = r0 + r;
-        t.v[q] = (gr >= 0 && gr < n) ? *reinterpret_cast<const float4*>(src + (size_t)gr * ld + 4 * c4)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int gr = r0 + (idx >> 4);
+        t.v[q] = (gr >= 0 && gr < n)
+                     ? *reinterpret_cast<const float4*>(src + (size_t)gr * ld + c0 + 4 * (idx & 15))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
-__device__ inline void store_tile(float* tile, const TileRegs& t)
+__device__ inline void store_half(float* tile, const TileRegs& t)
 {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4; ++q) {
+        const int idx = threadIdx.x + 256 * q;
+        *reinterpret_cast<float4*>(tile + (idx >> 4) * kHalfLd + 4 * (idx & 15)) = t.v[q];
+    }
+}
+
+__device__ inline void load_vtile(TileRegs& t, const float* src, int ld, int r0, int n)
+{
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int idx = threadIdx.x + 256 * q;
+        const int gr = r0 + (idx >> 5);
+        t.v[q] = gr < n ? *reinterpret_cast<const float4*>(src + (size_t)gr * ld + 4 * (idx & 31))
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+__device__ inline void store_vtile(float* tile, const TileRegs& t)
+{
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
         const int idx = threadIdx.x + 256 * q;
         *reinterpret_cast<float4*>(tile + (idx >> 5) * kTileLd + 4 * (idx & 31)) = t.v[q];
     }
 }
 
-// One 4-row x 64-column tile of NT dot products for two row groups of a wave:
-// a[g][kb] holds rows (4g..4g+3) in broadcast layout for k in [16kb, 16kb+16).
-// The B fragments of the next 16 k-steps are read from LDS while the current
-// 32 MFMAs issue (the scheduling barrier keeps that order).
-__device__ inline void score_tile(const float* tile, const float (&a)[2][8], float (&out)[2][4])
+// One 4-row x 64-column tile of NT dot products for two row groups of a wave,
+// accumulated over the two 64-column halves of k: a[g][kb] holds rows
+// (4g..4g+3) in broadcast layout for k in [16kb, 16kb+16); half H covers
+// kb = 4H..4H+3 from the half tile in LDS.  Chain t % 8 of each output takes
+// k ascending across both halves.  The B fragments of the next 16 k-steps are
+// read from LDS while the current 32 MFMAs issue (the scheduling barrier
+// keeps that order).
+template <int H>
+__device__ inline void score_half(const float* tile, const float (&a)[2][8], v4f (&acc)[2][8])
 {
     const int lane = threadIdx.x & 63;
-    v4f acc[2][8];
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int l = 0; l < 8; ++l) acc[g][l] = v4f{0.f, 0.f, 0.f, 0.f};
-    const float* trow = tile + lane * kTileLd;
+    const float* trow = tile + lane * kHalfLd;
     float b[2][16];
     auto fetch = [&](float (&dst)[16], int kb) {
 #pragma unroll
@@ -214,13 +238,17 @@ __device__ inline void score_tile(const float* tile, const float (&a)[2][8], flo
     };
     fetch(b[0], 0);
 #pragma unroll
-    for (int kb = 0; kb < kDh / 16; ++kb) {
-        if (kb + 1 < kDh / 16) fetch(b[(kb + 1) & 1], kb + 1);
+    for (int kb = 0; kb < 4; ++kb) {
+        if (kb + 1 < 4) fetch(b[(kb + 1) & 1], kb + 1);
         __builtin_amdgcn_sched_barrier(0);
-        const float ak[2] = {a[0][kb], a[1][kb]};
+        const float ak[2] = {a[0][4 * H + kb], a[1][4 * H + kb]};
         score_steps(std::make_integer_sequence<int, 16>{}, ak, b[kb & 1], acc);
         __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+__device__ inline void score_sums(const v4f (&acc)[2][8], float (&out)[2][4])
+{
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
@@ -230,6 +258,31 @@ __device__ inline void score_tile(const float* tile, const float (&a)[2][8], flo
             for (int l = 0; l < 8; ++l) p[l] = acc[g][l][i];
             out[g][i] = hsum8(p);
         }
+}
+
+// The 32 x 64 scores of source rows [c, c + 64) (keys or positions; rows
+// outside [0, n) read 0), through the two half tiles: pre holds the first
+// half on entry and the next tile's first half (rows [c + 64, ...), when
+// next is set) on return.  Both barriers of each half are taken by the whole
+// workgroup.
+__device__ inline void score_block(float* tile, TileRegs& pre, const float* src, int ld, int c,
+                                   int n, bool next, const float (&a)[2][8], float (&out)[2][4])
+{
+    v4f acc[2][8];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) acc[g][l] = v4f{0.f, 0.f, 0.f, 0.f};
+    store_half(tile, pre);
+    __syncthreads();
+    load_half(pre, src, ld, c, n, 64);
+    score_half<0>(tile, a, acc);
+    __syncthreads();
+    store_half(tile, pre);
+    __syncthreads();
+    if (next) load_half(pre, src, ld, c + 64, n, 0);
+    score_half<1>(tile, a, acc);
+    score_sums(acc, out);
 }
 
 // scores x V: acc[g][d] += S[row 4g+i][j0 + t] * V[j0 + t][64d + lane].
@@ -260,16 +313,18 @@ __device__ inline void pv_steps(std::integer_sequence<int, Ts...>, const float (
                : 0), ...);
 }
 
-__global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
+__global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
 {
-    __shared__ float S[kAttnRows * kAttnSld];
-    __shared__ float tile[64 * kTileLd];
+    // Scores of the block's rows [kAttnRows][sld], then one staging tile.
+    extern __shared__ float smem[];
+    const int sld = attn_sld(p.T);
+    float* S = smem;
+    float* tile = smem + kAttnRows * sld;
 
     // Workgroups are dispatched to the 8 XCDs round-robin; renumber them so
     // each XCD runs a contiguous run of (row block, head, chunk) tasks, row
     // block fastest: the row blocks of one head of one chunk then share one
     // XCD's L2 for their K, P and V tiles.
-    const int T = p.T;
     int rb, h, z;
     {
         const int nrb = gridDim.x, nh = gridDim.y, total = nrb * nh * gridDim.z;
@@ -281,14 +336,16 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
         h = (task / nrb) % nh;
         z = task / (nrb * nh);
     }
+    const int T = p.chunk_T ? p.chunk_T[z] : p.T;           // this chunk's rows
     const int r0 = rb * kAttnRows;
+    if (r0 >= T) return;                                     // the whole workgroup
     const int row0 = p.chunk_rows ? p.chunk_rows[z] : 0;   // first row of this chunk
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int D = p.H * kDh;
     const float* qkv = p.qkv + (size_t)row0 * p.ldq;
     const float* K = qkv + D + h * kDh;
     const float* V = qkv + 2 * D + h * kDh;
-    const float* P = p.P + h * kDh;
+    const float* P = p.P + (size_t)(p.T - T) * p.ldp + h * kDh;
 
     // Q_u, Q_v rows of this wave in broadcast layout (encoder.c:319-338).
     float au[2][8], av[2][8];
@@ -322,19 +379,16 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
 
     // AC: S[row][j] = Q_u[row] . K[j]
     TileRegs pre;
-    load_tile(pre, K, p.ldq, 0, T);
+    load_half(pre, K, p.ldq, 0, T, 0);
     for (int j0 = 0; j0 < T; j0 += 64) {
-        store_tile(tile, pre);
-        __syncthreads();
-        if (j0 + 64 < T) load_tile(pre, K, p.ldq, j0 + 64, T);
         float o[2][4];
-        score_tile(tile, au, o);
+        score_block(tile, pre, K, p.ldq, j0, T, j0 + 64 < T, au, o);
         const int j = j0 + lane;
         if (j < T)
 #pragma unroll
             for (int g = 0; g < 2; ++g)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) S[(8 * w + 4 * g + i) * kAttnSld + j] = o[g][i];
+                for (int i = 0; i < 4; ++i) S[(8 * w + 4 * g + i) * sld + j] = o[g][i];
         __syncthreads();
     }
 
@@ -342,13 +396,10 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
     const int r_hi = min(r0 + kAttnRows, T) - 1;
     const int L = 2 * T - 1;
     const int m_first = T - 1 - r_hi, m_last = 2 * T - 2 - r0;
-    load_tile(pre, P, p.ldp, m_first, L);
+    load_half(pre, P, p.ldp, m_first, L, 0);
     for (int m0 = m_first; m0 <= m_last; m0 += 64) {
-        store_tile(tile, pre);
-        __syncthreads();
-        if (m0 + 64 <= m_last) load_tile(pre, P, p.ldp, m0 + 64, L);
         float o[2][4];
-        score_tile(tile, av, o);
+        score_block(tile, pre, P, p.ldp, m0, L, m0 + 64 <= m_last, av, o);
         // every (row, j) takes exactly one shifted BD value: read the eight
         // scores first, then write them back combined
         const int m = m0 + lane;
@@ -361,8 +412,8 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
                 const int rl = 8 * w + 4 * g + i, r = r0 + rl;
                 const int j = m - (T - 1 - r);
                 const bool ok = r < T && j >= 0 && j < T;
-                at[g][i] = ok ? rl * kAttnSld + j : -1;
-                sc[g][i] = S[ok ? rl * kAttnSld + j : 0];
+                at[g][i] = ok ? rl * sld + j : -1;
+                sc[g][i] = S[ok ? rl * sld + j : 0];
             }
 #pragma unroll
         for (int g = 0; g < 2; ++g)
@@ -371,12 +422,12 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
                 if (at[g][i] >= 0) S[at[g][i]] = __fmul_rn(__fadd_rn(sc[g][i], o[g][i]), kScoreScale);
         __syncthreads();
     }
-    load_tile(pre, V, p.ldq, 0, T);      // the first value tile, during the softmax
+    load_vtile(pre, V, p.ldq, 0, T);      // the first value tile, during the softmax
 
     // Softmax of each row: 8 lanes per row, lane q owns j = q, q+8, ...
     {
         const int rl = 8 * w + (lane >> 3), q = lane & 7, r = r0 + rl;
-        float* s = S + rl * kAttnSld;
+        float* s = S + rl * sld;
         if (r < T) {
             float mx = s[0];
 #pragma unroll 8
@@ -411,27 +462,31 @@ __global__ __launch_bounds__(256) void rel_pos_attention(AttnArgs p)
     }
     __syncthreads();
 
-    // out[row][h*128 + d] = sum over j ascending of S[row][j] * V[j][d]
+    // out[row][h*128 + d] = sum over j ascending of S[row][j] * V[j][d],
+    // through 32-row value tiles
     v4f acc[2][2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) acc[g][0] = acc[g][1] = v4f{0.f, 0.f, 0.f, 0.f};
     const int i = lane & 3, t = lane >> 2;
-    for (int j0 = 0; j0 < T; j0 += 64) {
-        store_tile(tile, pre);
+    for (int j0 = 0; j0 < T; j0 += 32) {
+        store_vtile(tile, pre);
         __syncthreads();
-        if (j0 + 64 < T) load_tile(pre, V, p.ldq, j0 + 64, T);
-        const int nt = min(64, T - j0);
-        for (int jb = 0; jb < nt; jb += 16) {
-            float a[2];
+        if (j0 + 32 < T) load_vtile(pre, V, p.ldq, j0 + 32, T);
+        const int nt = min(32, T - j0);
 #pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const int jj = j0 + jb + t;
-                a[g] = jj < T ? S[(8 * w + 4 * g + i) * kAttnSld + jj] : 0.0f;
+        for (int jb = 0; jb < 32; jb += 16) {
+            if (jb < nt) {
+                float a[2];
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    const int jj = j0 + jb + t;
+                    a[g] = jj < T ? S[(8 * w + 4 * g + i) * sld + jj] : 0.0f;
+                }
+                if (nt - jb >= 16)
+                    pv_steps_full(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, acc);
+                else
+                    pv_steps(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, nt - jb, acc);
             }
-            if (nt - jb >= 16)
-                pv_steps_full(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, acc);
-            else
-                pv_steps(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, nt - jb, acc);
         }
         __syncthreads();
     }
@@ -635,8 +690,13 @@ hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s)
 {
     if (a.T <= 0 || n_chunks <= 0) return hipSuccess;
     if (a.T > kAttnMaxT) return hipErrorInvalidValue;
+    // LDS above the default dynamic limit is granted once per process.
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&rel_pos_attention), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)attn_lds_bytes(kAttnMaxT));
+    if (attr != hipSuccess) return attr;
     dim3 grid((a.T + kAttnRows - 1) / kAttnRows, a.H, n_chunks);
-    hipLaunchKernelGGL(rel_pos_attention, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(rel_pos_attention, grid, dim3(256), attn_lds_bytes(a.T), s, a);
     return hipGetLastError();
 }
 

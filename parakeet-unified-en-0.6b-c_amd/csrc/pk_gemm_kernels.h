@@ -40,13 +40,15 @@ struct GemmProblem {
     Epilogue epi = EPI_NONE;         // the residual epilogues require beta == 0
 };
 
-// Kernel tile configuration chosen for a shape (see choose_config).
+// Kernel tile configuration chosen for a shape (see choose_config_index).
 //   family 'R': rows on MFMA lanes, one MFMA = 64 rows x mfma columns,
 //               cw column tiles (independent chains) per wave;
 //   family 'X': columns on MFMA lanes with A broadcast, one MFMA = mfma rows
 //               x 64 columns, cw row groups (independent chains) per wave;
 //   family 'S': the 'X' tiles with wgm*wgn additional producer waves that
-//               stage the operands while the others only multiply.
+//               stage the operands while the others only multiply;
+//   family 'Y': the 'X' tiles with two LDS chunks of operands in flight
+//               instead of four (fewer registers: more waves per SIMD).
 struct TileConfig {
     char family;
     int mfma;   // 32, 16 or 4: v_mfma_f32_{32x32x1_2b,16x16x1_4b,4x4x1_16b}_f32
@@ -60,14 +62,14 @@ struct TileConfig {
 };
 
 // Pick the tile configuration with the lowest modelled time on 256 CUs.
-TileConfig choose_config(int M, int N, int K);
+int choose_config_index(int M, int N, int K, WeightKind kind);
 // Number of configurations and access by index (for tests and sweeps).
 int num_configs();
 TileConfig config_at(int i);
 
 // Launch the whole GEMM (beta pre-pass semantics, early exits, int8 edge
 // columns) on `stream`.  Returns hipSuccess or the launch error.
-// cfg_index < 0 selects choose_config().
+// cfg_index < 0 selects choose_config_index().
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index);
 
 // Swish y = x * (1 / (1 + exp(-x))) with the reference's polynomial exp

@@ -68,9 +68,12 @@ TileConfig config_at(int i) { return kConfigs[i]; }
 //   M*N < 1M            config 13 (S 4x4, 2 chains)   out/pos/conv: 15-26
 //   M*N < 1.6M          config 14 (S 4x4, 3 chains)   FF up M=375: 35.1
 //   M*N < 3M            config 18 (S 16x16)           FF up M=416/500: 41
-//   otherwise           config 11 (X 32x32)           M=3312: 183-275
-//                       fp32 weights: config 10 (X 16x16, 2 chains, 2x2 waves):
-//                       pointwise convs M=3312: 143.7 vs 163.1, 71.9 vs 79.2
+//   otherwise, M=3312:  int4 up     config 20 (Y 32x32)  242-252 (config 11: 249-257)
+//                       int4 down   config 11 (X 32x32)  264-271
+//                       int8        config 21 (Y 32x32, k 16)  QKV 180, out 70.0
+//                                   (config 11: 183-185, 72.5-72.9)
+//                       fp32 2048   config 23 (Y 16x16)  132.6 (config 10: 141-144)
+//                       fp32 1024   config 21            68.8 (config 10: 71.6-71.7)
 static int choose_index(int M, int N, int K, WeightKind kind = W_I8)
 {
     const double outputs = (double)M * (double)N;
@@ -78,10 +81,18 @@ static int choose_index(int M, int N, int K, WeightKind kind = W_I8)
     if (outputs < 1.0e6) return K >= 2048 ? 17 : 13;
     if (outputs < 1.6e6) return 14;
     if (outputs < 3.0e6) return 18;
-    return kind == W_F32 ? 10 : 11;
+    // Long M (the encoder's batched chunks): measured per weight format at
+    // M = 3312.  Two LDS chunks in flight (fewer registers, 3 waves per SIMD)
+    // win except for the int4 down projection, whose 1656 wave-long chains
+    // fill 1024 SIMDs unevenly whatever the occupancy.
+    switch (kind) {
+    case W_I4:  return N >= K ? 20 : 11;
+    case W_I8:  return 21;
+    default:    return outputs >= 6.0e6 ? 23 : 21;
+    }
 }
 
-TileConfig choose_config(int M, int N, int K) { return kConfigs[choose_index(M, N, K)]; }
+int choose_config_index(int M, int N, int K, WeightKind kind) { return choose_index(M, N, K, kind); }
 
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
 {

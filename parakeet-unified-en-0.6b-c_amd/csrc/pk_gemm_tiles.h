@@ -918,7 +918,11 @@ void chain_gemm_xs(KArgs p)
     X(16, 'S', 4, 2, 4, 1, 128)  /*  32 x 64,  4 + 4 waves, 2 chains   */  \
     X(17, 'S', 4, 1, 8, 1, 128)  /*  32 x 64,  8 + 8 waves, 1 chain    */  \
     X(18, 'S', 16, 1, 4, 1, 64)  /*  64 x 64,  4 + 4 waves             */  \
-    X(19, 'S', 32, 1, 4, 1, 32)  /* 128 x 64,  4 + 4 waves             */
+    X(19, 'S', 32, 1, 4, 1, 32)  /* 128 x 64,  4 + 4 waves             */  \
+    X(20, 'Y', 32, 1, 4, 1, 32)  /* 128 x 64,  as 11, 2 chunks in flight */ \
+    X(21, 'Y', 32, 1, 4, 1, 16)  /* 128 x 64,  k 16, 2 chunks in flight */  \
+    X(22, 'X', 32, 1, 4, 1, 16)  /* 128 x 64,  k 16 per chunk          */  \
+    X(23, 'Y', 16, 1, 4, 1, 32)  /*  64 x 64,  2 chunks in flight      */
 
 #define PK_CFG_ENTRY(i, fam, mf, c, wm, wn, kt) {fam, mf, c, wm, wn, kt},
 static const TileConfig kConfigs[] = {PK_CONFIGS(PK_CFG_ENTRY)};
@@ -934,9 +938,9 @@ hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
     case i:                                                                               \
         if constexpr (fam == 'R')                                                         \
             hipLaunchKernelGGL((chain_gemm<WK, mf, c, wm, wn, kt, 2, VEC, A1>), grid, block, 0, s, a); \
-        else if constexpr (fam == 'X')                                                    \
-            hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, VEC ? 4 : 2, VEC, A1>), grid, block, \
-                               0, s, a);                                                  \
+        else if constexpr (fam == 'X' || fam == 'Y')                                      \
+            hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, (VEC && fam == 'X') ? 4 : 2, VEC, A1>), \
+                               grid, block, 0, s, a);                                     \
         else                                                                              \
             hipLaunchKernelGGL((chain_gemm_xs<WK, mf, c, wm, wn, kt, 2, VEC, A1>), grid, block, 0, s, a); \
         break;

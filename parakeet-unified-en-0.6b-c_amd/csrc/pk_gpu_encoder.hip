@@ -88,8 +88,9 @@ struct pk_gpu_encoder {
     // workspace, grown on demand
     size_t ws_rows = 0, ws_prow = 0;
     float *x = nullptr, *ln = nullptr, *h = nullptr, *att = nullptr, *P = nullptr;
-    int* rows_tab = nullptr;            // device chunk-row table
+    int* rows_tab = nullptr;            // device: chunk rows [rows_cap], then chunk lengths [rows_cap]
     size_t rows_cap = 0;
+    std::vector<int> tab_host;          // what rows_tab was last given (kept alive for the copy)
     size_t ws_bytes = 0;
     // per-stage timing (pk_gpu_encoder_profile)
     bool prof = false;
@@ -237,6 +238,7 @@ void free_workspace(pk_gpu_encoder* e)
     if (e->rows_tab) (void)hipFree(e->rows_tab);
     e->x = e->ln = e->h = e->att = e->P = nullptr;
     e->rows_tab = nullptr;
+    e->tab_host.clear();
     e->ws_rows = e->ws_prow = e->rows_cap = e->ws_bytes = 0;
 }
 
@@ -260,7 +262,7 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t prow, size_t n_chunks, hipS
         }
         e->ws_bytes += bytes[i];
     }
-    if (hipMalloc(reinterpret_cast<void**>(&e->rows_tab), n_chunks * sizeof(int)) != hipSuccess) {
+    if (hipMalloc(reinterpret_cast<void**>(&e->rows_tab), 2 * n_chunks * sizeof(int)) != hipSuccess) {
         free_workspace(e);
         return error(PK_GPU_ENOMEM, "encoder chunk table failed");
     }
@@ -416,17 +418,24 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
     if ((rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s))) return rc;
     const float* pe_slice = e->pe + (size_t)(e->pe_center - Tmax + 1) * kD;
     if ((rc = gemm(e, b.pos, pe_slice, 2 * Tmax - 1, e->P, nullptr, pkgpu::EPI_NONE, s))) return rc;
-    for (const auto& g : groups) {
-        const int T = g.first, n = g.second.second;
+    {
+        // every chunk in one launch, each with its own length
+        int n = 0;
+        double flops = 0.0, bytes = 4.0 * (2 * Tmax - 1) * kD;
+        for (const auto& g : groups) {
+            const double T = g.first, c = g.second.second;
+            n += g.second.second;
+            flops += 6.0 * T * T * kD * c;     // Q_u K^T, shifted Q_v P^T, scores x V
+            bytes += (4.0 * T * 3 * kD + 4.0 * T * kD) * c;
+        }
         pkgpu::AttnArgs a{};
         a.qkv = h; a.ldq = 3 * kD;
-        a.P = e->P + (size_t)(Tmax - T) * kD; a.ldp = kD;
+        a.P = e->P; a.ldp = kD;
         a.pos_bias_u = b.pu; a.pos_bias_v = b.pv;
         a.out = att; a.ldo = kD;
-        a.chunk_rows = e->rows_tab + g.second.first;
-        a.T = T; a.H = kHeads;
-        const double flops = 6.0 * T * T * kD * n;     // Q_u K^T, shifted Q_v P^T, scores x V
-        const double bytes = (4.0 * T * 3 * kD + 4.0 * T * kD) * n + 4.0 * (2 * T - 1) * kD;
+        a.chunk_rows = e->rows_tab;
+        a.chunk_T = e->rows_tab + e->rows_cap;
+        a.T = Tmax; a.H = kHeads;
         rc = timed(e, PK_GPU_STAGE_ATTENTION, flops, bytes, s, [&] {
             return check(pkgpu::launch_attention(a, n, s), "attention");
         });
@@ -480,20 +489,32 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
     if (e->pe_center - Tmax + 1 < 0 || e->pe_center + Tmax > e->pe_rows)
         return error(PK_GPU_EINVAL, "positional table too small for %d frames", Tmax);
 
-    // chunks grouped by length: table entries [first, first + count) hold their rows
+    // chunks grouped by length: table entries [first, first + count) hold their
+    // rows; the lengths follow at entry rows_cap
     std::map<int, std::vector<int>> by_len;
     for (const Chunk& c : chunks) by_len[c.in_len].push_back(c.row);
-    std::vector<int> table;
+    std::vector<int> table, lens;
     std::map<int, std::pair<int, int>> groups;
     for (const auto& g : by_len) {
         groups[g.first] = {(int)table.size(), (int)g.second.size()};
         table.insert(table.end(), g.second.begin(), g.second.end());
+        lens.insert(lens.end(), g.second.size(), g.first);
     }
     int rc = workspace(e, (size_t)R, (size_t)(2 * Tmax - 1), table.size(), s);
     if (rc) return rc;
-    if ((rc = check(hipMemcpyAsync(e->rows_tab, table.data(), table.size() * sizeof(int),
-                                   hipMemcpyHostToDevice, s), "chunk table")))
-        return rc;
+    std::vector<int> want(2 * e->rows_cap, 0);
+    std::copy(table.begin(), table.end(), want.begin());
+    std::copy(lens.begin(), lens.end(), want.begin() + e->rows_cap);
+    if (want != e->tab_host) {
+        // A previous copy may still be queued: wait for it before the host
+        // table it reads is rewritten.
+        if ((rc = check(hipStreamSynchronize(s), "encoder stream"))) return rc;
+        e->tab_host.swap(want);
+        if ((rc = check(hipMemcpyAsync(e->rows_tab, e->tab_host.data(),
+                                       e->tab_host.size() * sizeof(int), hipMemcpyHostToDevice, s),
+                        "chunk table")))
+            return rc;
+    }
     // every chunk's input rows (encoder.c:552-553)
     for (const Chunk& c : chunks) {
         const size_t n = (size_t)c.in_len * kD * 4;

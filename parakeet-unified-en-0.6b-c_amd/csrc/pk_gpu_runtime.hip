@@ -503,16 +503,16 @@ int pk_gpu_config_info(int index, int* family, int* mfma, int* cw, int* wgm, int
     return PK_GPU_OK;
 }
 
-int pk_gpu_pick_config(int M, int N, int K)
+int pk_gpu_pick_config(int M, int N, int K) { return pkgpu::choose_config_index(M, N, K, pkgpu::W_I8); }
+
+int pk_gpu_pick_config_bits(int M, int N, int K, int bits)
 {
-    pkgpu::TileConfig t = pkgpu::choose_config(M, N, K);
-    for (int i = 0; i < pkgpu::num_configs(); ++i) {
-        pkgpu::TileConfig u = pkgpu::config_at(i);
-        if (u.family == t.family && u.mfma == t.mfma && u.cw == t.cw && u.wgm == t.wgm &&
-            u.wgn == t.wgn && u.kt == t.kt)
-            return i;
+    switch (bits) {
+    case 4: return pkgpu::choose_config_index(M, N, K, pkgpu::W_I4);
+    case 8: return pkgpu::choose_config_index(M, N, K, pkgpu::W_I8);
+    case 32: return pkgpu::choose_config_index(M, N, K, pkgpu::W_F32);
+    default: return -1;
     }
-    return 0;
 }
 
 int pk_gpu_force_config(int index)

@@ -42,6 +42,7 @@ _PROTOS = {
     "pk_gpu_num_configs": (_i, []),
     "pk_gpu_config_info": (_i, [_i, _p, _p, _p, _p, _p, _p]),
     "pk_gpu_pick_config": (_i, [_i, _i, _i]),
+    "pk_gpu_pick_config_bits": (_i, [_i, _i, _i, _i]),
     "pk_gpu_force_config": (_i, [_i]),
     "pk_gpu_layer_norm_dev": (_i, [_p, _p, _p, _p, _i, _i, _p]),
     "pk_gpu_attention_dev": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p]),

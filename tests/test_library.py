@@ -80,7 +80,7 @@ def test_tile_configs_are_well_formed():
     cfgs = pk.configs()
     assert len(cfgs) >= 3
     for fam, mf, cw, wgm, wgn, kt in cfgs:
-        assert fam in "RXS" and mf in (4, 16, 32) and cw >= 1 and wgm >= 1 and wgn >= 1
+        assert fam in "RXSY" and mf in (4, 16, 32) and cw >= 1 and wgm >= 1 and wgn >= 1
         assert (128 if fam == "S" else 64) * wgm * wgn <= 1024 and kt % 16 == 0
     lib = pk.load()
     for shape in [(32, 3072, 1024), (375, 4096, 1024), (375, 1024, 4096), (3312, 4096, 1024)]:
