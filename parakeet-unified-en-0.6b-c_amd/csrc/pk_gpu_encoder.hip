@@ -50,6 +50,9 @@ struct DevBlock {
     DevWeight ff1_w1, ff1_w2, ff2_w1, ff2_w2, qkv, pos, out, pw1t, pw2t;
     const float *ff1_b1, *ff1_b2, *ff2_b1, *ff2_b2, *qkv_b, *out_b, *pu, *pv;
     const float *pw1_b, *dw_w, *dw_b, *pw2_b;
+    // linear_pos(pe_slice(p_T)) [2 p_T - 1][kD], computed once at creation: a
+    // chunk of T <= p_T rows reads its rows [p_T - T, p_T + T - 1)
+    const float* P = nullptr;
 };
 
 struct Chunk {
@@ -84,10 +87,11 @@ struct pk_gpu_encoder {
     size_t weight_bytes = 0;
     const float* pe = nullptr;          // [pe_rows][kD]
     int pe_rows = 0, pe_center = 0;
+    int p_T = 0;                        // longest chunk the blocks' projections cover
     hipStream_t stream = nullptr;
     // workspace, grown on demand
-    size_t ws_rows = 0, ws_prow = 0;
-    float *x = nullptr, *ln = nullptr, *h = nullptr, *att = nullptr, *P = nullptr;
+    size_t ws_rows = 0;
+    float *x = nullptr, *ln = nullptr, *h = nullptr, *att = nullptr;
     int* rows_tab = nullptr;            // device: chunk rows [rows_cap], then chunk lengths [rows_cap]
     size_t rows_cap = 0;
     std::vector<int> tab_host;          // what rows_tab was last given (kept alive for the copy)
@@ -233,29 +237,27 @@ void drop_graphs(pk_gpu_encoder* e)
 void free_workspace(pk_gpu_encoder* e)
 {
     drop_graphs(e);
-    for (float* p : {e->x, e->ln, e->h, e->att, e->P})
+    for (float* p : {e->x, e->ln, e->h, e->att})
         if (p) (void)hipFree(p);
     if (e->rows_tab) (void)hipFree(e->rows_tab);
-    e->x = e->ln = e->h = e->att = e->P = nullptr;
+    e->x = e->ln = e->h = e->att = nullptr;
     e->rows_tab = nullptr;
     e->tab_host.clear();
-    e->ws_rows = e->ws_prow = e->rows_cap = e->ws_bytes = 0;
+    e->ws_rows = e->rows_cap = e->ws_bytes = 0;
 }
 
 // Grows the workspace; the old one may still be read by work queued on `s`.
-int workspace(pk_gpu_encoder* e, size_t rows, size_t prow, size_t n_chunks, hipStream_t s)
+int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, hipStream_t s)
 {
-    if (rows <= e->ws_rows && prow <= e->ws_prow && n_chunks <= e->rows_cap) return PK_GPU_OK;
+    if (rows <= e->ws_rows && n_chunks <= e->rows_cap) return PK_GPU_OK;
     hipError_t r = hipStreamSynchronize(s);
     if (r != hipSuccess) return hip_error(r, "encoder stream");
     rows = std::max(rows, e->ws_rows);
-    prow = std::max(prow, e->ws_prow);
     n_chunks = std::max(n_chunks, e->rows_cap);
     free_workspace(e);
-    const size_t bytes[5] = {rows * kD * 4, rows * kD * 4, rows * kFF * 4, rows * kD * 4,
-                             prow * kD * 4};
-    float** dst[5] = {&e->x, &e->ln, &e->h, &e->att, &e->P};
-    for (int i = 0; i < 5; ++i) {
+    const size_t bytes[4] = {rows * kD * 4, rows * kD * 4, rows * kFF * 4, rows * kD * 4};
+    float** dst[4] = {&e->x, &e->ln, &e->h, &e->att};
+    for (int i = 0; i < 4; ++i) {
         if (hipMalloc(reinterpret_cast<void**>(dst[i]), bytes[i]) != hipSuccess) {
             free_workspace(e);
             return error(PK_GPU_ENOMEM, "encoder workspace of %zu bytes failed", bytes[i]);
@@ -267,7 +269,6 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t prow, size_t n_chunks, hipS
         return error(PK_GPU_ENOMEM, "encoder chunk table failed");
     }
     e->ws_rows = rows;
-    e->ws_prow = prow;
     e->rows_cap = n_chunks;
     return PK_GPU_OK;
 }
@@ -416,12 +417,10 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
     // self-attention (encoder.c:300-424)
     if ((rc = layer_norm(e, x, b.ln_sa_w, b.ln_sa_b, ln, R, s))) return rc;
     if ((rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s))) return rc;
-    const float* pe_slice = e->pe + (size_t)(e->pe_center - Tmax + 1) * kD;
-    if ((rc = gemm(e, b.pos, pe_slice, 2 * Tmax - 1, e->P, nullptr, pkgpu::EPI_NONE, s))) return rc;
     {
         // every chunk in one launch, each with its own length
         int n = 0;
-        double flops = 0.0, bytes = 4.0 * (2 * Tmax - 1) * kD;
+        double flops = 0.0, bytes = 4.0 * (2 * Tmax - 1) * kD;   // the P rows read
         for (const auto& g : groups) {
             const double T = g.first, c = g.second.second;
             n += g.second.second;
@@ -430,7 +429,7 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
         }
         pkgpu::AttnArgs a{};
         a.qkv = h; a.ldq = 3 * kD;
-        a.P = e->P; a.ldp = kD;
+        a.P = b.P + (size_t)(e->p_T - Tmax) * kD; a.ldp = kD;
         a.pos_bias_u = b.pu; a.pos_bias_v = b.pv;
         a.out = att; a.ldo = kD;
         a.chunk_rows = e->rows_tab;
@@ -486,7 +485,7 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
     if (Tmax > pkgpu::kAttnMaxT)
         return error(PK_GPU_ENOTSUP, "a sequence of %d frames exceeds the %d-frame attention limit "
                      "(use chunks)", Tmax, pkgpu::kAttnMaxT);
-    if (e->pe_center - Tmax + 1 < 0 || e->pe_center + Tmax > e->pe_rows)
+    if (Tmax > e->p_T)
         return error(PK_GPU_EINVAL, "positional table too small for %d frames", Tmax);
 
     // chunks grouped by length: table entries [first, first + count) hold their
@@ -500,7 +499,7 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
         table.insert(table.end(), g.second.begin(), g.second.end());
         lens.insert(lens.end(), g.second.size(), g.first);
     }
-    int rc = workspace(e, (size_t)R, (size_t)(2 * Tmax - 1), table.size(), s);
+    int rc = workspace(e, (size_t)R, table.size(), s);
     if (rc) return rc;
     std::vector<int> want(2 * e->rows_cap, 0);
     std::copy(table.begin(), table.end(), want.begin());
@@ -658,6 +657,27 @@ int dev_stream(void* stream, hipStream_t* s)
     return rc;
 }
 
+// Every block's linear_pos over the positional slice of the longest chunk
+// the table allows (attention's limit at most).  A chunk of T rows uses the
+// slice pe[centre - T + 1, centre + T - 1], rows p_T - T onwards of this one,
+// and each projected row depends only on its own input row, so the rows are
+// the ones the reference computes per chunk (encoder.c:319-338).
+int project_positions(pk_gpu_encoder* e)
+{
+    e->p_T = std::min({pkgpu::kAttnMaxT, e->pe_center + 1, e->pe_rows - e->pe_center});
+    const int L = 2 * e->p_T - 1;
+    const float* slice = e->pe + (size_t)(e->pe_center - e->p_T + 1) * kD;
+    for (DevBlock& b : e->blocks) {
+        void* d = nullptr;
+        int rc = dev_alloc(e, (size_t)L * kD * 4, &d);
+        if (!rc) rc = gemm(e, b.pos, slice, L, static_cast<float*>(d), nullptr, pkgpu::EPI_NONE,
+                           e->stream);
+        if (rc) return rc;
+        b.P = static_cast<const float*>(d);
+    }
+    return PK_GPU_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -683,6 +703,7 @@ int pk_gpu_encoder_create(pk_gpu_encoder** out, const pk_gpu_block_weights* bloc
     if (!rc) rc = upload_f(e, pe_table, (size_t)pe_rows * kD, "pe_table", &e->pe);
     e->pe_rows = pe_rows;
     e->pe_center = pe_center;
+    if (!rc) rc = project_positions(e);
     if (!rc) rc = check(hipStreamSynchronize(e->stream), "weight upload");
     if (rc) {
         pk_gpu_encoder_destroy(e);
