@@ -436,6 +436,8 @@ def encoder_mode(args):
     enc = ctypes.c_void_p()
     pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(model.blocks, ctypes.c_void_p),
             N_BLOCKS, model.pe.ctypes.data, PE_ROWS, PE_CENTER)
+    if args.groups:
+        pk.call("pk_gpu_encoder_set_groups", enc, args.groups)
     dx = torch.from_numpy(x).to(dev)
     dout = torch.empty_like(dx)
 
@@ -507,7 +509,8 @@ def encoder_mode(args):
                                "3200 frames, 8 chunks (408/416 rows) run as one batch, "
                                f"GEMM M = {sum(rows)}",
                    "frames": ENC_FRAMES, "chunk": ENC_CHUNK, "overlap": ENC_OVERLAP,
-                   "chunk_rows": rows, "blocks": N_BLOCKS, "d_model": D, "d_ff": FF,
+                   "chunk_rows": rows, "row_groups": args.groups or 2, "blocks": N_BLOCKS,
+                   "d_model": D, "d_ff": FF,
                    "device_bytes": lib.pk_gpu_encoder_bytes(enc)},
         "stages": stages,
         "profiled_ms_per_step": round(prof_ms / KP, 3),
@@ -538,6 +541,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 256 MiB device-to-device copies (the reference "
                          "reading for FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--groups", type=int, default=0,
+                    help="encoder row groups replayed concurrently (default: the library's)")
     ap.add_argument("--gemm", action="append", default=[], metavar="KIND:MxNxK",
                     help="instead of the encoder, time single GEMMs (kind i4, i8 or f32); "
                          "one JSON line each")

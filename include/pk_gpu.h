@@ -305,6 +305,16 @@ int pk_gpu_encoder_profile(pk_gpu_encoder *enc, int enable);
  * once).  Waits for the profiled runs to finish.  Any pointer may be NULL. */
 int pk_gpu_encoder_profile_read(pk_gpu_encoder *enc, int stage, double *ms, long long *launches,
                                 double *flops, double *bytes);
+/* Rows of a chunked input are split into n_groups groups of whole chunks
+ * (default 2, at most PK_GPU_MAX_GROUPS; never more than the chunks) that
+ * run_dev replays concurrently: group 0 on the caller's stream, the others on
+ * the encoder's side streams, joined before the output copies.  Every
+ * operation of a block is row-wise or per chunk, so the result does not
+ * depend on the grouping.  No counterpart in the reference (which runs the
+ * chunks one after another); it overlaps one group's latency-bound kernels
+ * and launch tails with the other's GEMMs.  Profiled runs use one group. */
+#define PK_GPU_MAX_GROUPS 4
+int pk_gpu_encoder_set_groups(pk_gpu_encoder *enc, int n_groups);
 void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
 
 /* ---- tuning / introspection ------------------------------------------- */

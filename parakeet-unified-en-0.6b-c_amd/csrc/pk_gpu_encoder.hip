@@ -59,6 +59,16 @@ struct Chunk {
     int in_start, in_len, out_start, out_len, left_ov, row;   // row: first row in the batch
 };
 
+// Whole chunks occupying batch rows [r0, r0 + R), run as one unit: its
+// chunks are entries [tab, tab + n) of the device chunk table, with rows
+// relative to r0, ordered by length; by_len maps a length to (first entry,
+// count).  Every workspace buffer is partitioned by rows, so groups do not
+// share memory and may run concurrently.
+struct RowGroup {
+    int r0 = 0, R = 0, Tmax = 0, tab = 0, n = 0;
+    std::map<int, std::pair<int, int>> by_len;
+};
+
 constexpr int kMels = 128;        // PK_N_MELS
 constexpr int kSub = 256;         // PK_SUB_CHANNELS
 
@@ -105,7 +115,13 @@ struct pk_gpu_encoder {
     // the 24 blocks' launches captured once per (T, chunk, overlap) and
     // replayed; their device pointers are the workspace's, so a workspace
     // change drops them
-    std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
+    std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;   // (T, chunk, overlap, group)
+    // Row groups replayed concurrently: group 0 on the caller's stream, group
+    // g > 0 on side[g - 1], joined through events around the replay.
+    int n_groups = 2;
+    std::vector<hipStream_t> side;
+    std::vector<hipEvent_t> side_done;
+    hipEvent_t inputs_ready = nullptr;
     // pre-encode: weights and two ping-pong buffers, grown on demand
     DevPreEncode pre;
     float *pre_a = nullptr, *pre_b = nullptr, *pre_x = nullptr;
@@ -398,15 +414,22 @@ int layer_norm(pk_gpu_encoder* e, const float* x, const float* g, const float* b
     });
 }
 
-// One conformer block (encoder.c:479-491) over all chunks' rows.
-int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
-              const std::map<int, std::pair<int, int>>& groups, hipStream_t s)
+// One conformer block (encoder.c:479-491) over one row group.
+int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream_t s)
 {
     int rc;
-    float *x = e->x, *ln = e->ln, *h = e->h, *att = e->att;
-    auto ffn = [&](const float* g, const float* be, const DevWeight& w1, const float* b1,
+    const int R = g.R, Tmax = g.Tmax;
+    // h holds [R][4096], [R][3072] or [R][2048] rows: a group's part is sized
+    // for the widest
+    float* x = e->x + (size_t)g.r0 * kD;
+    float* ln = e->ln + (size_t)g.r0 * kD;
+    float* h = e->h + (size_t)g.r0 * kFF;
+    float* att = e->att + (size_t)g.r0 * kD;
+    const int* rows = e->rows_tab + g.tab;
+    const int* lens = e->rows_tab + e->rows_cap + g.tab;
+    auto ffn = [&](const float* gm, const float* be, const DevWeight& w1, const float* b1,
                    const DevWeight& w2, const float* b2) {
-        int r = layer_norm(e, x, g, be, ln, R, s);
+        int r = layer_norm(e, x, gm, be, ln, R, s);
         if (!r) r = gemm(e, w1, ln, R, h, b1, pkgpu::EPI_SWISH, s);            // encoder.c:193-196
         if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s);     // encoder.c:198-216
         return r;
@@ -418,12 +441,10 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
     if ((rc = layer_norm(e, x, b.ln_sa_w, b.ln_sa_b, ln, R, s))) return rc;
     if ((rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s))) return rc;
     {
-        // every chunk in one launch, each with its own length
-        int n = 0;
+        // every chunk of the group in one launch, each with its own length
         double flops = 0.0, bytes = 4.0 * (2 * Tmax - 1) * kD;   // the P rows read
-        for (const auto& g : groups) {
-            const double T = g.first, c = g.second.second;
-            n += g.second.second;
+        for (const auto& l : g.by_len) {
+            const double T = l.first, c = l.second.second;
             flops += 6.0 * T * T * kD * c;     // Q_u K^T, shifted Q_v P^T, scores x V
             bytes += (4.0 * T * 3 * kD + 4.0 * T * kD) * c;
         }
@@ -432,11 +453,11 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
         a.P = b.P + (size_t)(e->p_T - Tmax) * kD; a.ldp = kD;
         a.pos_bias_u = b.pu; a.pos_bias_v = b.pv;
         a.out = att; a.ldo = kD;
-        a.chunk_rows = e->rows_tab;
-        a.chunk_T = e->rows_tab + e->rows_cap;
+        a.chunk_rows = rows;
+        a.chunk_T = lens;
         a.T = Tmax; a.H = kHeads;
         rc = timed(e, PK_GPU_STAGE_ATTENTION, flops, bytes, s, [&] {
-            return check(pkgpu::launch_attention(a, n, s), "attention");
+            return check(pkgpu::launch_attention(a, g.n, s), "attention");
         });
         if (rc) return rc;
     }
@@ -449,16 +470,16 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
         return check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu");
     });
     if (rc) return rc;
-    for (const auto& g : groups) {
+    for (const auto& l : g.by_len) {
         pkgpu::DwArgs d{};
         d.x = att; d.ldx = kD;
         d.w = b.dw_w; d.b = b.dw_b;
         d.out = ln; d.ldo = kD;
-        d.chunk_rows = e->rows_tab + g.second.first;
-        d.T = g.first; d.C = kD; d.K = kConvK; d.swish = 1;
-        const double bytes = 8.0 * g.first * kD * g.second.second;
+        d.chunk_rows = rows + l.second.first;
+        d.T = l.first; d.C = kD; d.K = kConvK; d.swish = 1;
+        const double bytes = 8.0 * l.first * kD * l.second.second;
         rc = timed(e, PK_GPU_STAGE_CONV, 0.0, bytes, s, [&] {
-            return check(pkgpu::launch_depthwise(d, g.second.second, s), "depthwise conv");
+            return check(pkgpu::launch_depthwise(d, l.second.second, s), "depthwise conv");
         });
         if (rc) return rc;
     }
@@ -467,6 +488,54 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, int R, int Tmax,
     // feed-forward 2 and the block's output LayerNorm (encoder.c:486-487)
     if ((rc = ffn(b.ln_ff2_w, b.ln_ff2_b, b.ff2_w1, b.ff2_b1, b.ff2_w2, b.ff2_b2))) return rc;
     return layer_norm(e, x, b.ln_out_w, b.ln_out_b, x, R, s);
+}
+
+// At least n side streams and their completion events, plus the event that
+// marks the inputs copied (created on first use, kept until destroy).
+int side_streams(pk_gpu_encoder* e, int n)
+{
+    if (n > 0 && !e->inputs_ready) {
+        hipError_t r = hipEventCreateWithFlags(&e->inputs_ready, hipEventDisableTiming);
+        if (r != hipSuccess) return hip_error(r, "hipEventCreate");
+    }
+    while ((int)e->side.size() < n) {
+        hipStream_t st = nullptr;
+        hipEvent_t ev = nullptr;
+        hipError_t r = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+        if (r != hipSuccess) return hip_error(r, "hipStreamCreate");
+        r = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (r != hipSuccess) {
+            (void)hipStreamDestroy(st);
+            return hip_error(r, "hipEventCreate");
+        }
+        e->side.push_back(st);
+        e->side_done.push_back(ev);
+    }
+    return PK_GPU_OK;
+}
+
+// Consecutive chunks split into at most n groups of about equal rows (every
+// group at least one chunk).
+std::vector<RowGroup> plan_groups(const std::vector<Chunk>& chunks, int n)
+{
+    const int nc = (int)chunks.size();
+    n = std::max(1, std::min(n, nc));
+    int R = 0;
+    for (const Chunk& c : chunks) R += c.in_len;
+    std::vector<RowGroup> groups(n);
+    int i = 0;
+    for (int g = 0; g < n; ++g) {
+        RowGroup& rg = groups[g];
+        rg.r0 = chunks[i].row;
+        const long long target = (long long)R * (g + 1) / n;   // rows groups 0..g cover
+        do {
+            rg.R += chunks[i].in_len;
+            rg.Tmax = std::max(rg.Tmax, chunks[i].in_len);
+            ++i;
+        } while (i < nc - (n - 1 - g) &&
+                 (g == n - 1 || chunks[i].row + chunks[i].in_len / 2 <= target));
+    }
+    return groups;
 }
 
 int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out, hipStream_t s,
@@ -488,16 +557,27 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
     if (Tmax > e->p_T)
         return error(PK_GPU_EINVAL, "positional table too small for %d frames", Tmax);
 
-    // chunks grouped by length: table entries [first, first + count) hold their
-    // rows; the lengths follow at entry rows_cap
-    std::map<int, std::vector<int>> by_len;
-    for (const Chunk& c : chunks) by_len[c.in_len].push_back(c.row);
+    // Row groups; each group's chunks are table entries [tab, tab + n), by
+    // length, with rows relative to the group; the lengths follow at entry
+    // rows_cap.
+    std::vector<RowGroup> groups = plan_groups(chunks, e->prof ? 1 : e->n_groups);
     std::vector<int> table, lens;
-    std::map<int, std::pair<int, int>> groups;
-    for (const auto& g : by_len) {
-        groups[g.first] = {(int)table.size(), (int)g.second.size()};
-        table.insert(table.end(), g.second.begin(), g.second.end());
-        lens.insert(lens.end(), g.second.size(), g.first);
+    {
+        size_t ci = 0;
+        for (RowGroup& g : groups) {
+            std::map<int, std::vector<int>> by_len;
+            for (int got = 0; got < g.R; ++ci) {
+                by_len[chunks[ci].in_len].push_back(chunks[ci].row - g.r0);
+                got += chunks[ci].in_len;
+            }
+            g.tab = (int)table.size();
+            for (const auto& l : by_len) {
+                g.by_len[l.first] = {(int)table.size() - g.tab, (int)l.second.size()};
+                table.insert(table.end(), l.second.begin(), l.second.end());
+                lens.insert(lens.end(), l.second.size(), l.first);
+            }
+            g.n = (int)table.size() - g.tab;
+        }
     }
     int rc = workspace(e, (size_t)R, table.size(), s);
     if (rc) return rc;
@@ -523,30 +603,50 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
         });
         if (rc) return rc;
     }
-    if (e->prof) {            // eager, with an event pair around every launch
+    if (e->prof) {            // eager, one group, with an event pair around every launch
         for (const DevBlock& b : e->blocks)
-            if ((rc = run_block(e, b, R, Tmax, groups, s))) return rc;
+            if ((rc = run_block(e, b, groups[0], s))) return rc;
     } else {
-        // One graph per chunking of the input: captured on the encoder's own
-        // stream (the null stream cannot capture), launched on `s`.
-        const auto key = std::make_tuple(T, chunk, ov);
-        auto it = e->graphs.find(key);
-        if (it == e->graphs.end()) {
-            if ((rc = check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal),
-                            "graph capture")))
-                return rc;
-            for (const DevBlock& b : e->blocks)
-                if ((rc = run_block(e, b, R, Tmax, groups, e->stream))) break;
-            hipGraph_t g = nullptr;
-            const hipError_t end = hipStreamEndCapture(e->stream, &g);
-            if (!rc && end != hipSuccess) rc = hip_error(end, "graph capture");
-            hipGraphExec_t ex = nullptr;
-            if (!rc) rc = check(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "graph instantiate");
-            if (g) (void)hipGraphDestroy(g);
-            if (rc) return rc;
-            it = e->graphs.emplace(key, ex).first;
+        if ((rc = side_streams(e, (int)groups.size() - 1))) return rc;
+        // One graph per chunking of the input and group: captured on the
+        // encoder's own stream (the null stream cannot capture).
+        std::vector<hipGraphExec_t> ex(groups.size(), nullptr);
+        for (size_t gi = 0; gi < groups.size(); ++gi) {
+            const auto key = std::make_tuple(T, chunk, ov, (int)gi);
+            auto it = e->graphs.find(key);
+            if (it == e->graphs.end()) {
+                if ((rc = check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal),
+                                "graph capture")))
+                    return rc;
+                for (const DevBlock& b : e->blocks)
+                    if ((rc = run_block(e, b, groups[gi], e->stream))) break;
+                hipGraph_t g = nullptr;
+                const hipError_t end = hipStreamEndCapture(e->stream, &g);
+                if (!rc && end != hipSuccess) rc = hip_error(end, "graph capture");
+                hipGraphExec_t x_ = nullptr;
+                if (!rc) rc = check(hipGraphInstantiate(&x_, g, nullptr, nullptr, 0), "graph instantiate");
+                if (g) (void)hipGraphDestroy(g);
+                if (rc) return rc;
+                it = e->graphs.emplace(key, x_).first;
+            }
+            ex[gi] = it->second;
         }
-        if ((rc = check(hipGraphLaunch(it->second, s), "graph launch"))) return rc;
+        // group 0 on `s`; the others on side streams that start after the
+        // input copies and that `s` waits for before the output copies
+        if (groups.size() > 1 &&
+            (rc = check(hipEventRecord(e->inputs_ready, s), "encoder event")))
+            return rc;
+        for (size_t gi = 1; gi < groups.size(); ++gi) {
+            hipStream_t ss = e->side[gi - 1];
+            if ((rc = check(hipStreamWaitEvent(ss, e->inputs_ready, 0), "encoder event")) ||
+                (rc = check(hipGraphLaunch(ex[gi], ss), "graph launch")) ||
+                (rc = check(hipEventRecord(e->side_done[gi - 1], ss), "encoder event")))
+                return rc;
+        }
+        if ((rc = check(hipGraphLaunch(ex[0], s), "graph launch"))) return rc;
+        for (size_t gi = 1; gi < groups.size(); ++gi)
+            if ((rc = check(hipStreamWaitEvent(s, e->side_done[gi - 1], 0), "encoder event")))
+                return rc;
     }
     // the centre rows of every chunk (encoder.c:567-569)
     for (const Chunk& c : chunks) {
@@ -771,13 +871,33 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
 {
     if (!enc) return;
     if (enc->stream) (void)hipStreamSynchronize(enc->stream);
+    for (hipStream_t st : enc->side) (void)hipStreamSynchronize(st);
     (void)collect(enc);
     for (hipEvent_t ev : enc->event_pool) (void)hipEventDestroy(ev);
     free_workspace(enc);
     free_pre(enc);
     for (void* p : enc->allocs) (void)hipFree(p);
+    for (hipEvent_t ev : enc->side_done) (void)hipEventDestroy(ev);
+    if (enc->inputs_ready) (void)hipEventDestroy(enc->inputs_ready);
+    for (hipStream_t st : enc->side) (void)hipStreamDestroy(st);
     if (enc->stream) (void)hipStreamDestroy(enc->stream);
     delete enc;
+}
+
+int pk_gpu_encoder_set_groups(pk_gpu_encoder* enc, int n_groups)
+{
+    if (!enc) return error(PK_GPU_EINVAL, "encoder is NULL");
+    if (n_groups < 1 || n_groups > PK_GPU_MAX_GROUPS)
+        return error(PK_GPU_EINVAL, "n_groups = %d (1..%d)", n_groups, PK_GPU_MAX_GROUPS);
+    int rc = pkgpu::rt::bind(nullptr);
+    if (rc) return rc;
+    if (n_groups != enc->n_groups) {
+        (void)hipStreamSynchronize(enc->stream);
+        for (hipStream_t st : enc->side) (void)hipStreamSynchronize(st);
+        drop_graphs(enc);
+        enc->n_groups = n_groups;
+    }
+    return PK_GPU_OK;
 }
 
 int pk_gpu_encoder_set_pre_encode(pk_gpu_encoder* enc, const pk_gpu_pre_encode_weights* w)

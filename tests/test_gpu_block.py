@@ -249,6 +249,40 @@ def test_encoder_graph_replays_match_eager(dev, enc2):
     pk.call("pk_gpu_encoder_profile_read", enc2.h, 0, ctypes.byref(ms), None, None, None)
 
 
+@pytest.mark.parametrize("n_groups", [1, 2, 3, 4])
+def test_encoder_row_groups_are_bit_identical(dev, enc2, n_groups):
+    """Replays split the chunks into row groups replayed concurrently (group 0
+    on the caller's stream, the others on side streams); eager profiled runs
+    use one group.  The output must not depend on the grouping, through both
+    the host and the device-pointer entry points."""
+    for T in (3200, 900):              # 8 chunks; 3 chunks (4 groups clamp to 3)
+        x = rows(T, 1024)
+        pk.call("pk_gpu_encoder_profile", enc2.h, 1)
+        want = enc2.run(x, chunk=400)
+        pk.call("pk_gpu_encoder_profile", enc2.h, 0)
+        pk.call("pk_gpu_encoder_set_groups", enc2.h, n_groups)
+        try:
+            for rep in range(3):
+                assert bits_equal(enc2.run(x, chunk=400), want), f"T {T} replay {rep}"
+            dx = dev.put(x)
+            dout = dev.torch.empty_like(dx)
+            for rep in range(2):
+                dout.fill_(float("nan"))
+                pk.call("pk_gpu_encoder_run_dev", enc2.h, dx.data_ptr(), T, 400, 8, dout.data_ptr(),
+                        dev.stream())
+                sync(dev)
+                assert bits_equal(dout.cpu().numpy(), want), f"T {T} dev replay {rep}"
+        finally:
+            pk.call("pk_gpu_encoder_set_groups", enc2.h, 2)
+
+
+def test_encoder_group_count_is_checked(dev, enc2):
+    lib = pk.load()
+    assert lib.pk_gpu_encoder_set_groups(enc2.h, 0) == -1
+    assert lib.pk_gpu_encoder_set_groups(enc2.h, 5) == -1
+    assert lib.pk_gpu_encoder_set_groups(None, 2) == -1
+
+
 def test_encoder_rejects_oversized_sequence(dev, enc2):
     x = np.zeros((600, 1024), np.float32)
     out = np.empty_like(x)
