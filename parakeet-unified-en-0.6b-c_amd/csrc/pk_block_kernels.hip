@@ -175,15 +175,34 @@ struct TileRegs {
     float4 v[4];
 };
 
-__device__ inline void load_half(TileRegs& t, const float* src, int ld, int r0, int n, int c0)
+// The rows of one head's keys, values or positions: row r at src + r * ld,
+// rows [0, n) valid, 128 columns each.  A tile's loads go through a buffer
+// descriptor that starts at the tile's first row and ends after row n - 1,
+// so rows past the end read as 0 without a predicate (the hardware's range
+// check) and each thread's offsets are the same for every tile.
+struct TileSrc {
+    const float* src;
+    int ld, n;
+    __device__ __amdgpu_buffer_rsrc_t at(int r0) const     // r0 >= 0, uniform
+    {
+        const long long left = ((long long)(n - 1 - r0) * ld + kDh) * 4;
+        return tiles::make_rsrc(src + (size_t)r0 * ld, left > 0 ? (uint32_t)left : 0u);
+    }
+};
+
+__device__ inline float4 as_float4(tiles::v4u u)
 {
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                       __uint_as_float(u.w));
+}
+
+__device__ inline void load_half(TileRegs& t, const TileSrc& s, int r0, int c0)
+{
+    const __amdgpu_buffer_rsrc_t rs = s.at(r0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int idx = threadIdx.x + 256 * q;
-        const int gr = r0 + (idx >> 4);
-        t.v[q] = (gr >= 0 && gr < n)
-                     ? *reinterpret_cast<const float4*>(src + (size_t)gr * ld + c0 + 4 * (idx & 15))
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        t.v[q] = as_float4(tiles::ld_v4(rs, (uint32_t)((idx >> 4) * s.ld + c0 + 4 * (idx & 15)) * 4u));
     }
 }
 
@@ -196,14 +215,13 @@ __device__ inline void store_half(float* tile, const TileRegs& t)
     }
 }
 
-__device__ inline void load_vtile(TileRegs& t, const float* src, int ld, int r0, int n)
+__device__ inline void load_vtile(TileRegs& t, const TileSrc& s, int r0)
 {
+    const __amdgpu_buffer_rsrc_t rs = s.at(r0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int idx = threadIdx.x + 256 * q;
-        const int gr = r0 + (idx >> 5);
-        t.v[q] = gr < n ? *reinterpret_cast<const float4*>(src + (size_t)gr * ld + 4 * (idx & 31))
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        t.v[q] = as_float4(tiles::ld_v4(rs, (uint32_t)((idx >> 5) * s.ld + 4 * (idx & 31)) * 4u));
     }
 }
 
@@ -261,12 +279,12 @@ __device__ inline void score_sums(const v4f (&acc)[2][8], float (&out)[2][4])
 }
 
 // The 32 x 64 scores of source rows [c, c + 64) (keys or positions; rows
-// outside [0, n) read 0), through the two half tiles: pre holds the first
-// half on entry and the next tile's first half (rows [c + 64, ...), when
-// next is set) on return.  Both barriers of each half are taken by the whole
+// past the end read 0), through the two half tiles: pre holds the first half
+// on entry and the next tile's first half (rows [c + 64, ...), when next is
+// set) on return.  Both barriers of each half are taken by the whole
 // workgroup.
-__device__ inline void score_block(float* tile, TileRegs& pre, const float* src, int ld, int c,
-                                   int n, bool next, const float (&a)[2][8], float (&out)[2][4])
+__device__ inline void score_block(float* tile, TileRegs& pre, const TileSrc& src, int c, bool next,
+                                   const float (&a)[2][8], float (&out)[2][4])
 {
     v4f acc[2][8];
 #pragma unroll
@@ -275,12 +293,12 @@ __device__ inline void score_block(float* tile, TileRegs& pre, const float* src,
         for (int l = 0; l < 8; ++l) acc[g][l] = v4f{0.f, 0.f, 0.f, 0.f};
     store_half(tile, pre);
     __syncthreads();
-    load_half(pre, src, ld, c, n, 64);
+    load_half(pre, src, c, 64);
     score_half<0>(tile, a, acc);
     __syncthreads();
     store_half(tile, pre);
     __syncthreads();
-    if (next) load_half(pre, src, ld, c + 64, n, 0);
+    if (next) load_half(pre, src, c + 64, 0);
     score_half<1>(tile, a, acc);
     score_sums(acc, out);
 }
@@ -379,10 +397,11 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
 
     // AC: S[row][j] = Q_u[row] . K[j]
     TileRegs pre;
-    load_half(pre, K, p.ldq, 0, T, 0);
+    const TileSrc ks{K, p.ldq, T};
+    load_half(pre, ks, 0, 0);
     for (int j0 = 0; j0 < T; j0 += 64) {
         float o[2][4];
-        score_block(tile, pre, K, p.ldq, j0, T, j0 + 64 < T, au, o);
+        score_block(tile, pre, ks, j0, j0 + 64 < T, au, o);
         const int j = j0 + lane;
         if (j < T)
 #pragma unroll
@@ -396,10 +415,11 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
     const int r_hi = min(r0 + kAttnRows, T) - 1;
     const int L = 2 * T - 1;
     const int m_first = T - 1 - r_hi, m_last = 2 * T - 2 - r0;
-    load_half(pre, P, p.ldp, m_first, L, 0);
+    const TileSrc ps{P, p.ldp, L};
+    load_half(pre, ps, m_first, 0);
     for (int m0 = m_first; m0 <= m_last; m0 += 64) {
         float o[2][4];
-        score_block(tile, pre, P, p.ldp, m0, L, m0 + 64 <= m_last, av, o);
+        score_block(tile, pre, ps, m0, m0 + 64 <= m_last, av, o);
         // every (row, j) takes exactly one shifted BD value: read the eight
         // scores first, then write them back combined
         const int m = m0 + lane;
@@ -422,7 +442,8 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
                 if (at[g][i] >= 0) S[at[g][i]] = __fmul_rn(__fadd_rn(sc[g][i], o[g][i]), kScoreScale);
         __syncthreads();
     }
-    load_vtile(pre, V, p.ldq, 0, T);      // the first value tile, during the softmax
+    const TileSrc vs{V, p.ldq, T};
+    load_vtile(pre, vs, 0);               // the first value tile, during the softmax
 
     // Softmax of each row: 8 lanes per row, lane q owns j = q, q+8, ...
     {
@@ -471,7 +492,7 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
     for (int j0 = 0; j0 < T; j0 += 32) {
         store_vtile(tile, pre);
         __syncthreads();
-        if (j0 + 32 < T) load_vtile(pre, V, p.ldq, j0 + 32, T);
+        if (j0 + 32 < T) load_vtile(pre, vs, j0 + 32);
         const int nt = min(32, T - j0);
 #pragma unroll
         for (int jb = 0; jb < 32; jb += 16) {
