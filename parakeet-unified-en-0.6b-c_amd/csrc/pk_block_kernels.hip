@@ -420,26 +420,27 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
     for (int m0 = m_first; m0 <= m_last; m0 += 64) {
         float o[2][4];
         score_block(tile, pre, ps, m0, m0 + 64 <= m_last, av, o);
-        // every (row, j) takes exactly one shifted BD value: read the eight
-        // scores first, then write them back combined
-        const int m = m0 + lane;
+        // every (row, j) takes exactly one shifted BD value: row rl of the
+        // block takes column j = jb + rl, whose score is at S[jb + rl (sld + 1)].
+        // Read the eight scores first, then write them back combined.
+        const int jb = m0 + lane - (T - 1) + r0;
         float sc[2][4];
-        int at[2][4];
+        bool ok[2][4];
 #pragma unroll
         for (int g = 0; g < 2; ++g)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int rl = 8 * w + 4 * g + i, r = r0 + rl;
-                const int j = m - (T - 1 - r);
-                const bool ok = r < T && j >= 0 && j < T;
-                at[g][i] = ok ? rl * sld + j : -1;
-                sc[g][i] = S[ok ? rl * sld + j : 0];
+                const int rl = 8 * w + 4 * g + i;           // uniform in the wave
+                ok[g][i] = r0 + rl < T && (unsigned)(jb + rl) < (unsigned)T;
+                sc[g][i] = S[ok[g][i] ? jb + rl * (sld + 1) : 0];
             }
 #pragma unroll
         for (int g = 0; g < 2; ++g)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (at[g][i] >= 0) S[at[g][i]] = __fmul_rn(__fadd_rn(sc[g][i], o[g][i]), kScoreScale);
+                if (ok[g][i])
+                    S[jb + (8 * w + 4 * g + i) * (sld + 1)] =
+                        __fmul_rn(__fadd_rn(sc[g][i], o[g][i]), kScoreScale);
         __syncthreads();
     }
     const TileSrc vs{V, p.ldq, T};
@@ -484,32 +485,35 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
     __syncthreads();
 
     // out[row][h*128 + d] = sum over j ascending of S[row][j] * V[j][d],
-    // through 32-row value tiles
+    // through 32-row value tiles: whole blocks of 16 keys in the loop, the
+    // last T % 16 keys after it, from the last tile (still in LDS: the loop's
+    // last pass takes no closing barrier).
     v4f acc[2][2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) acc[g][0] = acc[g][1] = v4f{0.f, 0.f, 0.f, 0.f};
     const int i = lane & 3, t = lane >> 2;
-    for (int j0 = 0; j0 < T; j0 += 32) {
+    const float* srow[2] = {S + (8 * w + i) * sld + t, S + (8 * w + 4 + i) * sld + t};
+    int j0 = 0;
+    for (;; j0 += 32) {
         store_vtile(tile, pre);
         __syncthreads();
-        if (j0 + 32 < T) load_vtile(pre, vs, j0 + 32);
-        const int nt = min(32, T - j0);
+        const bool more = j0 + 32 < T;
+        if (more) load_vtile(pre, vs, j0 + 32);
 #pragma unroll
         for (int jb = 0; jb < 32; jb += 16) {
-            if (jb < nt) {
-                float a[2];
-#pragma unroll
-                for (int g = 0; g < 2; ++g) {
-                    const int jj = j0 + jb + t;
-                    a[g] = jj < T ? S[(8 * w + 4 * g + i) * sld + jj] : 0.0f;
-                }
-                if (nt - jb >= 16)
-                    pv_steps_full(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, acc);
-                else
-                    pv_steps(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, nt - jb, acc);
+            if (j0 + jb + 16 <= T) {
+                const float a[2] = {srow[0][j0 + jb], srow[1][j0 + jb]};
+                pv_steps_full(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, acc);
             }
         }
+        if (!more) break;
         __syncthreads();
+    }
+    if (T & 15) {
+        const int jb = (T & ~15) - j0;                  // 0 or 16 within the last tile
+        const int jj = (T & ~15) + t;
+        const float a[2] = {jj < T ? srow[0][T & ~15] : 0.0f, jj < T ? srow[1][T & ~15] : 0.0f};
+        pv_steps(std::make_integer_sequence<int, 16>{}, a, tile + jb * kTileLd, T & 15, acc);
     }
     float* out = p.out + (size_t)row0 * p.ldo + h * kDh;
 #pragma unroll
