@@ -506,8 +506,8 @@ def encoder_mode(args):
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "24-block mixed int4/int8 FastConformer encoder, 256 s of audio = "
-                               "3200 frames, 8 chunks (408/416 rows) run as one batch, "
-                               f"GEMM M = {sum(rows)}",
+                               f"3200 frames, 8 chunks (408/416 rows, {sum(rows)} in all) replayed "
+                               f"as {args.groups or 2} concurrent row group(s) of whole chunks",
                    "frames": ENC_FRAMES, "chunk": ENC_CHUNK, "overlap": ENC_OVERLAP,
                    "chunk_rows": rows, "row_groups": args.groups or 2, "blocks": N_BLOCKS,
                    "d_model": D, "d_ff": FF,
@@ -521,7 +521,11 @@ def encoder_mode(args):
                                "residual)",
                      "achieved": round(i4_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(i4_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": traffic, "launches_per_step": i4_launches // KP},
+                     "traffic": traffic, "launches_per_step": i4_launches // KP,
+                     "measured_in": "the profiled pass: the same steps launched one by one with one "
+                                    "row group and HIP events around every launch on its stream (the "
+                                    "timed replay overlaps two groups' kernels, which events cannot "
+                                    "separate)"},
     }
     out["cpu_baseline"] = None if args.no_cpu else encoder_cpu_baseline(model, x, args.cpu_seconds)
     lib.pk_gpu_encoder_destroy(enc)
