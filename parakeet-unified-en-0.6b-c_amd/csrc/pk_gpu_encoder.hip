@@ -35,6 +35,7 @@ constexpr int kD = 1024;          // PK_D_MODEL
 constexpr int kFF = 4096;         // PK_FF_DIM
 constexpr int kHeads = 8;         // PK_N_HEADS
 constexpr int kConvK = 9;         // PK_CONV_KERNEL
+constexpr size_t kMaxGraphs = 64; // captured block graphs kept per encoder
 
 struct DevWeight {
     WeightKind kind = pkgpu::W_F32;
@@ -609,7 +610,16 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
     } else {
         if ((rc = side_streams(e, (int)groups.size() - 1))) return rc;
         // One graph per chunking of the input and group: captured on the
-        // encoder's own stream (the null stream cannot capture).
+        // encoder's own stream (the null stream cannot capture).  A caller
+        // that sees many input lengths would keep adding graphs; past
+        // kMaxGraphs they are all dropped and recaptured on demand.
+        if (e->graphs.size() + groups.size() > kMaxGraphs &&
+            !e->graphs.count(std::make_tuple(T, chunk, ov, 0))) {
+            if ((rc = check(hipStreamSynchronize(s), "encoder stream"))) return rc;
+            for (hipStream_t st : e->side)
+                if ((rc = check(hipStreamSynchronize(st), "encoder stream"))) return rc;
+            drop_graphs(e);
+        }
         std::vector<hipGraphExec_t> ex(groups.size(), nullptr);
         for (size_t gi = 0; gi < groups.size(); ++gi) {
             const auto key = std::make_tuple(T, chunk, ov, (int)gi);

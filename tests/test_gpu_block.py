@@ -276,6 +276,18 @@ def test_encoder_row_groups_are_bit_identical(dev, enc2, n_groups):
             pk.call("pk_gpu_encoder_set_groups", enc2.h, 2)
 
 
+def test_encoder_many_chunkings(dev, enc2):
+    """Each chunking of the input keeps captured graphs (one per row group);
+    past the encoder's limit they are dropped and recaptured.  Forty input
+    lengths, each compared with its eager run, cross that limit twice over."""
+    x = rows(840, 1024)
+    for T in range(801, 841):
+        pk.call("pk_gpu_encoder_profile", enc2.h, 1)
+        want = enc2.run(x[:T], chunk=400)
+        pk.call("pk_gpu_encoder_profile", enc2.h, 0)
+        assert bits_equal(enc2.run(x[:T], chunk=400), want), f"T {T}"
+
+
 def test_encoder_group_count_is_checked(dev, enc2):
     lib = pk.load()
     assert lib.pk_gpu_encoder_set_groups(enc2.h, 0) == -1
