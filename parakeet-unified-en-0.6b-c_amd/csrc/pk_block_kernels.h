@@ -14,8 +14,11 @@ constexpr int kAttnMaxT = 512;
 constexpr int kAttnRows = 32;          // query rows per workgroup
 // LDS row stride of a workgroup's score rows for chunks of T rows, and the
 // workgroup's LDS: the score rows plus one staging tile of 64 x 68 floats.
-// At T = 416 two workgroups fit in a CU's 160 KiB.
-__host__ __device__ constexpr int attn_sld(int T) { return ((T + 15) & ~15) + 16; }
+// The stride is 8 more than a multiple of 32 floats, so rows 8 apart in
+// banks: the softmax's 4 rows x 8 lanes and the value loop's 4 rows x 8
+// keys per half wave reach 32 distinct banks.  At T = 416 two workgroups
+// fit in a CU's 160 KiB.
+__host__ __device__ constexpr int attn_sld(int T) { return ((T + 31) & ~31) + 8; }
 __host__ __device__ constexpr unsigned attn_lds_bytes(int T)
 {
     return 4u * (unsigned)(kAttnRows * attn_sld(T) + 64 * 68);
