@@ -43,13 +43,15 @@ struct AttnArgs {
 };
 
 // Depthwise convolution over time with optional Swish (tensor_ops.c:476-548,
-// encoder.c:467-469), channel c of chunk z: x[chunk_rows[z] + t][c].
+// encoder.c:467-469), channel c of chunk z: x[chunk_rows[z] + t][c] for t in
+// [0, chunk_T[z]) (all T when chunk_T is null).
 struct DwArgs {
     const float* x; int ldx;
     const float* w;            // [C][K]
     const float* b;            // [C] or null
     float* out; int ldo;
     const int* chunk_rows;     // device, n entries (null: one chunk at row 0)
+    const int* chunk_T;        // device, n entries, each in [1, T] (null: all T)
     int T, C, K;
     int swish;
 };

@@ -552,14 +552,15 @@ __global__ void glu_rows(const float* __restrict__ in, int ldi, float* out, int 
 template <int KK>
 __global__ void depthwise_swish(DwArgs p)
 {
+    const int T = p.chunk_T ? p.chunk_T[blockIdx.y] : p.T;   // this chunk's rows
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)p.T * p.C) return;
+    if (idx >= (long long)T * p.C) return;
     const int t = (int)(idx / p.C), c = (int)(idx % p.C);
     const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.y] : 0;
     const float* x = p.x + (size_t)row0 * p.ldx + c;
     const int K = KK ? KK : p.K;
     const float* wc = p.w + (size_t)c * K;
-    const int T = p.T, pad = (K - 1) / 2;
+    const int pad = (K - 1) / 2;
     const int t_hi = T - pad > pad ? T - pad : pad;
     const int t_vec = pad + (t_hi - pad) / 8 * 8;
     float val = p.b ? p.b[c] : 0.0f;

@@ -471,16 +471,17 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         return check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu");
     });
     if (rc) return rc;
-    for (const auto& l : g.by_len) {
+    {
+        // every chunk of the group in one launch, each with its own length
         pkgpu::DwArgs d{};
         d.x = att; d.ldx = kD;
         d.w = b.dw_w; d.b = b.dw_b;
         d.out = ln; d.ldo = kD;
-        d.chunk_rows = rows + l.second.first;
-        d.T = l.first; d.C = kD; d.K = kConvK; d.swish = 1;
-        const double bytes = 8.0 * l.first * kD * l.second.second;
-        rc = timed(e, PK_GPU_STAGE_CONV, 0.0, bytes, s, [&] {
-            return check(pkgpu::launch_depthwise(d, l.second.second, s), "depthwise conv");
+        d.chunk_rows = rows;
+        d.chunk_T = lens;
+        d.T = Tmax; d.C = kD; d.K = kConvK; d.swish = 1;
+        rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 8.0 * R * kD, s, [&] {
+            return check(pkgpu::launch_depthwise(d, g.n, s), "depthwise conv");
         });
         if (rc) return rc;
     }
