@@ -176,17 +176,20 @@ def test_conformer_block_gemms(dev, kind, M, N, K, name):
     assert_same(run(dev, kind, A, W, extra, Z), oracle(kind, A, W, extra, Z), name)
 
 
+@pytest.mark.parametrize("M", [3312, 1656])
 @pytest.mark.parametrize("kind,N,K", [("i4", 4096, 1024), ("i4", 1024, 4096), ("i8", 3072, 1024),
-                                      ("f32", 1024, 1024)])
-def test_batched_chunks_sampled_rows(dev, kind, N, K):
-    """M = 3312 (2x408 + 6x416 rows): full GPU GEMM, oracle on sampled rows."""
-    M = 3312
-    A, W, extra, _ = make(kind, M, N, K, f"big.{kind}.{N}")
+                                      ("i8", 1024, 1024), ("f32", 2048, 1024), ("f32", 1024, 1024)])
+def test_batched_chunks_sampled_rows(dev, kind, N, K, M):
+    """All chunks as one batch (M = 3312: 2x408 + 6x416 rows) and as one of the
+    encoder's two row groups (M = 1656), each with the tile the dispatcher
+    picks for it: full GPU GEMM, oracle on sampled rows."""
+    A, W, extra, _ = make(kind, M, N, K, f"big.{kind}.{N}.{K}.{M}")
     got = run(dev, kind, A, W, extra, np.zeros((M, N), np.float32))
-    rows = sorted({0, 1, 63, 64, 127, 128, 408, 1000, 2047, 2048, 3199, 3247, 3248, 3310, 3311})
+    rows = sorted({r for r in (0, 1, 63, 64, 127, 128, 408, 1000, 1599, 1600, 1654, 1655, 2047, 2048,
+                               3199, 3247, 3248, 3310, 3311) if r < M})
     Ar = np.ascontiguousarray(A[rows])
     want = oracle(kind, Ar, W, extra, np.zeros((len(rows), N), np.float32))
-    assert_same(got[rows], want, f"M=3312 {kind} rows {rows}")
+    assert_same(got[rows], want, f"M={M} {kind} rows {rows}")
     assert np.isfinite(got).all()
 
 
