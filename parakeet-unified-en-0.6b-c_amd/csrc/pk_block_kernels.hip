@@ -605,31 +605,46 @@ __global__ void depthwise_swish(DwArgs p)
 constexpr int kSub = 256;          // PK_SUB_CHANNELS
 
 // conv.0: 1 -> 256 channels, 3x3, stride 2, pad 1, over the image whose row
-// t is mel frame t (mel [n_mels][T], encoder.c:110-120), then ReLU.
-__global__ void conv0_relu(const float* __restrict__ mel, int T, int n_mels,
-                           const float* __restrict__ w, const float* __restrict__ b, float* out,
-                           int H1, int W1)
+// t is mel frame t (mel [n_mels][T], encoder.c:110-120), then ReLU.  One
+// workgroup per output row oh and run of kC0Run output columns, one thread
+// per channel: the run's input window (3 frames x 2 kC0Run + 1 mel bins, 0
+// outside the image) is staged in LDS by one load per thread, a channel's
+// nine weights and bias are read once, and each position stores 256
+// consecutive floats.  pk_conv2d skips the taps outside the image; here they
+// take part with x = 0.  fma(0, w, v) is v except that a zero v may change
+// sign, and the ReLU maps either zero to +0, so the outputs are the same.
+constexpr int kC0Run = 16;
+constexpr int kC0Win = 2 * kC0Run + 1;
+
+__global__ __launch_bounds__(kSub) void conv0_relu(const float* __restrict__ mel, int T, int n_mels,
+                                                   const float* __restrict__ w,
+                                                   const float* __restrict__ b, float* out, int H1,
+                                                   int W1)
 {
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)H1 * W1 * kSub) return;
-    const int c = (int)(idx % kSub);
-    const int pos = (int)(idx / kSub), ow = pos % W1, oh = pos / W1;
-    // every tap loaded first (out-of-range ones from a clamped address and
-    // skipped), then the chain over the in-range taps in order
-    float xv[9], wv[9];
-    bool ok[9];
-#pragma unroll
-    for (int k = 0; k < 9; ++k) {
-        const int ih = 2 * oh - 1 + k / 3, iw = 2 * ow - 1 + k % 3;
-        ok[k] = ih >= 0 && ih < T && iw >= 0 && iw < n_mels;
-        xv[k] = mel[(size_t)min(max(iw, 0), n_mels - 1) * T + min(max(ih, 0), T - 1)];
-        wv[k] = w[c * 9 + k];
+    __shared__ float win[3 * kC0Win];
+    const int c = threadIdx.x;
+    const int oh = blockIdx.x, ow0 = blockIdx.y * kC0Run;
+    const int ih0 = 2 * oh - 1, iw0 = 2 * ow0 - 1;
+    if (c < 3 * kC0Win) {
+        const int ih = ih0 + c / kC0Win, iw = iw0 + c % kC0Win;
+        win[c] = ih >= 0 && ih < T && iw >= 0 && iw < n_mels ? mel[(size_t)iw * T + ih] : 0.0f;
     }
-    float v = b[c];
+    float wv[9];
 #pragma unroll
-    for (int k = 0; k < 9; ++k)
-        if (ok[k]) v = __fmaf_rn(xv[k], wv[k], v);
-    out[idx] = v > 0.0f ? v : 0.0f;
+    for (int k = 0; k < 9; ++k) wv[k] = w[c * 9 + k];
+    const float bias = b[c];
+    __syncthreads();
+    const int nr = min(kC0Run, W1 - ow0);
+    float* o = out + ((size_t)oh * W1 + ow0) * kSub + c;
+#pragma unroll
+    for (int r = 0; r < kC0Run; ++r) {
+        if (r < nr) {
+            float v = bias;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) v = __fmaf_rn(win[(k / 3) * kC0Win + 2 * r + k % 3], wv[k], v);
+            o[(size_t)r * kSub] = v > 0.0f ? v : 0.0f;
+        }
+    }
 }
 
 // Depthwise 3x3, stride 2, pad 1 (conv.2 and conv.5, groups = 256).
@@ -759,9 +774,9 @@ static unsigned blocks_of(long long n) { return (unsigned)((n + 255) / 256); }
 hipError_t launch_conv0_relu(const float* mel, int T, int n_mels, const float* w, const float* b,
                              float* out, int H1, int W1, hipStream_t s)
 {
-    const long long n = (long long)H1 * W1 * kSub;
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(conv0_relu, dim3(blocks_of(n)), dim3(256), 0, s, mel, T, n_mels, w, b, out, H1, W1);
+    if (H1 <= 0 || W1 <= 0) return hipSuccess;
+    hipLaunchKernelGGL(conv0_relu, dim3(H1, (W1 + kC0Run - 1) / kC0Run), dim3(kSub), 0, s, mel, T,
+                       n_mels, w, b, out, H1, W1);
     return hipGetLastError();
 }
 
