@@ -68,7 +68,6 @@ hipError_t launch_conv0_relu(const float* mel, int T, int n_mels, const float* w
                              float* out, int H1, int W1, hipStream_t s);
 hipError_t launch_dwconv3x3s2(const float* in, int H, int W, const float* w, const float* b,
                               float* out, int Ho, int Wo, hipStream_t s);
-hipError_t launch_fill_rows(float* C, const float* bias, long long rows, int n, hipStream_t s);
 hipError_t launch_flatten_rows(const float* in, float* out, int H, int W, hipStream_t s);
 hipError_t launch_scale(float* x, long long n, float sc, hipStream_t s);
 

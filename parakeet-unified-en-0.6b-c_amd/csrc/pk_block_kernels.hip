@@ -600,7 +600,7 @@ __global__ void depthwise_swish(DwArgs p)
 // Activations channel-last, [H][W][256].  pk_conv2d (tensor_ops.c:436-475)
 // computes every output as val = bias, then val = fma(x, w, val) over its
 // in-range taps (ic, kh, kw ascending), which the kernels below repeat; the
-// 1x1 convolutions are chain GEMMs started from the bias (fill_rows, beta 1).
+// 1x1 convolutions are chain GEMMs started from the bias (the GEMM's chain_bias).
 
 constexpr int kSub = 256;          // PK_SUB_CHANNELS
 
@@ -674,12 +674,6 @@ __global__ void dwconv3x3s2(const float* __restrict__ in, int H, int W,
 
 // rows x n of C set to bias[0..n): the starting value of a chain that the
 // reference begins at the bias.
-__global__ void fill_rows(float* C, const float* __restrict__ bias, long long rows, int n)
-{
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= rows * n) return;
-    C[idx] = bias[idx % n];
-}
 
 // [H][W][256] -> [H][256*W], element (c, w) of row h at c*W + w
 // (encoder.c:152-158).
@@ -786,13 +780,6 @@ hipError_t launch_dwconv3x3s2(const float* in, int H, int W, const float* w, con
     const long long n = (long long)Ho * Wo * kSub;
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(dwconv3x3s2, dim3(blocks_of(n)), dim3(256), 0, s, in, H, W, w, b, out, Ho, Wo);
-    return hipGetLastError();
-}
-
-hipError_t launch_fill_rows(float* C, const float* bias, long long rows, int n, hipStream_t s)
-{
-    if (rows * n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(fill_rows, dim3(blocks_of(rows * n)), dim3(256), 0, s, C, bias, rows, n);
     return hipGetLastError();
 }
 

@@ -38,6 +38,9 @@ struct GemmProblem {
     float* C; int ldc;
     const float* bias = nullptr;     // length N, or null
     Epilogue epi = EPI_NONE;         // the residual epilogues require beta == 0
+    // Chains start from chain_bias[j] instead of beta*C (beta must be 0 and
+    // bias null): a convolution whose sum starts from its bias (pk_conv2d).
+    const float* chain_bias = nullptr;
 };
 
 // Kernel tile configuration chosen for a shape (see choose_config_index).

@@ -99,6 +99,9 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
     if (p.M <= 0 || p.N <= 0) return hipSuccess;
     if ((p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL) && p.beta != 0.0f)
         return hipErrorInvalidValue;
+    if (p.chain_bias && (p.beta != 0.0f || p.bias || p.alpha == 0.0f || p.K <= 0 ||
+                         (p.kind == W_I8 && p.scale == 0.0f)))
+        return hipErrorInvalidValue;
 
     KArgs a = {};
     a.M = p.M; a.N = p.N; a.K = p.K;
@@ -109,6 +112,7 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index)
     a.scales = p.scales; a.n_groups = p.N / 32;
     a.C = p.C; a.ldc = p.ldc;
     a.bias = p.bias; a.epi = p.epi;
+    a.chain_bias = p.chain_bias;
     // Long-M GEMMs (M*N >= 3M outputs) keep the larger operand's blocks within
     // one XCD's L2 (tile_origin); measured 1-3% faster there.  For the
     // shorter shapes that order halves the traffic but costs 1.5-3% in time

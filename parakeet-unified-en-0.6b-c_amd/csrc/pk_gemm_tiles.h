@@ -63,6 +63,7 @@ struct KArgs {
     uint32_t a_bytes, b_bytes, s_bytes;
     int vec_a, vec_b;
     const float* bias;       // fused epilogue (Epilogue in pk_gemm_kernels.h)
+    const float* chain_bias; // chains start from chain_bias[col] (then beta == 0)
     int epi;
     int tile_order;          // TileOrder: which operand an XCD's tiles share
 };
@@ -449,10 +450,13 @@ __device__ inline void store_c(const KArgs& p, float v, int row, int col)
     *c = (p.bias == nullptr && p.epi == EPI_NONE) ? v : epilogue(p, v, row, col);
 }
 
-// Chains start from beta*C exactly as scale_c leaves it (blas.c:89-99).
+// Chains start from beta*C exactly as scale_c leaves it (blas.c:89-99), or
+// from the column's bias when chain_bias is set.
 __device__ inline float beta_c(const KArgs& p, int row, int col)
 {
-    if (p.beta == 0.0f || row >= p.M || col >= p.N) return 0.0f;
+    if (row >= p.M || col >= p.N) return 0.0f;
+    if (p.chain_bias) return p.chain_bias[col];
+    if (p.beta == 0.0f) return 0.0f;
     const float cv = p.C[(size_t)row * p.ldc + col];
     return (p.beta == 1.0f) ? cv : __fmul_rn(cv, p.beta);
 }

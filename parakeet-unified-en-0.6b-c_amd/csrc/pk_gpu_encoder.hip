@@ -726,16 +726,16 @@ int pre_encode(pk_gpu_encoder* e, const float* mel, int T, float* x, hipStream_t
     if ((rc = check(pkgpu::launch_conv0_relu(mel, T, kMels, w.w0, w.b0, A, H1, W1, s), "conv.0"))) return rc;
     // conv.2 (depthwise) -> B; conv.3 (pointwise) + ReLU -> A
     if ((rc = check(pkgpu::launch_dwconv3x3s2(A, H1, W1, w.w2, w.b2, B, H2, W2, s), "conv.2"))) return rc;
-    if ((rc = check(pkgpu::launch_fill_rows(A, w.b3, (long long)H2 * W2, kSub, s), "conv.3 bias"))) return rc;
     // Rows are independent, so long inputs run in slabs whose operands stay
     // under the chain kernels' 2 GiB extent.
-    auto pointwise = [&](const DevWeight& wt, const float* in, float* out, int rows) {
+    auto pointwise = [&](const DevWeight& wt, const float* bias, const float* in, float* out, int rows) {
         const int slab = (1 << 28) / kSub;          // 1 GiB of A per launch
         for (int r0 = 0; r0 < rows; r0 += slab) {
             GemmProblem p{};
             p.kind = pkgpu::W_F32;
             p.M = std::min(slab, rows - r0); p.N = kSub; p.K = kSub;
-            p.alpha = 1.0f; p.beta = 1.0f;
+            p.alpha = 1.0f; p.beta = 0.0f;
+            p.chain_bias = bias;                    // the chain starts from the bias
             p.A = in + (size_t)r0 * kSub; p.lda = kSub;
             p.B = wt.data; p.ldb = kSub;
             p.C = out + (size_t)r0 * kSub; p.ldc = kSub;
@@ -745,11 +745,10 @@ int pre_encode(pk_gpu_encoder* e, const float* mel, int T, float* x, hipStream_t
         }
         return (int)PK_GPU_OK;
     };
-    if ((rc = pointwise(w.w3t, B, A, H2 * W2))) return rc;
+    if ((rc = pointwise(w.w3t, w.b3, B, A, H2 * W2))) return rc;
     // conv.5 (depthwise) -> B; conv.6 (pointwise) + ReLU -> A
     if ((rc = check(pkgpu::launch_dwconv3x3s2(A, H2, W2, w.w5, w.b5, B, H3, W3, s), "conv.5"))) return rc;
-    if ((rc = check(pkgpu::launch_fill_rows(A, w.b6, (long long)H3 * W3, kSub, s), "conv.6 bias"))) return rc;
-    if ((rc = pointwise(w.w6t, B, A, H3 * W3))) return rc;
+    if ((rc = pointwise(w.w6t, w.b6, B, A, H3 * W3))) return rc;
     // flatten -> B [T'][256*W3]; out linear + bias -> x; times sqrt(1024)
     if ((rc = check(pkgpu::launch_flatten_rows(A, B, H3, W3, s), "flatten"))) return rc;
     const int slab = (1 << 28) / (kSub * W3);        // 1 GiB of A per launch
