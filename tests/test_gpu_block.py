@@ -276,6 +276,19 @@ def test_encoder_row_groups_are_bit_identical(dev, enc2, n_groups):
             pk.call("pk_gpu_encoder_set_groups", enc2.h, 2)
 
 
+def test_encoder_long_input(dev, enc2):
+    """12000 frames: 30 chunks, two row groups of 15, a workspace four times the
+    bench's; the replay equals the eager one-group run bit for bit."""
+    T = 12000
+    x = rows(T, 1024)
+    pk.call("pk_gpu_encoder_profile", enc2.h, 1)
+    want = enc2.run(x, chunk=400)
+    pk.call("pk_gpu_encoder_profile", enc2.h, 0)
+    for rep in range(2):
+        assert bits_equal(enc2.run(x, chunk=400), want), f"replay {rep}"
+    assert np.isfinite(want).all()
+
+
 def test_encoder_many_chunkings(dev, enc2):
     """Each chunking of the input keeps captured graphs (one per row group);
     past the encoder's limit they are dropped and recaptured.  Forty input
