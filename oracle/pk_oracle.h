@@ -2,7 +2,7 @@
  *
  *  TEST INFRASTRUCTURE ONLY.  Nothing in the product library links this
  *  file; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
- *  leg load it, and only as the checker.
+ *  leg load it, and only to check results.
  *
  *  Each function restates one piece of the reference arithmetic
  *  (csrc/blas.c, csrc/tensor_ops.c, csrc/weights.c of

@@ -1,8 +1,8 @@
 """ctypes view of the CPU oracle and of the compiled reference.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
-by bench.py's cpu_baseline leg, always as the checker or the CPU baseline,
-never as the thing measured on the GPU.
+by bench.py's cpu_baseline leg, always to check results or as the CPU
+baseline, never as the thing measured on the GPU.
 
   Oracle      oracle/_build/liboracle.so   (pk_oracle.c, scalar restatement)
   Reference   oracle/_ref/libpkref.so      (csrc/*.c of the reference, built

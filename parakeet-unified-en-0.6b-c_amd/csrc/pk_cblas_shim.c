@@ -4,7 +4,8 @@
  *  Exports cblas_sgemm, cblas_sgemm_qb and cblas_sgemm_q4b with the exact
  *  signatures of csrc/blas.h:38-69, so the reference's encoder.c and
  *  tensor_ops.c bind to them unchanged when blas.c's own definitions are
- *  left out of the link.  The reference functions
+ *  left out of the link (the reference's Makefile drops blas.o and links
+ *  this library instead).  The reference functions
  *  return void and have no error channel; a failure here prints the library
  *  message and aborts rather than computing anything on the CPU.
  *
