@@ -3,9 +3,9 @@
  *
  *  Exports cblas_sgemm, cblas_sgemm_qb and cblas_sgemm_q4b with the exact
  *  signatures of csrc/blas.h:38-69, so the reference's encoder.c and
- *  tensor_ops.c bind to them unchanged when blas.c's own definitions are
- *  left out of the link (the reference's Makefile drops blas.o and links
- *  this library instead).  The reference functions
+ *  tensor_ops.c bind to them unchanged when blas.c's own three definitions
+ *  are renamed out of the way (blas.c compiled with -Dcblas_sgemm=... and so
+ *  on) and this library is linked.  The reference functions
  *  return void and have no error channel; a failure here prints the library
  *  message and aborts rather than computing anything on the CPU.
  *
