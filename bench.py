@@ -21,6 +21,8 @@ Prints one JSON line: encoder frames/s, plus
   roofline      the dominant kernel, the int4 feed-forward GEMM at M = 3312:
                 algorithmic flops / its HIP-event time, against the fp32 dense
                 MFMA peak (the instruction it issues)
+  host_path     frames/s through the host-pointer entry points (features or
+                mel spectrogram in host memory, PCIe copies included)
   cpu_baseline  the reference's own 24 conformer blocks (compiled from its
                 sources, oracle/_ref/libpkref_block_x86.so) on a bounded
                 sample of the same workload: whole 416-row chunks, PK_THREADS
@@ -416,6 +418,78 @@ def encoder_cpu_baseline(model, x, budget_s):
             "s_per_chunk": round(el / n, 3)}
 
 
+MELS = 128
+MEL_FRAMES = 8 * ENC_FRAMES    # three stride-2 stages: 25600 mel frames -> 3200
+
+
+class PreEncodeModel:
+    """Random-init pre-encode parameters (pk_gpu_pre_encode_weights): 3x3
+    convolutions ~N(0, 0.3), pointwise ~N(0, 1/16), biases ~N(0, 0.02), the
+    int8 output projection [4096][1024] with codes in [-127, 127] and scale
+    0.01 / 64."""
+
+    def __init__(self, pk):
+        self.keep = []
+        t = iter(range(16))
+
+        def normal(shape, sd):
+            a = np.ascontiguousarray(enc_rng(0xC0DE, next(t)).standard_normal(shape) * sd,
+                                     np.float32)
+            self.keep.append(a)
+            return a.ctypes.data
+
+        w = pk.PreEncodeWeights()
+        w.conv0_w, w.conv0_b = normal((256, 9), 0.3), normal(256, 0.02)
+        w.conv2_w, w.conv2_b = normal((256, 9), 0.3), normal(256, 0.02)
+        w.conv3_w, w.conv3_b = normal((256, 256), 1.0 / 16), normal(256, 0.02)
+        w.conv5_w, w.conv5_b = normal((256, 9), 0.3), normal(256, 0.02)
+        w.conv6_w, w.conv6_b = normal((256, 256), 1.0 / 16), normal(256, 0.02)
+        q = enc_rng(0xC0DE, next(t)).integers(-127, 128, (4 * D, D), dtype=np.int8)
+        self.keep.append(q)
+        w.out_w = pk.Weight(q.ctypes.data, 0.01 / 64, None, 8)
+        w.out_b = normal(D, 0.02)
+        self.w = w
+
+
+def host_path_rates(pk, lib, enc, x, steps):
+    """Frames/s through the host-pointer entry points, PCIe copies included:
+    pk_gpu_encoder_run (features in, encoder output out; pinned and pageable
+    host buffers) and pk_gpu_encoder_run_mel (mel spectrogram in, through the
+    device pre-encode).  Each call returns after its output is in host
+    memory.  Reported beside the device-resident rate, never as it."""
+    import ctypes
+    import torch
+    pre = PreEncodeModel(pk)
+    pk.call("pk_gpu_encoder_set_pre_encode", enc, ctypes.byref(pre.w))
+    assert lib.pk_gpu_encoder_frames(MEL_FRAMES) == ENC_FRAMES
+    x_pin = torch.from_numpy(x).pin_memory()
+    out_pin = torch.empty_like(x_pin).pin_memory()
+    mel = enc_rng(0x3E1, 0).standard_normal((MELS, MEL_FRAMES)).astype(np.float32)
+    mel_pin = torch.from_numpy(mel).pin_memory()
+    out_np = np.empty_like(x)
+    calls = {
+        "features_pinned": ("pk_gpu_encoder_run", lambda: lib.pk_gpu_encoder_run(
+            enc, x_pin.data_ptr(), ENC_FRAMES, ENC_CHUNK, ENC_OVERLAP, out_pin.data_ptr())),
+        "features_pageable": ("pk_gpu_encoder_run", lambda: lib.pk_gpu_encoder_run(
+            enc, x.ctypes.data, ENC_FRAMES, ENC_CHUNK, ENC_OVERLAP, out_np.ctypes.data)),
+        "mel_pinned": ("pk_gpu_encoder_run_mel", lambda: lib.pk_gpu_encoder_run_mel(
+            enc, mel_pin.data_ptr(), MEL_FRAMES, ENC_CHUNK, ENC_OVERLAP, out_pin.data_ptr())),
+    }
+    res = {}
+    for name, (fn, call) in calls.items():
+        pk.check(fn, call())                      # warm-up (graphs for this stream exist)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            pk.check(fn, call())
+        el = time.perf_counter() - t0
+        res[name] = {"frames_per_s": round(ENC_FRAMES * steps / el, 1),
+                     "ms_per_step": round(1e3 * el / steps, 3)}
+    res["note"] = (f"{steps} synchronous calls each: host input ({D} x {ENC_FRAMES} features, "
+                   f"or {MELS} x {MEL_FRAMES} mel) copied in, the encoder, the output copied "
+                   "back; wall clock")
+    return res
+
+
 STAGES = ["gemm_i4", "gemm_i8", "gemm_f32", "attention", "layer_norm", "conv_glu_depthwise",
           "chunk_copies"]
 
@@ -527,6 +601,10 @@ def encoder_mode(args):
                                     "timed replay overlaps two groups' kernels, which events cannot "
                                     "separate)"},
     }
+    try:
+        out["host_path"] = host_path_rates(pk, lib, enc, x, 5)
+    except Exception as e:        # reported in the line; the device-resident figures stand
+        out["host_path"] = {"error": str(e)}
     out["cpu_baseline"] = None if args.no_cpu else encoder_cpu_baseline(model, x, args.cpu_seconds)
     lib.pk_gpu_encoder_destroy(enc)
     print(json.dumps(out), flush=True)
