@@ -249,7 +249,10 @@ int pk_gpu_encoder_run(pk_gpu_encoder *enc, const float *x, int T, int chunk_siz
                        int overlap, float *out);
 /* The same with device pointers, enqueued on `stream` (NULL = HIP's null
  * stream, as for every *_dev entry point); returns without synchronising.
- * Runs of one encoder share its workspace: do not overlap them.  The blocks'
+ * Runs and pre-encodes of one encoder share its workspace: one enqueued on
+ * another stream than the previous call's first waits on the device for
+ * that call, so they never overlap.  One encoder takes calls from one host
+ * thread at a time.  The blocks'
  * launches are captured in a HIP graph on the first run of each (T,
  * chunk_size, overlap) and replayed afterwards (not while profiling). */
 int pk_gpu_encoder_run_dev(pk_gpu_encoder *enc, const float *dx, int T, int chunk_size,

@@ -123,6 +123,13 @@ struct pk_gpu_encoder {
     std::vector<hipStream_t> side;
     std::vector<hipEvent_t> side_done;
     hipEvent_t inputs_ready = nullptr;
+    // Runs and pre-encodes share the workspace.  Each records last_done on
+    // its stream when it is enqueued; a call on another stream waits for it
+    // on the device first (follow_last), so calls on different streams never
+    // overlap, and host-side waits on the current stream cover the previous
+    // call too.
+    hipEvent_t last_done = nullptr;
+    hipStream_t last_stream = nullptr;
     // pre-encode: weights and two ping-pong buffers, grown on demand
     DevPreEncode pre;
     float *pre_a = nullptr, *pre_b = nullptr, *pre_x = nullptr;
@@ -263,7 +270,8 @@ void free_workspace(pk_gpu_encoder* e)
     e->ws_rows = e->rows_cap = e->ws_bytes = 0;
 }
 
-// Grows the workspace; the old one may still be read by work queued on `s`.
+// Grows the workspace; the old one may still be read by work queued on `s`
+// (which already waits for the previous call, whatever its stream).
 int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, hipStream_t s)
 {
     if (rows <= e->ws_rows && n_chunks <= e->rows_cap) return PK_GPU_OK;
@@ -315,6 +323,31 @@ int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float
 
 int check(hipError_t r, const char* what) { return r == hipSuccess ? PK_GPU_OK : hip_error(r, what); }
 
+// Order a call on `s` after the previous call of this encoder (see last_done).
+int follow_last(pk_gpu_encoder* e, hipStream_t s)
+{
+    if (!e->last_done || e->last_stream == s) return PK_GPU_OK;
+    return check(hipStreamWaitEvent(s, e->last_done, 0), "encoder event");
+}
+
+int mark_last(pk_gpu_encoder* e, hipStream_t s)
+{
+    if (!e->last_done) {
+        const hipError_t r = hipEventCreateWithFlags(&e->last_done, hipEventDisableTiming);
+        if (r != hipSuccess) return hip_error(r, "hipEventCreate");
+    }
+    e->last_stream = s;
+    return check(hipEventRecord(e->last_done, s), "encoder event");
+}
+
+// Host wait for every queued call of this encoder, whatever its stream.
+void wait_all(pk_gpu_encoder* e)
+{
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    for (hipStream_t st : e->side) (void)hipStreamSynchronize(st);
+    if (e->last_done) (void)hipEventSynchronize(e->last_done);
+}
+
 hipEvent_t take_event(pk_gpu_encoder* e)
 {
     if (!e->event_pool.empty()) {
@@ -332,12 +365,17 @@ int timed(pk_gpu_encoder* e, int stage, double flops, double bytes, hipStream_t 
 {
     if (!e->prof) return launch();
     hipEvent_t a = take_event(e), b = take_event(e);
-    if (!a || !b) return error(PK_GPU_EHIP, "profiling events");
-    hipEventRecord(a, s);
-    int rc = launch();
-    hipEventRecord(b, s);
+    int rc = (a && b) ? check(hipEventRecord(a, s), "profiling event")
+                      : error(PK_GPU_EHIP, "profiling events");
+    if (!rc) rc = launch();
+    if (!rc) rc = check(hipEventRecord(b, s), "profiling event");
+    if (rc) {                                   // the pair is not pending: back to the pool
+        if (a) e->event_pool.push_back(a);
+        if (b) e->event_pool.push_back(b);
+        return rc;
+    }
     e->pending.push_back({stage, a, b, flops, bytes});
-    return rc;
+    return PK_GPU_OK;
 }
 
 // Fold finished events into the totals.
@@ -540,10 +578,9 @@ std::vector<RowGroup> plan_groups(const std::vector<Chunk>& chunks, int n)
     return groups;
 }
 
-int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out, hipStream_t s,
-        hipMemcpyKind in_kind, hipMemcpyKind out_kind)
+int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
+               hipStream_t s, hipMemcpyKind in_kind, hipMemcpyKind out_kind)
 {
-    if (!e) return error(PK_GPU_EINVAL, "encoder is NULL");
     if (T <= 0) return error(PK_GPU_EINVAL, "T = %d", T);
     if (!x || !out) return error(PK_GPU_EINVAL, "x or out is NULL");
     if (chunk > 0 && ov < 0) return error(PK_GPU_EINVAL, "overlap = %d", ov);
@@ -672,6 +709,17 @@ int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
     return PK_GPU_OK;
 }
 
+int run(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out, hipStream_t s,
+        hipMemcpyKind in_kind, hipMemcpyKind out_kind)
+{
+    if (!e) return error(PK_GPU_EINVAL, "encoder is NULL");
+    int rc = follow_last(e, s);
+    if (rc) return rc;
+    rc = run_queued(e, x, T, chunk, ov, out, s, in_kind, out_kind);
+    const int m = mark_last(e, s);          // also after a failure: work may be queued
+    return rc ? rc : m;
+}
+
 // Upload into the pre-encode's own allocations (freed when it is replaced).
 int pre_upload(pk_gpu_encoder* e, const void* host, size_t bytes, const char* what, const void** out)
 {
@@ -712,7 +760,7 @@ int grow(float** buf, size_t* cap, size_t n, hipStream_t s)
 // pre_encode_and_scale (encoder.c:103-174, 578-592): mel [128][T] to
 // x [T'][1024].  Channel-last throughout; the 1x1 convolutions and the output
 // linear are chain GEMMs (the convolutions started from their bias).
-int pre_encode(pk_gpu_encoder* e, const float* mel, int T, float* x, hipStream_t s)
+int pre_encode_queued(pk_gpu_encoder* e, const float* mel, int T, float* x, hipStream_t s)
 {
     const DevPreEncode& w = e->pre;
     const int H1 = half_up(T), W1 = half_up(kMels);
@@ -757,6 +805,15 @@ int pre_encode(pk_gpu_encoder* e, const float* mel, int T, float* x, hipStream_t
                               x + (size_t)r0 * kD, w.out_b, pkgpu::EPI_NONE, s)))
             return rc;
     return check(pkgpu::launch_scale(x, (long long)H3 * kD, 32.0f, s), "scale");
+}
+
+int pre_encode(pk_gpu_encoder* e, const float* mel, int T, float* x, hipStream_t s)
+{
+    int rc = follow_last(e, s);
+    if (rc) return rc;
+    rc = pre_encode_queued(e, mel, T, x, s);
+    const int m = mark_last(e, s);
+    return rc ? rc : m;
 }
 
 int dev_stream(void* stream, hipStream_t* s)
@@ -880,8 +937,7 @@ int pk_gpu_encoder_profile_read(pk_gpu_encoder* enc, int stage, double* ms, long
 void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
 {
     if (!enc) return;
-    if (enc->stream) (void)hipStreamSynchronize(enc->stream);
-    for (hipStream_t st : enc->side) (void)hipStreamSynchronize(st);
+    wait_all(enc);
     (void)collect(enc);
     for (hipEvent_t ev : enc->event_pool) (void)hipEventDestroy(ev);
     free_workspace(enc);
@@ -889,6 +945,7 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
     for (void* p : enc->allocs) (void)hipFree(p);
     for (hipEvent_t ev : enc->side_done) (void)hipEventDestroy(ev);
     if (enc->inputs_ready) (void)hipEventDestroy(enc->inputs_ready);
+    if (enc->last_done) (void)hipEventDestroy(enc->last_done);
     for (hipStream_t st : enc->side) (void)hipStreamDestroy(st);
     if (enc->stream) (void)hipStreamDestroy(enc->stream);
     delete enc;
@@ -902,8 +959,7 @@ int pk_gpu_encoder_set_groups(pk_gpu_encoder* enc, int n_groups)
     int rc = pkgpu::rt::bind(nullptr);
     if (rc) return rc;
     if (n_groups != enc->n_groups) {
-        (void)hipStreamSynchronize(enc->stream);
-        for (hipStream_t st : enc->side) (void)hipStreamSynchronize(st);
+        wait_all(enc);
         drop_graphs(enc);
         enc->n_groups = n_groups;
     }
@@ -915,7 +971,7 @@ int pk_gpu_encoder_set_pre_encode(pk_gpu_encoder* enc, const pk_gpu_pre_encode_w
     if (!enc || !w) return error(PK_GPU_EINVAL, "encoder or weights is NULL");
     int rc = pkgpu::rt::bind(nullptr);
     if (rc) return rc;
-    (void)hipStreamSynchronize(enc->stream);
+    wait_all(enc);
     free_pre(enc);
     DevPreEncode& d = enc->pre;
     const void* v = nullptr;

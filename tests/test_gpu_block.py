@@ -229,6 +229,29 @@ def test_encoder_dev_entry_and_in_place(dev, enc2):
     assert bits_equal(xi, want)
 
 
+def test_encoder_runs_on_two_streams_are_ordered(dev, enc2):
+    """Runs share the encoder's workspace and chunk table.  A run enqueued on
+    another stream than the previous run's waits for that run on the device,
+    so two runs issued back to back on two streams, with no host wait between
+    them, each give what they give alone.  The second input is longer: its
+    chunk table is rewritten while the first run may still be queued."""
+    torch = dev.torch
+    xa, xb = rows(900, 1024), rows(1300, 1024)
+    want_a, want_b = enc2.run(xa, chunk=400), enc2.run(xb, chunk=400)
+    for _ in range(2):
+        da, db = dev.put(xa), dev.put(xb)
+        oa, ob = torch.empty_like(da), torch.empty_like(db)
+        sync(dev)
+        sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+        pk.call("pk_gpu_encoder_run_dev", enc2.h, da.data_ptr(), 900, 400, 8, oa.data_ptr(),
+                sa.cuda_stream)
+        pk.call("pk_gpu_encoder_run_dev", enc2.h, db.data_ptr(), 1300, 400, 8, ob.data_ptr(),
+                sb.cuda_stream)
+        torch.cuda.synchronize()
+        assert bits_equal(oa.cpu().numpy(), want_a)
+        assert bits_equal(ob.cpu().numpy(), want_b)
+
+
 def test_encoder_graph_replays_match_eager(dev, enc2):
     """Without profiling the blocks run as a HIP graph captured on the first
     run of a chunking and replayed after; with profiling they launch one by
