@@ -45,7 +45,10 @@ typedef enum {
 /* Select the device (-1: $PK_GPU_DEVICE or 0) and check it is gfx950.
  * Idempotent; the GEMM entry points call it on first use. */
 int pk_gpu_init(int device);
-/* Free resident weights and per-thread resources of the calling thread. */
+/* Free resident weights (after the device's queued work), the calling
+ * thread's stream and staging buffers, and those left by exited threads.
+ * A thread that exits without calling this leaves its stream and buffers
+ * for the next thread to reuse. */
 void pk_gpu_shutdown(void);
 /* Message for the last failing call on this thread ("" if none). */
 const char *pk_gpu_last_error(void);

@@ -20,6 +20,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 using pkgpu::GemmProblem;
 using pkgpu::WeightKind;
@@ -46,7 +47,30 @@ struct ThreadCtx {
     void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
     size_t cap[4] = {0, 0, 0, 0};
 };
-thread_local ThreadCtx* t_ctx = nullptr;
+// A thread's context goes back to g_free_ctx when the thread exits (no HIP
+// call at exit: the stream is idle, since every host-pointer call waits for
+// it) and is reused by the next thread that needs one, so threads that come
+// and go (one per input file) hold at most as many contexts as ran at once.
+std::vector<ThreadCtx*> g_free_ctx;        // guarded by g_mu
+struct CtxHolder {
+    ThreadCtx* c = nullptr;
+    ~CtxHolder()
+    {
+        if (!c) return;
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_free_ctx.push_back(c);
+    }
+};
+thread_local CtxHolder t_holder;
+
+void free_ctx(ThreadCtx* c)
+{
+    (void)hipStreamSynchronize(c->stream);
+    for (int i = 0; i < 4; ++i)
+        if (c->buf[i]) (void)hipFree(c->buf[i]);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+}
 
 int fail(int code, const char* fmt, ...)
 {
@@ -97,18 +121,28 @@ int thread_ctx(ThreadCtx** out)
 {
     int rc = ensure_init();
     if (rc) return rc;
-    if (!t_ctx) {
+    if (!t_holder.c) {
         hipError_t e = hipSetDevice(g_device);
         if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
-        ThreadCtx* c = new ThreadCtx;
-        e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-        if (e != hipSuccess) {
-            delete c;
-            return hip_fail(e, "hipStreamCreate");
+        ThreadCtx* c = nullptr;
+        {
+            std::lock_guard<std::mutex> lk(g_mu);
+            if (!g_free_ctx.empty()) {
+                c = g_free_ctx.back();
+                g_free_ctx.pop_back();
+            }
         }
-        t_ctx = c;
+        if (!c) {
+            c = new ThreadCtx;
+            e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+            if (e != hipSuccess) {
+                delete c;
+                return hip_fail(e, "hipStreamCreate");
+            }
+        }
+        t_holder.c = c;
     }
-    *out = t_ctx;
+    *out = t_holder.c;
     return PK_GPU_OK;
 }
 
@@ -274,19 +308,19 @@ int pk_gpu_init(int device)
 
 void pk_gpu_shutdown(void)
 {
+    std::vector<ThreadCtx*> idle;
     {
         std::lock_guard<std::mutex> lk(g_mu);
+        if (!g_weights.empty()) (void)hipDeviceSynchronize();   // queued work may read them
         for (auto& kv : g_weights) (void)hipFree(kv.second.dev);
         g_weights.clear();
         g_resident_bytes = 0;
+        idle.swap(g_free_ctx);
     }
-    if (t_ctx) {
-        (void)hipStreamSynchronize(t_ctx->stream);
-        for (int i = 0; i < 4; ++i)
-            if (t_ctx->buf[i]) (void)hipFree(t_ctx->buf[i]);
-        (void)hipStreamDestroy(t_ctx->stream);
-        delete t_ctx;
-        t_ctx = nullptr;
+    for (ThreadCtx* c : idle) free_ctx(c);
+    if (t_holder.c) {
+        free_ctx(t_holder.c);
+        t_holder.c = nullptr;
     }
 }
 

@@ -237,6 +237,39 @@ def test_host_pointer_dropin_strided(dev, kind, resident):
     assert np.all(Cpad[:, N:] == 3.5), "columns beyond N were written"
 
 
+def test_host_pointer_calls_from_threads(dev):
+    """The reference may call its BLAS from one thread per input file
+    (main.c:167-188).  Three waves of eight threads, each calling the
+    host-pointer GEMMs on its own operands at once and then exiting: every
+    result equals the oracle's, and later waves run on the streams and
+    staging buffers that exited threads left behind."""
+    import threading
+    M, N, K = 40, 128, 96
+    cases = [make(kind, M, N, K, f"thr.{kind}.{i}") for i in range(4) for kind in ("i8", "i4")]
+    want = [oracle(kind, *c) for c, kind in zip(cases, ["i8", "i4"] * 4)]
+    for wave in range(3):
+        got, errs = [None] * len(cases), []
+
+        def work(i):
+            try:
+                kind = "i8" if i % 2 == 0 else "i4"
+                A, W, extra, C0 = cases[i]
+                C = C0.copy()
+                _host_call(kind, M, N, K, A, K, W, extra, C, N, 1.0, 0.0)
+                got[i] = C
+            except Exception as e:          # reported below, on the main thread
+                errs.append(f"thread {i}: {e}")
+
+        threads = [threading.Thread(target=work, args=(i,)) for i in range(len(cases))]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert not errs, errs
+        for i, (g, w) in enumerate(zip(got, want)):
+            assert_same(g, w, f"wave {wave}, thread {i}")
+
+
 def test_pointwise_conv_weight_as_A(dev):
     """pk_pointwise_conv1d: C[Cout][T] = W[Cout][Cin] * x[Cin][T] (tensor_ops.c:579-590),
     with the weight registered as the A operand."""
