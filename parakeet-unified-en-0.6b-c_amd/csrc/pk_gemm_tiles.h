@@ -391,13 +391,21 @@ __device__ __forceinline__ void chunk_tail(F& f, int c0, int nchunks)
         }
     }
 }
-template <int PD, typename F>
+// FULLK: the launcher guarantees K % (PD * KT) == 0, so no tail exists and
+// the guarded form is not compiled.  Its copy of the accumulators costs
+// registers: the 32x32 tile with two 32-deep chunks in flight needs 105 VGPRs
+// + 64 AGPRs with it (2 waves per SIMD) and 101 + 32 without (3 waves, as
+// many as its 48 KB of LDS allows; the int4 GEMMs of a 3312-row encoder pass
+// took 27.4 instead of 28.2 ms on one box).  The launcher uses it for tiles
+// with 32-deep chunks only: the 16-deep 32x32 tile would go from 3 to 4 waves
+// per SIMD, and its int8 GEMMs measured 7% slower there.
+template <int PD, bool FULLK = false, typename F>
 __device__ __forceinline__ void run_chunks(F& f, int K, int KT)
 {
     const int nfull = K / KT, nchunks = (K + KT - 1) / KT;
     int c0 = 0;
     for (; c0 + PD <= nfull; c0 += PD) chunk_group<0, PD>(f, c0);
-    chunk_tail<0, PD>(f, c0, nchunks);
+    if constexpr (!FULLK) chunk_tail<0, PD>(f, c0, nchunks);
 }
 
 // Swish as tensor_ops.c:381-388 / 98-120 write it: e = exp(-x) from a
@@ -662,7 +670,8 @@ template <> struct XPad<4> { static constexpr int v = 4; };
 template <> struct XPad<16> { static constexpr int v = 16; };
 template <> struct XPad<32> { static constexpr int v = 0; };
 
-template <int WK, int MF, int R, int NWM, int NWN, int KT, int PD, bool VEC, bool A1>
+template <int WK, int MF, int R, int NWM, int NWN, int KT, int PD, bool VEC, bool A1,
+          bool FULLK = false>
 __global__ __launch_bounds__(64 * NWM * NWN)
 void chain_gemm_x(KArgs p)
 {
@@ -760,7 +769,7 @@ void chain_gemm_x(KArgs p)
         // with it a wait on loads still in flight) into this one.
         __builtin_amdgcn_sched_barrier(0);
     };
-    run_chunks<PD>(chunk, p.K, KT);
+    run_chunks<PD, FULLK>(chunk, p.K, KT);
 
 #pragma unroll
     for (int g = 0; g < R; ++g) {
@@ -942,9 +951,16 @@ hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
     case i:                                                                               \
         if constexpr (fam == 'R')                                                         \
             hipLaunchKernelGGL((chain_gemm<WK, mf, c, wm, wn, kt, 2, VEC, A1>), grid, block, 0, s, a); \
-        else if constexpr (fam == 'X' || fam == 'Y')                                      \
-            hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, (VEC && fam == 'X') ? 4 : 2, VEC, A1>), \
-                               grid, block, 0, s, a);                                     \
+        else if constexpr (fam == 'X' || fam == 'Y') {                                    \
+            constexpr int pd = (VEC && fam == 'X') ? 4 : 2;                               \
+            constexpr bool fk = VEC && A1 && kt == 32;                                    \
+            if (fk && a.K % (pd * kt) == 0)                                               \
+                hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, pd, VEC, A1, fk>), \
+                                   grid, block, 0, s, a);                                 \
+            else                                                                          \
+                hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, pd, VEC, A1>),    \
+                                   grid, block, 0, s, a);                                 \
+        }                                                                                 \
         else                                                                              \
             hipLaunchKernelGGL((chain_gemm_xs<WK, mf, c, wm, wn, kt, 2, VEC, A1>), grid, block, 0, s, a); \
         break;
