@@ -68,13 +68,16 @@ TileConfig config_at(int i) { return kConfigs[i]; }
 //   M*N < 1M            config 13 (S 4x4, 2 chains)   out/pos/conv: 15-26
 //   M*N < 1.6M          config 14 (S 4x4, 3 chains)   FF up M=375: 35.1
 //   M*N < 3M            config 18 (S 16x16)           FF up M=416/500: 41
-//   otherwise, M=1656:  int4 up     config 19 (S 32x32): beside the other row group's
-//                                   kernels 0.7% less encoder time than config 20
+//   otherwise, M=1656:  int4 up     config 20 (Y 32x32, full chunks, 3 waves per
+//                                   SIMD): beside the other row group's kernels 1.2%
+//                                   less encoder time than config 19 (S 32x32), which
+//                                   had won while config 20 held 2 waves per SIMD
 //   otherwise, M=3312:  int4 up     config 20 (Y 32x32)  242-252 (config 11: 249-257)
 //                       int4 down   config 11 (X 32x32)  264-271
 //                       int8        config 21 (Y 32x32, k 16)  QKV 180, out 70.0
 //                                   (config 11: 183-185, 72.5-72.9)
-//                       fp32 2048   config 23 (Y 16x16)  132.6 (config 10: 141-144)
+//                       fp32 2048   config 23 (Y 16x16)  132.6 (config 10: 141-144); also
+//                                   at M=1656 (0.4% less encoder time than config 21)
 //                       fp32 1024   config 21            68.8 (config 10: 71.6-71.7)
 static int choose_index(int M, int N, int K, WeightKind kind = W_I8)
 {
@@ -84,16 +87,15 @@ static int choose_index(int M, int N, int K, WeightKind kind = W_I8)
     if (outputs < 1.6e6) return 14;
     if (outputs < 3.0e6) return 18;
     // Long M (the encoder's batched chunks): measured per weight format at
-    // M = 3312, and for the int4 up projection also at M = 1656 (one of two
-    // row groups whose kernels run side by side; there the producer-wave
-    // tile shares the chip better).  Two LDS chunks in flight (fewer
-    // registers, 3 waves per SIMD) win except for the int4 down projection,
-    // whose 1656 wave-long chains fill 1024 SIMDs unevenly whatever the
-    // occupancy.
+    // M = 3312, and for the int4 projections also at M = 1656 (one of two
+    // row groups whose kernels run side by side).  Two LDS chunks in flight
+    // (fewer registers, 3 waves per SIMD) win except for the int4 down
+    // projection, whose 1656 wave-long chains fill 1024 SIMDs unevenly
+    // whatever the occupancy.
     switch (kind) {
-    case W_I4:  return N < K ? 11 : outputs < 1.0e7 ? 19 : 20;
+    case W_I4:  return N < K ? 11 : 20;
     case W_I8:  return 21;
-    default:    return outputs >= 6.0e6 ? 23 : 21;
+    default:    return outputs >= 3.0e6 && N >= 2048 ? 23 : 21;
     }
 }
 
