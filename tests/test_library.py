@@ -87,6 +87,26 @@ def test_tile_configs_are_well_formed():
         assert 0 <= lib.pk_gpu_pick_config(*shape) < len(cfgs)
 
 
+# The encoder's GEMMs at 3200 frames: one row group (M = 3312) and each of two
+# row groups (M = 1656).  These picks were measured on the encoder itself;
+# a change to the dispatcher that moves one of them needs a new measurement.
+ENCODER_PICKS = [
+    # bits, M, N, K, config
+    (4, 3312, 4096, 1024, 20), (4, 3312, 1024, 4096, 11),
+    (4, 1656, 4096, 1024, 20), (4, 1656, 1024, 4096, 18),
+    (8, 3312, 3072, 1024, 21), (8, 3312, 1024, 1024, 21),
+    (8, 1656, 3072, 1024, 21), (8, 1656, 1024, 1024, 18),
+    (32, 3312, 2048, 1024, 23), (32, 3312, 1024, 1024, 21),
+    (32, 1656, 2048, 1024, 23), (32, 1656, 1024, 1024, 18),
+    (8, 32, 3072, 1024, 12), (4, 375, 1024, 4096, 17), (4, 375, 4096, 1024, 14),
+]
+
+
+@pytest.mark.parametrize("bits,M,N,K,cfg", ENCODER_PICKS)
+def test_dispatcher_picks_for_encoder_shapes(bits, M, N, K, cfg):
+    assert pk.load().pk_gpu_pick_config_bits(M, N, K, bits) == cfg
+
+
 def test_epilogue_validation_precedes_device_use():
     lib = pk.load()
     A = np.ones((2, 4), np.float32)
