@@ -125,8 +125,7 @@ int pk_gpu_sgemm_dev(int M, int N, int K, float alpha,
  *                             encoder.c:132-150)
  * Bias and residual are exact IEEE operations, so results equal the
  * reference's GEMM + pk_bias_add (+ x += 0.5 * out) bit for bit; Swish is
- * the device swish (within a few ulp of the reference's, see
- * pk_gpu_swish_dev).  No counterpart exists in blas.h: the reference runs
+ * pk_gpu_swish_dev's.  No counterpart exists in blas.h: the reference runs
  * these as separate host loops; these entry points serve GPU-resident
  * callers that chain the block on the device. */
 #define PK_GPU_EPI_NONE 0
@@ -144,17 +143,20 @@ int pk_gpu_sgemm_ex_dev(int M, int N, int K, float alpha, const float *dA, int l
                         const float *dB, int ldb, float beta, float *dC, int ldc,
                         const float *dbias, int epilogue, void *stream);
 
-/* Swish y = x * sigmoid(x) with the reference's polynomial exp
- * (tensor_ops.c:98-120, 367-389); x may equal y. */
+/* Swish y = x * (1 / (1 + e)), e = exp(-x) by the reference's polynomial
+ * (tensor_ops.c:98-120, 367-389), with the IEEE division its source writes
+ * (the reference's -ffast-math build computes 1/(1 + e) with vrcpps plus a
+ * Newton step instead, within a few ulp of this); x may equal y. */
 int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);
 
 /* ---- conformer-block operations (device pointers, no synchronisation) --
  * The operations between the weight GEMMs of one FastConformer block, for
  * callers that keep activations on the device (encoder.c:179-491).  Rows are
  * time-major.  Results equal the reference's bit for bit where its order of
- * operations is fixed (noted per function); where the reference uses a
- * CPU-model-specific approximation (vrsqrtss, vrcpps, glibc's vector expf),
- * the correctly rounded value is taken instead. */
+ * operations is fixed (noted per function); where the reference's build
+ * uses a CPU-model-specific approximation (vrsqrtss, vrcpps) or glibc's
+ * vector expf, the value here is the one its source's IEEE operations
+ * define, or a correctly rounded exp (see pk_gpu_glu_dev). */
 
 /* LayerNorm of `rows` rows of D = 1024 floats (pk_layer_norm_rows,
  * tensor_ops.c:150-185, 187-211; d_model); dout may equal dx.  The sums are
@@ -170,13 +172,17 @@ int pk_gpu_layer_norm_dev(const float *dx, const float *dgamma, const float *dbe
  *   out  [T][ldo]      head h in columns [128h, 128h+128)
  * Head dimension 128 (PK_HEAD_DIM), 1 <= T <= 512; ldq, ldp, ldo multiples of
  * 4 and 16-byte aligned rows.  Bit-identical to the reference when T % 8 == 0
- * (softmax's scalar tail otherwise uses a correctly rounded expf). */
+ * (softmax's scalar tail otherwise uses the exp of pk_gpu_glu_dev). */
 int pk_gpu_attention_dev(const float *dqkv, int ldq, const float *dP, int ldp,
                          const float *dpos_bias_u, const float *dpos_bias_v,
                          float *dout, int ldo, int T, int H, void *stream);
 
 /* GLU over rows of [va | vb] (2*D wide) into rows of D (encoder.c:453-461):
- * va * (1 / (1 + exp(-vb))), exp correctly rounded. */
+ * va * (1 / (1 + exp(-vb))) with IEEE division.  exp is evaluated in double
+ * (range reduction by ln2, degree-12 Taylor polynomial, one rounding to
+ * float): the correctly rounded expf except where e^x lies within about
+ * 2^-51 (relative) of a rounding boundary, and the same bits as the same
+ * double operations give on any IEEE machine. */
 int pk_gpu_glu_dev(const float *din, float *dout, int rows, int D, void *stream);
 
 /* Depthwise convolution over time with zero padding (pk_depthwise_conv1d,

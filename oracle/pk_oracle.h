@@ -74,8 +74,14 @@ void  pkor_layer_norm_rows(const float *x, const float *gamma, const float *beta
                            float *out, int rows, int D, int x86_rsqrt);
 /* pk_exp_avx2 (tensor_ops.c:98-120) per element, as the build contracts it. */
 float pkor_exp_poly(float x);
-/* Correctly rounded expf. */
-float pkor_expf_cr(float x);
+/* e^x evaluated in double by fixed IEEE operations, rounded once to float
+ * (the GPU's expf for GLU and softmax tails). */
+float pkor_expf_ieee(float x);
+void  pkor_expf_ieee_rows(const float *x, float *y, size_t n);
+/* pk_swish (tensor_ops.c:367-389) per element with the source's IEEE
+ * division; pkor_swish_rows applies it to n elements (y may equal x). */
+float pkor_swish(float v);
+void  pkor_swish_rows(const float *x, float *y, size_t n);
 /* In-place softmax of `rows` rows of length len (tensor_ops.c:336-357). */
 void  pkor_softmax_rows(float *x, int rows, int len);
 /* One NT dot product as kernel_nt_*x16_avx2 computes it (blas.c:221-249). */
@@ -92,6 +98,18 @@ void  pkor_glu_rows(const float *in, float *out, int rows, int D);
  * (tensor_ops.c:476-548). */
 void  pkor_depthwise_conv1d(const float *x, const float *w, const float *b,
                             float *out, int C, int T, int K);
+
+/* ---- the whole encoder (pk_oracle_encoder.c) --------------------------- */
+
+/* The conformer blocks 0..n_blocks-1 (blocks: an array of
+ * pk_gpu_block_weights, include/pk_gpu.h) over x [T][1024], chunked as
+ * encode_blocks_chunked (encoder.c:514-575; chunk <= 0: one sequence), into
+ * out [T][1024].  pe_table [pe_rows][1024] with centre row pe_center.
+ * snapshots (optional, [n_blocks][T][1024]) receives the gathered output
+ * after every block.  Returns 0, or -1 on a bad argument or no memory. */
+int pkor_encoder_run(const void *blocks, int n_blocks, const float *pe_table, int pe_rows,
+                     int pe_center, const float *x, int T, int chunk, int overlap, float *out,
+                     float *snapshots);
 
 #ifdef __cplusplus
 }

@@ -30,8 +30,8 @@
  *    1/sum by an IEEE division, x*inv.  Pinned bit-for-bit against the
  *    compiled pk_softmax for len % 8 == 0.  The scalar tail (len % 8 != 0)
  *    is left to the C library's expf in the reference, which the compiler
- *    may also vectorise; here it is the correctly rounded expf, so tails
- *    agree with the reference only within tolerance (tested).
+ *    may also vectorise; here it is pkor_expf_ieee (below), so tails agree
+ *    with the reference only within tolerance (tested).
  *
  *    NT dot products of the attention scores (cblas_sgemm_st NT,
  *    blas.c:221-249): eight interleaved fma chains over k = l, l+8, ...,
@@ -54,8 +54,20 @@
  *    GLU, encoder.c:453-461: gated = va * (1 / (1 + expf(-vb))).  The
  *    compiled reference takes expf from glibc's vector library and 1/(1+e)
  *    from rcpps plus a Newton step (CPU-model specific), so no restatement
- *    can be bit-exact; here exp is correctly rounded and the division IEEE
+ *    can be bit-exact; here exp is pkor_expf_ieee and the division IEEE
  *    (GPU and oracle agree bit for bit; the reference within tolerance).
+ *
+ *    expf_ieee: e^x evaluated in double by a fixed sequence of IEEE
+ *    operations and rounded once to float, so the GPU and this oracle agree
+ *    bit for bit.  Pinned against the correctly rounded e^x (expl) over
+ *    every float input.
+ *
+ *    Swish, tensor_ops.c:367-389: e = pk_exp_avx2(-v) as compiled (the
+ *    build also contracts 1 + poly*2^k into one fma), s = 1/(1+e) by the
+ *    IEEE division the source writes (_mm256_div_ps; the -ffast-math build
+ *    turns it into rcpps plus a Newton step), y = v*s.  Pinned within a few
+ *    ulp of the compiled pk_swish and against the same polynomial evaluated
+ *    in double.
  *
  *    depthwise conv, tensor_ops.c:476-548: per channel, val = bias, then in
  *    the 8-wide interior (t in [pad, pad + 8*floor((T-2pad)/8))) the
@@ -101,6 +113,7 @@ void pkor_layer_norm_rows(const float *x, const float *gamma, const float *beta,
                           float *out, int rows, int D, int x86_rsqrt)
 {
     const int D8 = D & ~7;
+    #pragma omp parallel for schedule(static)
     for (int r = 0; r < rows; r++) {
         const float *xr = x + (size_t)r * D;
         float *o = out + (size_t)r * D;
@@ -141,9 +154,65 @@ float pkor_exp_poly(float x)
     return y * p2;
 }
 
-float pkor_expf_cr(float x)
+/* e^x in double, rounded once to float: x = k*ln2 + r (ln2 in two parts,
+ * each step one fma), the degree-12 Taylor polynomial of e^r by Horner in
+ * fmas, times 2^k (exact), then the conversion to float.  Every step is one
+ * IEEE double operation, so any IEEE machine gets these bits.  Pinned
+ * against the correctly rounded value (expl, 64-bit significand) over all
+ * float inputs in tests/test_oracle_block.py. */
+float pkor_expf_ieee(float x)
 {
-    return (float)exp((double)x);
+    if (!(x > -104.0f)) return isnan(x) ? x : 0.0f;   /* e^x < 2^-150 */
+    if (x > 89.0f) return INFINITY;                   /* e^89 > FLT_MAX */
+    const double xd = (double)x;
+    const double k = rint(xd * 0x1.71547652b82fep+0);
+    double r = fma(-k, 0x1.62e42fefa39efp-1, xd);
+    r = fma(-k, 0x1.abc9e3b39803fp-56, r);
+    static const double inv_fact[13] = {
+        1.0, 1.0, 0.5, 0x1.5555555555555p-3, 0x1.5555555555555p-5, 0x1.1111111111111p-7,
+        0x1.6c16c16c16c17p-10, 0x1.a01a01a01a01ap-13, 0x1.a01a01a01a01ap-16,
+        0x1.71de3a556c734p-19, 0x1.27e4fb7789f5cp-22, 0x1.ae64567f544e4p-26,
+        0x1.1eed8eff8d898p-29};                       /* 1/n!, n = 0..12, rounded */
+    double p = inv_fact[12];
+    for (int n = 11; n >= 0; n--) p = fma(p, r, inv_fact[n]);
+    const uint64_t bits = (uint64_t)((int64_t)k + 1023) << 52;
+    double s;
+    memcpy(&s, &bits, 8);
+    return (float)(p * s);
+}
+
+void pkor_expf_ieee_rows(const float *x, float *y, size_t n)
+{
+    #pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; i++) y[i] = pkor_expf_ieee(x[i]);
+}
+
+/* pk_swish (tensor_ops.c:367-389): e = pk_exp_avx2(0 - v) with the
+ * reference build's contraction of 1 + poly*2^k into one fma, then the
+ * source's IEEE division s = 1/(1 + e) and y = v*s. */
+float pkor_swish(float v)
+{
+    const float t = fminf(fmaxf(-v, -87.0f), 87.0f);
+    const float kf = rintf(t * 1.44269504088896341f);
+    const int ki = (int)kf;
+    const float r = fmaf(-kf, 0.69314718055994529f, t);
+    float q = 1.0f / 120.0f;
+    q = fmaf(q, r, 1.0f / 24.0f);
+    q = fmaf(q, r, 1.0f / 6.0f);
+    q = fmaf(q, r, 0.5f);
+    q = fmaf(q, r, 1.0f);
+    q = fmaf(q, r, 1.0f);
+    uint32_t bits = (uint32_t)(ki + 127) << 23;
+    float p2;
+    memcpy(&p2, &bits, 4);
+    const float d = fmaf(q, p2, 1.0f);
+    return (1.0f / d) * v;
+}
+
+void pkor_swish_rows(const float *x, float *y, size_t n)
+{
+    #pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; i++) y[i] = pkor_swish(x[i]);
 }
 
 void pkor_softmax_rows(float *x, int rows, int len)
@@ -161,7 +230,7 @@ void pkor_softmax_rows(float *x, int rows, int len)
                 p[l] = p[l] + e;
             }
         float sum = hsum8(p);
-        for (int i = L8; i < len; i++) { v[i] = pkor_expf_cr(v[i] - mx); sum += v[i]; }
+        for (int i = L8; i < len; i++) { v[i] = pkor_expf_ieee(v[i] - mx); sum += v[i]; }
         const float inv = 1.0f / sum;
         for (int i = 0; i < len; i++) v[i] = v[i] * inv;
     }
@@ -184,11 +253,12 @@ void pkor_attention_core(const float *qkv, int ldq, const float *P, int ldp,
 {
     const int D = H * Dh, L = 2 * T - 1;
     const float scale = 0.0883883461356163f;      /* 0x3db504f3 */
-    float *qu = (float *)malloc((size_t)Dh * sizeof(float));
-    float *qv = (float *)malloc((size_t)Dh * sizeof(float));
-    float *s = (float *)malloc((size_t)T * sizeof(float));
+    #pragma omp parallel for collapse(2) schedule(dynamic, 8)
     for (int h = 0; h < H; h++) {
         for (int i = 0; i < T; i++) {
+            float *qu = (float *)malloc((size_t)Dh * sizeof(float));
+            float *qv = (float *)malloc((size_t)Dh * sizeof(float));
+            float *s = (float *)malloc((size_t)T * sizeof(float));
             const float *q = qkv + (size_t)i * ldq + h * Dh;
             for (int d = 0; d < Dh; d++) {
                 qu[d] = q[d] + pos_bias_u[h * Dh + d];
@@ -202,25 +272,28 @@ void pkor_attention_core(const float *qkv, int ldq, const float *P, int ldp,
                 s[j] = (ac + bd) * scale;
             }
             pkor_softmax_rows(s, 1, T);
+            /* o[d] = fma chain over j ascending (sgemm NN); the d loop is
+             * inside only so that the chains advance side by side */
             float *o = out + (size_t)i * ldo + h * Dh;
-            for (int d = 0; d < Dh; d++) {
-                float c = 0.0f;
-                for (int j = 0; j < T; j++) c = fmaf(s[j], qkv[(size_t)j * ldq + 2 * D + h * Dh + d], c);
-                o[d] = c;
+            for (int d = 0; d < Dh; d++) o[d] = 0.0f;
+            for (int j = 0; j < T; j++) {
+                const float *vj = qkv + (size_t)j * ldq + 2 * D + h * Dh;
+                for (int d = 0; d < Dh; d++) o[d] = fmaf(s[j], vj[d], o[d]);
             }
+            free(qu);
+            free(qv);
+            free(s);
         }
     }
-    free(qu);
-    free(qv);
-    free(s);
 }
 
 void pkor_glu_rows(const float *in, float *out, int rows, int D)
 {
+    #pragma omp parallel for schedule(static)
     for (int r = 0; r < rows; r++) {
         const float *a = in + (size_t)r * 2 * D;
         for (int d = 0; d < D; d++) {
-            const float e = pkor_expf_cr(-a[D + d]);
+            const float e = pkor_expf_ieee(-a[D + d]);
             const float sg = 1.0f / (1.0f + e);
             out[(size_t)r * D + d] = a[d] * sg;
         }

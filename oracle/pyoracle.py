@@ -71,14 +71,22 @@ def oracle():
         lib.pkor_layer_norm_rows.argtypes = [_p, _p, _p, _p, _i, _i, _i]
         lib.pkor_exp_poly.argtypes = [_f]
         lib.pkor_exp_poly.restype = _f
-        lib.pkor_expf_cr.argtypes = [_f]
-        lib.pkor_expf_cr.restype = _f
+        lib.pkor_expf_ieee.argtypes = [_f]
+        lib.pkor_expf_ieee.restype = _f
+        lib.pkor_expf_ieee_rows.argtypes = [_p, _p, _sz]
+        lib.pkor_expf_ieee_rows.restype = None
+        lib.pkor_swish.argtypes = [_f]
+        lib.pkor_swish.restype = _f
+        lib.pkor_swish_rows.argtypes = [_p, _p, _sz]
+        lib.pkor_swish_rows.restype = None
         lib.pkor_softmax_rows.argtypes = [_p, _i, _i]
         lib.pkor_dot8.argtypes = [_p, _p, _i]
         lib.pkor_dot8.restype = _f
         lib.pkor_attention_core.argtypes = [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i]
         lib.pkor_glu_rows.argtypes = [_p, _p, _i, _i]
         lib.pkor_depthwise_conv1d.argtypes = [_p, _p, _p, _p, _i, _i, _i]
+        lib.pkor_encoder_run.argtypes = [_p, _i, _p, _i, _i, _p, _i, _i, _i, _p, _p]
+        lib.pkor_encoder_run.restype = _i
         for fn in (lib.pkor_layer_norm_rows, lib.pkor_softmax_rows, lib.pkor_attention_core,
                    lib.pkor_glu_rows, lib.pkor_depthwise_conv1d):
             fn.restype = None
@@ -202,6 +210,22 @@ def dequant_i8(Q, scale):
     out = np.empty((K, N), np.float32)
     oracle().pkor_dequant_i8_matrix(_ptr(Q), K, N, N, scale, _ptr(out))
     return out
+
+
+def swish(x):
+    """Oracle Swish (the source's IEEE division) of every element of x."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    oracle().pkor_swish_rows(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def expf_ieee(x):
+    """The oracle's expf (double evaluation, one rounding) of every element."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    oracle().pkor_expf_ieee_rows(_ptr(x), _ptr(y), x.size)
+    return y
 
 
 def ref_swish(x):
@@ -351,3 +375,21 @@ def ref_pre_encode(w, mel, variant="portable"):
     if got != tp:
         raise RuntimeError(f"pkref_pre_encode returned {got}, expected {tp}")
     return out
+
+
+def encoder(blocks, n_blocks, pe_table, pe_center, x, chunk, overlap, snapshots=False):
+    """The oracle's whole encoder (pk_oracle_encoder.c): n_blocks conformer
+    blocks (a ctypes array of pk_gpu_block_weights) over x [T][1024], chunked
+    as the reference chunks.  Returns the output, or (output, [n_blocks][T][1024]
+    outputs after every block) with snapshots."""
+    x = _f32(x)
+    pe_table = _f32(pe_table)
+    T = x.shape[0]
+    out = np.empty_like(x)
+    snap = np.empty((n_blocks, T, x.shape[1]), np.float32) if snapshots else None
+    rc = oracle().pkor_encoder_run(ctypes.cast(blocks, _p), n_blocks, _ptr(pe_table),
+                                   pe_table.shape[0], pe_center, _ptr(x), T, chunk, overlap,
+                                   _ptr(out), _ptr(snap))
+    if rc:
+        raise RuntimeError("pkor_encoder_run failed")
+    return (out, snap) if snapshots else out

@@ -14,9 +14,12 @@
 // the reference rounds separately): where the reference's
 // order of operations is fixed by its source or by how it is compiled, the
 // result is bit-identical (attention for T % 8 == 0, depthwise convolution,
-// the LayerNorm sums).  Where the reference uses CPU-model-specific
-// approximations (vrsqrtss for LayerNorm's 1/sqrt, vrcpps for Swish and GLU,
-// glibc's vector expf for GLU), the value here is the correctly rounded one.
+// the LayerNorm sums).  Where the reference's build uses CPU-model-specific
+// approximations (vrsqrtss for LayerNorm's 1/sqrt, vrcpps for Swish's and
+// GLU's reciprocal) the value here is the IEEE operation its source writes
+// (1/sqrtf, a division); glibc's vector expf in GLU is replaced by
+// expf_ieee (pk_device_math.h).  Every function here is therefore a fixed
+// sequence of IEEE operations that a CPU reproduces bit for bit.
 #include "pk_block_kernels.h"
 #include "pk_gemm_tiles.h"
 
@@ -43,25 +46,6 @@ __device__ inline float hsum8(const float (&p)[8])
     return __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[4]), __fadd_rn(p[2], p[6])),
                      __fadd_rn(__fadd_rn(p[1], p[5]), __fadd_rn(p[3], p[7])));
 }
-
-// pk_exp_avx2 (tensor_ops.c:98-120) as the reference build compiles it.
-__device__ inline float exp_poly(float x)
-{
-    x = fminf(fmaxf(x, -87.0f), 87.0f);
-    const float kf = __builtin_rintf(__fmul_rn(x, 1.44269504088896341f));
-    const int ki = (int)kf;
-    const float r = __fmaf_rn(-kf, 0.69314718055994529f, x);
-    float y = 1.0f / 120.0f;
-    y = __fmaf_rn(y, r, 1.0f / 24.0f);
-    y = __fmaf_rn(y, r, 1.0f / 6.0f);
-    y = __fmaf_rn(y, r, 0.5f);
-    y = __fmaf_rn(y, r, 1.0f);
-    y = __fmaf_rn(y, r, 1.0f);
-    return __fmul_rn(y, __int_as_float((ki + 127) << 23));
-}
-
-// Correctly rounded expf (rounding the double-precision exp).
-__device__ inline float exp_cr(float x) { return (float)exp((double)x); }
 
 // ---- LayerNorm (tensor_ops.c:150-185) ---------------------------------------
 // One wave per 8 rows, 8 lanes per row; lane l of a row holds the partial
@@ -469,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
             if (T8 < T) {                 // scalar tail, one lane, in order
                 if (q == 0)
                     for (int j = T8; j < T; ++j) {
-                        const float e = exp_cr(__fsub_rn(s[j], mx));
+                        const float e = expf_ieee(__fsub_rn(s[j], mx));
                         s[j] = e;
                         sum = __fadd_rn(sum, e);
                     }
@@ -536,7 +520,7 @@ __global__ void glu_rows(const float* __restrict__ in, int ldi, float* out, int 
     if (idx >= (long long)rows * D) return;
     const int r = (int)(idx / D), d = (int)(idx % D);
     const float va = in[(size_t)r * ldi + d], vb = in[(size_t)r * ldi + D + d];
-    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_cr(-vb)));
+    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ieee(-vb)));
     out[(size_t)r * ldo + d] = __fmul_rn(va, s);
 }
 
@@ -593,7 +577,7 @@ __global__ void depthwise_swish(DwArgs p)
             if (src >= 0 && src < T) val = __fmaf_rn(x[(size_t)src * p.ldx], wc[k], val);
         }
     }
-    p.out[(size_t)(row0 + t) * p.ldo + c] = p.swish ? tiles::swish_f(val) : val;
+    p.out[(size_t)(row0 + t) * p.ldo + c] = p.swish ? swish_f(val) : val;
 }
 
 // ---- pre-encode subsampling (encoder.c:103-174) ------------------------------

@@ -48,7 +48,7 @@ __global__ void swish(const float* x, float* y, long long n)
 {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    y[i] = tiles::swish_f(x[i]);
+    y[i] = swish_f(x[i]);
 }
 
 }  // namespace

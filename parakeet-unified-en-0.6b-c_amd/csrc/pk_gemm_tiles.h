@@ -34,6 +34,7 @@
 // own (pk_gemm_f32.hip, pk_gemm_i8.hip, pk_gemm_i4.hip).
 #pragma once
 
+#include "pk_device_math.h"
 #include "pk_gemm_kernels.h"
 
 #include <algorithm>
@@ -406,33 +407,6 @@ __device__ __forceinline__ void run_chunks(F& f, int K, int KT)
     int c0 = 0;
     for (; c0 + PD <= nfull; c0 += PD) chunk_group<0, PD>(f, c0);
     if constexpr (!FULLK) chunk_tail<0, PD>(f, c0, nchunks);
-}
-
-// Swish as tensor_ops.c:381-388 / 98-120 write it: e = exp(-x) from a
-// 2^k * poly(r) range reduction, s = 1/(1+e), y = x*s.  The reference build
-// contracts r = t - k*ln2 and 1 + poly*2^k into FMAs, which is followed here.
-// Its 1/(1+e) is rcpps (a CPU-model-specific 12-bit table) plus one Newton
-// step, which no GPU can reproduce bit for bit; here it is v_rcp_f32 (about
-// 1 ulp) plus one Newton step, at least as accurate (agreement with the
-// reference within a few ulp is tested).  d = 1 + e lies in [1, e^87], so
-// 1/d stays normal.
-__device__ inline float swish_f(float v)
-{
-    const float t = fminf(fmaxf(-v, -87.0f), 87.0f);
-    const float kf = __builtin_rintf(__fmul_rn(t, 1.44269504088896341f));
-    const int ki = (int)kf;
-    const float r = __fmaf_rn(-kf, 0.69314718055994529f, t);
-    float q = 1.0f / 120.0f;
-    q = __fmaf_rn(q, r, 1.0f / 24.0f);
-    q = __fmaf_rn(q, r, 1.0f / 6.0f);
-    q = __fmaf_rn(q, r, 0.5f);
-    q = __fmaf_rn(q, r, 1.0f);
-    q = __fmaf_rn(q, r, 1.0f);
-    const float p2 = __int_as_float((ki + 127) << 23);
-    const float d = __fmaf_rn(q, p2, 1.0f);
-    float s = __builtin_amdgcn_rcpf(d);
-    s = __fmaf_rn(__fmaf_rn(-d, s, 1.0f), s, s);         // one Newton step
-    return __fmul_rn(s, v);
 }
 
 // The fused output step for C[row][col] (row < M, col < N): bias add, then

@@ -316,10 +316,11 @@ def test_cblas_shim_symbols(dev):
 
 @pytest.mark.skipif(not po.have_ref(), reason="needs oracle/_ref")
 def test_swish_matches_reference_within_tolerance(dev):
-    """tensor_ops.c:367-389.  The reference divides with rcpps plus one Newton
-    step (CPU-model specific), so agreement is bounded, not exact:
-    |gpu - ref| <= 4 ulp(ref) + 1e-37, checked on 1.5M values incl. the
-    clamp range."""
+    """tensor_ops.c:367-389.  The reference build divides with rcpps plus one
+    Newton step (CPU-model specific), so agreement with it is bounded, not
+    exact: |gpu - ref| <= 4 ulp(ref) + 1e-37, checked on 1.5M values incl.
+    the clamp range.  The device takes the IEEE division the source writes,
+    which is the oracle's Swish bit for bit."""
     n = 375 * 4096
     x = po.normal((n,), 0.0, 4.0, po.seed(SEED, "swish.x"))
     x[:16] = [0.0, -0.0, 1e-30, -1e-30, 87.0, -87.0, 88.0, -88.0, 200.0, -200.0,
@@ -334,3 +335,6 @@ def test_swish_matches_reference_within_tolerance(dev):
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     worst = float(np.max(err / np.maximum(ulp, 1e-45)))
     assert np.all(err <= 4 * ulp + 1e-37), f"worst {worst:.2f} ulp"
+    # the source's IEEE division: bit for bit the oracle's Swish
+    oracle_y = po.swish(x)
+    assert np.array_equal(got.view(np.uint32), oracle_y.view(np.uint32))

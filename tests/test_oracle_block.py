@@ -7,7 +7,11 @@ softmax for row lengths that are multiples of 8, the NT dot products of
 the attention scores, the whole attention core for T % 8 == 0, and the
 depthwise convolution for every T.  Tolerance pins (the reference uses
 CPU-model-specific approximations there): LayerNorm with a correctly
-rounded 1/sqrt, softmax tails, GLU."""
+rounded 1/sqrt, softmax tails, GLU, Swish with the source's IEEE division.
+Closed-form pins: the double-evaluated expf against the correctly rounded
+e^x, Swish against its polynomial evaluated in double, GLU.  The whole
+encoder composed of these operations is pinned against the reference's own
+conformer blocks within tolerance, and is independent of the thread count."""
 import numpy as np
 import pytest
 
@@ -212,3 +216,117 @@ def test_reference_sensitivity(attn_scale, lo, hi):
         assert rel > lo
     if hi is not None:
         assert rel < hi
+
+
+def expl_rounded(x):
+    """e^x with a 64-bit significand (x87 expl), rounded once to float: the
+    correctly rounded expf except within 2^-39 of a rounding boundary."""
+    return np.exp(x.astype(np.longdouble)).astype(np.float32)
+
+
+def test_expf_ieee_correctly_rounded():
+    """pkor_expf_ieee against the correctly rounded e^x: every 61st float bit
+    pattern of [-104, 89] (about 35 M inputs), the overflow and underflow
+    boundaries, and special values.  (The same comparison over all 2^32
+    inputs found no difference.)"""
+    assert np.finfo(np.longdouble).nmant >= 63
+    lo = np.float32(-104.0).view(np.uint32)              # negative floats: descending bits
+    hi = np.float32(89.0).view(np.uint32)
+    for bits in (np.arange(0x80000000, lo + 1, 61, dtype=np.uint64),
+                 np.arange(0, hi + 1, 61, dtype=np.uint64)):
+        for part in np.array_split(bits.astype(np.uint32), 16):
+            x = part.view(np.float32)
+            got = po.expf_ieee(x)
+            want = expl_rounded(x)
+            bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+            assert bad.size == 0, f"x={x[bad[:4]]!r} got {got[bad[:4]]!r} want {want[bad[:4]]!r}"
+    edge = np.array([0.0, -0.0, 1e-30, -1e-30, 88.72283, 88.72284, 88.7229, 89.0, 89.5,
+                     -87.33654, -87.33655, -103.27893, -103.97207, -103.97208, -104.0, -120.0,
+                     1e30, -1e30, np.inf, -np.inf], np.float32)
+    with np.errstate(over="ignore"):
+        want = np.exp(edge.astype(np.longdouble)).astype(np.float32)
+    assert np.array_equal(po.expf_ieee(edge).view(np.uint32), want.view(np.uint32))
+    assert np.isnan(po.expf_ieee(np.array([np.nan], np.float32))[0])
+
+
+def swish_closed_form(v):
+    """pk_swish's polynomial evaluated in double: the same k and the float
+    constants of tensor_ops.c:98-120, every other step exact."""
+    v = np.asarray(v, np.float32)
+    t = np.clip(-v, np.float32(-87.0), np.float32(87.0)).astype(np.float32)
+    k = np.rint(t * np.float32(1.44269504088896341)).astype(np.float64)
+    r = t.astype(np.float64) - k * np.float64(np.float32(0.69314718055994529))
+    c = [np.float64(np.float32(1.0 / n)) for n in (120, 24, 6)] + [0.5, 1.0, 1.0]
+    y = np.zeros_like(r) + c[0]
+    for ci in c[1:]:
+        y = y * r + ci
+    return v.astype(np.float64) / (1.0 + y * np.exp2(k))
+
+
+def test_swish_closed_form():
+    """Each float step of the oracle's Swish rounds once (fmas, the product
+    with 2^k, the division, the multiply): within 4 ulp of the closed form.
+    A wrong or missing polynomial term would be off by hundreds of ulp."""
+    x = (RNG.standard_normal(2_000_000) * 6.0).astype(np.float32)
+    x[:8] = [0.0, -0.0, 87.0, -87.0, 90.0, -90.0, 1e-30, -3.5]
+    got = po.swish(x).astype(np.float64)
+    want = swish_closed_form(x)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4 * ulp + 1e-44)
+
+
+@needs_ref
+def test_swish_within_tolerance_of_reference():
+    """The reference build's rcpps + Newton step against the source's IEEE
+    division: a few ulp."""
+    x = (RNG.standard_normal(1_000_000) * 4.0).astype(np.float32)
+    got, want = po.swish(x), po.ref_swish(x)
+    ulp = np.spacing(np.abs(want).astype(np.float32))
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 4 * ulp + 1e-37)
+    assert np.mean(got == want) > 0.3
+
+
+@pytest.mark.skipif(not po.have_ref_block(), reason="reference block harness missing")
+@pytest.mark.parametrize("T,chunk", [(72, 0), (150, 64)])
+def test_encoder_oracle_matches_reference_blocks(T, chunk):
+    """The oracle's whole encoder against the reference's own conformer
+    blocks (ref_block_harness.c) chunk by chunk, trained-like attention
+    weights: they differ only where the reference build uses vrsqrtss,
+    vrcpps and libmvec's expf, well below 1e-4 after four blocks."""
+    import blockgen as bg
+    blocks = [bg.Block(0xB10D0 + i, attn_scale=0.0005) for i in range(4)]
+    arr = bg.block_array(blocks)
+    pe = bg.pe_table()
+    x = rows(T, 1024)
+    got = po.encoder(arr, 4, pe, 4999, x, chunk, 8)
+    want = np.empty_like(x)
+    C = chunk if chunk > 0 else T
+    for o0 in range(0, T, C):
+        o1 = min(o0 + C, T)
+        i0, i1 = max(o0 - 8, 0) if chunk > 0 else 0, min(o1 + 8, T) if chunk > 0 else T
+        y = po.ref_blocks(arr, 4, bg.pe_slice(pe, i1 - i0), x[i0:i1])
+        want[o0:o1] = y[o0 - i0:o1 - i0]
+    rel = np.abs(got - want).max() / np.abs(want).max()
+    assert rel < 1e-4, rel
+
+
+def test_encoder_oracle_thread_count_invariant():
+    """Rows and chunks are spread over threads; no chain or sum is split, so
+    one thread and all threads give the same bits."""
+    import subprocess
+    import sys
+    code = ("import sys, hashlib, numpy as np; sys.path[:0] = {paths!r}; import blockgen as bg, "
+            "pyoracle as po; blocks = [bg.Block(0xB10C0)]; arr = bg.block_array(blocks); "
+            "x = np.random.default_rng(7).standard_normal((100, 1024)).astype(np.float32); "
+            "print(hashlib.sha256(po.encoder(arr, 1, bg.pe_table(), 4999, x, 40, 8).tobytes())"
+            ".hexdigest())")
+    import os
+    here = os.path.dirname(os.path.abspath(__file__))
+    paths = [here, os.path.join(os.path.dirname(here), "oracle")]
+    digests = set()
+    for threads in ("1", "5"):
+        out = subprocess.run([sys.executable, "-c", code.format(paths=paths)], capture_output=True,
+                             text=True, env=dict(os.environ, OMP_NUM_THREADS=threads), timeout=300)
+        assert out.returncode == 0, out.stderr[-2000:]
+        digests.add(out.stdout.strip())
+    assert len(digests) == 1
