@@ -61,8 +61,14 @@ const char *pk_gpu_last_error(void);
  * read-only mmap'd or load-time buffers, weights.c:294-302, 404-546).
  * Registering an overlapping range is PK_GPU_EINVAL. */
 int pk_gpu_register_weight(const void *host, size_t bytes);
+/* Later calls no longer find the range; the device copy is freed after the
+ * work queued on the device (a host-pointer GEMM that already found it keeps
+ * it until that call returns).  Unregister only while no thread is in a
+ * GEMM call that reads the weight: unregistering during such calls is not
+ * supported. */
 int pk_gpu_unregister_weight(const void *host);
-/* Device address of a registered host pointer (or NULL). */
+/* Device address of a registered host pointer (or NULL), valid until the
+ * weight is unregistered. */
 const void *pk_gpu_device_ptr(const void *host);
 /* Bytes currently resident. */
 size_t pk_gpu_resident_bytes(void);
@@ -263,7 +269,8 @@ int pk_gpu_encoder_run(pk_gpu_encoder *enc, const float *x, int T, int chunk_siz
  * that call, so they never overlap.  One encoder takes calls from one host
  * thread at a time.  The blocks'
  * launches are captured in a HIP graph on the first run of each (T,
- * chunk_size, overlap) and replayed afterwards (not while profiling). */
+ * chunk_size, overlap, configuration forced with pk_gpu_force_config on the
+ * calling thread) and replayed afterwards (not while profiling). */
 int pk_gpu_encoder_run_dev(pk_gpu_encoder *enc, const float *dx, int T, int chunk_size,
                            int overlap, float *dout, void *stream);
 /* Pre-encode parameters (PreEncodeWeights, parakeet.h), host pointers:
@@ -300,8 +307,10 @@ int pk_gpu_encoder_run_mel(pk_gpu_encoder *enc, const float *mel, int n_frames, 
 size_t pk_gpu_encoder_bytes(const pk_gpu_encoder *enc);
 
 /* Per-stage timing of later runs: with enable != 0, every launch of a run is
- * bracketed by HIP events on its stream (the reference's pk_verbose timers
- * have no finer granularity); 0 stops and clears.  Stages: */
+ * bracketed by HIP events on the caller's stream (the reference's pk_verbose
+ * timers have no finer granularity): the launches of a replayed run, same
+ * row groups and tiles, issued one by one and one group after another, so
+ * each kernel is timed alone; 0 stops and clears.  Stages: */
 #define PK_GPU_STAGE_GEMM_I4    0   /* feed-forward GEMMs (int4)              */
 #define PK_GPU_STAGE_GEMM_I8    1   /* QKV, position, output GEMMs (int8)     */
 #define PK_GPU_STAGE_GEMM_F32   2   /* pointwise-convolution GEMMs (fp32)     */
@@ -324,7 +333,8 @@ int pk_gpu_encoder_profile_read(pk_gpu_encoder *enc, int stage, double *ms, long
  * operation of a block is row-wise or per chunk, so the result does not
  * depend on the grouping.  No counterpart in the reference (which runs the
  * chunks one after another); it overlaps one group's latency-bound kernels
- * and launch tails with the other's GEMMs.  Profiled runs use one group. */
+ * and launch tails with the other's GEMMs.  Profiled runs issue the groups
+ * one after another. */
 #define PK_GPU_MAX_GROUPS 4
 int pk_gpu_encoder_set_groups(pk_gpu_encoder *enc, int n_groups);
 void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
@@ -346,7 +356,9 @@ int pk_gpu_config_info(int index, int *family, int *mfma, int *cw, int *wgm, int
  * other value). */
 int pk_gpu_pick_config(int M, int N, int K);
 int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
-/* Force a configuration for later calls on this thread (-1 = automatic). */
+/* Force a configuration for later calls on this thread (-1 = automatic),
+ * encoder runs included: an encoder keeps its captured graphs per forced
+ * configuration, so a change takes effect on the next run. */
 int pk_gpu_force_config(int index);
 
 #ifdef __cplusplus

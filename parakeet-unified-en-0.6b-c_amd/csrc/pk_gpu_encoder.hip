@@ -116,7 +116,10 @@ struct pk_gpu_encoder {
     // the 24 blocks' launches captured once per (T, chunk, overlap) and
     // replayed; their device pointers are the workspace's, so a workspace
     // change drops them
-    std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;   // (T, chunk, overlap, group)
+    // (T, chunk, overlap, group, forced tile config): a graph freezes the
+    // tiles its GEMMs were launched with, so a pk_gpu_force_config in force
+    // at capture is part of what the graph is
+    std::map<std::tuple<int, int, int, int, int>, hipGraphExec_t> graphs;
     // Row groups replayed concurrently: group 0 on the caller's stream, group
     // g > 0 on side[g - 1], joined through events around the replay.
     int n_groups = 2;
@@ -599,7 +602,7 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
     // Row groups; each group's chunks are table entries [tab, tab + n), by
     // length, with rows relative to the group; the lengths follow at entry
     // rows_cap.
-    std::vector<RowGroup> groups = plan_groups(chunks, e->prof ? 1 : e->n_groups);
+    std::vector<RowGroup> groups = plan_groups(chunks, e->n_groups);
     std::vector<int> table, lens;
     {
         size_t ci = 0;
@@ -642,17 +645,21 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
         });
         if (rc) return rc;
     }
-    if (e->prof) {            // eager, one group, with an event pair around every launch
-        for (const DevBlock& b : e->blocks)
-            if ((rc = run_block(e, b, groups[0], s))) return rc;
+    if (e->prof) {
+        // eager, with an event pair around every launch: the replay's own
+        // kernels (same groups, same tiles), one group after another on s
+        for (const RowGroup& g : groups)
+            for (const DevBlock& b : e->blocks)
+                if ((rc = run_block(e, b, g, s))) return rc;
     } else {
         if ((rc = side_streams(e, (int)groups.size() - 1))) return rc;
         // One graph per chunking of the input and group: captured on the
         // encoder's own stream (the null stream cannot capture).  A caller
         // that sees many input lengths would keep adding graphs; past
         // kMaxGraphs they are all dropped and recaptured on demand.
+        const int forced = pkgpu::rt::forced_config();
         if (e->graphs.size() + groups.size() > kMaxGraphs &&
-            !e->graphs.count(std::make_tuple(T, chunk, ov, 0))) {
+            !e->graphs.count(std::make_tuple(T, chunk, ov, 0, forced))) {
             if ((rc = check(hipStreamSynchronize(s), "encoder stream"))) return rc;
             for (hipStream_t st : e->side)
                 if ((rc = check(hipStreamSynchronize(st), "encoder stream"))) return rc;
@@ -660,7 +667,7 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
         }
         std::vector<hipGraphExec_t> ex(groups.size(), nullptr);
         for (size_t gi = 0; gi < groups.size(); ++gi) {
-            const auto key = std::make_tuple(T, chunk, ov, (int)gi);
+            const auto key = std::make_tuple(T, chunk, ov, (int)gi, forced);
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 if ((rc = check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal),

@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -31,11 +32,26 @@ std::mutex g_mu;                 // guards everything below
 bool g_inited = false;
 int g_device = -1;
 
+// A registered weight's device copy.  Host-pointer GEMMs hold a reference
+// from the lookup until their stream has finished, so an unregister on
+// another thread only removes the entry; the copy is freed (after the
+// device's queued work) when the last holder lets go.
 struct Resident {
-    size_t bytes;
-    void* dev;
+    size_t bytes = 0;
+    void* dev = nullptr;
+    Resident(size_t b, void* d) : bytes(b), dev(d) {}
+    Resident(const Resident&) = delete;
+    Resident& operator=(const Resident&) = delete;
+    ~Resident()
+    {
+        (void)hipDeviceSynchronize();     // queued device-pointer work may still read it
+        (void)hipFree(dev);
+    }
 };
-std::map<uintptr_t, Resident> g_weights;   // host begin -> device copy
+// host begin -> device copy; never destroyed, so no HIP call runs from a
+// static destructor after the runtime has gone
+std::map<uintptr_t, std::shared_ptr<Resident>>& g_weights =
+    *new std::map<uintptr_t, std::shared_ptr<Resident>>;
 size_t g_resident_bytes = 0;
 
 thread_local std::string t_err;
@@ -163,8 +179,8 @@ int staging(ThreadCtx* c, int slot, size_t bytes, void** out)
 }
 
 // Device copy of [host, host+need) if the whole range lies in one registered
-// weight, else nullptr.
-const void* resident(const void* host, size_t need)
+// weight, else nullptr; *hold (if given) then keeps that copy alive.
+const void* resident(const void* host, size_t need, std::shared_ptr<Resident>* hold = nullptr)
 {
     if (!host) return nullptr;
     std::lock_guard<std::mutex> lk(g_mu);
@@ -172,18 +188,21 @@ const void* resident(const void* host, size_t need)
     auto it = g_weights.upper_bound(h);
     if (it == g_weights.begin()) return nullptr;
     --it;
-    if (h >= it->first && h + need <= it->first + it->second.bytes)
-        return static_cast<const char*>(it->second.dev) + (h - it->first);
+    if (h >= it->first && h + need <= it->first + it->second->bytes) {
+        if (hold) *hold = it->second;
+        return static_cast<const char*>(it->second->dev) + (h - it->first);
+    }
     return nullptr;
 }
 
 // Operand rows x cols elements of elem bytes with row pitch ld: either its
-// resident copy (keeps pitch ld) or a packed staged copy (pitch cols).
+// resident copy (keeps pitch ld; *hold keeps it alive) or a packed staged
+// copy (pitch cols).
 int operand(ThreadCtx* c, int slot, const void* host, int rows, int cols, int ld, size_t elem,
-            const void** dev, int* dev_ld)
+            const void** dev, int* dev_ld, std::shared_ptr<Resident>* hold)
 {
     const size_t extent = rows > 0 ? ((size_t)(rows - 1) * ld + cols) * elem : 0;
-    if (const void* r = resident(host, extent)) {
+    if (const void* r = resident(host, extent, hold)) {
         *dev = r;
         *dev_ld = ld;
         return PK_GPU_OK;
@@ -242,23 +261,27 @@ int host_gemm(GemmProblem p, const float* hA, const void* hB, const float* hScal
     int rc = thread_ctx(&c);
     if (rc) return rc;
 
+    // resident operands stay registered until this call's stream is done
+    // (or, on an error return, until the device's queued work is)
+    std::shared_ptr<Resident> hold[3];
     if (mul) {
         const void* dA = nullptr;
         int lda = 0;
-        rc = operand(c, 0, hA, p.M, p.K, p.lda, sizeof(float), &dA, &lda);
+        rc = operand(c, 0, hA, p.M, p.K, p.lda, sizeof(float), &dA, &lda, &hold[0]);
         if (rc) return rc;
         p.A = static_cast<const float*>(dA);
         p.lda = lda;
         const void* dB = nullptr;
         int ldb = 0;
-        rc = operand(c, 1, hB, p.K, b_cols, p.ldb, b_elem, &dB, &ldb);
+        rc = operand(c, 1, hB, p.K, b_cols, p.ldb, b_elem, &dB, &ldb, &hold[1]);
         if (rc) return rc;
         p.B = dB;
         p.ldb = ldb;
         if (p.kind == pkgpu::W_I4) {
             const void* dS = nullptr;
             int lds = 0;
-            rc = operand(c, 3, hScales, p.K, p.N / 32, p.N / 32, sizeof(float), &dS, &lds);
+            rc = operand(c, 3, hScales, p.K, p.N / 32, p.N / 32, sizeof(float), &dS, &lds,
+                         &hold[2]);
             if (rc) return rc;
             p.scales = static_cast<const float*>(dS);
         }
@@ -309,14 +332,14 @@ int pk_gpu_init(int device)
 void pk_gpu_shutdown(void)
 {
     std::vector<ThreadCtx*> idle;
+    std::map<uintptr_t, std::shared_ptr<Resident>> weights;
     {
         std::lock_guard<std::mutex> lk(g_mu);
-        if (!g_weights.empty()) (void)hipDeviceSynchronize();   // queued work may read them
-        for (auto& kv : g_weights) (void)hipFree(kv.second.dev);
-        g_weights.clear();
+        weights.swap(g_weights);
         g_resident_bytes = 0;
         idle.swap(g_free_ctx);
     }
+    weights.clear();          // each copy freed after queued work, or by its last holder
     for (ThreadCtx* c : idle) free_ctx(c);
     if (t_holder.c) {
         free_ctx(t_holder.c);
@@ -333,7 +356,7 @@ static bool overlaps_registered(uintptr_t h, size_t bytes)
     if (it != g_weights.end() && it->first < h + bytes) return true;
     if (it != g_weights.begin()) {
         --it;
-        if (it->first + it->second.bytes > h) return true;
+        if (it->first + it->second->bytes > h) return true;
     }
     return false;
 }
@@ -363,7 +386,7 @@ int pk_gpu_register_weight(const void* host, size_t bytes)
     {
         std::lock_guard<std::mutex> lk(g_mu);
         if (!overlaps_registered(h, bytes)) {
-            g_weights[h] = Resident{bytes, d};
+            g_weights[h] = std::make_shared<Resident>(bytes, d);
             g_resident_bytes += bytes;
             return PK_GPU_OK;
         }
@@ -374,18 +397,19 @@ int pk_gpu_register_weight(const void* host, size_t bytes)
 
 int pk_gpu_unregister_weight(const void* host)
 {
-    void* dev = nullptr;
+    std::shared_ptr<Resident> r;
     {
         std::lock_guard<std::mutex> lk(g_mu);
         auto it = g_weights.find(reinterpret_cast<uintptr_t>(host));
         if (it == g_weights.end()) return fail(PK_GPU_EINVAL, "unregister: not registered");
-        dev = it->second.dev;
-        g_resident_bytes -= it->second.bytes;
+        r = std::move(it->second);
+        g_resident_bytes -= r->bytes;
         g_weights.erase(it);
     }
-    // Work already queued on any thread's stream may still read it.
-    (void)hipDeviceSynchronize();
-    (void)hipFree(dev);
+    // Later lookups miss it.  A host-pointer GEMM that found it holds it until
+    // its stream is done; otherwise it is freed here, after the device's
+    // queued work.
+    r.reset();
     return PK_GPU_OK;
 }
 
@@ -585,6 +609,8 @@ int bind(hipStream_t* thread_stream)
 }
 
 int gemm(const GemmProblem& p, hipStream_t s) { return launch(p, s); }
+
+int forced_config() { return t_force_cfg; }
 
 }  // namespace rt
 }  // namespace pkgpu

@@ -272,11 +272,29 @@ def test_encoder_graph_replays_match_eager(dev, enc2):
     pk.call("pk_gpu_encoder_profile_read", enc2.h, 0, ctypes.byref(ms), None, None, None)
 
 
+def test_encoder_forced_config_is_part_of_the_graph(dev, enc2):
+    """A pk_gpu_force_config in force when a run's graphs are captured is
+    frozen into them, so graphs are kept per forced configuration: forcing,
+    then resetting, takes effect on the next run (each run captures or finds
+    its own graph), and every configuration gives the same bits."""
+    T = 900
+    x = rows(T, 1024)
+    want = enc2.run(x, chunk=400)
+    for cfg in (13, 20, -1, 13):
+        pk.call("pk_gpu_force_config", cfg)
+        try:
+            for _ in range(2):                  # capture (or reuse), then replay
+                assert bits_equal(enc2.run(x, chunk=400), want), f"forced config {cfg}"
+        finally:
+            pk.call("pk_gpu_force_config", -1)
+
+
 @pytest.mark.parametrize("n_groups", [1, 2, 3, 4])
 def test_encoder_row_groups_are_bit_identical(dev, enc2, n_groups):
     """Replays split the chunks into row groups replayed concurrently (group 0
     on the caller's stream, the others on side streams); eager profiled runs
-    use one group.  The output must not depend on the grouping, through both
+    issue the groups one after another.  The output must not depend on the
+    grouping, through both
     the host and the device-pointer entry points."""
     for T in (3200, 900):              # 8 chunks; 3 chunks (4 groups clamp to 3)
         x = rows(T, 1024)
