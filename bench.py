@@ -188,8 +188,11 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20):
         tf = 2.0 * m * n * k / us / 1e6
         gbs = alg_bytes(kind, m, n, k) / us / 1e3
         bits = {"i4": 4, "i8": 8}.get(kind, 32)
+        small_m = bool(lib.pk_gpu_uses_small_m(m, n, k, bits))
         print(json.dumps({"gemm": f"{kind} {m}x{n}x{k}",
-                          "config": lib.pk_gpu_pick_config_bits(m, n, k, bits),
+                          "kernel": "small-M (bf16 split, tolerance path)" if small_m else
+                                    "exact chains",
+                          "config": None if small_m else lib.pk_gpu_pick_config_bits(m, n, k, bits),
                           "avg_us": round(us, 2), "tflops": round(tf, 2), "gbps": round(gbs, 1),
                           "frac_mfma_fp32": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_replicas": reps,

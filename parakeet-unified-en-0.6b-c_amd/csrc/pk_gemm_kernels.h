@@ -70,10 +70,35 @@ int choose_config_index(int M, int N, int K, WeightKind kind);
 int num_configs();
 TileConfig config_at(int i);
 
+// ---- small-M kernels (pk_smallm.hip): the tolerance path for M <= 64 -----
+// Split-K partial tiles and per-column-tile arrival counters; the counters
+// are zero between launches (each launch resets the ones it used).  Launches
+// that share a scratch must not run concurrently.
+constexpr int kSmallMaxM = 64;
+struct SmallmScratch {
+    float* part = nullptr;
+    size_t part_bytes = 0;
+    unsigned* cnt = nullptr;
+    int cnt_n = 0;
+};
+// Whether a shape and its operands' alignment suit the small-M kernels
+// (int8 or int4 weights, M <= 64, K % 32 == 0, 16-byte aligned A rows, ...).
+bool smallm_supports(const GemmProblem& p);
+// Scratch the launch needs: partial bytes (0 when one k segment suffices)
+// and counters (one per 128-column tile).
+size_t smallm_scratch_bytes(const GemmProblem& p);
+int smallm_counters(const GemmProblem& p);
+// Launch on `stream`; hipErrorNotSupported if the shape is not handled or
+// the scratch is too small (the caller then takes the exact kernels).
+hipError_t launch_smallm(const GemmProblem& p, hipStream_t stream, const SmallmScratch& sc);
+
 // Launch the whole GEMM (beta pre-pass semantics, early exits, int8 edge
 // columns) on `stream`.  Returns hipSuccess or the launch error.
-// cfg_index < 0 selects choose_config_index().
-hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index);
+// cfg_index < 0 selects choose_config_index().  With `small` given (and no
+// forced configuration) shapes the small-M kernels handle go there; *used_small
+// (if given) says whether they did.
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index,
+                       const SmallmScratch* small = nullptr, bool* used_small = nullptr);
 
 // Swish y = x * (1 / (1 + exp(-x))) with the reference's polynomial exp
 // (tensor_ops.c:98-120, 381-388), n elements, in place allowed.

@@ -56,12 +56,33 @@ size_t g_resident_bytes = 0;
 
 thread_local std::string t_err;
 thread_local int t_force_cfg = -1;
+// PK_GPU_NUMERICS_DEFAULT or _EXACT for this thread's later calls; the
+// environment's PK_GPU_NUMERICS=exact sets every thread's default.
+int default_numerics()
+{
+    const char* e = getenv("PK_GPU_NUMERICS");
+    return (e && strcmp(e, "exact") == 0) ? PK_GPU_NUMERICS_EXACT : PK_GPU_NUMERICS_DEFAULT;
+}
+thread_local int t_numerics = default_numerics();
 
-// Per-thread stream and staging buffers (slot 0: A, 1: B, 2: C, 3: scales).
+// Split-K scratch of the small-M kernels, per thread context: partial tiles
+// for the encoder's shapes at M <= 64 (the FFN up projection, N = 4096,
+// needs 8.4 MB at 64 rows) and one counter per 128 columns of N <= 128 K.
+constexpr size_t kSmallPartBytes = 16u << 20;
+constexpr int kSmallCounters = 1024;
+
+// Per-thread stream and staging buffers (slot 0: A, 1: B, 2: C, 3: scales),
+// and the small-M scratch with the event that marks its last use: a later
+// small-M launch on another stream waits for it, so two launches sharing
+// the scratch never overlap.
 struct ThreadCtx {
     hipStream_t stream = nullptr;
     void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
     size_t cap[4] = {0, 0, 0, 0};
+    pkgpu::SmallmScratch sm;
+    hipEvent_t sm_done = nullptr;
+    hipStream_t sm_stream = nullptr;     // stream of the last small-M launch
+    bool sm_pending = false;             // sm_done marks a launch
 };
 // A thread's context goes back to g_free_ctx when the thread exits (no HIP
 // call at exit: the stream is idle, since every host-pointer call waits for
@@ -82,6 +103,12 @@ thread_local CtxHolder t_holder;
 void free_ctx(ThreadCtx* c)
 {
     (void)hipStreamSynchronize(c->stream);
+    if (c->sm_done) {
+        (void)hipEventSynchronize(c->sm_done);
+        (void)hipEventDestroy(c->sm_done);
+    }
+    if (c->sm.part) (void)hipFree(c->sm.part);
+    if (c->sm.cnt) (void)hipFree(c->sm.cnt);
     for (int i = 0; i < 4; ++i)
         if (c->buf[i]) (void)hipFree(c->buf[i]);
     (void)hipStreamDestroy(c->stream);
@@ -154,6 +181,24 @@ int thread_ctx(ThreadCtx** out)
             if (e != hipSuccess) {
                 delete c;
                 return hip_fail(e, "hipStreamCreate");
+            }
+            // the small-M scratch, counters zeroed once (each launch leaves
+            // them zero); without it the thread takes the exact kernels
+            void* part = nullptr;
+            void* cnt = nullptr;
+            if (hipMalloc(&part, kSmallPartBytes) == hipSuccess &&
+                hipMalloc(&cnt, kSmallCounters * sizeof(unsigned)) == hipSuccess &&
+                hipMemset(cnt, 0, kSmallCounters * sizeof(unsigned)) == hipSuccess &&
+                hipEventCreateWithFlags(&c->sm_done, hipEventDisableTiming) == hipSuccess) {
+                c->sm.part = static_cast<float*>(part);
+                c->sm.part_bytes = kSmallPartBytes;
+                c->sm.cnt = static_cast<unsigned*>(cnt);
+                c->sm.cnt_n = kSmallCounters;
+            } else {
+                if (part) (void)hipFree(part);
+                if (cnt) (void)hipFree(cnt);
+                c->sm_done = nullptr;
+                (void)hipGetLastError();
             }
         }
         t_holder.c = c;
@@ -236,9 +281,35 @@ bool does_multiply(const GemmProblem& p)
            !(p.kind == pkgpu::W_I8 && p.scale == 0.0f);
 }
 
-int launch(const GemmProblem& p, hipStream_t s)
+// small_ok: the call may take the small-M kernels (the public GEMM entry
+// points, unless this thread asked for exact numerics or forced a tile).
+int launch(const GemmProblem& p, hipStream_t s, bool small_ok)
 {
-    hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg);
+    ThreadCtx* c = t_holder.c;
+    const pkgpu::SmallmScratch* sm = nullptr;
+    bool capturing = false;
+    if (small_ok && t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0 && c && c->sm.part &&
+        pkgpu::smallm_supports(p)) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        const hipError_t ce = hipStreamIsCapturing(s, &cs);
+        if (ce != hipSuccess) return hip_fail(ce, "stream capture status");
+        capturing = cs != hipStreamCaptureStatusNone;
+        // after this thread's previous small-M launch if that went to another
+        // stream (inside a capture, the graph's own order applies)
+        if (!capturing && c->sm_pending && c->sm_stream != s) {
+            const hipError_t w = hipStreamWaitEvent(s, c->sm_done, 0);
+            if (w != hipSuccess) return hip_fail(w, "small-M ordering");
+        }
+        sm = &c->sm;
+    }
+    bool used_small = false;
+    hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, sm, &used_small);
+    if (e == hipSuccess && used_small && !capturing) {
+        const hipError_t r = hipEventRecord(c->sm_done, s);
+        if (r != hipSuccess) return hip_fail(r, "small-M ordering");
+        c->sm_stream = s;
+        c->sm_pending = true;
+    }
     if (e == hipErrorInvalidValue)
         return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
                     p.M, p.N, p.K);
@@ -298,7 +369,7 @@ int host_gemm(GemmProblem p, const float* hA, const void* hB, const float* hScal
     const int ldc_host = p.ldc;
     p.C = static_cast<float*>(dC);
     p.ldc = p.N;
-    rc = launch(p, c->stream);
+    rc = launch(p, c->stream, true);
     if (rc) return rc;
     e = hipMemcpy2DAsync(hC, (size_t)ldc_host * 4, dC, (size_t)p.N * 4, (size_t)p.N * 4, p.M,
                          hipMemcpyDeviceToHost, c->stream);
@@ -479,7 +550,7 @@ static int dev_gemm(GemmProblem p, const float* dbias, int epi, void* stream)
     if (rc) return rc;
     p.bias = dbias;
     p.epi = static_cast<pkgpu::Epilogue>(epi);
-    return launch(p, s);
+    return launch(p, s, true);
 }
 
 int pk_gpu_gemm_i8_ex_dev(int M, int N, int K, float alpha, const float* dA, int lda,
@@ -580,6 +651,30 @@ int pk_gpu_force_config(int index)
     return PK_GPU_OK;
 }
 
+int pk_gpu_set_numerics(int mode)
+{
+    if (mode != PK_GPU_NUMERICS_DEFAULT && mode != PK_GPU_NUMERICS_EXACT)
+        return fail(PK_GPU_EINVAL, "numerics mode %d is not one of PK_GPU_NUMERICS_*", mode);
+    t_numerics = mode;
+    return PK_GPU_OK;
+}
+
+int pk_gpu_get_numerics(void) { return t_numerics; }
+
+int pk_gpu_uses_small_m(int M, int N, int K, int bits)
+{
+    GemmProblem p{};
+    p.kind = bits == 4 ? pkgpu::W_I4 : bits == 8 ? pkgpu::W_I8 : pkgpu::W_F32;
+    p.M = M; p.N = N; p.K = K;
+    p.alpha = 1.0f; p.scale = 1.0f;
+    p.A = reinterpret_cast<const float*>(uintptr_t(256));
+    p.B = reinterpret_cast<const void*>(uintptr_t(256));
+    p.scales = reinterpret_cast<const float*>(uintptr_t(256));
+    p.lda = K; p.ldb = bits == 4 ? N / 2 : N; p.ldc = N;
+    return t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0 && pkgpu::smallm_supports(p) &&
+           pkgpu::smallm_scratch_bytes(p) <= kSmallPartBytes && pkgpu::smallm_counters(p) <= kSmallCounters;
+}
+
 }  // extern "C"
 
 // Hooks for the other host translation units (pk_gpu_internal.h).
@@ -608,7 +703,7 @@ int bind(hipStream_t* thread_stream)
     return PK_GPU_OK;
 }
 
-int gemm(const GemmProblem& p, hipStream_t s) { return launch(p, s); }
+int gemm(const GemmProblem& p, hipStream_t s) { return launch(p, s, false); }
 
 int forced_config() { return t_force_cfg; }
 

@@ -44,6 +44,9 @@ _PROTOS = {
     "pk_gpu_pick_config": (_i, [_i, _i, _i]),
     "pk_gpu_pick_config_bits": (_i, [_i, _i, _i, _i]),
     "pk_gpu_force_config": (_i, [_i]),
+    "pk_gpu_set_numerics": (_i, [_i]),
+    "pk_gpu_get_numerics": (_i, []),
+    "pk_gpu_uses_small_m": (_i, [_i, _i, _i, _i]),
     "pk_gpu_layer_norm_dev": (_i, [_p, _p, _p, _p, _i, _i, _p]),
     "pk_gpu_attention_dev": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
     "pk_gpu_glu_dev": (_i, [_p, _p, _i, _i, _p]),
@@ -63,6 +66,7 @@ _PROTOS = {
 }
 
 EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL, EPI_RESIDUAL = 0, 1, 2, 3
+NUMERICS_DEFAULT, NUMERICS_EXACT = 0, 1
 
 
 class Weight(ctypes.Structure):

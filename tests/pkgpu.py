@@ -62,9 +62,20 @@ class Dev:
         self.torch.cuda.synchronize(self.dev)
 
     def gemm(self, kind, A, W, C0, alpha=1.0, beta=0.0, scale=None, scales=None, cfg=-1,
-             bias=None, epi=None):
+             bias=None, epi=None, exact=True):
         """Run C = beta*C0 + alpha*A*W through the *_dev entry points (the *_ex_dev
-        ones when a bias or an epilogue is given); returns numpy C."""
+        ones when a bias or an epilogue is given); returns numpy C.  exact: with
+        PK_GPU_NUMERICS_EXACT on this thread (bit-identical chains for every
+        shape); otherwise the default numerics (the small-M kernels for M <= 64)."""
+        lib = pk.load()
+        prev = lib.pk_gpu_get_numerics()
+        pk.call("pk_gpu_set_numerics", pk.NUMERICS_EXACT if exact else pk.NUMERICS_DEFAULT)
+        try:
+            return self._gemm(kind, A, W, C0, alpha, beta, scale, scales, cfg, bias, epi)
+        finally:
+            pk.call("pk_gpu_set_numerics", prev)
+
+    def _gemm(self, kind, A, W, C0, alpha, beta, scale, scales, cfg, bias, epi):
         M, K = A.shape
         dA, dC = self.put(A), self.put(C0)
         ex = bias is not None or epi is not None

@@ -27,6 +27,21 @@ def dev():
     return Dev()
 
 
+@pytest.fixture(scope="module", autouse=True)
+def exact_numerics():
+    """Every call here is the bit-identical path (PK_GPU_NUMERICS_EXACT on the
+    test thread; _host_call sets it on worker threads).  The small-M path has
+    its own tests (test_gpu_smallm.py)."""
+    if not __import__("pkgpu").gpu_available():
+        yield
+        return
+    lib = pk.load()
+    prev = lib.pk_gpu_get_numerics()
+    pk.call("pk_gpu_set_numerics", pk.NUMERICS_EXACT)
+    yield
+    pk.call("pk_gpu_set_numerics", prev)
+
+
 def make(kind, M, N, K, tag, wstd=0.02):
     A = po.normal((M, K), 0.0, 1.0, po.seed(SEED, f"{tag}.A"))
     C0 = po.normal((M, N), 0.0, 1.0, po.seed(SEED, f"{tag}.C"))
@@ -199,6 +214,7 @@ def test_batched_chunks_sampled_rows(dev, kind, N, K, M):
 
 def _host_call(kind, M, N, K, A, lda, W, extra, C, ldc, alpha, beta):
     lib = pk.load()
+    pk.call("pk_gpu_set_numerics", pk.NUMERICS_EXACT)     # also on worker threads
     if kind == "i4":
         rc = lib.pk_gpu_gemm_i4(M, N, K, alpha, A.ctypes.data, lda, W.ctypes.data,
                                 extra.ctypes.data, N // 2, beta, C.ctypes.data, ldc)
