@@ -24,9 +24,13 @@ Prints one JSON line: encoder frames/s, plus
   host_path     frames/s through the host-pointer entry points (features or
                 mel spectrogram in host memory, PCIe copies included)
   cpu_baseline  the reference's own 24 conformer blocks (compiled from its
-                sources, oracle/_ref/libpkref_block_x86.so) on a bounded
-                sample of the same workload: whole 416-row chunks, PK_THREADS
-                = 16 host threads (the reference's clamp).
+                sources, oracle/_ref/libpkref_block_x86.so) on whole passes
+                of the same workload, PK_THREADS = the usable host CPUs (the
+                reference clamps its pool to 16).
+  workloads     the per-GEMM workloads beside it: the int8 QKV at M = 32
+                (small-M and exact kernels), the int4 FFN pair at M = 375,
+                the fp32 pair at M = 500 and one block on a 416-row chunk,
+                each with the reference's CPU time on the same inputs.
 
 Other modes: --ffn times the int4 feed-forward pair at M = 375 (30 s of
 audio); --gemm KIND:MxNxK times single weight GEMMs.
@@ -447,6 +451,204 @@ def encoder_cpu_baseline(model, x, budget_s):
             "s_per_pass": round(el / passes, 3)}
 
 
+# ---- the per-GEMM workloads (0-3), timed beside the encoder ----------------
+
+def graph_us(torch, dev, call, steps, warmup):
+    """Average microseconds of call(i): HIP events around a graph replay of
+    `steps` calls captured back to back (a host loop of ctypes launches cannot
+    keep a queue of few-microsecond kernels full)."""
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            call(i)
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    del graph
+    return e0.elapsed_time(e1) / steps * 1e3
+
+
+def cpu_seconds_per_call(fn, budget_s, max_calls=10000):
+    """Seconds per fn() call over ~budget_s (one untimed call first)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= max_calls:
+            return el / n, n
+
+
+def workload_timings(pk, lib, torch, dev, cpu_budget_s):
+    """Workloads 0-3 of the benchmark definition, each on the GPU (inputs
+    resident, weights rotating over replicas that exceed the 256 MB Infinity
+    Cache, graph replays) and through the reference's own x86 build
+    (oracle/_ref, PK_THREADS = 16) on the same inputs for ~cpu_budget_s."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+    have_ref = po.have_ref("ref")
+    os.environ["PK_THREADS"] = str(CPU_THREADS)
+    cur = lambda: torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+
+    def ref_time(fn):
+        if not have_ref:
+            return None, 0
+        return cpu_seconds_per_call(fn, cpu_budget_s)
+
+    # 0: int8 fused QKV of a 2.56 s clip, M = 32 (cblas_sgemm_qb)
+    m, n, k = 32, 3072, 1024
+    r0 = np.random.Generator(np.random.PCG64([0x5EED0000, 0]))
+    X = r0.standard_normal((m, k)).astype(np.float32)
+    Q = r0.integers(-127, 128, (k, n), dtype=np.int8)
+    dX, dC = torch.from_numpy(X).to(dev), torch.zeros((m, n), device=dev)
+    reps = 128                                          # 128 x 3 MiB
+    dQ = [torch.from_numpy(Q).to(dev)] + [torch.randint(-127, 128, (k, n), dtype=torch.int8, device=dev)
+                                          for _ in range(reps - 1)]
+    call = lambda i: pk.check("pk_gpu_gemm_i8_dev", lib.pk_gpu_gemm_i8_dev(
+        m, n, k, 1.0, dX.data_ptr(), k, dQ[i % reps].data_ptr(), 0.01, n, 0.0, dC.data_ptr(), n, cur()))
+    us_small = graph_us(torch, dev, call, 200, 10)
+    call(0)
+    torch.cuda.synchronize(dev)
+    got = dC.cpu().numpy()
+    pk.call("pk_gpu_set_numerics", pk.NUMERICS_EXACT)
+    try:
+        us_exact = graph_us(torch, dev, call, 200, 10)
+        call(0)
+        torch.cuda.synchronize(dev)
+        got_exact = dC.cpu().numpy()
+    finally:
+        pk.call("pk_gpu_set_numerics", pk.NUMERICS_DEFAULT)
+    R = np.zeros((m, n), np.float32)
+    cpu_s, cpu_n = ref_time(lambda: po.sgemm_qb(X, Q, 0.01, R, impl="ref"))
+    by = alg_bytes("i8", m, n, k)
+    w0 = {"gemm": f"int8 {m}x{n}x{k}, per-tensor scale 0.01",
+          "small_m_us": round(us_small, 2), "small_m_gbps": round(by / us_small / 1e3, 1),
+          "small_m_frac_hbm": round(by / us_small / 1e3 / PEAK_HBM_GBS, 4),
+          "exact_us": round(us_exact, 2), "exact_gbps": round(by / us_exact / 1e3, 1),
+          "cpu_ref_us": round(cpu_s * 1e6, 1) if cpu_s else None, "cpu_ref_calls": cpu_n}
+    if have_ref:
+        w0["small_m_max_rel_err_vs_ref"] = float(np.abs(got.astype(np.float64) - R).max() / np.abs(R).max())
+        w0["exact_bit_identical_to_ref"] = bool(np.array_equal(got_exact.view(np.uint32), R.view(np.uint32)))
+    out["0_int8_qkv_m32"] = w0
+    del dQ
+
+    # 1: int4 feed-forward pair at 30 s of audio, M = 375 (cblas_sgemm_q4b x2 + pk_swish)
+    X1, P1, S1, P2, S2 = make_inputs()
+    d1 = torch.from_numpy(X1).to(dev)
+    reps1 = 64                                          # 64 x 5.2 MB
+    w1 = [tuple(torch.from_numpy(a).to(dev) for a in (P1, S1, P2, S2))]
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(SEED)
+    for _ in range(reps1 - 1):
+        w1.append((torch.randint(0, 256, (D, FF // 2), dtype=torch.uint8, device=dev, generator=g1), w1[0][1],
+                   torch.randint(0, 256, (FF, D // 2), dtype=torch.uint8, device=dev, generator=g1), w1[0][3]))
+    dH, dO = torch.empty((M, FF), device=dev), torch.empty((M, D), device=dev)
+
+    def pair(i):
+        P1d, S1d, P2d, S2d = w1[i % reps1]
+        pk.check("up", lib.pk_gpu_gemm_i4_ex_dev(M, FF, D, 1.0, d1.data_ptr(), D, P1d.data_ptr(),
+                                                 S1d.data_ptr(), FF // 2, 0.0, dH.data_ptr(), FF, None,
+                                                 pk.EPI_SWISH, cur()))
+        pk.check("down", lib.pk_gpu_gemm_i4_dev(M, D, FF, 1.0, dH.data_ptr(), FF, P2d.data_ptr(),
+                                                S2d.data_ptr(), D // 2, 0.0, dO.data_ptr(), D, cur()))
+    us1 = graph_us(torch, dev, pair, 100, 5)
+    cpu1 = None if not have_ref else cpu_baseline(X1, P1, S1, P2, S2, cpu_budget_s)
+    fl1 = 4.0 * M * D * FF
+    out["1_int4_ffn_pair_m375"] = {
+        "gemm": "int4 375x4096x1024 (+ Swish) then 375x1024x4096, 32-column fp32 scales",
+        "gpu_us": round(us1, 2), "tflops": round(fl1 / us1 / 1e6, 2),
+        "frac_mfma_fp32": round(fl1 / us1 / 1e6 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "cpu_ref_us": cpu1["ms_per_step"] * 1e3 if cpu1 else None,
+        "note": "the reference's x86 AVX2 int4 unpack decodes nibbles differently from its "
+                "portable path (the format definition, which the GPU follows), so only its time "
+                "is compared here; parity is in the tests"}
+    del w1
+
+    # 2: fp32 pair at the full-sequence threshold, M = 500 (cblas_sgemm)
+    m2 = 500
+    r2 = np.random.Generator(np.random.PCG64([0x5EED0002, 0]))
+    X2 = r2.standard_normal((m2, D)).astype(np.float32)
+    W2a = (r2.standard_normal((D, FF)) * 0.02).astype(np.float32)
+    W2b = (r2.standard_normal((FF, D)) * 0.02).astype(np.float32)
+    d2 = torch.from_numpy(X2).to(dev)
+    reps2 = 10                                          # 10 x 32 MiB
+    w2 = [(torch.from_numpy(W2a).to(dev), torch.from_numpy(W2b).to(dev))]
+    for _ in range(reps2 - 1):
+        w2.append((torch.randn((D, FF), device=dev) * 0.02, torch.randn((FF, D), device=dev) * 0.02))
+    dH2, dO2 = torch.empty((m2, FF), device=dev), torch.empty((m2, D), device=dev)
+
+    def fp32_pair(i):
+        a, b = w2[i % reps2]
+        pk.check("sgemm", lib.pk_gpu_sgemm_dev(m2, FF, D, 1.0, d2.data_ptr(), D, a.data_ptr(), FF, 0.0,
+                                               dH2.data_ptr(), FF, cur()))
+        pk.check("sgemm", lib.pk_gpu_sgemm_dev(m2, D, FF, 1.0, dH2.data_ptr(), FF, b.data_ptr(), D, 0.0,
+                                               dO2.data_ptr(), D, cur()))
+    us2 = graph_us(torch, dev, fp32_pair, 50, 3)
+    fp32_pair(0)
+    torch.cuda.synchronize(dev)
+    got2 = dO2.cpu().numpy()
+    H2, O2 = np.zeros((m2, FF), np.float32), np.zeros((m2, D), np.float32)
+
+    def ref2():
+        po.sgemm(X2, W2a, H2, impl="ref")
+        po.sgemm(H2, W2b, O2, impl="ref")
+    cpu2, n2 = ref_time(ref2)
+    fl2 = 4.0 * m2 * D * FF
+    out["2_fp32_pair_m500"] = {
+        "gemm": "fp32 500x4096x1024 then 500x1024x4096", "gpu_us": round(us2, 2),
+        "tflops": round(fl2 / us2 / 1e6, 2),
+        "frac_mfma_fp32": round(fl2 / us2 / 1e6 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "cpu_ref_us": round(cpu2 * 1e6, 1) if cpu2 else None, "cpu_ref_calls": n2,
+        "bit_identical_to_ref": bool(np.array_equal(got2.view(np.uint32), O2.view(np.uint32)))
+        if have_ref else None}
+    del w2
+
+    # 3: one conformer block on a 416-row chunk (the resident encoder, 1 block)
+    import ctypes
+    one = EncoderModel(pk, n_blocks=1)
+    x3 = enc_rng(0xFEA7, 3).standard_normal((416, D)).astype(np.float32)
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(one.blocks, ctypes.c_void_p), 1,
+            one.pe.ctypes.data, PE_ROWS, PE_CENTER)
+    try:
+        dx3 = torch.from_numpy(x3).to(dev)
+        dy3 = torch.empty_like(dx3)
+        s3 = torch.cuda.current_stream(dev)
+        run = lambda: pk.check("pk_gpu_encoder_run_dev", lib.pk_gpu_encoder_run_dev(
+            enc, dx3.data_ptr(), 416, 416, ENC_OVERLAP, dy3.data_ptr(), s3.cuda_stream))
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s3)
+        for _ in range(50):
+            run()
+        e1.record(s3)
+        torch.cuda.synchronize(dev)
+        us3 = e0.elapsed_time(e1) / 50 * 1e3
+    finally:
+        lib.pk_gpu_encoder_destroy(enc)
+    cpu3 = None
+    if po.have_ref_block("x86"):
+        pe3 = np.ascontiguousarray(one.pe[PE_CENTER - 416 + 1:PE_CENTER + 416])
+        cpu3, _ = cpu_seconds_per_call(lambda: po.ref_blocks(one.blocks, 1, pe3, x3, variant="x86"),
+                                       cpu_budget_s, 200)
+    out["3_block_m416"] = {
+        "work": "one mixed int4/int8 conformer block on a 416-row chunk (the resident encoder "
+                "with 1 block; its position projection is computed at creation)",
+        "gpu_us": round(us3, 1), "cpu_ref_us": round(cpu3 * 1e6, 1) if cpu3 else None}
+    return out
+
+
 MELS = 128
 MEL_FRAMES = 8 * ENC_FRAMES    # three stride-2 stages: 25600 mel frames -> 3200
 
@@ -686,6 +888,10 @@ def encoder_mode(args):
         out["host_path"] = {"error": str(e)}
     out["cpu_baseline"] = None if args.no_cpu else encoder_cpu_baseline(model, x, args.cpu_seconds)
     lib.pk_gpu_encoder_destroy(enc)
+    try:
+        out["workloads"] = workload_timings(pk, lib, torch, dev, 0.0 if args.no_cpu else 1.5)
+    except Exception as e:        # reported in the line; the encoder figures stand
+        out["workloads"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
 
 

@@ -11,11 +11,11 @@
  *    alpha == 0 (or, for int8, B_scale == 0), C += alpha * A * W, row-major,
  *    where every C[i][j] is the same sequential fused multiply-add chain over
  *    k ascending that the reference evaluates, so results are bit-identical.
- *    The one exception is the small-M path (pk_gpu_set_numerics): int8 and
- *    int4 GEMMs with M <= 64 stream the weights once through bf16 matrix
- *    cores and sum the same products in another order, within
- *    max |C - R| / max |R| <= 1e-3 of the reference (about 1e-5 measured),
- *    unless the calling thread asks for exact numerics.
+ *    The one exception is the small-M path (pk_gpu_set_numerics): GEMMs
+ *    with M <= 64 stream the weights once through bf16 matrix cores and sum
+ *    the same products in another order, within max |C - R| / max |R| <=
+ *    1e-3 of the reference (about 1e-5 measured), unless the calling thread
+ *    asks for exact numerics.
  *
  *  Host-pointer entry points (pk_gpu_gemm_i8, pk_gpu_gemm_i4, pk_gpu_sgemm)
  *  take host memory, exactly as the reference BLAS does.  A weight operand
@@ -362,21 +362,20 @@ int pk_gpu_config_info(int index, int *family, int *mfma, int *cw, int *wgm, int
 int pk_gpu_pick_config(int M, int N, int K);
 int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
 /* Numerics of later GEMM calls on this thread:
- *   PK_GPU_NUMERICS_DEFAULT  int8 and int4 GEMMs with M <= 64 (K a multiple
- *       of 32, N of 8 for int8, 16-byte aligned A rows; blas.c's
- *       cblas_sgemm_qb / _q4b at a short clip's M = 33) take the small-M
- *       kernels: the weights stream once, K is split across waves and
- *       workgroups and the partial sums are added in a fixed order, so the
- *       result is deterministic and within max |C - R| / max |R| <= 1e-3 of
- *       the reference R.  Every other shape is bit-identical to the
- *       reference.
+ *   PK_GPU_NUMERICS_DEFAULT  GEMMs with M <= 64 (K a multiple of 32,
+ *       16-byte aligned A rows, dword-aligned weight rows (16-byte for
+ *       int4 and fp32), N a multiple of 32 for int4; blas.c's cblas_sgemm_qb
+ *       / _q4b / cblas_sgemm at a short clip's M = 33) take the small-M
+ *       kernels: the weights stream once, each workgroup sums all of K for
+ *       its tile across its waves in a fixed order, so the result is
+ *       deterministic and within max |C - R| / max |R| <= 1e-3 of the
+ *       reference R.  They use no memory beyond the operands.  Every other
+ *       shape is bit-identical to the reference.
  *   PK_GPU_NUMERICS_EXACT  every shape bit-identical to the reference.
  * The environment variable PK_GPU_NUMERICS=exact makes EXACT every thread's
  * default.  A forced configuration (pk_gpu_force_config) implies exact
  * chains.  The device-resident encoder (pk_gpu_encoder_*) is always exact.
- * Small-M launches of one thread on different streams are ordered on the
- * device (they share the thread's scratch); inside a stream capture the
- * graph's order applies.  No counterpart in the reference. */
+ * No counterpart in the reference. */
 #define PK_GPU_NUMERICS_DEFAULT 0
 #define PK_GPU_NUMERICS_EXACT   1
 int pk_gpu_set_numerics(int mode);
@@ -384,6 +383,12 @@ int pk_gpu_get_numerics(void);
 /* Whether a GEMM of this shape and weight format (bits 4, 8 or 32) would take
  * the small-M kernels on this thread, given aligned operands. */
 int pk_gpu_uses_small_m(int M, int N, int K, int bits);
+/* Force the small-M tile for later calls on this thread: rb 16-row blocks
+ * (1..4) and nct 16-column tiles (1..2, rb * nct <= 4; fp32 takes nct = 1,
+ * rb <= 3) per workgroup; (0, 0) = the modelled choice.  A tuning and test
+ * hook with no counterpart in the reference.  Returns PK_GPU_EINVAL for
+ * other values. */
+int pk_gpu_force_small_tile(int rb, int nct);
 /* Force a configuration for later calls on this thread (-1 = automatic),
  * encoder runs included: an encoder keeps its captured graphs per forced
  * configuration, so a change takes effect on the next run. */

@@ -71,34 +71,26 @@ int num_configs();
 TileConfig config_at(int i);
 
 // ---- small-M kernels (pk_smallm.hip): the tolerance path for M <= 64 -----
-// Split-K partial tiles and per-column-tile arrival counters; the counters
-// are zero between launches (each launch resets the ones it used).  Launches
-// that share a scratch must not run concurrently.
 constexpr int kSmallMaxM = 64;
-struct SmallmScratch {
-    float* part = nullptr;
-    size_t part_bytes = 0;
-    unsigned* cnt = nullptr;
-    int cnt_n = 0;
-};
 // Whether a shape and its operands' alignment suit the small-M kernels
-// (int8 or int4 weights, M <= 64, K % 32 == 0, 16-byte aligned A rows, ...).
+// (M <= 64, K % 32 == 0, 16-byte aligned A rows, dword-aligned weight rows,
+// int4: N % 32 == 0, ...).
 bool smallm_supports(const GemmProblem& p);
-// Scratch the launch needs: partial bytes (0 when one k segment suffices)
-// and counters (one per 128-column tile).
-size_t smallm_scratch_bytes(const GemmProblem& p);
-int smallm_counters(const GemmProblem& p);
-// Launch on `stream`; hipErrorNotSupported if the shape is not handled or
-// the scratch is too small (the caller then takes the exact kernels).
-hipError_t launch_smallm(const GemmProblem& p, hipStream_t stream, const SmallmScratch& sc);
+// Tile the small-M kernel takes for a shape: rb 16-row blocks and nct
+// 16-column tiles per workgroup.
+void smallm_tile(const GemmProblem& p, int* rb, int* nct);
+// Force the tile of later launches on the calling thread ((0, 0): the model's
+// choice); false for an invalid tile.  fp32 clamps to nct = 1, rb <= 3.
+bool smallm_force_tile(int rb, int nct);
+// Launch on `stream`; hipErrorNotSupported if the shape is not handled (the
+// caller then takes the exact kernels).
+hipError_t launch_smallm(const GemmProblem& p, hipStream_t stream);
 
 // Launch the whole GEMM (beta pre-pass semantics, early exits, int8 edge
 // columns) on `stream`.  Returns hipSuccess or the launch error.
-// cfg_index < 0 selects choose_config_index().  With `small` given (and no
-// forced configuration) shapes the small-M kernels handle go there; *used_small
-// (if given) says whether they did.
-hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index,
-                       const SmallmScratch* small = nullptr, bool* used_small = nullptr);
+// cfg_index < 0 selects choose_config_index().  With `small` (and no forced
+// configuration) shapes the small-M kernels handle go there.
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, bool small = false);
 
 // Swish y = x * (1 / (1 + exp(-x))) with the reference's polynomial exp
 // (tensor_ops.c:98-120, 381-388), n elements, in place allowed.

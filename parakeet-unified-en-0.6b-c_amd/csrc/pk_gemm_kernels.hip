@@ -101,10 +101,8 @@ static int choose_index(int M, int N, int K, WeightKind kind = W_I8)
 
 int choose_config_index(int M, int N, int K, WeightKind kind) { return choose_index(M, N, K, kind); }
 
-hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index,
-                       const SmallmScratch* small, bool* used_small)
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, bool small)
 {
-    if (used_small) *used_small = false;
     if (p.M <= 0 || p.N <= 0) return hipSuccess;
     if ((p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL) && p.beta != 0.0f)
         return hipErrorInvalidValue;
@@ -145,11 +143,8 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index,
     }
 
     if (small && cfg_index < 0 && smallm_supports(p)) {
-        const hipError_t e = launch_smallm(p, stream, *small);
-        if (e != hipErrorNotSupported) {
-            if (used_small) *used_small = e == hipSuccess;
-            return e;
-        }
+        const hipError_t e = launch_smallm(p, stream);
+        if (e != hipErrorNotSupported) return e;
     }
 
     // Exact extents of what the call may read; the kernels address operands

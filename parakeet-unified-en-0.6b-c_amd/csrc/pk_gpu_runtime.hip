@@ -32,6 +32,7 @@ std::mutex g_mu;                 // guards everything below
 bool g_inited = false;
 int g_device = -1;
 
+
 // A registered weight's device copy.  Host-pointer GEMMs hold a reference
 // from the lookup until their stream has finished, so an unregister on
 // another thread only removes the entry; the copy is freed (after the
@@ -65,24 +66,11 @@ int default_numerics()
 }
 thread_local int t_numerics = default_numerics();
 
-// Split-K scratch of the small-M kernels, per thread context: partial tiles
-// for the encoder's shapes at M <= 64 (the FFN up projection, N = 4096,
-// needs 8.4 MB at 64 rows) and one counter per 128 columns of N <= 128 K.
-constexpr size_t kSmallPartBytes = 16u << 20;
-constexpr int kSmallCounters = 1024;
-
-// Per-thread stream and staging buffers (slot 0: A, 1: B, 2: C, 3: scales),
-// and the small-M scratch with the event that marks its last use: a later
-// small-M launch on another stream waits for it, so two launches sharing
-// the scratch never overlap.
+// Per-thread stream and staging buffers (slot 0: A, 1: B, 2: C, 3: scales).
 struct ThreadCtx {
     hipStream_t stream = nullptr;
     void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
     size_t cap[4] = {0, 0, 0, 0};
-    pkgpu::SmallmScratch sm;
-    hipEvent_t sm_done = nullptr;
-    hipStream_t sm_stream = nullptr;     // stream of the last small-M launch
-    bool sm_pending = false;             // sm_done marks a launch
 };
 // A thread's context goes back to g_free_ctx when the thread exits (no HIP
 // call at exit: the stream is idle, since every host-pointer call waits for
@@ -103,12 +91,6 @@ thread_local CtxHolder t_holder;
 void free_ctx(ThreadCtx* c)
 {
     (void)hipStreamSynchronize(c->stream);
-    if (c->sm_done) {
-        (void)hipEventSynchronize(c->sm_done);
-        (void)hipEventDestroy(c->sm_done);
-    }
-    if (c->sm.part) (void)hipFree(c->sm.part);
-    if (c->sm.cnt) (void)hipFree(c->sm.cnt);
     for (int i = 0; i < 4; ++i)
         if (c->buf[i]) (void)hipFree(c->buf[i]);
     (void)hipStreamDestroy(c->stream);
@@ -181,24 +163,6 @@ int thread_ctx(ThreadCtx** out)
             if (e != hipSuccess) {
                 delete c;
                 return hip_fail(e, "hipStreamCreate");
-            }
-            // the small-M scratch, counters zeroed once (each launch leaves
-            // them zero); without it the thread takes the exact kernels
-            void* part = nullptr;
-            void* cnt = nullptr;
-            if (hipMalloc(&part, kSmallPartBytes) == hipSuccess &&
-                hipMalloc(&cnt, kSmallCounters * sizeof(unsigned)) == hipSuccess &&
-                hipMemset(cnt, 0, kSmallCounters * sizeof(unsigned)) == hipSuccess &&
-                hipEventCreateWithFlags(&c->sm_done, hipEventDisableTiming) == hipSuccess) {
-                c->sm.part = static_cast<float*>(part);
-                c->sm.part_bytes = kSmallPartBytes;
-                c->sm.cnt = static_cast<unsigned*>(cnt);
-                c->sm.cnt_n = kSmallCounters;
-            } else {
-                if (part) (void)hipFree(part);
-                if (cnt) (void)hipFree(cnt);
-                c->sm_done = nullptr;
-                (void)hipGetLastError();
             }
         }
         t_holder.c = c;
@@ -285,31 +249,8 @@ bool does_multiply(const GemmProblem& p)
 // points, unless this thread asked for exact numerics or forced a tile).
 int launch(const GemmProblem& p, hipStream_t s, bool small_ok)
 {
-    ThreadCtx* c = t_holder.c;
-    const pkgpu::SmallmScratch* sm = nullptr;
-    bool capturing = false;
-    if (small_ok && t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0 && c && c->sm.part &&
-        pkgpu::smallm_supports(p)) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        const hipError_t ce = hipStreamIsCapturing(s, &cs);
-        if (ce != hipSuccess) return hip_fail(ce, "stream capture status");
-        capturing = cs != hipStreamCaptureStatusNone;
-        // after this thread's previous small-M launch if that went to another
-        // stream (inside a capture, the graph's own order applies)
-        if (!capturing && c->sm_pending && c->sm_stream != s) {
-            const hipError_t w = hipStreamWaitEvent(s, c->sm_done, 0);
-            if (w != hipSuccess) return hip_fail(w, "small-M ordering");
-        }
-        sm = &c->sm;
-    }
-    bool used_small = false;
-    hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, sm, &used_small);
-    if (e == hipSuccess && used_small && !capturing) {
-        const hipError_t r = hipEventRecord(c->sm_done, s);
-        if (r != hipSuccess) return hip_fail(r, "small-M ordering");
-        c->sm_stream = s;
-        c->sm_pending = true;
-    }
+    const bool small = small_ok && t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0;
+    const hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, small);
     if (e == hipErrorInvalidValue)
         return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
                     p.M, p.N, p.K);
@@ -661,6 +602,13 @@ int pk_gpu_set_numerics(int mode)
 
 int pk_gpu_get_numerics(void) { return t_numerics; }
 
+int pk_gpu_force_small_tile(int rb, int nct)
+{
+    if (!pkgpu::smallm_force_tile(rb, nct))
+        return fail(PK_GPU_EINVAL, "small-M tile rb = %d, nct = %d (rb 1..4, nct 1..2, rb * nct <= 4)", rb, nct);
+    return PK_GPU_OK;
+}
+
 int pk_gpu_uses_small_m(int M, int N, int K, int bits)
 {
     GemmProblem p{};
@@ -671,8 +619,7 @@ int pk_gpu_uses_small_m(int M, int N, int K, int bits)
     p.B = reinterpret_cast<const void*>(uintptr_t(256));
     p.scales = reinterpret_cast<const float*>(uintptr_t(256));
     p.lda = K; p.ldb = bits == 4 ? N / 2 : N; p.ldc = N;
-    return t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0 && pkgpu::smallm_supports(p) &&
-           pkgpu::smallm_scratch_bytes(p) <= kSmallPartBytes && pkgpu::smallm_counters(p) <= kSmallCounters;
+    return t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0 && pkgpu::smallm_supports(p);
 }
 
 }  // extern "C"

@@ -17,30 +17,26 @@
 // 2^-16 |x|, and bf16 keeps fp32's exponent range, so no prescaling is needed.
 //   int8: the codes q are exact in bf16; C = alpha*s * (A_hi Q + A_lo Q)
 //         (2 MFMAs per tile), s the per-tensor scale.
-//   int4: w = fl(q * s[k][n/32]) exactly as blas.c:834-840 dequantises it,
-//         split into w_hi + w_lo; C = alpha * (A_hi W_hi + A_lo W_hi +
-//         A_hi W_lo) (3 MFMAs; the dropped A_lo W_lo term is below 2^-16).
+//   int4: the codes q are exact in bf16 and a workgroup's columns share one
+//         scale group, so the scale folds into the activations: A' =
+//         fl(A * s[k][n/32]) (the products of blas.c:834-840's dequantised
+//         weight fl(q*s) with A differ from fl(A*s)*q by one rounding of
+//         2^-24), C = alpha * (A'_hi Q + A'_lo Q).
+//   fp32: B = B_hi + B_lo as well; C = alpha * (A_hi B_hi + A_lo B_hi +
+//         A_hi B_lo) (3 MFMAs; the dropped A_lo B_lo term is below 2^-16).
 // The activations are never quantised: they stay fp32-valued to 16 bits.
 //
-// Work split.  A workgroup of 4 waves owns 128 columns; its waves take
-// consecutive 32-deep k steps of one k segment (KS steps each).  A wave's
-// lane (i, g) = (lane % 16, lane / 16) loads, per k step, rows k0 + 8g ..
-// k0 + 8g + 7 of columns c0 + 8i .. c0 + 8i + 7: 16 lanes read one 128-byte
-// run of each row (int8; 64 bytes for int4, with the row's scales), and the
-// weights reach the MFMA operand layout (8 k values of one column per lane)
-// in registers, with no LDS pass.  MFMA slice j (0..7) multiplies column
-// c0 + 8i + j into output slot i.
-// The 4 waves' partial tiles are summed in LDS in a fixed order,
-// (w0 + w2) + (w1 + w3).  With S > 1 segments per column tile each
-// workgroup writes its partial to scratch at device scope; the last to
-// arrive (an atomic counter per tile) sums the S partials in segment order,
-// applies the epilogue and resets the counter.  Every sum has a fixed order, so results
-// are deterministic.  The S segments of a tile go to workgroups on one XCD.
+// Work split: see the narrow-tile kernel below.  Every workgroup sums all of
+// K for its tile, in a fixed order, so results are deterministic and no
+// partial sums leave the workgroup.
 #include "pk_gemm_kernels.h"
 #include "pk_device_math.h"
 
 #include <algorithm>
+#include <cmath>
+#include <cstdio>
 #include <cstdlib>
+#include <utility>
 
 namespace pkgpu {
 namespace {
@@ -53,10 +49,7 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-constexpr int kCols = 128;     // columns per workgroup
-constexpr int kWaves = 4;
 constexpr int kXcd = 8;
-constexpr int kSc1 = 16;       // buffer-op cache policy: device-scope coherence (sc1)
 
 struct SmArgs {
     int M, N, K;
@@ -67,11 +60,7 @@ struct SmArgs {
     const float* scales; int n_groups;
     float* C; int ldc;
     const float* bias; int epi;
-    uint32_t a_bytes, b_bytes, s_bytes;
-    int NT, S;                 // column tiles, k segments per tile
-    float* part;               // [NT][S][16*RB][128] partial tiles (S > 1)
-    uint32_t part_bytes;
-    unsigned* cnt;             // [NT] arrival counters, zero between launches
+    uint32_t a_bytes, b_bytes, s_bytes;   // buffer extents (reads past them return 0)
 };
 
 __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
@@ -109,332 +98,226 @@ __device__ inline v4f mfma(v8bf a, v8bf b, v4f c)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Raw weight bits of one lane's 8 columns in one row.
-template <int WK> struct RowBits;
-template <> struct RowBits<W_I8> { typedef v2u T; };     // 8 int8
-template <> struct RowBits<W_I4> { typedef uint32_t T; }; // 8 nibbles
-
-template <int WK>
-__device__ inline typename RowBits<WK>::T load_row(__amdgpu_buffer_rsrc_t r, const SmArgs& p, int k, int c)
-{
-    if constexpr (WK == W_I8)
-        return __builtin_amdgcn_raw_buffer_load_b64(r, (int)((uint32_t)k * (uint32_t)p.ldb + (uint32_t)c), 0, 0);
-    else
-        return __builtin_amdgcn_raw_buffer_load_b32(r, (int)((uint32_t)k * (uint32_t)p.ldb + (uint32_t)(c >> 1)), 0, 0);
-}
-
-// Weight value of column j (0..7) of a lane's row bits.
-__device__ inline float w_i8(v2u b, int j)
-{
-    const uint32_t w = j < 4 ? b[0] : b[1];
-    return (float)(signed char)(w >> (8 * (j & 3)));
-}
+// Signed nibble j (0: low, 1: high) of byte b.
 __device__ inline int q_i4(uint32_t b, int j)
 {
     return (int)(b << (28 - 4 * j)) >> 28;          // low nibble = even column
 }
 
-// SMAX: at least the k segments S (1: one segment, no partials).
-template <int WK, int RB, int KS, int SMAX>
-__global__ __launch_bounds__(256) void smallm_gemm(SmArgs p)
-{
-    constexpr int MP = 16 * RB;                     // padded rows
-    __shared__ float lds[2][MP][kCols];
-    __shared__ int last;
+// ---- narrow tiles: all of K per workgroup, no partials --------------------
+// A workgroup of 16 waves owns NCT 16-column tiles and RB 16-row blocks and
+// the whole k range: wave w takes the k steps [w*ns/16, (w+1)*ns/16) of the
+// ns = K/32 steps, kChunk steps at a time.  Per chunk a wave copies the RW
+// bytes of each of its rows that hold the tile's 16*NCT columns into its own
+// LDS slab with U-byte loads (U = 16 where the weights are 16-byte aligned),
+// and lane (i, g) then reads column 16ct + i of rows 8g .. 8g + 7 of each
+// step from the slab, which is the MFMA operand layout.  Chunk row r =
+// 32st + 8g + e lives in slab slot 32st + 4e + g, so the 64 lanes of one read
+// touch 4 consecutive slots (distinct banks).  The next chunk's loads are
+// issued before the current chunk's MFMAs.  The 16*NCT columns of an int4
+// workgroup lie in one 32-column scale group, so the scale folds into the
+// activations (A' = fl(A * s[k][g]), then split) and the codes enter the
+// MFMA exactly.  The 16 waves' partial tiles are summed in LDS in wave order,
+// then the epilogue.  Row blocks beyond RB go to more workgroups (grid.y);
+// the workgroups of one column tile sit on one XCD, sharing its L2.
+constexpr int kNW = 16;                 // waves per narrow workgroup
+constexpr int kChunk = 2;               // k steps per chunk
 
-    // workgroup -> (column tile t, k segment s); the S segments of a tile on one XCD
-    const int x = blockIdx.x, xcd = x % kXcd, r = x / kXcd;
-    const int s = r % p.S, t = (r / p.S) * kXcd + xcd;
-    if (t >= p.NT) return;                          // padding workgroups (uniform)
+template <int WK, int NCT> struct Narrow {
+    static constexpr int RW = (WK == W_I8 ? 16 : WK == W_I4 ? 8 : 64) * NCT;   // row bytes
+    static constexpr int SLAB = 32 * kChunk * RW;                             // bytes per wave
+    static constexpr int SSLAB = WK == W_I4 ? 32 * kChunk * 4 : 0;            // scales per wave
+};
+
+template <int N> struct UnitT;
+template <> struct UnitT<4> { typedef uint32_t T; };
+template <> struct UnitT<8> { typedef v2u T; };
+template <> struct UnitT<16> { typedef v4u T; };
+
+template <int U>
+__device__ inline typename UnitT<U>::T load_unit(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    if constexpr (U == 16) return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    else if constexpr (U == 8) return __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    else return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+template <int WK, int RB, int NCT, int UB>
+__global__ __launch_bounds__(64 * kNW) void smallm_narrow(SmArgs p)
+{
+    typedef Narrow<WK, NCT> L;
+    constexpr int RW = L::RW;
+    constexpr int U = UB < RW ? UB : RW;            // load unit bytes
+    constexpr int UPR = RW / U;                     // units per row
+    constexpr int NU = 32 * kChunk * UPR / 64;      // units per lane per chunk
+    constexpr int STAGE = kNW * (L::SLAB + L::SSLAB);
+    constexpr int RED = kNW * RB * NCT * 64 * 16;
+    constexpr bool kPrefetchA = RB <= 2;            // registers for two chunks of A
+    typedef typename UnitT<U>::T Unit;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[STAGE > RED ? STAGE : RED];
+
+    // column tiles in XCD-sized runs (workgroups reach the XCDs round-robin)
+    const int x = blockIdx.x, per = gridDim.x / kXcd;
+    const int t = (x % kXcd) * per + x / kXcd;
+    if (t * 16 * NCT >= p.N) return;                // padding workgroup (uniform)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int i = lane & 15, g = lane >> 4;
-    const int c0 = t * kCols;
-    const int kw = s * (kWaves * KS * 32) + wave * (KS * 32);   // this wave's first k
+    const int c0 = t * 16 * NCT;
+    const int m0 = 16 * RB * blockIdx.y;
+    const int ns = p.K / 32, s0 = wave * ns / kNW, s1 = (wave + 1) * ns / kNW;
 
     const auto rA = rsrc(p.A, p.a_bytes), rB = rsrc(p.B, p.b_bytes);
     const auto rS = rsrc(p.scales, p.s_bytes);
+    const uint32_t ldb_bytes = (uint32_t)p.ldb * (WK == W_F32 ? 4u : 1u);
+    const uint32_t c0_bytes = WK == W_F32 ? 4u * c0 : WK == W_I8 ? (uint32_t)c0 : (uint32_t)c0 / 2;
+    const uint32_t grp = (uint32_t)c0 >> 5;
+    unsigned char* slab = smem + wave * L::SLAB;
+    float* sslab = reinterpret_cast<float*>(smem + kNW * L::SLAB) + wave * (32 * kChunk);
 
-    v4f acc[RB][8];
+    Unit wu[NU];
+    float sc = 0.0f;
+    v4u ar[kChunk][RB][2];
+
+    // global loads of chunk `cs` (steps cs .. cs + kChunk - 1, clipped at s1)
+    auto issue_w = [&](int cs) {
+        const int rows = 32 * min(kChunk, s1 - cs);
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const int u = lane + 64 * j, r = u / UPR, part = u % UPR;
+            if (r < rows)
+                wu[j] = load_unit<U>(rB, (uint32_t)(32 * cs + r) * ldb_bytes + c0_bytes + (uint32_t)(part * U));
+        }
+        if constexpr (WK == W_I4) {
+            if (lane < rows)
+                sc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    rS, (int)(((uint32_t)(32 * cs + lane) * (uint32_t)p.n_groups + grp) * 4u), 0, 0));
+        }
+    };
+    auto issue_a = [&](int cs, v4u (&dst)[kChunk][RB][2]) {
+#pragma unroll
+        for (int st = 0; st < kChunk; ++st) {
+            if (cs + st >= s1) break;                // uniform per wave
+            const int k0 = 32 * (cs + st);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                // row m0 + 16rb + i, k0 + 8g .. +7: rows >= M read 0 (past the extent)
+                const uint32_t off = ((uint32_t)(m0 + 16 * rb + i) * (uint32_t)p.lda + (uint32_t)(k0 + 8 * g)) * 4u;
+                dst[st][rb][0] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)off, 0, 0);
+                dst[st][rb][1] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)(off + 16), 0, 0);
+            }
+        }
+    };
+
+    v4f acc[RB][NCT];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[rb][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ct = 0; ct < NCT; ++ct) acc[rb][ct] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    // every weight load of the wave first: the HBM stream is the latency to hide
-    typename RowBits<WK>::T wb[KS][8];
-    float sc[KS][8];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const int k = kw + 32 * ks + 8 * g + rr;        // rows >= K read 0 (past the extent)
-            wb[ks][rr] = load_row<WK>(rB, p, k, c0 + 8 * i);
-            if constexpr (WK == W_I4)
-                sc[ks][rr] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    rS, (int)(((uint32_t)k * (uint32_t)p.n_groups + (uint32_t)((c0 + 8 * i) >> 5)) * 4u), 0, 0));
-        }
-
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const int k0 = kw + 32 * ks;
-        if (k0 >= p.K) break;                       // K % 32 == 0: whole steps only (uniform)
-        v8bf ahi[RB], alo[RB];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            // row 16rb + i, k0 + 8g .. +7: rows >= M read 0 (past the extent)
-            const uint32_t off = ((uint32_t)(16 * rb + i) * (uint32_t)p.lda + (uint32_t)(k0 + 8 * g)) * 4u;
-            const v4u a0 = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)off, 0, 0);
-            const v4u a1 = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)(off + 16), 0, 0);
-            const float xa[8] = {__uint_as_float(a0[0]), __uint_as_float(a0[1]), __uint_as_float(a0[2]),
-                                 __uint_as_float(a0[3]), __uint_as_float(a1[0]), __uint_as_float(a1[1]),
-                                 __uint_as_float(a1[2]), __uint_as_float(a1[3])};
-            split8(xa, ahi[rb], alo[rb]);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if constexpr (WK == W_I8) {
-                const v8bf b = cat(to_bf2(w_i8(wb[ks][0], j), w_i8(wb[ks][1], j)),
-                                   to_bf2(w_i8(wb[ks][2], j), w_i8(wb[ks][3], j)),
-                                   to_bf2(w_i8(wb[ks][4], j), w_i8(wb[ks][5], j)),
-                                   to_bf2(w_i8(wb[ks][6], j), w_i8(wb[ks][7], j)));
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb) {
-                    acc[rb][j] = mfma(ahi[rb], b, acc[rb][j]);
-                    acc[rb][j] = mfma(alo[rb], b, acc[rb][j]);
-                }
-            } else {
-                float w[8];
-#pragma unroll
-                for (int rr = 0; rr < 8; ++rr) w[rr] = __fmul_rn((float)q_i4(wb[ks][rr], j), sc[ks][rr]);
-                v8bf bhi, blo;
-                split8(w, bhi, blo);
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb) {
-                    acc[rb][j] = mfma(ahi[rb], bhi, acc[rb][j]);
-                    acc[rb][j] = mfma(alo[rb], bhi, acc[rb][j]);
-                    acc[rb][j] = mfma(ahi[rb], blo, acc[rb][j]);
-                }
-            }
-        }
+    if (s0 < s1) {
+        issue_w(s0);
+        issue_a(s0, ar);
     }
-
-    // fixed-order sum of the 4 waves' tiles: (w0 + w2) + (w1 + w3), in LDS.
-    // Lane (i, g) holds rows 16rb + 4g + v, columns 8i + j.
-    auto put = [&](int slot) {
+    for (int cs = s0; cs < s1; cs += kChunk) {
+        const int rows = 32 * min(kChunk, s1 - cs);
+        // this chunk's weights into the slab (slot 32st + 4e + g for row 32st + 8g + e)
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                float* row = &lds[slot][16 * rb + 4 * g + v][8 * i];
-                *reinterpret_cast<v4f*>(row) = v4f{acc[rb][0][v], acc[rb][1][v], acc[rb][2][v], acc[rb][3][v]};
-                *reinterpret_cast<v4f*>(row + 4) = v4f{acc[rb][4][v], acc[rb][5][v], acc[rb][6][v], acc[rb][7][v]};
-            }
-    };
-    auto add = [&](int slot) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const float* row = &lds[slot][16 * rb + 4 * g + v][8 * i];
-                const v4f a = *reinterpret_cast<const v4f*>(row), b = *reinterpret_cast<const v4f*>(row + 4);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[rb][j][v] = __fadd_rn(acc[rb][j][v], a[j]);
-                    acc[rb][4 + j][v] = __fadd_rn(acc[rb][4 + j][v], b[j]);
-                }
-            }
-    };
-    if (wave >= 2) put(wave - 2);
-    __syncthreads();
-    if (wave < 2) add(wave);
-    __syncthreads();
-    if (wave == 1) put(0);
-    __syncthreads();
-    if (wave == 0) {
-        add(0);
-        put(1);                                     // the workgroup's partial tile
-    }
-    __syncthreads();
-
-    // all 256 threads: 16*RB rows x 128 columns as float4s, U per thread
-    constexpr int kVec = MP * kCols / 4, U = kVec / 256;
-    const v4f* tile = reinterpret_cast<const v4f*>(&lds[1][0][0]);
-    auto finish = [&](int e, v4f sum) {
-        const int m = (4 * e) / kCols, col = c0 + (4 * e) % kCols;
-        if (m >= p.M) return;
-        float* crow = p.C + (size_t)m * p.ldc;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int n = col + u;
-            if (n >= p.N) break;
-            float v = __fmul_rn(p.alpha, sum[u]);
-            if (p.beta != 0.0f) v = __fadd_rn(p.beta == 1.0f ? crow[n] : __fmul_rn(p.beta, crow[n]), v);
-            if (p.bias) v = __fadd_rn(v, p.bias[n]);
-            switch (p.epi) {
-            case EPI_SWISH:         v = swish_f(v); break;
-            case EPI_HALF_RESIDUAL: v = __fmaf_rn(v, 0.5f, crow[n]); break;
-            case EPI_RESIDUAL:      v = __fadd_rn(crow[n], v); break;
-            case EPI_RELU:          v = v > 0.0f ? v : 0.0f; break;
-            default:                break;
-            }
-            crow[n] = v;
+        for (int j = 0; j < NU; ++j) {
+            const int u = lane + 64 * j, r = u / UPR, part = u % UPR;
+            const int slot = (r & ~31) | ((r & 7) << 2) | ((r >> 3) & 3);
+            if (r < rows) *reinterpret_cast<Unit*>(slab + slot * RW + part * U) = wu[j];
         }
-    };
-    if constexpr (SMAX == 1) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) finish(threadIdx.x + 256 * u, tile[threadIdx.x + 256 * u]);
-    } else {
-        // The partials pass between workgroups that may sit on different XCDs,
-        // whose L2s are not coherent with each other: they are stored and
-        // loaded at device scope (sc1: written through to, and read from, the
-        // device's coherence point), so no L2-wide write-back or invalidate
-        // (what a device-scope fence costs) is needed.  The stores complete
-        // (vmcnt 0) before the workgroup's arrival is counted.
-        const auto rP = rsrc(p.part, p.part_bytes);
-        const uint32_t mine = (uint32_t)(((size_t)t * p.S + s) * (MP * kCols) * 4);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const v4f v = tile[threadIdx.x + 256 * u];
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rP,
-                                                   (int)(mine + 16u * (threadIdx.x + 256 * u)), 0, kSc1);
+        if constexpr (WK == W_I4) {
+            if (lane < rows) sslab[lane] = sc;
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(&p.cnt[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
-                   (unsigned)(p.S - 1);
-        __syncthreads();
-        if (!last) return;
-        // every partial load of a batch in flight at once, then the sums in
-        // segment order; batches of UB float4s per thread keep <= 32 in flight
-        const uint32_t seg0 = (uint32_t)((size_t)t * p.S * (MP * kCols) * 4);
-        constexpr int UB = (32 / SMAX) < 1 ? 1 : ((32 / SMAX) > U ? U : (32 / SMAX));
-#pragma unroll
-        for (int u0 = 0; u0 < U; u0 += UB) {
-            v4f q[UB][SMAX];
-#pragma unroll
-            for (int ub = 0; ub < UB; ++ub)
-#pragma unroll
-                for (int s2 = 0; s2 < SMAX; ++s2)
-                    if (s2 < p.S)
-                        q[ub][s2] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                            rP, (int)(seg0 + 16u * ((uint32_t)s2 * kVec + threadIdx.x + 256 * (u0 + ub))),
-                            0, kSc1));
-#pragma unroll
-            for (int ub = 0; ub < UB; ++ub) {
-                v4f sum = q[ub][0];
-#pragma unroll
-                for (int s2 = 1; s2 < SMAX; ++s2)
-                    if (s2 < p.S)
-                        sum = v4f{__fadd_rn(sum[0], q[ub][s2][0]), __fadd_rn(sum[1], q[ub][s2][1]),
-                                  __fadd_rn(sum[2], q[ub][s2][2]), __fadd_rn(sum[3], q[ub][s2][3])};
-                finish(threadIdx.x + 256 * (u0 + ub), sum);
-            }
-        }
-        if (threadIdx.x == 0)                       // every segment has arrived
-            __hip_atomic_store(&p.cnt[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-}
+        // the wave's own LDS writes complete before its reads (LDS keeps a wave's order)
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-// ---- narrow tiles: 16 columns and all of K per workgroup, no partials ----
-// A workgroup of NW waves owns 16 columns (one MFMA's width) and the whole k
-// range: wave w takes k steps [w*ns/NW, (w+1)*ns/NW) of the ns = K/32 steps,
-// at most kMaxSteps, every load of them issued before the first MFMA.
-// Lane (i, g) reads column c0 + i of rows k0 + 8g .. k0 + 8g + 7 (bytes for
-// int8 / int4, words for fp32): the 16 lanes of a row read one 16-byte run,
-// and consecutive tiles run on one XCD, so each 128-byte line of a row comes
-// through that XCD's L2 once.  The 16 columns of an int4 tile lie in one
-// 32-column scale group, so the scale folds into the activations
-// (A' = fl(A * s[k][g]), then split) and the codes enter the MFMA exactly.
-// The NW partial tiles are summed in LDS in wave order, then the epilogue.
-template <int WK, int RB, int NW, int kMaxSteps>
-__global__ __launch_bounds__(64 * NW) void smallm_narrow(SmArgs p)
-{
-    __shared__ v4f red[NW][RB][64];
-    // consecutive tiles on one XCD (workgroups reach the XCDs round-robin)
-    const int x = blockIdx.x, per = gridDim.x / kXcd;
-    const int t = (x % kXcd) * per + x / kXcd;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int i = lane & 15, g = lane >> 4;
-    const int c = t * 16 + i;                        // this lane's column (>= N reads 0 or junk, never stored)
-    const int ns = p.K / 32, s0 = wave * ns / NW, s1 = (wave + 1) * ns / NW;
-
-    const auto rA = rsrc(p.A, p.a_bytes), rB = rsrc(p.B, p.b_bytes);
-    const auto rS = rsrc(p.scales, p.s_bytes);
-
-    float wv[kMaxSteps][8], sv[kMaxSteps][8];
-    v4u ar[kMaxSteps][RB][2];
+        v4u cur[kChunk][RB][2];
+        const bool more = cs + kChunk < s1;
+        if constexpr (kPrefetchA) {
 #pragma unroll
-    for (int st = 0; st < kMaxSteps; ++st) {
-        if (s0 + st >= s1) break;                    // uniform per wave
-        const int k0 = 32 * (s0 + st);
+            for (int st = 0; st < kChunk; ++st)
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const uint32_t k = (uint32_t)(k0 + 8 * g + rr);
-            if constexpr (WK == W_I8) {
-                wv[st][rr] = (float)(signed char)__builtin_amdgcn_raw_buffer_load_b8(
-                    rB, (int)(k * (uint32_t)p.ldb + (uint32_t)c), 0, 0);
-            } else if constexpr (WK == W_I4) {
-                const uint32_t b = __builtin_amdgcn_raw_buffer_load_b8(
-                    rB, (int)(k * (uint32_t)p.ldb + (uint32_t)(c >> 1)), 0, 0);
-                wv[st][rr] = (float)q_i4(b, c & 1);
-                sv[st][rr] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    rS, (int)((k * (uint32_t)p.n_groups + (uint32_t)(c >> 5)) * 4u), 0, 0));
-            } else {
-                wv[st][rr] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    rB, (int)((k * (uint32_t)p.ldb + (uint32_t)c) * 4u), 0, 0));
-            }
-        }
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const uint32_t off = ((uint32_t)(16 * rb + i) * (uint32_t)p.lda + (uint32_t)(k0 + 8 * g)) * 4u;
-            ar[st][rb][0] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)off, 0, 0);
-            ar[st][rb][1] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)(off + 16), 0, 0);
-        }
-    }
-
-    v4f acc[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) acc[rb] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < kMaxSteps; ++st) {
-        if (s0 + st >= s1) break;
-        v8bf bhi, blo;
-        if constexpr (WK == W_F32) {
-            split8(wv[st], bhi, blo);
+                for (int rb = 0; rb < RB; ++rb) { cur[st][rb][0] = ar[st][rb][0]; cur[st][rb][1] = ar[st][rb][1]; }
+            if (more) { issue_w(cs + kChunk); issue_a(cs + kChunk, ar); }
         } else {
-            bhi = cat(to_bf2(wv[st][0], wv[st][1]), to_bf2(wv[st][2], wv[st][3]),
-                      to_bf2(wv[st][4], wv[st][5]), to_bf2(wv[st][6], wv[st][7]));   // exact
+            if (more) issue_w(cs + kChunk);
         }
+
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            float xa[8] = {__uint_as_float(ar[st][rb][0][0]), __uint_as_float(ar[st][rb][0][1]),
-                           __uint_as_float(ar[st][rb][0][2]), __uint_as_float(ar[st][rb][0][3]),
-                           __uint_as_float(ar[st][rb][1][0]), __uint_as_float(ar[st][rb][1][1]),
-                           __uint_as_float(ar[st][rb][1][2]), __uint_as_float(ar[st][rb][1][3])};
-            if constexpr (WK == W_I4) {
+        for (int st = 0; st < kChunk; ++st) {
+            if (cs + st >= s1) break;                // uniform per wave
+            v8bf bhi[NCT], blo[NCT];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xa[e] = __fmul_rn(xa[e], sv[st][e]);
+            for (int ct = 0; ct < NCT; ++ct) {
+                float wv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned char* row = slab + (32 * st + 4 * e + g) * RW;
+                    const int col = 16 * ct + i;
+                    if constexpr (WK == W_I8) wv[e] = (float)(signed char)row[col];
+                    else if constexpr (WK == W_I4) wv[e] = (float)q_i4(row[col >> 1], col & 1);
+                    else wv[e] = reinterpret_cast<const float*>(row)[col];
+                }
+                if constexpr (WK == W_F32) {
+                    split8(wv, bhi[ct], blo[ct]);
+                } else {
+                    bhi[ct] = cat(to_bf2(wv[0], wv[1]), to_bf2(wv[2], wv[3]),
+                                  to_bf2(wv[4], wv[5]), to_bf2(wv[6], wv[7]));   // exact
+                }
             }
-            v8bf ahi, alo;
-            split8(xa, ahi, alo);
-            acc[rb] = mfma(ahi, bhi, acc[rb]);
-            acc[rb] = mfma(alo, bhi, acc[rb]);
-            if constexpr (WK == W_F32) acc[rb] = mfma(ahi, blo, acc[rb]);
+            float sv[8];
+            if constexpr (WK == W_I4) {
+                const v4f s_lo = *reinterpret_cast<const v4f*>(sslab + 32 * st + 8 * g);
+                const v4f s_hi = *reinterpret_cast<const v4f*>(sslab + 32 * st + 8 * g + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { sv[e] = s_lo[e]; sv[4 + e] = s_hi[e]; }
+            }
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const v4u a0 = kPrefetchA ? cur[st][rb][0] : ar[st][rb][0];
+                const v4u a1 = kPrefetchA ? cur[st][rb][1] : ar[st][rb][1];
+                float xa[8] = {__uint_as_float(a0[0]), __uint_as_float(a0[1]), __uint_as_float(a0[2]),
+                               __uint_as_float(a0[3]), __uint_as_float(a1[0]), __uint_as_float(a1[1]),
+                               __uint_as_float(a1[2]), __uint_as_float(a1[3])};
+                if constexpr (WK == W_I4) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xa[e] = __fmul_rn(xa[e], sv[e]);
+                }
+                v8bf ahi, alo;
+                split8(xa, ahi, alo);
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) {
+                    acc[rb][ct] = mfma(ahi, bhi[ct], acc[rb][ct]);
+                    acc[rb][ct] = mfma(alo, bhi[ct], acc[rb][ct]);
+                    if constexpr (WK == W_F32) acc[rb][ct] = mfma(ahi, blo[ct], acc[rb][ct]);
+                }
+            }
         }
+        if constexpr (!kPrefetchA) {
+            if (more) issue_a(cs + kChunk, ar);
+        }
+        // this chunk's slab reads are done before the next chunk overwrites it
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
     // fixed-order sum over the waves, one output per thread
+    __syncthreads();                                 // every slab read done: reuse as `red`
+    v4f* red = reinterpret_cast<v4f*>(smem);         // [kNW][RB][NCT][64]
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) red[wave][rb][lane] = acc[rb];
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) red[((wave * RB + rb) * NCT + ct) * 64 + lane] = acc[rb][ct];
     __syncthreads();
-    const int o = threadIdx.x;                       // output (rb, lane l, v)
-    if (o >= RB * 256) return;
-    const int rb = o >> 8, l = (o >> 2) & 63, v = o & 3;
-    float sum = red[0][rb][l][v];
+    const int o = threadIdx.x;                       // output (rb, ct, lane l, v)
+    if (o >= RB * NCT * 256) return;
+    const int rb = o / (NCT * 256), ct = (o >> 8) % NCT, l = (o >> 2) & 63, v = o & 3;
+    const float* rf = reinterpret_cast<const float*>(red);
+    float sum = rf[((rb * NCT + ct) * 64 + l) * 4 + v];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) sum = __fadd_rn(sum, red[w][rb][l][v]);
-    const int m = 16 * rb + 4 * (l >> 4) + v, n = t * 16 + (l & 15);
+    for (int w = 1; w < kNW; ++w) sum = __fadd_rn(sum, rf[(((w * RB + rb) * NCT + ct) * 64 + l) * 4 + v]);
+    const int m = m0 + 16 * rb + 4 * (l >> 4) + v, n = c0 + 16 * ct + (l & 15);
     if (m >= p.M || n >= p.N) return;
     float* cp = p.C + (size_t)m * p.ldc + n;
     float r = __fmul_rn(p.alpha, sum);
@@ -450,113 +333,147 @@ __global__ __launch_bounds__(64 * NW) void smallm_narrow(SmArgs p)
     *cp = r;
 }
 
-// 16 waves of at most 2 k steps (K <= 1024); 4 steps would spill registers
-// at 48 and 64 rows (a wave of a 1024-thread workgroup holds 128).
-template <int WK, int RB>
-hipError_t launch_narrow_rb(const SmArgs& a, hipStream_t st)
+template <int WK, int RB, int NCT>
+hipError_t launch_narrow_t(const SmArgs& a, int ub, hipStream_t st)
 {
-    const int tiles = (a.N + 15) / 16;
-    const dim3 grid((unsigned)(((tiles + kXcd - 1) / kXcd) * kXcd));
-    hipLaunchKernelGGL((smallm_narrow<WK, RB, 16, 2>), grid, dim3(1024), 0, st, a);
+    const int tiles = (a.N + 16 * NCT - 1) / (16 * NCT);
+    const int RBs = (a.M + 15) / 16;
+    const dim3 grid((unsigned)(((tiles + kXcd - 1) / kXcd) * kXcd), (unsigned)((RBs + RB - 1) / RB));
+    if constexpr (WK == W_I8) {
+        if (ub == 4) {
+            hipLaunchKernelGGL((smallm_narrow<WK, RB, NCT, 4>), grid, dim3(64 * kNW), 0, st, a);
+            return hipGetLastError();
+        }
+    }
+    if (ub != 16) return hipErrorNotSupported;
+    hipLaunchKernelGGL((smallm_narrow<WK, RB, NCT, 16>), grid, dim3(64 * kNW), 0, st, a);
     return hipGetLastError();
 }
 
+// (RB, NCT) in {1..4} x {1} and {1, 2} x {2} for int8 / int4; fp32 takes
+// NCT = 1 and RB <= 3 (its 64-byte rows need the registers).
 template <int WK>
-hipError_t launch_narrow(int RB, const SmArgs& a, hipStream_t st)
+hipError_t launch_narrow(int RB, int NCT, int ub, const SmArgs& a, hipStream_t st)
 {
-    switch (RB) {
-    case 1: return launch_narrow_rb<WK, 1>(a, st);
-    case 2: return launch_narrow_rb<WK, 2>(a, st);
-    case 3: return launch_narrow_rb<WK, 3>(a, st);
-    default: return launch_narrow_rb<WK, 4>(a, st);
-    }
-}
-
-template <int WK, int RB, int KS>
-hipError_t launch_ks(const SmArgs& a, hipStream_t st)
-{
-    const dim3 grid((unsigned)(((a.NT + kXcd - 1) / kXcd) * kXcd * a.S)), block(256);
-    if (a.S == 1)
-        hipLaunchKernelGGL((smallm_gemm<WK, RB, KS, 1>), grid, block, 0, st, a);
-    else if (a.S <= 8)
-        hipLaunchKernelGGL((smallm_gemm<WK, RB, KS, 8>), grid, block, 0, st, a);
-    else
-        hipLaunchKernelGGL((smallm_gemm<WK, RB, KS, 16>), grid, block, 0, st, a);
-    return hipGetLastError();
-}
-
-template <int WK, int RB>
-hipError_t launch_rb(int KS, const SmArgs& a, hipStream_t st)
-{
-    switch (KS) {
-    case 1: return launch_ks<WK, RB, 1>(a, st);
-    case 2: return launch_ks<WK, RB, 2>(a, st);
-    default: return launch_ks<WK, RB, 4>(a, st);
-    }
-}
-
-template <int WK>
-hipError_t launch_kind(int RB, int KS, const SmArgs& a, hipStream_t st)
-{
-    switch (RB) {
-    case 1: return launch_rb<WK, 1>(KS, a, st);
-    case 2: return launch_rb<WK, 2>(KS, a, st);
-    case 3: return launch_rb<WK, 3>(KS, a, st);
-    default: return launch_rb<WK, 4>(KS, a, st);
+    if constexpr (WK == W_F32) {
+        switch (RB) {
+        case 1: return launch_narrow_t<WK, 1, 1>(a, ub, st);
+        case 2: return launch_narrow_t<WK, 2, 1>(a, ub, st);
+        default: return launch_narrow_t<WK, 3, 1>(a, ub, st);
+        }
+    } else {
+        if (NCT == 2) return RB == 1 ? launch_narrow_t<WK, 1, 2>(a, ub, st) : launch_narrow_t<WK, 2, 2>(a, ub, st);
+        switch (RB) {
+        case 1: return launch_narrow_t<WK, 1, 1>(a, ub, st);
+        case 2: return launch_narrow_t<WK, 2, 1>(a, ub, st);
+        case 3: return launch_narrow_t<WK, 3, 1>(a, ub, st);
+        default: return launch_narrow_t<WK, 4, 1>(a, ub, st);
+        }
     }
 }
 
 }  // namespace
 
-// K up to 1024 takes the narrow tiles (no partials); longer K the wide ones.
-constexpr int kNarrowMaxK = 1024;
+namespace {
+
+// Bytes of one load unit for the weight rows: 16 where rows and base are
+// 16-byte aligned, else (int8 only) 4 where they are dword aligned; 0 if
+// neither.
+int narrow_unit(const GemmProblem& p)
+{
+    const size_t pitch = (size_t)p.ldb * (p.kind == W_F32 ? 4 : 1);
+    const uintptr_t pb = reinterpret_cast<uintptr_t>(p.B);
+    if (pitch % 16 == 0 && pb % 16 == 0) return 16;
+    if (p.kind == W_I8 && pitch % 4 == 0 && pb % 4 == 0) return 4;
+    return 0;
+}
+
+// Modelled cycles of the slowest CU: the workgroups (one per CU at a time)
+// run in rounds of 256 (a partial round costs 4x its fraction, at most a
+// whole one: a few extra workgroups start while the first round drains, as
+// measured); a workgroup's time is its L1 bytes at 64 B/clk plus its VALU
+// lane operations at 64 per clock (activation split ~3 per value, weight
+// conversion 1.5 (int8), 2.5 (int4), 4.5 (fp32, split too)).  It picks the
+// fastest measured tile for the encoder's M = 33 shapes and for M = 1, 16,
+// 32, 64 at K = 1024.
+double narrow_cost(const GemmProblem& p, int RB, int NCT)
+{
+    const int MB = (p.M + 15) / 16;
+    const int groups = (MB + RB - 1) / RB, tiles = (p.N + 16 * NCT - 1) / (16 * NCT);
+    const double r = (double)groups * tiles / 256.0, whole = std::floor(r);
+    const double rounds = std::max(1.0, whole + std::min(1.0, 4.0 * (r - whole)));
+    const double rw = (p.kind == W_I8 ? 16.0 : p.kind == W_I4 ? 8.0 : 64.0) * NCT;
+    const double bytes = RB * 16.0 * p.K * 4 + p.K * rw + (p.kind == W_I4 ? p.K * 4.0 : 0.0);
+    const double conv = p.kind == W_I8 ? 1.5 : p.kind == W_I4 ? 2.5 : 4.5;
+    const double valu = RB * 16.0 * p.K * (p.kind == W_I4 ? 4.0 : 3.0) + p.K * 16.0 * NCT * conv;
+    return rounds * (bytes / 64.0 + valu / 64.0);
+}
+
+}  // namespace
 
 bool smallm_supports(const GemmProblem& p)
 {
     if (p.M < 1 || p.M > kSmallMaxM || p.N < 1 || p.K < 32 || p.K % 32) return false;
-    if (p.chain_bias || (p.kind == W_F32 && p.K > kNarrowMaxK)) return false;
+    if (p.chain_bias) return false;
     if (p.alpha == 0.0f || (p.kind == W_I8 && p.scale == 0.0f)) return false;   // beta-only step
-    const uintptr_t pa = reinterpret_cast<uintptr_t>(p.A), pb = reinterpret_cast<uintptr_t>(p.B);
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(p.A);
     if (p.lda % 4 || pa % 16) return false;
-    if (p.kind == W_F32) return pb % 4 == 0;
-    if (p.kind == W_I8) return p.N % 8 == 0 && p.ldb % 8 == 0 && pb % 8 == 0;
-    return p.N % 32 == 0 && p.ldb % 4 == 0 && pb % 4 == 0 &&
-           reinterpret_cast<uintptr_t>(p.scales) % 4 == 0;
+    if (!narrow_unit(p)) return false;
+    if (p.kind == W_I4)
+        return p.N % 32 == 0 && reinterpret_cast<uintptr_t>(p.scales) % 4 == 0;
+    return true;
 }
 
-int smallm_plan(const GemmProblem& p, int* ks_out, int* s_out)
+namespace {
+thread_local int t_tile_rb = 0, t_tile_nct = 0;     // forced tile of this thread (0: none)
+
+bool tile_ok(WeightKind kind, int rb, int nct)
 {
-    const int RB = (p.M + 15) / 16, NT = (p.N + kCols - 1) / kCols;
-    // KS = 1 (one 32-deep step per wave) spreads the weight stream over the
-    // most workgroups; deeper steps cut the number of k segments (partials)
-    // for long K.  PK_GPU_SMALLM_KS overrides the choice (tuning sweeps).
-    static const int forced = [] {
-        const char* e = getenv("PK_GPU_SMALLM_KS");
-        return e ? atoi(e) : 0;
+    if (rb < 1 || rb > 4 || nct < 1 || nct > 2 || rb * nct > 4) return false;
+    return kind != W_F32 || (nct == 1 && rb <= 3);
+}
+}  // namespace
+
+bool smallm_force_tile(int rb, int nct)
+{
+    if (rb == 0 && nct == 0) { t_tile_rb = t_tile_nct = 0; return true; }
+    if (!tile_ok(W_I8, rb, nct)) return false;
+    t_tile_rb = rb;
+    t_tile_nct = nct;
+    return true;
+}
+
+void smallm_tile(const GemmProblem& p, int* rb_out, int* nct_out)
+{
+    // PK_GPU_SMALLM_TILE="RB,NCT" overrides the modelled choice (tuning sweeps)
+    static const std::pair<int, int> forced = [] {
+        const char* e = getenv("PK_GPU_SMALLM_TILE");
+        int rb = 0, nct = 0;
+        if (e && sscanf(e, "%d,%d", &rb, &nct) == 2) return std::make_pair(rb, nct);
+        return std::make_pair(0, 0);
     }();
-    int KS = forced == 1 || forced == 2 || forced == 4 ? forced : 1;
-    if (!forced)
-        while (KS < 4 && (p.K + kWaves * 32 * KS - 1) / (kWaves * 32 * KS) > 8) KS *= 2;
-    (void)RB;
-    if (ks_out) *ks_out = KS;
-    if (s_out) *s_out = (p.K + kWaves * 32 * KS - 1) / (kWaves * 32 * KS);
-    return NT;
+    const int MB = (p.M + 15) / 16;
+    int best_rb = 1, best_nct = 1;
+    double best = 1e300;
+    for (int nct = 1; nct <= (p.kind == W_F32 ? 1 : 2); ++nct)
+        for (int rb = 1; rb <= std::min(MB, nct == 2 ? 2 : p.kind == W_F32 ? 3 : 4); ++rb) {
+            const double c = narrow_cost(p, rb, nct);
+            if (c < best) { best = c; best_rb = rb; best_nct = nct; }
+        }
+    if (tile_ok(p.kind, forced.first, forced.second)) {
+        best_rb = forced.first;
+        best_nct = forced.second;
+    }
+    if (t_tile_rb) {                                 // the thread's forced tile (fp32: nct 1, rb <= 3)
+        best_rb = p.kind == W_F32 ? std::min(t_tile_rb, 3) : t_tile_rb;
+        best_nct = p.kind == W_F32 ? 1 : t_tile_nct;
+    }
+    *rb_out = best_rb;
+    *nct_out = best_nct;
 }
 
-size_t smallm_scratch_bytes(const GemmProblem& p)
+static bool smallm_args(const GemmProblem& p, SmArgs* out)
 {
-    if (p.K <= kNarrowMaxK) return 0;
-    int KS = 1, S = 1;
-    const int NT = smallm_plan(p, &KS, &S);
-    if (S == 1) return 0;
-    return (size_t)NT * S * (16 * ((p.M + 15) / 16)) * kCols * sizeof(float);
-}
-
-int smallm_counters(const GemmProblem& p) { return p.K <= kNarrowMaxK ? 0 : smallm_plan(p, nullptr, nullptr); }
-
-hipError_t launch_smallm(const GemmProblem& p, hipStream_t st, const SmallmScratch& sc)
-{
-    if (!smallm_supports(p)) return hipErrorNotSupported;
     SmArgs a = {};
     a.M = p.M; a.N = p.N; a.K = p.K;
     a.alpha = p.kind == W_I8 ? p.alpha * p.scale : p.alpha;
@@ -571,30 +488,27 @@ hipError_t launch_smallm(const GemmProblem& p, hipStream_t st, const SmallmScrat
     const size_t b_ext = ((size_t)(p.K - 1) * p.ldb + b_row) * (p.kind == W_F32 ? 4 : 1);
     const size_t s_ext = p.kind == W_I4 ? (size_t)p.K * (p.N / 32) * 4 : 0;
     const size_t lim = (size_t)1 << 31;
-    if (a_ext >= lim || b_ext >= lim || s_ext >= lim) return hipErrorNotSupported;
+    if (a_ext >= lim || b_ext >= lim || s_ext >= lim) return false;
     a.a_bytes = (uint32_t)a_ext;
     a.b_bytes = (uint32_t)b_ext;
     a.s_bytes = (uint32_t)s_ext;
-    const int RB = (p.M + 15) / 16;
-    if (p.K <= kNarrowMaxK) {
-        switch (p.kind) {
-        case W_I8: return launch_narrow<W_I8>(RB, a, st);
-        case W_I4: return launch_narrow<W_I4>(RB, a, st);
-        default:   return launch_narrow<W_F32>(RB, a, st);
-        }
+    *out = a;
+    return true;
+}
+
+hipError_t launch_smallm(const GemmProblem& p, hipStream_t st)
+{
+    if (!smallm_supports(p)) return hipErrorNotSupported;
+    SmArgs a;
+    if (!smallm_args(p, &a)) return hipErrorNotSupported;
+    int RB = 1, NCT = 1;
+    smallm_tile(p, &RB, &NCT);
+    const int ub = narrow_unit(p);
+    switch (p.kind) {
+    case W_I8: return launch_narrow<W_I8>(RB, NCT, ub, a, st);
+    case W_I4: return launch_narrow<W_I4>(RB, NCT, ub, a, st);
+    default:   return launch_narrow<W_F32>(RB, NCT, ub, a, st);
     }
-    int KS = 1, S = 1;
-    a.NT = smallm_plan(p, &KS, &S);
-    if (S > 16) return hipErrorNotSupported;        // K > 8192: the exact kernels
-    a.S = S;
-    if (S > 1) {
-        if (!sc.part || !sc.cnt || smallm_scratch_bytes(p) > sc.part_bytes || a.NT > sc.cnt_n)
-            return hipErrorNotSupported;
-        a.part = sc.part;
-        a.part_bytes = (uint32_t)smallm_scratch_bytes(p);
-        a.cnt = sc.cnt;
-    }
-    return p.kind == W_I8 ? launch_kind<W_I8>(RB, KS, a, st) : launch_kind<W_I4>(RB, KS, a, st);
 }
 
 }  // namespace pkgpu

@@ -1,5 +1,5 @@
-"""GPU: the small-M kernels (pk_smallm.hip), which int8 and int4 GEMMs with
-M <= 64 take under the default numerics (pk_gpu_set_numerics).
+"""GPU: the small-M kernels (pk_smallm.hip), which GEMMs with M <= 64 take
+under the default numerics (pk_gpu_set_numerics).
 
 The reference computes every output as one fp32 fma chain over k
 (blas.c:187-218, 759-771, 950-963); these kernels take the same products
@@ -10,9 +10,11 @@ order.  The contract is max |C - R| / max |R| <= 1e-3 against the oracle R
 hold the measured error below 1e-4, so a lost term or a wrong scale (errors
 of 1e-3 and up) fails them.  Results must be deterministic: the same call
 twice, on two streams, from several threads or replayed from a graph gives
-the same bits.  The shapes include the int8 fused QKV of a 2.56 s clip
-(M = 32 and 33, K = 1024, N = 3072, encoder.c:312) and the int4
-feed-forward pair at M = 33 (encoder.c:193-198)."""
+the same bits, and every workgroup tile (rows x columns per workgroup) meets
+the same bound.  The shapes include the int8 fused QKV of a 2.56 s clip
+(M = 32 and 33, K = 1024, N = 3072, encoder.c:312), the int4 feed-forward
+pair at M = 33 (encoder.c:193-198), ragged N, rows that are dword- but not
+16-byte aligned, and K not a multiple of the 16 waves' 32-row steps."""
 import threading
 
 import numpy as np
@@ -30,7 +32,10 @@ SHAPES = [("i8", 32, 3072, 1024), ("i8", 33, 3072, 1024), ("i8", 33, 1024, 1024)
           ("i8", 33, 1024, 4096), ("i8", 48, 3072, 1024),
           ("i4", 33, 4096, 1024), ("i4", 33, 1024, 4096), ("i4", 1, 128, 64),
           ("i4", 64, 96, 32), ("i4", 40, 160, 224), ("i4", 32, 4096, 1024),
-          ("f32", 33, 1024, 1024), ("f32", 64, 200, 96), ("f32", 7, 3072, 1024)]
+          ("f32", 33, 1024, 1024), ("f32", 64, 200, 96), ("f32", 7, 3072, 1024),
+          ("f32", 33, 1024, 4096), ("i8", 33, 1000, 1056), ("i8", 3, 3068, 4096),
+          ("i4", 33, 1024, 8192), ("i8", 64, 4104, 2080)]
+TILES = [(1, 1), (2, 1), (3, 1), (4, 1), (1, 2), (2, 2)]
 
 
 @pytest.fixture(scope="module")
@@ -101,9 +106,30 @@ def alpha_beta_epilogues(dev, kind, M, N, K):
         assert rel_err(got, want) <= MEASURED, f"epilogue {epi}"
 
 
-def test_small_m_two_streams_are_ordered(dev):
+@pytest.mark.parametrize("rb,nct", TILES)
+def test_small_m_every_tile(dev, rb, nct):
+    """Every workgroup tile the model can pick, forced on each weight format
+    (fp32 clamps to one column tile and three row blocks): M = 50 spans four
+    16-row blocks with a partial last one, N is ragged for int8 and fp32,
+    and K = 1056 gives the 16 waves 2 or 3 steps each."""
+    lib = pk.load()
+    pk.call("pk_gpu_force_small_tile", rb, nct)
+    try:
+        for kind, M, N, K in [("i8", 50, 1000, 1056), ("i4", 50, 1024, 2048), ("f32", 50, 520, 1056)]:
+            assert lib.pk_gpu_uses_small_m(M, N, K, bits_of(kind)) == 1
+            A, W, extra, _ = make(kind, M, N, K, f"smt.{kind}.{rb}.{nct}")
+            Z = np.zeros((M, N), np.float32)
+            e = rel_err(small(dev, kind, A, W, extra, Z), oracle(kind, A, W, extra, Z))
+            print(f"tile {rb}x{nct} {kind} {M}x{N}x{K}: {e:.3g}")
+            assert e <= MEASURED, (kind, e)
+    finally:
+        pk.call("pk_gpu_force_small_tile", 0, 0)
+    assert lib.pk_gpu_force_small_tile(3, 2) == -1 and lib.pk_gpu_force_small_tile(5, 1) == -1
+
+
+def test_small_m_two_streams(dev):
     """One thread, two streams, no host sync in between: the launches share
-    the thread's scratch, so the second waits for the first on the device."""
+    no state, so each result equals its single-stream one bit for bit."""
     torch = dev.torch
     lib = pk.load()
     M, N, K = 33, 3072, 1024
@@ -126,8 +152,8 @@ def test_small_m_two_streams_are_ordered(dev):
 
 
 def test_small_m_graph_replays_equal_eager(dev):
-    """Captured into a graph (the counters are reset by the kernels, nothing
-    is memset), every replay equals the eager result bit for bit."""
+    """Captured into a graph, every replay equals the eager result bit for
+    bit, with eager work between the replays."""
     torch = dev.torch
     lib = pk.load()
     shapes = [("i8", 33, 3072, 1024), ("i4", 33, 4096, 1024), ("i4", 33, 1024, 4096)]
@@ -167,8 +193,8 @@ def test_small_m_graph_replays_equal_eager(dev):
 
 def test_small_m_host_pointer_from_threads(dev):
     """The drop-in host-pointer entry at the clip's M = 33 from four threads at
-    once (each with its own stream and scratch): every result equals the
-    single-threaded one bit for bit."""
+    once (each with its own stream): every result equals the single-threaded
+    one bit for bit."""
     lib = pk.load()
     M, N, K = 33, 3072, 1024
     cases = [make("i8", M, N, K, f"smt.{t}") for t in range(4)]
@@ -207,18 +233,20 @@ def test_small_m_host_pointer_from_threads(dev):
 
 
 def test_small_m_dispatch_rules(dev):
-    """Which shapes take the small-M kernels: M <= 64 and K % 32 == 0, int8
-    (N % 8 == 0), int4, or fp32 with K <= 1024, under the default numerics
-    only."""
+    """Which shapes take the small-M kernels: M <= 64 and K % 32 == 0; int8
+    rows dword aligned, int4 N % 32 == 0, fp32 rows 16-byte aligned; under the
+    default numerics only."""
     lib = pk.load()
     assert lib.pk_gpu_get_numerics() == pk.NUMERICS_DEFAULT
     assert lib.pk_gpu_uses_small_m(33, 3072, 1024, 8) == 1
     assert lib.pk_gpu_uses_small_m(64, 4096, 1024, 4) == 1
     assert lib.pk_gpu_uses_small_m(65, 3072, 1024, 8) == 0          # M > 64: exact chains
     assert lib.pk_gpu_uses_small_m(33, 3072, 1000, 8) == 0          # K % 32 != 0
-    assert lib.pk_gpu_uses_small_m(33, 3070, 1024, 8) == 0          # int8 N % 8 != 0
-    assert lib.pk_gpu_uses_small_m(33, 1024, 1024, 32) == 1         # fp32, K <= 1024
-    assert lib.pk_gpu_uses_small_m(33, 1024, 4096, 32) == 0         # fp32, longer K
+    assert lib.pk_gpu_uses_small_m(33, 3070, 1024, 8) == 0          # int8 rows not dword aligned
+    assert lib.pk_gpu_uses_small_m(33, 3068, 1024, 8) == 1          # dword aligned: 4-byte loads
+    assert lib.pk_gpu_uses_small_m(33, 1008, 1024, 4) == 0          # int4 N % 32 != 0
+    assert lib.pk_gpu_uses_small_m(33, 1024, 4096, 32) == 1         # fp32
+    assert lib.pk_gpu_uses_small_m(33, 1022, 1024, 32) == 0         # fp32 rows not 16-byte aligned
     pk.call("pk_gpu_set_numerics", pk.NUMERICS_EXACT)
     try:
         assert lib.pk_gpu_uses_small_m(33, 3072, 1024, 8) == 0
