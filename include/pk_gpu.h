@@ -87,6 +87,24 @@ int pk_gpu_gemm_i8(int M, int N, int K, float alpha,
                    const int8_t *B, float B_scale, int ldb,
                    float beta, float *C, int ldc);
 
+/* pk_gpu_gemm_i8 for callers that cannot allocate (serving loops that must
+ * not call hipMalloc, harnesses that forbid it).  No counterpart in the
+ * reference.  Same arguments and results as pk_gpu_gemm_i8 (host pointers;
+ * a registered B is read from its resident copy), but every staged operand
+ * (A, C, and B unless registered) goes to a fixed device array of
+ * PK_GPU_NOALLOC_BYTES that each device the library runs on holds until the
+ * process ends, and the work runs on `stream` (NULL: the null stream); the
+ * call waits for it before returning.  It calls no allocating routine.
+ * Returns PK_GPU_EINVAL, touching nothing, when the staged bytes (each
+ * operand rounded up to 256) exceed PK_GPU_NOALLOC_BYTES.  All calls in a
+ * process share the array and take turns (a lock): calls from several
+ * threads are serialised, not concurrent. */
+#define PK_GPU_NOALLOC_BYTES (64u << 20)
+int pk_gpu_gemm_i8_noalloc(int M, int N, int K, float alpha,
+                           const float *A, int lda,
+                           const int8_t *B, float B_scale, int ldb,
+                           float beta, float *C, int ldc, void *stream);
+
 /* Replaces cblas_sgemm_q4b (blas.h:64-69, blas.c:950-963): packed int4
  * B [K][ldb bytes] (two's-complement nibbles, low nibble = even column,
  * extract_weights.py:589-592) with fp32 scales [K][N/32] (blas.c:794, 958).

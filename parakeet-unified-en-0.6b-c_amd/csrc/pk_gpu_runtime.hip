@@ -32,6 +32,16 @@ std::mutex g_mu;                 // guards everything below
 bool g_inited = false;
 int g_device = -1;
 
+// Staging of pk_gpu_gemm_i8_noalloc: a fixed device array that every device
+// the library runs on holds until the process ends.  Host code reaches it
+// only through its device address, looked up per device at initialisation
+// (g_noalloc_base); the array's name is a host-side stand-in.  Calls that use
+// it take g_noalloc_mu, one at a time.
+constexpr size_t kNoallocBytes = PK_GPU_NOALLOC_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoallocBytes];
+constexpr int kMaxDevices = 64;
+void* g_noalloc_base[kMaxDevices] = {};  // written at initialisation, under g_mu
+std::mutex g_noalloc_mu;
 
 // A registered weight's device copy.  Host-pointer GEMMs hold a reference
 // from the lookup until their stream has finished, so an unregister on
@@ -130,6 +140,15 @@ int init_locked(int device)
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(PK_GPU_ENODEV, "device %d is %s; this library is built for gfx950 only",
                     device, prop.gcnArchName);
+    if (device >= kMaxDevices)
+        return fail(PK_GPU_ENODEV, "device %d above the library's %d", device, kMaxDevices);
+    // the no-allocation staging array of this device, at its own address
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    void* base = nullptr;
+    e = hipGetSymbolAddress(&base, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "staging array address");
+    g_noalloc_base[device] = base;
     g_device = device;
     g_inited = true;
     return PK_GPU_OK;
@@ -320,6 +339,92 @@ int host_gemm(GemmProblem p, const float* hA, const void* hB, const float* hScal
     return PK_GPU_OK;
 }
 
+// host_gemm with every staged operand in the fixed array (no allocation):
+// A and C, and B unless its host range is registered, at 256-byte aligned
+// offsets, on the caller's stream.  Nothing in the array needs clearing:
+// each call uploads what it reads and the GEMM writes all of C.
+int noalloc_gemm(GemmProblem p, const float* hA, const void* hB, float* hC, size_t b_elem,
+                 int b_cols, hipStream_t s)
+{
+    if (p.M == 0 || p.N == 0) return PK_GPU_OK;
+    const bool mul = does_multiply(p);
+    if (!mul && p.beta == 1.0f) return PK_GPU_OK;
+    if (!hC) return fail(PK_GPU_EINVAL, "C is NULL");
+    if (mul && (!hA || !hB)) return fail(PK_GPU_EINVAL, "A or B is NULL");
+    int rc = ensure_init();
+    if (rc) return rc;
+    unsigned char* base = static_cast<unsigned char*>(g_noalloc_base[g_device]);
+    if (!base) return fail(PK_GPU_ENODEV, "no staging array on device %d", g_device);
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (cur != g_device && (e = hipSetDevice(g_device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+
+    // the plan: which operands are staged, and at which offsets
+    auto round_up = [](size_t b) { return (b + 255) & ~size_t(255); };
+    std::shared_ptr<Resident> hold[2];
+    const void* rA = nullptr;
+    const void* rB = nullptr;
+    if (mul) {
+        rA = resident(hA, ((size_t)(p.M - 1) * p.lda + p.K) * sizeof(float), &hold[0]);
+        rB = resident(hB, ((size_t)(p.K - 1) * p.ldb + b_cols) * b_elem, &hold[1]);
+    }
+    const size_t a_bytes = mul && !rA ? (size_t)p.M * p.K * sizeof(float) : 0;
+    const size_t b_bytes = mul && !rB ? (size_t)p.K * b_cols * b_elem : 0;
+    const size_t c_bytes = (size_t)p.M * p.N * sizeof(float);
+    const size_t need = round_up(a_bytes) + round_up(b_bytes) + round_up(c_bytes);
+    if (need > kNoallocBytes)
+        return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM needs %zu bytes of staging, above the fixed "
+                    "array's %zu (PK_GPU_NOALLOC_BYTES)", p.M, p.N, p.K, need, kNoallocBytes);
+    unsigned char* dA = base;
+    unsigned char* dB = dA + round_up(a_bytes);
+    float* dC = reinterpret_cast<float*>(dB + round_up(b_bytes));
+
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (mul) {
+        if (rA) {
+            p.A = static_cast<const float*>(rA);
+        } else {
+            e = hipMemcpy2DAsync(dA, (size_t)p.K * 4, hA, (size_t)p.lda * 4, (size_t)p.K * 4, p.M,
+                                 hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return hip_fail(e, "A upload");
+            p.A = reinterpret_cast<const float*>(dA);
+            p.lda = p.K;
+        }
+        if (rB) {
+            p.B = rB;
+        } else {
+            e = hipMemcpy2DAsync(dB, (size_t)b_cols * b_elem, hB, (size_t)p.ldb * b_elem,
+                                 (size_t)b_cols * b_elem, p.K, hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return hip_fail(e, "B upload");
+            p.B = dB;
+            p.ldb = b_cols;
+        }
+    }
+    if (p.beta != 0.0f) {
+        e = hipMemcpy2DAsync(dC, (size_t)p.N * 4, hC, (size_t)p.ldc * 4, (size_t)p.N * 4, p.M,
+                             hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return hip_fail(e, "C upload");
+    }
+    const int ldc_host = p.ldc;
+    p.C = dC;
+    p.ldc = p.N;
+    rc = launch(p, s, true);
+    if (rc) {
+        (void)hipStreamSynchronize(s);              // the array is free again when the lock is
+        return rc;
+    }
+    e = hipMemcpy2DAsync(hC, (size_t)ldc_host * 4, dC, (size_t)p.N * 4, (size_t)p.N * 4, p.M,
+                         hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "C download");
+    }
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "stream synchronize");
+    return PK_GPU_OK;
+}
+
 // Device-pointer calls enqueue on the caller's stream; NULL is HIP's null
 // stream, as in every HIP API.  The calling thread is bound to the device.
 hipStream_t pick_stream(void* stream, int* rc)
@@ -441,6 +546,17 @@ int pk_gpu_gemm_i8(int M, int N, int K, float alpha, const float* A, int lda,
     GemmProblem p{pkgpu::W_I8, M, N, K, alpha, beta, nullptr, lda, nullptr, ldb,
                   B_scale, nullptr, nullptr, ldc};
     return host_gemm(p, A, B, nullptr, C, 1, N);
+}
+
+int pk_gpu_gemm_i8_noalloc(int M, int N, int K, float alpha, const float* A, int lda,
+                           const int8_t* B, float B_scale, int ldb, float beta, float* C, int ldc,
+                           void* stream)
+{
+    int rc = check_gemm(M, N, K, lda, N, ldb, ldc);
+    if (rc) return rc;
+    GemmProblem p{pkgpu::W_I8, M, N, K, alpha, beta, nullptr, lda, nullptr, ldb,
+                  B_scale, nullptr, nullptr, ldc};
+    return noalloc_gemm(p, A, B, C, 1, N, static_cast<hipStream_t>(stream));
 }
 
 int pk_gpu_gemm_i4(int M, int N, int K, float alpha, const float* A, int lda,

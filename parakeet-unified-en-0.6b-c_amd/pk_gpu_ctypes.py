@@ -30,6 +30,7 @@ _PROTOS = {
     "pk_gpu_device_ptr": (_p, [_p]),
     "pk_gpu_resident_bytes": (_sz, []),
     "pk_gpu_gemm_i8": (_i, [_i, _i, _i, _f, _p, _i, _p, _f, _i, _f, _p, _i]),
+    "pk_gpu_gemm_i8_noalloc": (_i, [_i, _i, _i, _f, _p, _i, _p, _f, _i, _f, _p, _i, _p]),
     "pk_gpu_gemm_i4": (_i, [_i, _i, _i, _f, _p, _i, _p, _p, _i, _f, _p, _i]),
     "pk_gpu_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
     "pk_gpu_gemm_i8_dev": (_i, [_i, _i, _i, _f, _p, _i, _p, _f, _i, _f, _p, _i, _p]),
@@ -68,6 +69,7 @@ _PROTOS = {
 
 EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL, EPI_RESIDUAL = 0, 1, 2, 3
 NUMERICS_DEFAULT, NUMERICS_EXACT = 0, 1
+NOALLOC_BYTES = 64 << 20          # PK_GPU_NOALLOC_BYTES
 
 
 class Weight(ctypes.Structure):
