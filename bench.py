@@ -135,10 +135,12 @@ def alg_bytes(kind, m, n, k):
     return w + 4 * m * k + 4 * m * n
 
 
-def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20):
+def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False):
     """One JSON line per GEMM shape ("kind:MxNxK"): resident inputs, weights
     rotating over enough replicas to exceed the Infinity Cache, average launch
-    time from HIP events around a graph replay of `steps` launches."""
+    time from HIP events around a graph replay of `steps` launches (eager: the
+    same launches from a host loop, for profilers that trace kernels one by
+    one; its average includes the host's launch gaps)."""
     import torch
     pk = load_binding()
     pk.call("pk_gpu_init", 0)
@@ -173,22 +175,29 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20):
         for i in range(warmup):
             assert call(i) == 0, lib.pk_gpu_last_error()
         torch.cuda.synchronize(dev)
-        # The launches are captured into one HIP graph and replayed, so they run
-        # back to back: a host loop of ctypes launches cannot keep a queue of
-        # ~10 us kernels full, and per-launch events would time its gaps.
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for i in range(steps):
-                call(i)
-        graph.replay()
-        torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        graph.replay()
-        e1.record()
-        torch.cuda.synchronize(dev)
+        if eager:
+            e0.record()
+            for i in range(steps):
+                assert call(i) == 0, lib.pk_gpu_last_error()
+            e1.record()
+            torch.cuda.synchronize(dev)
+        else:
+            # The launches are captured into one HIP graph and replayed, so they run
+            # back to back: a host loop of ctypes launches cannot keep a queue of
+            # ~10 us kernels full, and per-launch events would time its gaps.
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(steps):
+                    call(i)
+            graph.replay()
+            torch.cuda.synchronize(dev)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize(dev)
+            del graph
         us = e0.elapsed_time(e1) / steps * 1e3
-        del graph
         tf = 2.0 * m * n * k / us / 1e6
         gbs = alg_bytes(kind, m, n, k) / us / 1e3
         bits = {"i4": 4, "i8": 8}.get(kind, 32)
@@ -197,7 +206,8 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20):
                           "kernel": "small-M (bf16 split, tolerance path)" if small_m else
                                     "exact chains",
                           "config": None if small_m else lib.pk_gpu_pick_config_bits(m, n, k, bits),
-                          "avg_us": round(us, 2), "tflops": round(tf, 2), "gbps": round(gbs, 1),
+                          "avg_us": round(us, 2), "timing": "eager loop" if eager else "graph replay",
+                          "tflops": round(tf, 2), "gbps": round(gbs, 1),
                           "frac_mfma_fp32": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_replicas": reps,
                           "steps": steps}), flush=True)
@@ -913,6 +923,9 @@ def main():
     ap.add_argument("--gemm", action="append", default=[], metavar="KIND:MxNxK",
                     help="instead of the encoder, time single GEMMs (kind i4, i8 or f32); "
                          "one JSON line each")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --gemm: launch from a host loop instead of a graph replay "
+                         "(for kernel tracers)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
@@ -922,7 +935,8 @@ def main():
               "multi-GPU sharding is a design note, not built)", file=sys.stderr)
         sys.exit(2)
     if args.gemm:
-        gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup)
+        gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup,
+                  eager=args.eager)
         return
     if args.ffn:
         args.steps = args.steps or 200
