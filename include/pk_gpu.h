@@ -401,6 +401,16 @@ int pk_gpu_get_numerics(void);
 /* Whether a GEMM of this shape and weight format (bits 4, 8 or 32) would take
  * the small-M kernels on this thread, given aligned operands. */
 int pk_gpu_uses_small_m(int M, int N, int K, int bits);
+/* Debug: the weights the GEMM kernels multiply, written to dout [K][N] on
+ * `stream` through the kernels' own weight loads and conversions: int8
+ * (bits 8) fl(q * scale), int4 (bits 4) fl(q * dscales[k][n/32]) with the
+ * portable nibble decode, fp32 (bits 32) the weight.  unit_path 1 converts
+ * whole units (4 int8, 8 int4 or 4 fp32 columns; N a multiple of them), the
+ * kernels' path when rows allow vector loads; 0 one element at a time.  For
+ * tests that compare the decode with memcmp.  No counterpart in the
+ * reference. */
+int pk_gpu_dequant_dev(int bits, int K, int N, const void *dB, int ldb, float scale,
+                       const float *dscales, int unit_path, float *dout, void *stream);
 /* Force the small-M tile for later calls on this thread: rb 16-row blocks
  * (1..4) and nct 16-column tiles (1..2, rb * nct <= 4; fp32 takes nct = 1,
  * rb <= 3) per workgroup; (0, 0) = the modelled choice.  A tuning and test

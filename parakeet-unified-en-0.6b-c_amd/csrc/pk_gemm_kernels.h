@@ -92,6 +92,14 @@ hipError_t launch_smallm(const GemmProblem& p, hipStream_t stream);
 // configuration) shapes the small-M kernels handle go there.
 hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, bool small = false);
 
+// The weights the chain kernels multiply (fl(q*s), or the fp32 weight) into
+// out [K][N], through the staging's own load and conversion code: whole
+// units of dequant_unit_columns(kind) columns (N a multiple of them) or one
+// element at a time.  For tests of the decode.
+int dequant_unit_columns(WeightKind kind);
+hipError_t launch_dequant(WeightKind kind, int K, int N, const void* B, int ldb, float scale,
+                          const float* scales, bool unit_path, float* out, hipStream_t stream);
+
 // Swish y = x * (1 / (1 + exp(-x))) with the reference's polynomial exp
 // (tensor_ops.c:98-120, 381-388), n elements, in place allowed.
 hipError_t launch_swish(const float* x, float* y, long long n, hipStream_t stream);

@@ -189,6 +189,64 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
     return err;
 }
 
+// The weights the chain kernels multiply, written to out [K][N] through the
+// staging's own loads and conversions (WStage): unit_path takes whole VB-column
+// units (the kernels' path when rows allow vector loads), else one element
+// at a time (the path of narrow or unaligned rows).
+template <int WK>
+__global__ __launch_bounds__(256) void dequant_matrix(KArgs p, float* out, int unit_path)
+{
+    using WS = tiles::WStage<WK>;
+    const auto rb = tiles::make_rsrc(p.B, p.b_bytes), rs = tiles::make_rsrc(p.scales, p.s_bytes);
+    const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (unit_path) {
+        const int per_row = p.N / WS::VB;
+        if (t >= (long long)p.K * per_row) return;
+        const int k = (int)(t / per_row), n = (int)(t % per_row) * WS::VB;
+        float w[WS::VB];
+        WS::dequant_unit(p, WS::load_unit(p, rb, rs, k, n), w);
+#pragma unroll
+        for (int j = 0; j < WS::VB; ++j) out[(size_t)k * p.N + n + j] = w[j];
+    } else {
+        if (t >= (long long)p.K * p.N) return;
+        const int k = (int)(t / p.N), n = (int)(t % p.N);
+        out[(size_t)k * p.N + n] = WS::dequant_elem(p, WS::load_elem(p, rb, rs, k, n), n);
+    }
+}
+
+int dequant_unit_columns(WeightKind kind)
+{
+    return kind == W_I4 ? tiles::WStage<W_I4>::VB : kind == W_I8 ? tiles::WStage<W_I8>::VB : tiles::WStage<W_F32>::VB;
+}
+
+hipError_t launch_dequant(WeightKind kind, int K, int N, const void* B, int ldb, float scale,
+                          const float* scales, bool unit_path, float* out, hipStream_t stream)
+{
+    if (K <= 0 || N <= 0) return hipSuccess;
+    if (unit_path && N % dequant_unit_columns(kind)) return hipErrorInvalidValue;
+    KArgs a = {};
+    a.N = N; a.K = K;
+    a.B = B; a.ldb = ldb;
+    a.scale = scale;
+    a.scales = scales; a.n_groups = N / 32;
+    const size_t esz = kind == W_F32 ? 4 : 1;
+    const size_t b_row = kind == W_I4 ? (size_t)N / 2 : (size_t)N;
+    const size_t b_ext = ((size_t)(K - 1) * ldb + b_row) * esz;
+    const size_t s_ext = kind == W_I4 ? (size_t)K * (N / 32) * 4 : 0;
+    if (b_ext >= ((size_t)1 << 31) || s_ext >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    a.b_bytes = (uint32_t)b_ext;
+    a.s_bytes = (uint32_t)s_ext;
+    const long long items = unit_path ? (long long)K * (N / dequant_unit_columns(kind)) : (long long)K * N;
+    const dim3 grid((unsigned)((items + 255) / 256));
+    const int up = unit_path ? 1 : 0;
+    switch (kind) {
+    case W_F32: hipLaunchKernelGGL(dequant_matrix<W_F32>, grid, dim3(256), 0, stream, a, out, up); break;
+    case W_I8:  hipLaunchKernelGGL(dequant_matrix<W_I8>, grid, dim3(256), 0, stream, a, out, up); break;
+    case W_I4:  hipLaunchKernelGGL(dequant_matrix<W_I4>, grid, dim3(256), 0, stream, a, out, up); break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_swish(const float* x, float* y, long long n, hipStream_t stream)
 {
     if (n <= 0) return hipSuccess;

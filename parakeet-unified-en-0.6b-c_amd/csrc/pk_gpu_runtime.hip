@@ -718,6 +718,33 @@ int pk_gpu_set_numerics(int mode)
 
 int pk_gpu_get_numerics(void) { return t_numerics; }
 
+int pk_gpu_dequant_dev(int bits, int K, int N, const void* dB, int ldb, float scale,
+                       const float* dscales, int unit_path, float* dout, void* stream)
+{
+    if (bits != 4 && bits != 8 && bits != 32) return fail(PK_GPU_EINVAL, "bits = %d (4, 8 or 32)", bits);
+    if (K < 0 || N < 0) return fail(PK_GPU_EINVAL, "K = %d, N = %d", K, N);
+    if (K == 0 || N == 0) return PK_GPU_OK;
+    const pkgpu::WeightKind kind = bits == 4 ? pkgpu::W_I4 : bits == 8 ? pkgpu::W_I8 : pkgpu::W_F32;
+    if (bits == 4 && N % 32) return fail(PK_GPU_EINVAL, "int4: N = %d is not a multiple of 32", N);
+    if (ldb < (bits == 4 ? N / 2 : N)) return fail(PK_GPU_EINVAL, "ldb = %d too small for N = %d", ldb, N);
+    if (unit_path && N % pkgpu::dequant_unit_columns(kind))
+        return fail(PK_GPU_EINVAL, "unit path: N = %d is not a multiple of %d", N,
+                    pkgpu::dequant_unit_columns(kind));
+    if (!dB || !dout || (bits == 4 && !dscales)) return fail(PK_GPU_EINVAL, "NULL operand");
+    // the unit path's vector loads need what the kernels require before taking it
+    const uintptr_t pb = reinterpret_cast<uintptr_t>(dB);
+    if (unit_path && (ldb % 4 || pb % (bits == 32 ? 16 : 4)))
+        return fail(PK_GPU_EINVAL, "unit path: weight rows not aligned for vector loads");
+    int rc = 0;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    const hipError_t e = pkgpu::launch_dequant(kind, K, N, dB, ldb, scale, dscales, unit_path != 0,
+                                               dout, s);
+    if (e == hipErrorInvalidValue) return fail(PK_GPU_EINVAL, "weight extent exceeds 2 GiB");
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return PK_GPU_OK;
+}
+
 int pk_gpu_force_small_tile(int rb, int nct)
 {
     if (!pkgpu::smallm_force_tile(rb, nct))

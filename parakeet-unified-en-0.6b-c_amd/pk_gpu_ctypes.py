@@ -49,6 +49,7 @@ _PROTOS = {
     "pk_gpu_get_numerics": (_i, []),
     "pk_gpu_uses_small_m": (_i, [_i, _i, _i, _i]),
     "pk_gpu_force_small_tile": (_i, [_i, _i]),
+    "pk_gpu_dequant_dev": (_i, [_i, _i, _i, _p, _i, _f, _p, _i, _p, _p]),
     "pk_gpu_layer_norm_dev": (_i, [_p, _p, _p, _p, _i, _i, _p]),
     "pk_gpu_attention_dev": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
     "pk_gpu_glu_dev": (_i, [_p, _p, _i, _i, _p]),
