@@ -280,9 +280,14 @@ int pk_gpu_encoder_create(pk_gpu_encoder **enc, const pk_gpu_block_weights *bloc
  * chunk_size <= 0: one sequence (encode_blocks, encoder.c:495-512);
  * otherwise chunks of chunk_size output frames with `overlap` frames of
  * context on each side (encode_blocks_chunked, encoder.c:514-575; the
- * reference uses PK_CHUNK_SIZE 400 and PK_CHUNK_OVERLAP 8).  Every chunk
- * (or the sequence) must be at most 512 frames.  Host pointers; returns when
- * out is written. */
+ * reference uses PK_CHUNK_SIZE 400 and PK_CHUNK_OVERLAP 8).  A chunk (or
+ * the sequence) of T' frames needs the positional table's rows centre - T' + 1
+ * .. centre + T' - 1 (T' <= 5000 for the reference's 9999-row table; longer
+ * is PK_GPU_EINVAL).  Chunks up to 512 frames keep attention scores on chip;
+ * a longer one (chunking off, as PK_CHUNK=0 runs the reference) keeps them in
+ * a workspace of H * T'^2 floats, and the first run that long recomputes every
+ * block's position projection for the longer slice.  Host pointers; returns
+ * when out is written. */
 int pk_gpu_encoder_run(pk_gpu_encoder *enc, const float *x, int T, int chunk_size,
                        int overlap, float *out);
 /* The same with device pointers, enqueued on `stream` (NULL = HIP's null

@@ -7,9 +7,11 @@
 
 namespace pkgpu {
 
-// Longest chunk the attention kernel takes: its score rows live in LDS.
-// The reference's encoder never attends over more than 500 frames unless
-// chunking is forced off (PK_CHUNK_THRESHOLD, parakeet.h; encoder.c:595-610).
+// Longest chunk whose score rows the attention kernel keeps in LDS.  The
+// reference's encoder never attends over more than 500 frames unless
+// chunking is forced off (PK_CHUNK_THRESHOLD, parakeet.h; encoder.c:595-610);
+// longer sequences keep each workgroup's score rows in a device workspace
+// (AttnArgs::scores) and run the same arithmetic.
 constexpr int kAttnMaxT = 512;
 constexpr int kAttnRows = 32;          // query rows per workgroup
 // LDS row stride of a workgroup's score rows for chunks of T rows, and the
@@ -40,7 +42,17 @@ struct AttnArgs {
     const int* chunk_rows;     // device, n entries (null: one chunk at row 0)
     const int* chunk_T;        // device, n entries, each in [1, T] (null: all T)
     int T, H;
+    // T > kAttnMaxT: attn_scores_floats(T, H, n) floats of device workspace,
+    // one slice of score rows per workgroup (unused otherwise)
+    float* scores;
 };
+// Workspace floats the attention of n chunks of up to T rows needs (0 when
+// its score rows fit in LDS).
+inline size_t attn_scores_floats(int T, int H, int n_chunks)
+{
+    if (T <= kAttnMaxT) return 0;
+    return (size_t)((T + kAttnRows - 1) / kAttnRows) * H * n_chunks * kAttnRows * attn_sld(T);
+}
 
 // Depthwise convolution over time with optional Swish (tensor_ops.c:476-548,
 // encoder.c:467-469), channel c of chunk z: x[chunk_rows[z] + t][c] for t in

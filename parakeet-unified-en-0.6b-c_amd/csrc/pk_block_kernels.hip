@@ -315,19 +315,23 @@ __device__ inline void pv_steps(std::integer_sequence<int, Ts...>, const float (
                : 0), ...);
 }
 
+// kGlobal: the block's score rows live in its own slice of p.scores (task
+// order) instead of LDS, for sequences beyond kAttnMaxT; every operation and
+// its order are the same, and __syncthreads orders the workgroup's global
+// writes as it does its LDS writes.
+template <bool kGlobal>
 __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
 {
     // Scores of the block's rows [kAttnRows][sld], then one staging tile.
     extern __shared__ float smem[];
     const int sld = attn_sld(p.T);
-    float* S = smem;
-    float* tile = smem + kAttnRows * sld;
 
     // Workgroups are dispatched to the 8 XCDs round-robin; renumber them so
     // each XCD runs a contiguous run of (row block, head, chunk) tasks, row
     // block fastest: the row blocks of one head of one chunk then share one
     // XCD's L2 for their K, P and V tiles.
     int rb, h, z;
+    float* S;
     {
         const int nrb = gridDim.x, nh = gridDim.y, total = nrb * nh * gridDim.z;
         const int lin = blockIdx.x + nrb * (blockIdx.y + nh * blockIdx.z);
@@ -337,7 +341,9 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
         rb = task % nrb;
         h = (task / nrb) % nh;
         z = task / (nrb * nh);
+        S = kGlobal ? p.scores + (size_t)task * kAttnRows * sld : smem;
     }
+    float* tile = kGlobal ? smem : smem + kAttnRows * sld;
     const int T = p.chunk_T ? p.chunk_T[z] : p.T;           // this chunk's rows
     const int r0 = rb * kAttnRows;
     if (r0 >= T) return;                                     // the whole workgroup
@@ -708,14 +714,21 @@ hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const 
 hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s)
 {
     if (a.T <= 0 || n_chunks <= 0) return hipSuccess;
-    if (a.T > kAttnMaxT) return hipErrorInvalidValue;
+    dim3 grid((a.T + kAttnRows - 1) / kAttnRows, a.H, n_chunks);
+    if (a.T > kAttnMaxT) {
+        // score rows in the caller's workspace; LDS holds the staging tile only
+        if (!a.scores) return hipErrorInvalidValue;
+        if ((size_t)grid.x * grid.y * grid.z * kAttnRows * attn_sld(a.T) >= ((size_t)1 << 40))
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(rel_pos_attention<true>, grid, dim3(256), 4u * kTileFloats, s, a);
+        return hipGetLastError();
+    }
     // LDS above the default dynamic limit is granted once per process.
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&rel_pos_attention), hipFuncAttributeMaxDynamicSharedMemorySize,
+        reinterpret_cast<const void*>(&rel_pos_attention<false>), hipFuncAttributeMaxDynamicSharedMemorySize,
         (int)attn_lds_bytes(kAttnMaxT));
     if (attr != hipSuccess) return attr;
-    dim3 grid((a.T + kAttnRows - 1) / kAttnRows, a.H, n_chunks);
-    hipLaunchKernelGGL(rel_pos_attention, grid, dim3(256), attn_lds_bytes(a.T), s, a);
+    hipLaunchKernelGGL(rel_pos_attention<false>, grid, dim3(256), attn_lds_bytes(a.T), s, a);
     return hipGetLastError();
 }
 

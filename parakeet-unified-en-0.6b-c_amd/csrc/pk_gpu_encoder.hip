@@ -68,6 +68,7 @@ struct Chunk {
 struct RowGroup {
     int r0 = 0, R = 0, Tmax = 0, tab = 0, n = 0;
     std::map<int, std::pair<int, int>> by_len;
+    size_t scores_off = 0;      // its attention's score rows (Tmax > kAttnMaxT) in e->scores
 };
 
 constexpr int kMels = 128;        // PK_N_MELS
@@ -99,11 +100,14 @@ struct pk_gpu_encoder {
     const float* pe = nullptr;          // [pe_rows][kD]
     int pe_rows = 0, pe_center = 0;
     int p_T = 0;                        // longest chunk the blocks' projections cover
+    std::vector<void*> pos_allocs;      // the blocks' projections (replaced when p_T grows)
     hipStream_t stream = nullptr;
     // workspace, grown on demand
     size_t ws_rows = 0;
     float *x = nullptr, *ln = nullptr, *h = nullptr, *att = nullptr;
     int* rows_tab = nullptr;            // device: chunk rows [rows_cap], then chunk lengths [rows_cap]
+    float* scores = nullptr;            // attention score rows of sequences beyond kAttnMaxT
+    size_t scores_n = 0;                // floats
     size_t rows_cap = 0;
     std::vector<int> tab_host;          // what rows_tab was last given (kept alive for the copy)
     size_t ws_bytes = 0;
@@ -267,21 +271,25 @@ void free_workspace(pk_gpu_encoder* e)
     for (float* p : {e->x, e->ln, e->h, e->att})
         if (p) (void)hipFree(p);
     if (e->rows_tab) (void)hipFree(e->rows_tab);
+    if (e->scores) (void)hipFree(e->scores);
     e->x = e->ln = e->h = e->att = nullptr;
     e->rows_tab = nullptr;
+    e->scores = nullptr;
+    e->scores_n = 0;
     e->tab_host.clear();
     e->ws_rows = e->rows_cap = e->ws_bytes = 0;
 }
 
 // Grows the workspace; the old one may still be read by work queued on `s`
 // (which already waits for the previous call, whatever its stream).
-int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, hipStream_t s)
+int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, size_t scores_n, hipStream_t s)
 {
-    if (rows <= e->ws_rows && n_chunks <= e->rows_cap) return PK_GPU_OK;
+    if (rows <= e->ws_rows && n_chunks <= e->rows_cap && scores_n <= e->scores_n) return PK_GPU_OK;
     hipError_t r = hipStreamSynchronize(s);
     if (r != hipSuccess) return hip_error(r, "encoder stream");
     rows = std::max(rows, e->ws_rows);
     n_chunks = std::max(n_chunks, e->rows_cap);
+    scores_n = std::max(scores_n, e->scores_n);
     free_workspace(e);
     const size_t bytes[4] = {rows * kD * 4, rows * kD * 4, rows * kFF * 4, rows * kD * 4};
     float** dst[4] = {&e->x, &e->ln, &e->h, &e->att};
@@ -295,6 +303,15 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, hipStream_t s)
     if (hipMalloc(reinterpret_cast<void**>(&e->rows_tab), 2 * n_chunks * sizeof(int)) != hipSuccess) {
         free_workspace(e);
         return error(PK_GPU_ENOMEM, "encoder chunk table failed");
+    }
+    if (scores_n) {
+        if (hipMalloc(reinterpret_cast<void**>(&e->scores), scores_n * sizeof(float)) != hipSuccess) {
+            free_workspace(e);
+            return error(PK_GPU_ENOMEM, "attention score workspace of %zu bytes failed",
+                         scores_n * sizeof(float));
+        }
+        e->ws_bytes += scores_n * sizeof(float);
+        e->scores_n = scores_n;
     }
     e->ws_rows = rows;
     e->rows_cap = n_chunks;
@@ -498,6 +515,7 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         a.chunk_rows = rows;
         a.chunk_T = lens;
         a.T = Tmax; a.H = kHeads;
+        a.scores = Tmax > pkgpu::kAttnMaxT ? e->scores + g.scores_off : nullptr;
         rc = timed(e, PK_GPU_STAGE_ATTENTION, flops, bytes, s, [&] {
             return check(pkgpu::launch_attention(a, g.n, s), "attention");
         });
@@ -581,6 +599,8 @@ std::vector<RowGroup> plan_groups(const std::vector<Chunk>& chunks, int n)
     return groups;
 }
 
+int project_positions(pk_gpu_encoder* e, int T);
+
 int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
                hipStream_t s, hipMemcpyKind in_kind, hipMemcpyKind out_kind)
 {
@@ -593,11 +613,18 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
         R += c.in_len;
         Tmax = std::max(Tmax, c.in_len);
     }
-    if (Tmax > pkgpu::kAttnMaxT)
-        return error(PK_GPU_ENOTSUP, "a sequence of %d frames exceeds the %d-frame attention limit "
-                     "(use chunks)", Tmax, pkgpu::kAttnMaxT);
-    if (Tmax > e->p_T)
-        return error(PK_GPU_EINVAL, "positional table too small for %d frames", Tmax);
+    const int pe_limit = std::min(e->pe_center + 1, e->pe_rows - e->pe_center);
+    if (Tmax > pe_limit)
+        return error(PK_GPU_EINVAL, "positional table too small for %d frames (at most %d)", Tmax,
+                     pe_limit);
+    if (Tmax > e->p_T) {
+        // longer than every earlier chunk: each block's projection over the
+        // longer slice (the graphs read the old ones)
+        wait_all(e);
+        drop_graphs(e);
+        const int rc = project_positions(e, std::min(pe_limit, (Tmax + 63) & ~63));
+        if (rc) return rc;
+    }
 
     // Row groups; each group's chunks are table entries [tab, tab + n), by
     // length, with rows relative to the group; the lengths follow at entry
@@ -621,7 +648,13 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
             g.n = (int)table.size() - g.tab;
         }
     }
-    int rc = workspace(e, (size_t)R, table.size(), s);
+    // attention score rows of groups beyond the LDS limit, one region per group
+    size_t scores_n = 0;
+    for (RowGroup& g : groups) {
+        g.scores_off = scores_n;
+        scores_n += pkgpu::attn_scores_floats(g.Tmax, kHeads, g.n);
+    }
+    int rc = workspace(e, (size_t)R, table.size(), scores_n, s);
     if (rc) return rc;
     std::vector<int> want(2 * e->rows_cap, 0);
     std::copy(table.begin(), table.end(), want.begin());
@@ -831,24 +864,41 @@ int dev_stream(void* stream, hipStream_t* s)
     return rc;
 }
 
-// Every block's linear_pos over the positional slice of the longest chunk
-// the table allows (attention's limit at most).  A chunk of T rows uses the
-// slice pe[centre - T + 1, centre + T - 1], rows p_T - T onwards of this one,
-// and each projected row depends only on its own input row, so the rows are
-// the ones the reference computes per chunk (encoder.c:319-338).
-int project_positions(pk_gpu_encoder* e)
+// Every block's linear_pos over the positional slice of chunks of up to T
+// rows.  A chunk of T' <= T rows uses the slice pe[centre - T' + 1,
+// centre + T' - 1], rows T - T' onwards of this one, and each projected row
+// depends only on its own input row, so the rows are the ones the reference
+// computes per chunk (encoder.c:319-338).  Replaces the previous projections
+// (the caller has drained every stream and dropped the graphs that read them).
+int project_positions(pk_gpu_encoder* e, int T)
 {
-    e->p_T = std::min({pkgpu::kAttnMaxT, e->pe_center + 1, e->pe_rows - e->pe_center});
-    const int L = 2 * e->p_T - 1;
-    const float* slice = e->pe + (size_t)(e->pe_center - e->p_T + 1) * kD;
+    const int L = 2 * T - 1;
+    const size_t bytes = (size_t)L * kD * 4;
+    const float* slice = e->pe + (size_t)(e->pe_center - T + 1) * kD;
+    std::vector<void*> fresh;
+    int rc = PK_GPU_OK;
     for (DevBlock& b : e->blocks) {
         void* d = nullptr;
-        int rc = dev_alloc(e, (size_t)L * kD * 4, &d);
-        if (!rc) rc = gemm(e, b.pos, slice, L, static_cast<float*>(d), nullptr, pkgpu::EPI_NONE,
-                           e->stream);
-        if (rc) return rc;
-        b.P = static_cast<const float*>(d);
+        if (hipMalloc(&d, bytes) != hipSuccess) {
+            rc = error(PK_GPU_ENOMEM, "position projections of %zu bytes failed", bytes);
+            break;
+        }
+        fresh.push_back(d);
+        rc = gemm(e, b.pos, slice, L, static_cast<float*>(d), nullptr, pkgpu::EPI_NONE, e->stream);
+        if (rc) break;
     }
+    if (!rc) rc = check(hipStreamSynchronize(e->stream), "position projections");
+    if (rc) {
+        (void)hipStreamSynchronize(e->stream);
+        for (void* d : fresh) (void)hipFree(d);
+        return rc;
+    }
+    for (void* d : e->pos_allocs) (void)hipFree(d);
+    e->weight_bytes = e->weight_bytes - e->pos_allocs.size() * (size_t)(2 * e->p_T - 1) * kD * 4 +
+                      fresh.size() * bytes;
+    e->pos_allocs.swap(fresh);
+    for (size_t i = 0; i < e->blocks.size(); ++i) e->blocks[i].P = static_cast<const float*>(e->pos_allocs[i]);
+    e->p_T = T;
     return PK_GPU_OK;
 }
 
@@ -877,7 +927,7 @@ int pk_gpu_encoder_create(pk_gpu_encoder** out, const pk_gpu_block_weights* bloc
     if (!rc) rc = upload_f(e, pe_table, (size_t)pe_rows * kD, "pe_table", &e->pe);
     e->pe_rows = pe_rows;
     e->pe_center = pe_center;
-    if (!rc) rc = project_positions(e);
+    if (!rc) rc = project_positions(e, std::min({pkgpu::kAttnMaxT, pe_center + 1, pe_rows - pe_center}));
     if (!rc) rc = check(hipStreamSynchronize(e->stream), "weight upload");
     if (rc) {
         pk_gpu_encoder_destroy(e);
@@ -950,6 +1000,7 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
     free_workspace(enc);
     free_pre(enc);
     for (void* p : enc->allocs) (void)hipFree(p);
+    for (void* p : enc->pos_allocs) (void)hipFree(p);
     for (hipEvent_t ev : enc->side_done) (void)hipEventDestroy(ev);
     if (enc->inputs_ready) (void)hipEventDestroy(enc->inputs_ready);
     if (enc->last_done) (void)hipEventDestroy(enc->last_done);

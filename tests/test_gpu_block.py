@@ -349,11 +349,14 @@ def test_encoder_group_count_is_checked(dev, enc2):
     assert lib.pk_gpu_encoder_set_groups(None, 2) == -1
 
 
-def test_encoder_rejects_oversized_sequence(dev, enc2):
-    x = np.zeros((600, 1024), np.float32)
+def test_encoder_rejects_sequence_beyond_the_table(dev, enc2):
+    """An unchunked sequence longer than the positional table covers (5000
+    frames for a 9999-row table) is refused before any work is queued;
+    test_gpu_long_sequence.py runs the lengths up to it."""
+    x = np.zeros((5001, 1024), np.float32)
     out = np.empty_like(x)
-    rc = pk.load().pk_gpu_encoder_run(enc2.h, x.ctypes.data, 600, 0, 8, out.ctypes.data)
-    assert rc == -2                               # PK_GPU_ENOTSUP: chunk it
+    rc = pk.load().pk_gpu_encoder_run(enc2.h, x.ctypes.data, 5001, 0, 8, out.ctypes.data)
+    assert rc == -1                               # PK_GPU_EINVAL
 
 
 @pytest.mark.skipif(not po.have_ref_block(), reason="reference block harness missing")
