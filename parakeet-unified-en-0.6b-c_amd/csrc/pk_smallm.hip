@@ -142,18 +142,32 @@ __device__ inline typename UnitT<U>::T load_unit(__amdgpu_buffer_rsrc_t r, uint3
     else return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 
-template <int WK, int RB, int NCT, int UB>
+// Whether a tile's k steps get load instructions of their own (SPLIT: units
+// of at most half a row, so a step's multiplies start when its own loads are
+// in) or share them (units of up to a whole row: fewer, wider loads, both
+// steps written to LDS after one wait), measured per format and width.
+constexpr bool split_steps(int WK, int NCT) { return !(NCT == 1 && WK != W_F32); }
+
+template <int WK, int RB, int NCT, int UB, bool SPLIT = split_steps(WK, NCT)>
 __global__ __launch_bounds__(64 * kNW) void smallm_narrow(SmArgs p)
 {
     typedef Narrow<WK, NCT> L;
     constexpr int RW = L::RW;
-    constexpr int U = UB < RW ? UB : RW;            // load unit bytes
+    // load unit; with SPLIT at most half a row, so units j of step st are
+    // [st * NUS, (st + 1) * NUS)
+    constexpr int UMAX = SPLIT ? RW / 2 : RW;
+    constexpr int U = UB < UMAX ? UB : UMAX;
     constexpr int UPR = RW / U;                     // units per row
     constexpr int NU = 32 * kChunk * UPR / 64;      // units per lane per chunk
+    constexpr int NUS = SPLIT ? NU / kChunk : NU;   // units written before step 0 (all without SPLIT)
     constexpr int STAGE = kNW * (L::SLAB + L::SSLAB);
     constexpr int RED = kNW * RB * NCT * 64 * 16;
-    constexpr bool kPrefetchA = RB <= 2;            // registers for two chunks of A
+    // two register sets (chunk c + 1's loads in flight while c is multiplied)
+    // where the registers allow (no spills); otherwise the next chunk's loads
+    // follow its multiplies
+    constexpr int NB = (RB * NCT <= 2 && !(WK == W_F32 && RB > 1)) ? 2 : 1;
     typedef typename UnitT<U>::T Unit;
+    static_assert(!SPLIT || (UPR % 2 == 0 && NU % kChunk == 0), "whole units per step");
     __shared__ __attribute__((aligned(16))) unsigned char smem[STAGE > RED ? STAGE : RED];
 
     // column tiles in XCD-sized runs (workgroups reach the XCDs round-robin)
@@ -174,37 +188,40 @@ __global__ __launch_bounds__(64 * kNW) void smallm_narrow(SmArgs p)
     unsigned char* slab = smem + wave * L::SLAB;
     float* sslab = reinterpret_cast<float*>(smem + kNW * L::SLAB) + wave * (32 * kChunk);
 
-    Unit wu[NU];
-    float sc = 0.0f;
-    v4u ar[kChunk][RB][2];
+    Unit wu[NB][NU];
+    float sc[NB];
+    v4u ar[NB][kChunk][RB][2];
 
-    // global loads of chunk `cs` (steps cs .. cs + kChunk - 1, clipped at s1)
-    auto issue_w = [&](int cs) {
-        const int rows = 32 * min(kChunk, s1 - cs);
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const int u = lane + 64 * j, r = u / UPR, part = u % UPR;
-            if (r < rows)
-                wu[j] = load_unit<U>(rB, (uint32_t)(32 * cs + r) * ldb_bytes + c0_bytes + (uint32_t)(part * U));
-        }
-        if constexpr (WK == W_I4) {
-            if (lane < rows)
-                sc = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    rS, (int)(((uint32_t)(32 * cs + lane) * (uint32_t)p.n_groups + grp) * 4u), 0, 0));
-        }
-    };
-    auto issue_a = [&](int cs, v4u (&dst)[kChunk][RB][2]) {
+    // every global load of chunk `cs` into register set b: step 0's first
+    auto issue = [&](int b, int cs) {
+        const int steps = min(kChunk, s1 - cs);
 #pragma unroll
         for (int st = 0; st < kChunk; ++st) {
-            if (cs + st >= s1) break;                // uniform per wave
+            if (st >= steps) break;                  // uniform per wave
+#pragma unroll
+            for (int jj = 0; jj < NUS; ++jj) {
+                if (!SPLIT && st > 0) break;
+                const int j = (SPLIT ? st * NUS : 0) + jj;
+                const int u = lane + 64 * j, r = u / UPR, part = u % UPR;
+                if (r < 32 * steps)
+                    wu[b][j] = load_unit<U>(rB, (uint32_t)(32 * cs + r) * ldb_bytes + c0_bytes + (uint32_t)(part * U));
+            }
+            if constexpr (WK == W_I4) {
+                if (st == 0 && lane < 32 * steps)
+                    sc[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        rS, (int)(((uint32_t)(32 * cs + lane) * (uint32_t)p.n_groups + grp) * 4u), 0, 0));
+            }
             const int k0 = 32 * (cs + st);
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 // row m0 + 16rb + i, k0 + 8g .. +7: rows >= M read 0 (past the extent)
                 const uint32_t off = ((uint32_t)(m0 + 16 * rb + i) * (uint32_t)p.lda + (uint32_t)(k0 + 8 * g)) * 4u;
-                dst[st][rb][0] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)off, 0, 0);
-                dst[st][rb][1] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)(off + 16), 0, 0);
+                ar[b][st][rb][0] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)off, 0, 0);
+                ar[b][st][rb][1] = __builtin_amdgcn_raw_buffer_load_b128(rA, (int)(off + 16), 0, 0);
             }
+            // keep step st's loads ahead of the next step's: the wait before a
+            // step's multiplies then leaves the later steps' loads in flight
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -214,40 +231,27 @@ __global__ __launch_bounds__(64 * kNW) void smallm_narrow(SmArgs p)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) acc[rb][ct] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    if (s0 < s1) {
-        issue_w(s0);
-        issue_a(s0, ar);
-    }
-    for (int cs = s0; cs < s1; cs += kChunk) {
-        const int rows = 32 * min(kChunk, s1 - cs);
-        // this chunk's weights into the slab (slot 32st + 4e + g for row 32st + 8g + e)
-#pragma unroll
-        for (int j = 0; j < NU; ++j) {
-            const int u = lane + 64 * j, r = u / UPR, part = u % UPR;
-            const int slot = (r & ~31) | ((r & 7) << 2) | ((r >> 3) & 3);
-            if (r < rows) *reinterpret_cast<Unit*>(slab + slot * RW + part * U) = wu[j];
-        }
+    // multiply chunk `cs` from register set b, one step at a time: each step's
+    // weights go to the slab (slot 32st + 4e + g for row 32st + 8g + e) as
+    // soon as that step's loads are in
+    auto process = [&](int b, int cs) {
+        const int steps = min(kChunk, s1 - cs);
         if constexpr (WK == W_I4) {
-            if (lane < rows) sslab[lane] = sc;
+            if (lane < 32 * steps) sslab[lane] = sc[b];
         }
-        // the wave's own LDS writes complete before its reads (LDS keeps a wave's order)
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-
-        v4u cur[kChunk][RB][2];
-        const bool more = cs + kChunk < s1;
-        if constexpr (kPrefetchA) {
-#pragma unroll
-            for (int st = 0; st < kChunk; ++st)
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb) { cur[st][rb][0] = ar[st][rb][0]; cur[st][rb][1] = ar[st][rb][1]; }
-            if (more) { issue_w(cs + kChunk); issue_a(cs + kChunk, ar); }
-        } else {
-            if (more) issue_w(cs + kChunk);
-        }
-
 #pragma unroll
         for (int st = 0; st < kChunk; ++st) {
-            if (cs + st >= s1) break;                // uniform per wave
+            if (st >= steps) break;                  // uniform per wave
+#pragma unroll
+            for (int jj = 0; jj < NUS; ++jj) {
+                if (!SPLIT && st > 0) break;
+                const int j = (SPLIT ? st * NUS : 0) + jj;
+                const int u = lane + 64 * j, r = u / UPR, part = u % UPR;
+                const int slot = (r & ~31) | ((r & 7) << 2) | ((r >> 3) & 3);
+                if (r < 32 * steps) *reinterpret_cast<Unit*>(slab + slot * RW + part * U) = wu[b][j];
+            }
+            // the wave's own LDS writes complete before its reads (LDS keeps a wave's order)
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             v8bf bhi[NCT], blo[NCT];
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) {
@@ -276,8 +280,7 @@ __global__ __launch_bounds__(64 * kNW) void smallm_narrow(SmArgs p)
             }
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
-                const v4u a0 = kPrefetchA ? cur[st][rb][0] : ar[st][rb][0];
-                const v4u a1 = kPrefetchA ? cur[st][rb][1] : ar[st][rb][1];
+                const v4u a0 = ar[b][st][rb][0], a1 = ar[b][st][rb][1];
                 float xa[8] = {__uint_as_float(a0[0]), __uint_as_float(a0[1]), __uint_as_float(a0[2]),
                                __uint_as_float(a0[3]), __uint_as_float(a1[0]), __uint_as_float(a1[1]),
                                __uint_as_float(a1[2]), __uint_as_float(a1[3])};
@@ -295,11 +298,24 @@ __global__ __launch_bounds__(64 * kNW) void smallm_narrow(SmArgs p)
                 }
             }
         }
-        if constexpr (!kPrefetchA) {
-            if (more) issue_a(cs + kChunk, ar);
-        }
         // this chunk's slab reads are done before the next chunk overwrites it
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+
+    if (s0 < s1) issue(0, s0);
+    if constexpr (NB == 2) {
+        for (int cs = s0; cs < s1; cs += 2 * kChunk) {
+            if (cs + kChunk < s1) issue(1, cs + kChunk);
+            process(0, cs);
+            if (cs + kChunk >= s1) break;
+            if (cs + 2 * kChunk < s1) issue(0, cs + 2 * kChunk);
+            process(1, cs + kChunk);
+        }
+    } else {
+        for (int cs = s0; cs < s1; cs += kChunk) {
+            process(0, cs);
+            if (cs + kChunk < s1) issue(0, cs + kChunk);
+        }
     }
 
     // fixed-order sum over the waves, one output per thread
