@@ -135,7 +135,7 @@ def alg_bytes(kind, m, n, k):
     return w + 4 * m * k + 4 * m * n
 
 
-def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False):
+def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, force_config=-1):
     """One JSON line per GEMM shape ("kind:MxNxK"): resident inputs, weights
     rotating over enough replicas to exceed the Infinity Cache, average launch
     time from HIP events around a graph replay of `steps` launches (eager: the
@@ -145,6 +145,7 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False):
     pk = load_binding()
     pk.call("pk_gpu_init", 0)
     lib = pk.load()
+    pk.call("pk_gpu_force_config", force_config)          # -1: the library's choice
     dev = torch.device("cuda:0")
     cur = lambda: torch.cuda.current_stream(dev).cuda_stream   # the capture stream inside a graph
     g = torch.Generator(device=dev)
@@ -205,7 +206,8 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False):
         print(json.dumps({"gemm": f"{kind} {m}x{n}x{k}",
                           "kernel": "small-M (bf16 split, tolerance path)" if small_m else
                                     "exact chains",
-                          "config": None if small_m else lib.pk_gpu_pick_config_bits(m, n, k, bits),
+                          "config": None if small_m else (force_config if force_config >= 0 else
+                                                           lib.pk_gpu_pick_config_bits(m, n, k, bits)),
                           "avg_us": round(us, 2), "timing": "eager loop" if eager else "graph replay",
                           "tflops": round(tf, 2), "gbps": round(gbs, 1),
                           "frac_mfma_fp32": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
@@ -923,6 +925,8 @@ def main():
     ap.add_argument("--gemm", action="append", default=[], metavar="KIND:MxNxK",
                     help="instead of the encoder, time single GEMMs (kind i4, i8 or f32); "
                          "one JSON line each")
+    ap.add_argument("--force-config", type=int, default=-1,
+                    help="with --gemm: force this tile configuration (exact chains)")
     ap.add_argument("--eager", action="store_true",
                     help="with --gemm: launch from a host loop instead of a graph replay "
                          "(for kernel tracers)")
@@ -936,7 +940,7 @@ def main():
         sys.exit(2)
     if args.gemm:
         gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup,
-                  eager=args.eager)
+                  eager=args.eager, force_config=args.force_config)
         return
     if args.ffn:
         args.steps = args.steps or 200
