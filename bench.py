@@ -658,6 +658,45 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         "work": "one mixed int4/int8 conformer block on a 416-row chunk (the resident encoder "
                 "with 1 block; its position projection is computed at creation)",
         "gpu_us": round(us3, 1), "cpu_ref_us": round(cpu3 * 1e6, 1) if cpu3 else None}
+
+    # a 2.56 s clip (33 frames) through all 24 blocks: every GEMM at M = 33,
+    # on the exact chains and on the small-M kernels (pk_gpu_encoder_set_numerics)
+    full = EncoderModel(pk)
+    x4 = enc_rng(0xFEA7, 4).standard_normal((33, D)).astype(np.float32)
+    us4 = {}
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(full.blocks, ctypes.c_void_p),
+            N_BLOCKS, full.pe.ctypes.data, PE_ROWS, PE_CENTER)
+    try:
+        dx4 = torch.from_numpy(x4).to(dev)
+        dy4 = torch.empty_like(dx4)
+        s4 = torch.cuda.current_stream(dev)
+        for mode, name in ((pk.NUMERICS_EXACT, "exact"), (pk.NUMERICS_DEFAULT, "small_m")):
+            pk.call("pk_gpu_encoder_set_numerics", enc, mode)
+            run4 = lambda: pk.check("pk_gpu_encoder_run_dev", lib.pk_gpu_encoder_run_dev(
+                enc, dx4.data_ptr(), 33, 0, ENC_OVERLAP, dy4.data_ptr(), s4.cuda_stream))
+            for _ in range(3):
+                run4()
+            torch.cuda.synchronize(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s4)
+            for _ in range(50):
+                run4()
+            e1.record(s4)
+            torch.cuda.synchronize(dev)
+            us4[name] = e0.elapsed_time(e1) / 50 * 1e3
+    finally:
+        lib.pk_gpu_encoder_destroy(enc)
+    cpu4 = None
+    if po.have_ref_block("x86"):
+        pe4 = np.ascontiguousarray(full.pe[PE_CENTER - 33 + 1:PE_CENTER + 33])
+        cpu4, _ = cpu_seconds_per_call(lambda: po.ref_blocks(full.blocks, N_BLOCKS, pe4, x4, variant="x86"),
+                                       cpu_budget_s, 200)
+    out["4_short_clip_33_frames"] = {
+        "work": "the 24-block encoder on a 2.56 s clip (33 frames, one sequence): every weight "
+                "GEMM at M = 33; position projections computed at creation",
+        "gpu_exact_us": round(us4["exact"], 1), "gpu_small_m_us": round(us4["small_m"], 1),
+        "cpu_ref_us": round(cpu4 * 1e6, 1) if cpu4 else None}
     return out
 
 

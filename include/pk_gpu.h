@@ -365,6 +365,16 @@ int pk_gpu_encoder_profile_read(pk_gpu_encoder *enc, int stage, double *ms, long
  * one after another. */
 #define PK_GPU_MAX_GROUPS 4
 int pk_gpu_encoder_set_groups(pk_gpu_encoder *enc, int n_groups);
+/* Numerics of this encoder's weight GEMMs.  PK_GPU_NUMERICS_EXACT (the
+ * default): every GEMM is the reference's fma chain, and the whole encoder
+ * is bit-identical to the reference's arithmetic.  PK_GPU_NUMERICS_DEFAULT:
+ * GEMMs with at most 64 rows (a sequence or chunk batch of at most 64 frames
+ * per row group, such as a 2.56 s clip's 33) take the small-M kernels, each
+ * within max |C - R| / max |R| <= 1e-3 of the reference GEMM (about 1e-5);
+ * longer inputs are unaffected.  Captured graphs are kept per mode.  No
+ * counterpart in the reference.  get returns the mode, -1 for NULL. */
+int pk_gpu_encoder_set_numerics(pk_gpu_encoder *enc, int mode);
+int pk_gpu_encoder_get_numerics(pk_gpu_encoder *enc);
 void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
 
 /* ---- tuning / introspection ------------------------------------------- */
@@ -397,7 +407,8 @@ int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
  *   PK_GPU_NUMERICS_EXACT  every shape bit-identical to the reference.
  * The environment variable PK_GPU_NUMERICS=exact makes EXACT every thread's
  * default.  A forced configuration (pk_gpu_force_config) implies exact
- * chains.  The device-resident encoder (pk_gpu_encoder_*) is always exact.
+ * chains.  The device-resident encoder (pk_gpu_encoder_*) has a setting of
+ * its own (pk_gpu_encoder_set_numerics), exact by default.
  * No counterpart in the reference. */
 #define PK_GPU_NUMERICS_DEFAULT 0
 #define PK_GPU_NUMERICS_EXACT   1

@@ -123,7 +123,9 @@ struct pk_gpu_encoder {
     // (T, chunk, overlap, group, forced tile config): a graph freezes the
     // tiles its GEMMs were launched with, so a pk_gpu_force_config in force
     // at capture is part of what the graph is
-    std::map<std::tuple<int, int, int, int, int>, hipGraphExec_t> graphs;
+    // and the encoder's numerics (which kernels its GEMMs take)
+    std::map<std::tuple<int, int, int, int, int, int>, hipGraphExec_t> graphs;
+    int numerics = PK_GPU_NUMERICS_EXACT;     // pk_gpu_encoder_set_numerics
     // Row groups replayed concurrently: group 0 on the caller's stream, group
     // g > 0 on side[g - 1], joined through events around the replay.
     int n_groups = 2;
@@ -319,7 +321,7 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, size_t scores_n, 
 }
 
 int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float* bias,
-                Epilogue epi, hipStream_t s)
+                Epilogue epi, hipStream_t s, bool small = false)
 {
     GemmProblem p{};
     p.kind = w.kind;
@@ -338,7 +340,7 @@ int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float
     p.ldc = w.N;
     p.bias = bias;
     p.epi = epi;
-    return pkgpu::rt::gemm(p, s);
+    return pkgpu::rt::gemm(p, s, small);
 }
 
 int check(hipError_t r, const char* what) { return r == hipSuccess ? PK_GPU_OK : hip_error(r, what); }
@@ -461,8 +463,9 @@ int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
     double bytes = weight_bytes_of(w) + 4.0 * M * w.K + 4.0 * M * w.N;
     if (bias) bytes += 4.0 * w.N;
     if (epi == pkgpu::EPI_HALF_RESIDUAL || epi == pkgpu::EPI_RESIDUAL) bytes += 4.0 * M * w.N;
+    const bool small = e->numerics == PK_GPU_NUMERICS_DEFAULT;
     return timed(e, stage_of(w), flops, bytes, s,
-                 [&] { return gemm_launch(w, A, M, C, bias, epi, s); });
+                 [&] { return gemm_launch(w, A, M, C, bias, epi, s, small); });
 }
 
 int layer_norm(pk_gpu_encoder* e, const float* x, const float* g, const float* b, float* out, int R,
@@ -692,7 +695,7 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
         // kMaxGraphs they are all dropped and recaptured on demand.
         const int forced = pkgpu::rt::forced_config();
         if (e->graphs.size() + groups.size() > kMaxGraphs &&
-            !e->graphs.count(std::make_tuple(T, chunk, ov, 0, forced))) {
+            !e->graphs.count(std::make_tuple(T, chunk, ov, 0, forced, e->numerics))) {
             if ((rc = check(hipStreamSynchronize(s), "encoder stream"))) return rc;
             for (hipStream_t st : e->side)
                 if ((rc = check(hipStreamSynchronize(st), "encoder stream"))) return rc;
@@ -700,7 +703,7 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
         }
         std::vector<hipGraphExec_t> ex(groups.size(), nullptr);
         for (size_t gi = 0; gi < groups.size(); ++gi) {
-            const auto key = std::make_tuple(T, chunk, ov, (int)gi, forced);
+            const auto key = std::make_tuple(T, chunk, ov, (int)gi, forced, e->numerics);
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 if ((rc = check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal),
@@ -1007,6 +1010,20 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
     for (hipStream_t st : enc->side) (void)hipStreamDestroy(st);
     if (enc->stream) (void)hipStreamDestroy(enc->stream);
     delete enc;
+}
+
+int pk_gpu_encoder_set_numerics(pk_gpu_encoder* enc, int mode)
+{
+    if (!enc) return error(PK_GPU_EINVAL, "encoder is NULL");
+    if (mode != PK_GPU_NUMERICS_DEFAULT && mode != PK_GPU_NUMERICS_EXACT)
+        return error(PK_GPU_EINVAL, "numerics mode %d", mode);
+    enc->numerics = mode;          // graphs are kept per mode
+    return PK_GPU_OK;
+}
+
+int pk_gpu_encoder_get_numerics(pk_gpu_encoder* enc)
+{
+    return enc ? enc->numerics : -1;
 }
 
 int pk_gpu_encoder_set_groups(pk_gpu_encoder* enc, int n_groups)

@@ -18,7 +18,7 @@ int hip_error(hipError_t e, const char* what);
 int bind(hipStream_t* thread_stream);
 // Launch one weight GEMM (launch_gemm with the thread's forced config),
 // mapping launch errors to pk_gpu_status codes.
-int gemm(const GemmProblem& p, hipStream_t s);
+int gemm(const GemmProblem& p, hipStream_t s, bool small = false);
 // The calling thread's pk_gpu_force_config index (-1: the dispatcher picks).
 int forced_config();
 

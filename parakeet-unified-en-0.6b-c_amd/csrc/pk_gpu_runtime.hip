@@ -793,7 +793,16 @@ int bind(hipStream_t* thread_stream)
     return PK_GPU_OK;
 }
 
-int gemm(const GemmProblem& p, hipStream_t s) { return launch(p, s, false); }
+int gemm(const GemmProblem& p, hipStream_t s, bool small)
+{
+    // the caller's choice of numerics; a forced tile still implies exact chains
+    const hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, small && t_force_cfg < 0);
+    if (e == hipErrorInvalidValue)
+        return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
+                    p.M, p.N, p.K);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return PK_GPU_OK;
+}
 
 int forced_config() { return t_force_cfg; }
 

@@ -61,6 +61,8 @@ _PROTOS = {
     "pk_gpu_encoder_destroy": (None, [_p]),
     "pk_gpu_encoder_profile": (_i, [_p, _i]),
     "pk_gpu_encoder_set_groups": (_i, [_p, _i]),
+    "pk_gpu_encoder_set_numerics": (_i, [_p, _i]),
+    "pk_gpu_encoder_get_numerics": (_i, [_p]),
     "pk_gpu_encoder_set_pre_encode": (_i, [_p, _p]),
     "pk_gpu_encoder_frames": (_i, [_i]),
     "pk_gpu_encoder_pre_encode_dev": (_i, [_p, _p, _i, _p, _p]),

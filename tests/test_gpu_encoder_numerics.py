@@ -1,0 +1,103 @@
+"""GPU: the resident encoder's numerics setting (pk_gpu_encoder_set_numerics).
+
+Under PK_GPU_NUMERICS_EXACT (the default) every operation is the
+reference's, and the output equals the oracle's whole encoder
+(pk_oracle_encoder.c) bit for bit.  Under PK_GPU_NUMERICS_DEFAULT the weight
+GEMMs of a row group of at most 64 rows (a 2.56 s clip's 33 frames) take the
+small-M kernels, each within 1e-3 of the reference GEMM (about 1e-5); over
+24 blocks the deviations compound, so the model here has trained-like
+attention weights (the int8 attention projections' scales x 0.05, as
+oracle/ref_encode_main.c's PK_SYNTH_ATTN_GAIN does for the end-to-end token
+checks): with the workloads' statistics a 1-ulp difference grows about
+tenfold per block (test_oracle_block.test_reference_sensitivity).  Inputs
+longer than 64 rows per group are unaffected by the setting."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import bench
+import pyoracle as po
+from pkgpu import bits_equal, describe_mismatch, gpu_available, pk
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def model():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    import torch
+    pk.call("pk_gpu_init", 0)
+    torch.cuda.set_device(0)
+    m = bench.EncoderModel(pk)
+    for b in range(bench.N_BLOCKS):
+        w = m.blocks[b]
+        for name in ("linear_qkv_w", "linear_pos_w", "linear_out_w"):
+            wt = getattr(w, name)
+            wt.scale = wt.scale * 0.05
+            setattr(w, name, wt)
+    return m
+
+
+def run(m, x, chunk, mode):
+    import torch
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(m.blocks, ctypes.c_void_p),
+            bench.N_BLOCKS, m.pe.ctypes.data, bench.PE_ROWS, bench.PE_CENTER)
+    try:
+        pk.call("pk_gpu_encoder_set_numerics", enc, mode)
+        assert pk.load().pk_gpu_encoder_get_numerics(enc) == mode
+        dev = torch.device("cuda:0")
+        dx = torch.from_numpy(x).to(dev)
+        dout = torch.full_like(dx, float("nan"))
+        outs = []
+        for _ in range(2):               # capture, then replay
+            pk.call("pk_gpu_encoder_run_dev", enc, dx.data_ptr(), x.shape[0], chunk, 8,
+                    dout.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+            torch.cuda.synchronize(dev)
+            outs.append(dout.cpu().numpy())
+        return outs
+    finally:
+        pk.load().pk_gpu_encoder_destroy(enc)
+
+
+def rel_dev(got, want):
+    return float(np.abs(got.astype(np.float64) - want).max() / np.abs(want).max())
+
+
+@pytest.mark.parametrize("T", [33, 64, 1])
+def test_short_clip_small_m_within_tolerance(model, T):
+    x = bench.enc_rng(0xFEA7, 33).standard_normal((T, bench.D)).astype(np.float32)
+    want = po.encoder(model.blocks, bench.N_BLOCKS, model.pe, bench.PE_CENTER, x, 0, 0)
+    small = run(model, x, 0, pk.NUMERICS_DEFAULT)
+    exact = run(model, x, 0, pk.NUMERICS_EXACT)
+    e = rel_dev(small[0], want)
+    print(f"T {T}: small-M max |out - oracle| / max |oracle| = {e:.3g}", flush=True)
+    assert e <= TOL, e
+    assert bits_equal(small[1], small[0]), "small-M replay differs from its capture run"
+    for got in exact:
+        assert bits_equal(got, want), describe_mismatch(got, want)
+
+
+def test_long_input_unaffected(model):
+    """200 frames unchunked (one group of 200 rows): the setting changes nothing."""
+    x = bench.enc_rng(0xFEA7, 200).standard_normal((200, bench.D)).astype(np.float32)
+    want = po.encoder(model.blocks, bench.N_BLOCKS, model.pe, bench.PE_CENTER, x, 0, 0)
+    for got in run(model, x, 0, pk.NUMERICS_DEFAULT):
+        assert bits_equal(got, want), describe_mismatch(got, want)
+
+
+def test_numerics_argument_checks(model):
+    lib = pk.load()
+    assert lib.pk_gpu_encoder_set_numerics(None, 0) == -1
+    assert lib.pk_gpu_encoder_get_numerics(None) == -1
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(model.blocks, ctypes.c_void_p),
+            1, model.pe.ctypes.data, bench.PE_ROWS, bench.PE_CENTER)
+    try:
+        assert lib.pk_gpu_encoder_get_numerics(enc) == pk.NUMERICS_EXACT
+        assert lib.pk_gpu_encoder_set_numerics(enc, 5) == -1
+    finally:
+        lib.pk_gpu_encoder_destroy(enc)
