@@ -205,6 +205,18 @@ int pk_gpu_layer_norm_dev(const float *dx, const float *dgamma, const float *dbe
 int pk_gpu_attention_dev(const float *dqkv, int ldq, const float *dP, int ldp,
                          const float *dpos_bias_u, const float *dpos_bias_v,
                          float *dout, int ldo, int T, int H, void *stream);
+/* Workspace (floats) pk_gpu_attention_ws_dev needs for T rows and H heads:
+ * 0 up to T = 512 (the score rows stay on chip), else about H * T^2. */
+size_t pk_gpu_attention_ws_floats(int T, int H);
+/* pk_gpu_attention_dev for any T (the reference attends over a whole
+ * sequence when chunking is off, encoder.c:595-610), the score rows of
+ * T > 512 in the caller's 16-byte aligned workspace dws of ws_floats >=
+ * pk_gpu_attention_ws_floats(T, H) floats (unused up to 512).  Same
+ * operations and bits as pk_gpu_attention_dev. */
+int pk_gpu_attention_ws_dev(const float *dqkv, int ldq, const float *dP, int ldp,
+                            const float *dpos_bias_u, const float *dpos_bias_v,
+                            float *dout, int ldo, int T, int H, float *dws, size_t ws_floats,
+                            void *stream);
 
 /* GLU over rows of [va | vb] (2*D wide) into rows of D (encoder.c:453-461):
  * va * (1 / (1 + exp(-vb))) with IEEE division.  exp is evaluated in double

@@ -1167,10 +1167,12 @@ int pk_gpu_layer_norm_dev(const float* dx, const float* dgamma, const float* dbe
     return check(pkgpu::launch_layer_norm(dx, D, dgamma, dbeta, dout, D, rows, D, s), "layer norm");
 }
 
-int pk_gpu_attention_dev(const float* dqkv, int ldq, const float* dP, int ldp, const float* dpu,
-                         const float* dpv, float* dout, int ldo, int T, int H, void* stream)
+namespace {
+int attention_call(const float* dqkv, int ldq, const float* dP, int ldp, const float* dpu,
+                   const float* dpv, float* dout, int ldo, int T, int H, float* dws,
+                   size_t ws_floats, void* stream)
 {
-    if (T < 1 || T > pkgpu::kAttnMaxT) return error(PK_GPU_EINVAL, "T = %d (1..%d)", T, pkgpu::kAttnMaxT);
+    if (T < 1) return error(PK_GPU_EINVAL, "T = %d", T);
     if (H < 1) return error(PK_GPU_EINVAL, "H = %d", H);
     const int D = 128 * H;
     if (ldq < 3 * D || ldp < D || ldo < D || ldq % 4 || ldp % 4)
@@ -1179,6 +1181,10 @@ int pk_gpu_attention_dev(const float* dqkv, int ldq, const float* dP, int ldp, c
     if (!dqkv || !dP || !dpu || !dpv || !dout) return error(PK_GPU_EINVAL, "NULL operand");
     if ((reinterpret_cast<uintptr_t>(dqkv) | reinterpret_cast<uintptr_t>(dP)) % 16)
         return error(PK_GPU_EINVAL, "qkv and P must be 16-byte aligned");
+    const size_t need = pkgpu::attn_scores_floats(T, H, 1);
+    if (need && (!dws || ws_floats < need || reinterpret_cast<uintptr_t>(dws) % 16))
+        return error(PK_GPU_EINVAL, "T = %d needs a 16-byte aligned workspace of %zu floats "
+                     "(pk_gpu_attention_ws_floats)", T, need);
     hipStream_t s;
     int rc = dev_stream(stream, &s);
     if (rc) return rc;
@@ -1188,7 +1194,30 @@ int pk_gpu_attention_dev(const float* dqkv, int ldq, const float* dP, int ldp, c
     a.out = dout; a.ldo = ldo;
     a.chunk_rows = nullptr;
     a.T = T; a.H = H;
+    a.scores = need ? dws : nullptr;
     return check(pkgpu::launch_attention(a, 1, s), "attention");
+}
+}  // namespace
+
+int pk_gpu_attention_dev(const float* dqkv, int ldq, const float* dP, int ldp, const float* dpu,
+                         const float* dpv, float* dout, int ldo, int T, int H, void* stream)
+{
+    if (T > pkgpu::kAttnMaxT)
+        return error(PK_GPU_EINVAL, "T = %d (1..%d; longer sequences: pk_gpu_attention_ws_dev)", T,
+                     pkgpu::kAttnMaxT);
+    return attention_call(dqkv, ldq, dP, ldp, dpu, dpv, dout, ldo, T, H, nullptr, 0, stream);
+}
+
+size_t pk_gpu_attention_ws_floats(int T, int H)
+{
+    return T < 1 || H < 1 ? 0 : pkgpu::attn_scores_floats(T, H, 1);
+}
+
+int pk_gpu_attention_ws_dev(const float* dqkv, int ldq, const float* dP, int ldp, const float* dpu,
+                            const float* dpv, float* dout, int ldo, int T, int H, float* dws,
+                            size_t ws_floats, void* stream)
+{
+    return attention_call(dqkv, ldq, dP, ldp, dpu, dpv, dout, ldo, T, H, dws, ws_floats, stream);
 }
 
 int pk_gpu_glu_dev(const float* din, float* dout, int rows, int D, void* stream)

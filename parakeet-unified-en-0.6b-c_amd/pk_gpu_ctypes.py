@@ -52,6 +52,8 @@ _PROTOS = {
     "pk_gpu_dequant_dev": (_i, [_i, _i, _i, _p, _i, _f, _p, _i, _p, _p]),
     "pk_gpu_layer_norm_dev": (_i, [_p, _p, _p, _p, _i, _i, _p]),
     "pk_gpu_attention_dev": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
+    "pk_gpu_attention_ws_floats": (ctypes.c_size_t, [_i, _i]),
+    "pk_gpu_attention_ws_dev": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p, ctypes.c_size_t, _p]),
     "pk_gpu_glu_dev": (_i, [_p, _p, _i, _i, _p]),
     "pk_gpu_depthwise_dev": (_i, [_p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p]),
     "pk_gpu_encoder_create": (_i, [_p, _p, _i, _p, _i, _i]),

@@ -94,10 +94,33 @@ def test_attention_bit_exact_to_reference(dev, T):
     assert bits_equal(got, want), describe_mismatch(got, want)
 
 
+@pytest.mark.parametrize("T", [513, 640, 1000])
+def test_attention_long_sequence_bit_exact_to_oracle(dev, T):
+    """Past 512 rows the score rows live in the caller's workspace: the same
+    bits as the oracle (T = 1000: softmax's scalar tail)."""
+    lib = pk.load()
+    qkv, P, pu, pv = attention_inputs(T)
+    D = bg.H * bg.DH
+    n = lib.pk_gpu_attention_ws_floats(T, bg.H)
+    assert n >= bg.H * T * T
+    dq, dP, du, dv = dev.put(qkv), dev.put(P), dev.put(pu), dev.put(pv)
+    dout = dev.torch.full((T, D), float("nan"), device=dev.dev)
+    ws = dev.torch.empty(n, device=dev.dev)
+    assert lib.pk_gpu_attention_ws_dev(dq.data_ptr(), 3 * D, dP.data_ptr(), D, du.data_ptr(),
+                                       dv.data_ptr(), dout.data_ptr(), D, T, bg.H, ws.data_ptr(),
+                                       n - 1, dev.stream()) == -1          # too small
+    pk.call("pk_gpu_attention_ws_dev", dq.data_ptr(), 3 * D, dP.data_ptr(), D, du.data_ptr(),
+            dv.data_ptr(), dout.data_ptr(), D, T, bg.H, ws.data_ptr(), n, dev.stream())
+    got = dout.cpu().numpy()
+    want = po.attention_core(qkv, P, pu, pv)
+    assert bits_equal(got, want), describe_mismatch(got, want)
+
+
 def test_attention_rejects_bad_sizes(dev):
     lib = pk.load()
     assert lib.pk_gpu_attention_dev(None, 3072, None, 1024, None, None, None, 1024, 513, 8, None) == -1
     assert lib.pk_gpu_attention_dev(None, 3072, None, 1024, None, None, None, 1024, 0, 8, None) == -1
+    assert lib.pk_gpu_attention_ws_floats(512, 8) == 0
 
 
 @pytest.mark.parametrize("n", [1, 416, 3312])
