@@ -189,7 +189,8 @@ int pk_gpu_swish_dev(const float *dx, float *dy, long long n, void *stream);
 
 /* LayerNorm of `rows` rows of D = 1024 floats (pk_layer_norm_rows,
  * tensor_ops.c:150-185, 187-211; d_model); dout may equal dx.  The sums are
- * the reference's; 1/sqrt(var + 1e-5) is correctly rounded. */
+ * the reference's; 1/sqrt(var + 1e-5) is correctly rounded.  x, gamma, beta
+ * and out 16-byte aligned. */
 int pk_gpu_layer_norm_dev(const float *dx, const float *dgamma, const float *dbeta,
                           float *dout, int rows, int D, void *stream);
 

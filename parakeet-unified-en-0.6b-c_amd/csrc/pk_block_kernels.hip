@@ -53,7 +53,10 @@ __device__ inline float hsum8(const float (&p)[8])
 // come in with 16-byte loads into LDS (padded rows: the strided reads of the
 // 64 lanes hit distinct banks but for 2-way overlaps), each lane keeps its
 // NPL = D/8 elements in registers for the two sequential passes (sum,
-// squared deviations), and the outputs leave through LDS as 16-byte stores.
+// squared deviations) and writes the deviations back.  The outputs
+// fl(fl(dev * inv) * gamma + beta) are independent, so they are formed per
+// 16-byte group: each lane then needs 4 of gamma's and beta's groups
+// (loaded first, with the rows) instead of 2 x NPL scattered values.
 // In place (out == x) is safe: every row is read before any is written.
 
 template <int NPL>
@@ -62,20 +65,30 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
                                                       const float* __restrict__ beta,
                                                       float* out, int ldo, int rows)
 {
-    constexpr int D = 8 * NPL, LD = D + 8, V4 = D / 4;
+    constexpr int D = 8 * NPL, LD = D + 8, V4 = D / 4, NQ = 8 * V4 / 64;
+    static_assert(V4 % 64 == 0, "each lane's 16-byte groups repeat every 64 lanes");
+    constexpr int NG = V4 / 64;                     // distinct column groups per lane
     __shared__ float buf[8 * LD];
+    __shared__ float inv_row[8];
     const int lane = threadIdx.x;
     const int row0 = blockIdx.x * 8;
     const int nr = min(8, rows - row0);
-    // all 32 loads of a lane in flight at once (rows past the end read row 0)
-    float4 in[8 * V4 / 64];
+    // all of a lane's row loads in flight at once (rows past the end read row
+    // 0), then its gamma and beta groups: columns 4 * (lane + 64 j)
+    float4 in[NQ];
 #pragma unroll
-    for (int q = 0; q < 8 * V4 / 64; ++q) {
+    for (int q = 0; q < NQ; ++q) {
         const int idx = lane + 64 * q, r = idx / V4, c4 = idx % V4;
         in[q] = *reinterpret_cast<const float4*>(x + (size_t)(r < nr ? row0 + r : row0) * ldx + 4 * c4);
     }
+    float4 g4[NG], b4[NG];
 #pragma unroll
-    for (int q = 0; q < 8 * V4 / 64; ++q) {
+    for (int j = 0; j < NG; ++j) {
+        g4[j] = *reinterpret_cast<const float4*>(gamma + 4 * (lane + 64 * j));
+        b4[j] = *reinterpret_cast<const float4*>(beta + 4 * (lane + 64 * j));
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
         const int idx = lane + 64 * q;
         *reinterpret_cast<float4*>(buf + (idx / V4) * LD + 4 * (idx % V4)) = in[q];
     }
@@ -100,15 +113,22 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
     // native, approximate square root unless OCML_BASIC_ROUNDED_OPERATIONS).
     const float inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
 #pragma unroll
-    for (int i = 0; i < NPL; ++i)
-        br[8 * i] = __fmaf_rn(__fmul_rn(v[i], inv), gamma[l + 8 * i], beta[l + 8 * i]);
+    for (int i = 0; i < NPL; ++i) br[8 * i] = v[i];      // the deviations x - mean
+    if (l == 0) inv_row[r] = inv;
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < 8 * V4 / 64; ++q) {
-        const int idx = lane + 64 * q, rr = idx / V4, c4 = idx % V4;
-        if (rr < nr)
-            *reinterpret_cast<float4*>(out + (size_t)(row0 + rr) * ldo + 4 * c4) =
-                *reinterpret_cast<const float4*>(buf + rr * LD + 4 * c4);
+    for (int q = 0; q < NQ; ++q) {
+        const int idx = lane + 64 * q, rr = idx / V4, c4 = idx % V4, j = q % NG;
+        if (rr < nr) {
+            const float4 d = *reinterpret_cast<const float4*>(buf + rr * LD + 4 * c4);
+            const float s = inv_row[rr];
+            float4 o;
+            o.x = __fmaf_rn(__fmul_rn(d.x, s), g4[j].x, b4[j].x);
+            o.y = __fmaf_rn(__fmul_rn(d.y, s), g4[j].y, b4[j].y);
+            o.z = __fmaf_rn(__fmul_rn(d.z, s), g4[j].z, b4[j].z);
+            o.w = __fmaf_rn(__fmul_rn(d.w, s), g4[j].w, b4[j].w);
+            *reinterpret_cast<float4*>(out + (size_t)(row0 + rr) * ldo + 4 * c4) = o;
+        }
     }
 }
 
@@ -706,6 +726,11 @@ hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const 
 {
     if (rows <= 0) return hipSuccess;
     if (D != 1024) return hipErrorInvalidValue;   // d_model (PK_D_MODEL)
+    // 16-byte loads and stores of x, out, gamma and beta
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+         reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 ||
+        ldx % 4 || ldo % 4)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(layer_norm_rows<128>, dim3((rows + 7) / 8), dim3(64), 0, s, x, ldx, gamma,
                        beta, out, ldo, rows);
     return hipGetLastError();

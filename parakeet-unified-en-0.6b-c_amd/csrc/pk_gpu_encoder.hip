@@ -1159,8 +1159,9 @@ int pk_gpu_layer_norm_dev(const float* dx, const float* dgamma, const float* dbe
 {
     if (rows < 0 || D != kD) return error(PK_GPU_EINVAL, "rows = %d, D = %d (D must be %d)", rows, D, kD);
     if (rows && (!dx || !dgamma || !dbeta || !dout)) return error(PK_GPU_EINVAL, "NULL operand");
-    if ((reinterpret_cast<uintptr_t>(dx) | reinterpret_cast<uintptr_t>(dout)) % 16)
-        return error(PK_GPU_EINVAL, "x and out must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(dx) | reinterpret_cast<uintptr_t>(dout) |
+         reinterpret_cast<uintptr_t>(dgamma) | reinterpret_cast<uintptr_t>(dbeta)) % 16)
+        return error(PK_GPU_EINVAL, "x, gamma, beta and out must be 16-byte aligned");
     hipStream_t s;
     int rc = dev_stream(stream, &s);
     if (rc) return rc;
