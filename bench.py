@@ -939,10 +939,11 @@ def encoder_mode(args):
         out["host_path"] = {"error": str(e)}
     out["cpu_baseline"] = None if args.no_cpu else encoder_cpu_baseline(model, x, args.cpu_seconds)
     lib.pk_gpu_encoder_destroy(enc)
-    try:
-        out["workloads"] = workload_timings(pk, lib, torch, dev, 0.0 if args.no_cpu else 1.5)
-    except Exception as e:        # reported in the line; the encoder figures stand
-        out["workloads"] = {"error": repr(e)}
+    if not args.no_workloads:
+        try:
+            out["workloads"] = workload_timings(pk, lib, torch, dev, 0.0 if args.no_cpu else 1.5)
+        except Exception as e:        # reported in the line; the encoder figures stand
+            out["workloads"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
 
 
@@ -954,6 +955,8 @@ def main():
     ap.add_argument("--replicas", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the workloads 0-4 timings (profiler runs of the encoder)")
     ap.add_argument("--ffn", action="store_true",
                     help="time the int4 feed-forward pair at M = 375 instead of the encoder")
     ap.add_argument("--copy-calibration", action="store_true",

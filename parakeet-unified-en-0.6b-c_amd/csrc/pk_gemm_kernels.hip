@@ -120,12 +120,14 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
     a.C = p.C; a.ldc = p.ldc;
     a.bias = p.bias; a.epi = p.epi;
     a.chain_bias = p.chain_bias;
-    // Long-M GEMMs (M*N >= 3M outputs) keep the larger operand's blocks within
-    // one XCD's L2 (tile_origin); measured 1-3% faster there.  For the
-    // shorter shapes that order halves the traffic but costs 1.5-3% in time
-    // (bench A/B, cold weights), so they keep the dispatch order.
+    // GEMMs of at least 1.5M outputs (the encoder's row groups of 1656 rows
+    // and up) keep the larger operand's blocks within one XCD's L2
+    // (tile_origin): 1-3% faster at 3312 rows, 0.5% faster for the encoder's
+    // two concurrent 1656-row groups (bench A/B, three runs each), with less
+    // HBM traffic.  Smaller shapes keep the dispatch order, where the order
+    // cost 1.5-3% (cold weights).
     a.tile_order = tiles::ORDER_DISPATCH;
-    if ((double)p.M * p.N >= 3.0e6) {
+    if ((double)p.M * p.N >= 1.5e6) {
         const double a_total = 4.0 * p.M * p.K;
         const double w_total = p.kind == W_F32 ? 4.0 * p.K * p.N
                              : p.kind == W_I8  ? 1.0 * p.K * p.N
