@@ -129,6 +129,31 @@ def copy_calibration():
     print(json.dumps({"copy_bytes": src.numel() * 4, "copies": 10}), flush=True)
 
 
+def device_check(torch, dev, mib=1024, reps=5):
+    """The box's own bandwidth figure beside the published 8 TB/s: a device
+    copy of `mib` MiB, timed with HIP events over `reps` copies, counts its
+    read and its write (2 x mib MiB per copy)."""
+    src = torch.ones(mib * 256 * 1024, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize(dev)
+    sec = e0.elapsed_time(e1) / 1e3 / reps
+    props = torch.cuda.get_device_properties(dev)
+    out = {"name": props.name, "gcn_arch": getattr(props, "gcnArchName", None),
+           "compute_units": props.multi_processor_count,
+           "copy_gbps": round(2.0 * src.numel() * 4 / sec / 1e9, 1),
+           "copy_frac_of_peak_hbm": round(2.0 * src.numel() * 4 / sec / 1e9 / PEAK_HBM_GBS, 4),
+           "copy": f"{mib} MiB device-to-device copy (read + write counted), {reps} copies"}
+    del src, dst
+    return out
+
+
 def alg_bytes(kind, m, n, k):
     """Algorithmic bytes of one GEMM call: weights (+ int4 scales) + A + C."""
     w = {"i4": k * n // 2 + 4 * k * (n // 32), "i8": k * n + 4, "f32": 4 * k * n}[kind]
@@ -933,6 +958,10 @@ def encoder_mode(args):
                                  "excluded: computed at creation) / ms_per_step of the timed "
                                  "replay, against the fp32 dense MFMA peak"}},
     }
+    try:
+        out["device"] = device_check(torch, dev)
+    except Exception as e:        # reported in the line; the encoder figures stand
+        out["device"] = {"error": str(e)}
     try:
         out["host_path"] = host_path_rates(pk, lib, enc, x, 5)
     except Exception as e:        # reported in the line; the device-resident figures stand
