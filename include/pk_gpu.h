@@ -370,7 +370,9 @@ int pk_gpu_encoder_profile_read(pk_gpu_encoder *enc, int stage, double *ms, long
 /* Rows of a chunked input are split into n_groups groups of whole chunks
  * (default 2, at most PK_GPU_MAX_GROUPS; never more than the chunks) that
  * run_dev replays concurrently: group 0 on the caller's stream, the others on
- * the encoder's side streams, joined before the output copies.  Every
+ * the encoder's side streams (starting once group 0 has run block 0's first
+ * feed-forward module; PK_GPU_GROUP_LAG=0..3 modules in the environment sets
+ * that lead), joined before the output copies.  Every
  * operation of a block is row-wise or per chunk, so the result does not
  * depend on the grouping.  No counterpart in the reference (which runs the
  * chunks one after another); it overlaps one group's latency-bound kernels
