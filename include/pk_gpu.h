@@ -11,11 +11,12 @@
  *    alpha == 0 (or, for int8, B_scale == 0), C += alpha * A * W, row-major,
  *    where every C[i][j] is the same sequential fused multiply-add chain over
  *    k ascending that the reference evaluates, so results are bit-identical.
- *    The one exception is the small-M path (pk_gpu_set_numerics): GEMMs
+ *    The exceptions are the tolerance paths (pk_gpu_set_numerics): GEMMs
  *    with M <= 64 stream the weights once through bf16 matrix cores and sum
  *    the same products in another order, within max |C - R| / max |R| <=
  *    1e-3 of the reference (about 1e-5 measured), unless the calling thread
- *    asks for exact numerics.
+ *    asks for exact numerics; with PK_GPU_NUMERICS_FAST longer GEMMs do the
+ *    same through the split kernels.
  *
  *  Host-pointer entry points (pk_gpu_gemm_i8, pk_gpu_gemm_i4, pk_gpu_sgemm)
  *  take host memory, exactly as the reference BLAS does.  A weight operand
@@ -386,8 +387,12 @@ int pk_gpu_encoder_set_groups(pk_gpu_encoder *enc, int n_groups);
  * GEMMs with at most 64 rows (a sequence or chunk batch of at most 64 frames
  * per row group, such as a 2.56 s clip's 33) take the small-M kernels, each
  * within max |C - R| / max |R| <= 1e-3 of the reference GEMM (about 1e-5);
- * longer inputs are unaffected.  Captured graphs are kept per mode.  No
- * counterpart in the reference.  get returns the mode, -1 for NULL. */
+ * longer inputs are unaffected.  PK_GPU_NUMERICS_FAST: every weight GEMM
+ * takes the small-M or the split kernels (see pk_gpu_set_numerics), each
+ * within the same bound; over 24 blocks the deviations compound, so the
+ * output is not bit-identical at any length.  Captured graphs are kept per
+ * mode.  No counterpart in the reference.  get returns the mode, -1 for
+ * NULL. */
 int pk_gpu_encoder_set_numerics(pk_gpu_encoder *enc, int mode);
 int pk_gpu_encoder_get_numerics(pk_gpu_encoder *enc);
 void pk_gpu_encoder_destroy(pk_gpu_encoder *enc);
@@ -420,6 +425,15 @@ int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
  *       reference R.  They use no memory beyond the operands.  Every other
  *       shape is bit-identical to the reference.
  *   PK_GPU_NUMERICS_EXACT  every shape bit-identical to the reference.
+ *   PK_GPU_NUMERICS_FAST  as DEFAULT for M <= 64; every other shape with K a
+ *       multiple of 32, N a multiple of 32, 16-byte aligned A rows and
+ *       dword-aligned weight rows (16-byte for fp32), without a chain bias,
+ *       takes the split kernels: v_mfma_f32_32x32x16_bf16 on operands split
+ *       into two bf16 halves (the int8 codes and int4 codes exactly; int4
+ *       weights dequantised exactly first), fp32 accumulators, within
+ *       max |C - R| / max |R| <= 1e-3 of the reference (about 1e-5),
+ *       deterministic, no memory beyond the operands.  Shapes outside those
+ *       rules stay bit-identical.
  * The environment variable PK_GPU_NUMERICS=exact makes EXACT every thread's
  * default.  A forced configuration (pk_gpu_force_config) implies exact
  * chains.  The device-resident encoder (pk_gpu_encoder_*) has a setting of
@@ -427,11 +441,15 @@ int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
  * No counterpart in the reference. */
 #define PK_GPU_NUMERICS_DEFAULT 0
 #define PK_GPU_NUMERICS_EXACT   1
+#define PK_GPU_NUMERICS_FAST    2
 int pk_gpu_set_numerics(int mode);
 int pk_gpu_get_numerics(void);
 /* Whether a GEMM of this shape and weight format (bits 4, 8 or 32) would take
  * the small-M kernels on this thread, given aligned operands. */
 int pk_gpu_uses_small_m(int M, int N, int K, int bits);
+/* Whether such a GEMM would take the split kernels on this thread
+ * (PK_GPU_NUMERICS_FAST and a shape the small-M kernels do not take). */
+int pk_gpu_uses_split(int M, int N, int K, int bits);
 /* Debug: the weights the GEMM kernels multiply, written to dout [K][N] on
  * `stream` through the kernels' own weight loads and conversions: int8
  * (bits 8) fl(q * scale), int4 (bits 4) fl(q * dscales[k][n/32]) with the

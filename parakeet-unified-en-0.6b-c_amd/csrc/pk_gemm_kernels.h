@@ -86,11 +86,24 @@ bool smallm_force_tile(int rb, int nct);
 // caller then takes the exact kernels).
 hipError_t launch_smallm(const GemmProblem& p, hipStream_t stream);
 
+// Whether a shape and its operands suit the split kernels (pk_split.hip):
+// any M, K % 32 == 0, N % 32 == 0, 16-byte aligned A rows, dword-aligned
+// weight rows (16-byte for fp32), no chain_bias.
+bool split_supports(const GemmProblem& p);
+// Launch on `stream`; hipErrorNotSupported if the shape is not handled.
+hipError_t launch_split(const GemmProblem& p, hipStream_t stream);
+
+// Which shapes may leave the exact chains for a kernel within the 1e-3
+// contract: none; those the small-M kernels take (M <= 64); or those and
+// every other shape the split kernels take.
+enum Tolerance { TOL_NONE = 0, TOL_SMALL_M = 1, TOL_ALL = 2 };
+
 // Launch the whole GEMM (beta pre-pass semantics, early exits, int8 edge
 // columns) on `stream`.  Returns hipSuccess or the launch error.
-// cfg_index < 0 selects choose_config_index().  With `small` (and no forced
-// configuration) shapes the small-M kernels handle go there.
-hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, bool small = false);
+// cfg_index < 0 selects choose_config_index(); a forced configuration
+// (cfg_index >= 0) always runs the exact chains.
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index,
+                       Tolerance tol = TOL_NONE);
 
 // The weights the chain kernels multiply (fl(q*s), or the fp32 weight) into
 // out [K][N], through the staging's own load and conversion code: whole

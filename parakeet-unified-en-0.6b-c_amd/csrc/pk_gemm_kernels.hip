@@ -101,7 +101,7 @@ static int choose_index(int M, int N, int K, WeightKind kind = W_I8)
 
 int choose_config_index(int M, int N, int K, WeightKind kind) { return choose_index(M, N, K, kind); }
 
-hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, bool small)
+hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, Tolerance tol)
 {
     if (p.M <= 0 || p.N <= 0) return hipSuccess;
     if ((p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL) && p.beta != 0.0f)
@@ -144,9 +144,15 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
         return hipGetLastError();
     }
 
-    if (small && cfg_index < 0 && smallm_supports(p)) {
-        const hipError_t e = launch_smallm(p, stream);
-        if (e != hipErrorNotSupported) return e;
+    if (tol != TOL_NONE && cfg_index < 0) {
+        if (smallm_supports(p)) {
+            const hipError_t e = launch_smallm(p, stream);
+            if (e != hipErrorNotSupported) return e;
+        }
+        if (tol == TOL_ALL && split_supports(p)) {
+            const hipError_t e = launch_split(p, stream);
+            if (e != hipErrorNotSupported) return e;
+        }
     }
 
     // Exact extents of what the call may read; the kernels address operands

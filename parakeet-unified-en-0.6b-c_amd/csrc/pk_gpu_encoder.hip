@@ -322,7 +322,7 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, size_t scores_n, 
 }
 
 int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float* bias,
-                Epilogue epi, hipStream_t s, bool small = false)
+                Epilogue epi, hipStream_t s, pkgpu::Tolerance tol = pkgpu::TOL_NONE)
 {
     GemmProblem p{};
     p.kind = w.kind;
@@ -341,7 +341,7 @@ int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float
     p.ldc = w.N;
     p.bias = bias;
     p.epi = epi;
-    return pkgpu::rt::gemm(p, s, small);
+    return pkgpu::rt::gemm(p, s, tol);
 }
 
 int check(hipError_t r, const char* what) { return r == hipSuccess ? PK_GPU_OK : hip_error(r, what); }
@@ -464,9 +464,9 @@ int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
     double bytes = weight_bytes_of(w) + 4.0 * M * w.K + 4.0 * M * w.N;
     if (bias) bytes += 4.0 * w.N;
     if (epi == pkgpu::EPI_HALF_RESIDUAL || epi == pkgpu::EPI_RESIDUAL) bytes += 4.0 * M * w.N;
-    const bool small = e->numerics == PK_GPU_NUMERICS_DEFAULT;
+    const pkgpu::Tolerance tol = pkgpu::rt::tolerance_of(e->numerics);
     return timed(e, stage_of(w), flops, bytes, s,
-                 [&] { return gemm_launch(w, A, M, C, bias, epi, s, small); });
+                 [&] { return gemm_launch(w, A, M, C, bias, epi, s, tol); });
 }
 
 int layer_norm(pk_gpu_encoder* e, const float* x, const float* g, const float* b, float* out, int R,
@@ -1066,7 +1066,8 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
 int pk_gpu_encoder_set_numerics(pk_gpu_encoder* enc, int mode)
 {
     if (!enc) return error(PK_GPU_EINVAL, "encoder is NULL");
-    if (mode != PK_GPU_NUMERICS_DEFAULT && mode != PK_GPU_NUMERICS_EXACT)
+    if (mode != PK_GPU_NUMERICS_DEFAULT && mode != PK_GPU_NUMERICS_EXACT &&
+        mode != PK_GPU_NUMERICS_FAST)
         return error(PK_GPU_EINVAL, "numerics mode %d", mode);
     enc->numerics = mode;          // graphs are kept per mode
     return PK_GPU_OK;

@@ -264,12 +264,13 @@ bool does_multiply(const GemmProblem& p)
            !(p.kind == pkgpu::W_I8 && p.scale == 0.0f);
 }
 
-// small_ok: the call may take the small-M kernels (the public GEMM entry
-// points, unless this thread asked for exact numerics or forced a tile).
-int launch(const GemmProblem& p, hipStream_t s, bool small_ok)
+// tol_ok: the call may leave the exact chains as this thread's numerics
+// allow (the public GEMM entry points, unless a tile is forced).
+int launch(const GemmProblem& p, hipStream_t s, bool tol_ok)
 {
-    const bool small = small_ok && t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0;
-    const hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, small);
+    const pkgpu::Tolerance tol =
+        tol_ok && t_force_cfg < 0 ? pkgpu::rt::tolerance_of(t_numerics) : pkgpu::TOL_NONE;
+    const hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, tol);
     if (e == hipErrorInvalidValue)
         return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
                     p.M, p.N, p.K);
@@ -710,7 +711,8 @@ int pk_gpu_force_config(int index)
 
 int pk_gpu_set_numerics(int mode)
 {
-    if (mode != PK_GPU_NUMERICS_DEFAULT && mode != PK_GPU_NUMERICS_EXACT)
+    if (mode != PK_GPU_NUMERICS_DEFAULT && mode != PK_GPU_NUMERICS_EXACT &&
+        mode != PK_GPU_NUMERICS_FAST)
         return fail(PK_GPU_EINVAL, "numerics mode %d is not one of PK_GPU_NUMERICS_*", mode);
     t_numerics = mode;
     return PK_GPU_OK;
@@ -762,7 +764,21 @@ int pk_gpu_uses_small_m(int M, int N, int K, int bits)
     p.B = reinterpret_cast<const void*>(uintptr_t(256));
     p.scales = reinterpret_cast<const float*>(uintptr_t(256));
     p.lda = K; p.ldb = bits == 4 ? N / 2 : N; p.ldc = N;
-    return t_numerics == PK_GPU_NUMERICS_DEFAULT && t_force_cfg < 0 && pkgpu::smallm_supports(p);
+    return t_numerics != PK_GPU_NUMERICS_EXACT && t_force_cfg < 0 && pkgpu::smallm_supports(p);
+}
+
+int pk_gpu_uses_split(int M, int N, int K, int bits)
+{
+    GemmProblem p{};
+    p.kind = bits == 4 ? pkgpu::W_I4 : bits == 8 ? pkgpu::W_I8 : pkgpu::W_F32;
+    p.M = M; p.N = N; p.K = K;
+    p.alpha = 1.0f; p.scale = 1.0f;
+    p.A = reinterpret_cast<const float*>(uintptr_t(256));
+    p.B = reinterpret_cast<const void*>(uintptr_t(256));
+    p.scales = reinterpret_cast<const float*>(uintptr_t(256));
+    p.lda = K; p.ldb = bits == 4 ? N / 2 : N; p.ldc = N;
+    return t_numerics == PK_GPU_NUMERICS_FAST && t_force_cfg < 0 && !pkgpu::smallm_supports(p) &&
+           pkgpu::split_supports(p);
 }
 
 }  // extern "C"
@@ -793,10 +809,17 @@ int bind(hipStream_t* thread_stream)
     return PK_GPU_OK;
 }
 
-int gemm(const GemmProblem& p, hipStream_t s, bool small)
+Tolerance tolerance_of(int numerics)
+{
+    return numerics == PK_GPU_NUMERICS_DEFAULT ? TOL_SMALL_M
+         : numerics == PK_GPU_NUMERICS_FAST    ? TOL_ALL
+                                               : TOL_NONE;
+}
+
+int gemm(const GemmProblem& p, hipStream_t s, Tolerance tol)
 {
     // the caller's choice of numerics; a forced tile still implies exact chains
-    const hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, small && t_force_cfg < 0);
+    const hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, t_force_cfg < 0 ? tol : TOL_NONE);
     if (e == hipErrorInvalidValue)
         return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
                     p.M, p.N, p.K);

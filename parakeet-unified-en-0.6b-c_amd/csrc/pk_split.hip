@@ -1,0 +1,489 @@
+// pk_split.hip - weight GEMMs of any M on bf16 matrix cores with split
+// operands: the fast numerics mode (PK_GPU_NUMERICS_FAST).
+//
+// The exact kernels (pk_gemm_tiles.h) reproduce the reference's sequential
+// fma chain over k for every output (blas.c:198-208), which holds them to
+// the fp32 MFMA instructions (157.3 TFLOP/s dense).  Within the GEMM
+// contract max |C - R| / max |R| <= 1e-3 the same products can go through
+// v_mfma_f32_32x32x16_bf16 instead (2.5 PFLOP/s dense), with every fp32
+// operand x split as x = hi + lo + r, hi = bf16(x), lo = bf16(x - hi), both
+// to nearest: x - hi is exact in fp32, |r| <= 2^-16 |x|, and bf16 keeps
+// fp32's exponent range, so nothing is prescaled.  The accumulators are fp32.
+//   int8: the codes q are exact in bf16 and the scale is per tensor:
+//         C = alpha*s * (A_hi Q + A_lo Q)                    (2 MFMAs)
+//   int4: each weight is first dequantised exactly as the reference's pack
+//         step does, w = fl(q * s[k][n/32]) (blas.c:794, 834-840), then split:
+//         C = alpha * (A_hi W_hi + A_lo W_hi + A_hi W_lo)    (3 MFMAs)
+//   fp32: the weight split the same way                      (3 MFMAs)
+// The dropped A_lo W_lo term and the operands' residues r are below 2^-16 of
+// each product; the measured error is about 1e-5.
+//
+// Tiles.  A workgroup of WM x WN waves computes a (64 WM) x (64 WN) tile of
+// C, each wave 64 x 64 as 2 x 2 MFMA blocks of 32 x 32, over the whole of K
+// in 32-deep chunks.  Per chunk, every thread loads its share of the A rows
+// (16-byte loads) and of the weight rows (4 or 16 bytes per unit and two
+// consecutive k rows per unit), splits them, and writes them to LDS as
+// planes [row or column][k] of bf16 with a padded stride of 40, so the
+// MFMA operands (8 consecutive k of one row or column per lane) are single
+// 16-byte LDS reads.  Two LDS buffers: the next chunk's global loads are in
+// flight while the current chunk multiplies, and are split into the other
+// buffer after it.  Every workgroup sums its own tile over all of K in a
+// fixed order, so results are deterministic.
+#include "pk_gemm_kernels.h"
+#include "pk_device_math.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace pkgpu {
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kXcd = 8;
+constexpr int KT = 32;            // k per chunk
+constexpr int RS = KT + 8;        // LDS row stride of a plane, in bf16 (80 bytes)
+
+struct SpArgs {
+    int M, N, K;
+    float alpha;                  // int8: alpha * scale
+    float beta;
+    const float* A; int lda;
+    const void* B; int ldb;       // row pitch in elements (int4: bytes)
+    const float* scales; int n_groups;
+    float* C; int ldc;
+    const float* bias; int epi;
+    uint32_t a_bytes, b_bytes, s_bytes;   // buffer extents (reads past them return 0)
+    int tiles_n, tiles;           // column tiles, all tiles
+};
+
+__device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+__device__ inline v2bf to_bf2(float a, float b) { return __builtin_convertvector((v2f){a, b}, v2bf); }
+
+__device__ inline float bf_to_f(__bf16 h)
+{
+    return __uint_as_float((uint32_t)__builtin_bit_cast(unsigned short, h) << 16);
+}
+
+__device__ inline uint32_t bits2(v2bf v) { return __builtin_bit_cast(uint32_t, v); }
+
+// (x0, x1) -> hi = bf16 pair, lo = bf16 pair of the residues
+__device__ inline void split2(float x0, float x1, uint32_t& hi, uint32_t& lo)
+{
+    const v2bf h = to_bf2(x0, x1);
+    hi = bits2(h);
+    lo = bits2(to_bf2(__fsub_rn(x0, bf_to_f(h[0])), __fsub_rn(x1, bf_to_f(h[1]))));
+}
+
+// Signed nibble j (0: low, 1: high) of byte b.
+__device__ inline int q_i4(uint32_t w, int j)
+{
+    return (int)(w << (28 - 4 * j)) >> 28;
+}
+
+template <int WK> struct WUnit;
+template <> struct WUnit<W_I8> { uint32_t q[2]; };
+template <> struct WUnit<W_I4> { uint32_t q[2]; float s[2]; };
+template <> struct WUnit<W_F32> { v4u w[2]; };
+
+// Staging and multiplying one chunk of a BM x BN tile by NT threads.
+// A chunk's LDS planes: A_hi, A_lo [BM][RS], then W_hi (and W_lo) [BN][RS].
+template <int WK, int BM, int BN, int NT>
+struct Pipe {
+    static constexpr int NBP = WK == W_I8 ? 1 : 2;             // weight planes
+    static constexpr int A_PLANE = BM * RS, B_PLANE = BN * RS;   // bf16 elements
+    static constexpr int BUF = 2 * A_PLANE + NBP * B_PLANE;      // one chunk
+    // A: BM rows x 8 float4 per chunk
+    static constexpr int A_ITEMS = BM * (KT / 4) / NT;
+    // weight units of two consecutive k rows: 4 columns (int8, fp32) or 8 (int4)
+    static constexpr int UC = WK == W_I4 ? 8 : 4;
+    static constexpr int B_ITEMS = (KT / 2) * (BN / UC) / NT;
+    static_assert(A_ITEMS * NT == BM * (KT / 4) && B_ITEMS * NT == (KT / 2) * (BN / UC), "even split");
+
+    struct Raw {
+        v4u a[A_ITEMS];
+        WUnit<WK> w[B_ITEMS];
+    };
+
+    // the global loads of the chunk at k0 (rows past M, columns past the
+    // operands' extents read 0; columns past N only feed unstored outputs)
+    __device__ static void load(Raw& r, const SpArgs& p, __amdgpu_buffer_rsrc_t rA,
+                                __amdgpu_buffer_rsrc_t rB, __amdgpu_buffer_rsrc_t rS, int tid,
+                                int m0, int n0, int k0)
+    {
+#pragma unroll
+        for (int i = 0; i < A_ITEMS; ++i) {
+            const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
+            r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                rA, (int)(((uint32_t)(m0 + row) * (uint32_t)p.lda + (uint32_t)(k0 + 4 * kq)) * 4u), 0, 0);
+        }
+        // k pairs fastest across lanes: 16 lanes write 16 consecutive LDS words
+#pragma unroll
+        for (int i = 0; i < B_ITEMS; ++i) {
+            const int idx = tid + NT * i, kp = idx % (KT / 2), cu = idx / (KT / 2);
+            const int n = n0 + UC * cu;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t k = (uint32_t)(k0 + 2 * kp + h);
+                if constexpr (WK == W_I8) {
+                    r.w[i].q[h] = __builtin_amdgcn_raw_buffer_load_b32(rB, (int)(k * (uint32_t)p.ldb + n), 0, 0);
+                } else if constexpr (WK == W_I4) {
+                    r.w[i].q[h] = __builtin_amdgcn_raw_buffer_load_b32(rB, (int)(k * (uint32_t)p.ldb + (n >> 1)), 0, 0);
+                    r.w[i].s[h] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        rS, (int)((k * (uint32_t)p.n_groups + (uint32_t)(n >> 5)) * 4u), 0, 0));
+                } else {
+                    r.w[i].w[h] = __builtin_amdgcn_raw_buffer_load_b128(rB, (int)((k * (uint32_t)p.ldb + n) * 4u), 0, 0);
+                }
+            }
+        }
+    }
+
+    // split a loaded chunk into the planes at `base`
+    __device__ static void store(const Raw& r, __bf16* base, int tid)
+    {
+        __bf16* ah = base;
+        __bf16* al = ah + A_PLANE;
+        __bf16* bh = al + A_PLANE;
+        __bf16* bl = bh + B_PLANE;                   // int4, fp32 only
+#pragma unroll
+        for (int i = 0; i < A_ITEMS; ++i) {
+            const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
+            uint32_t h0, l0, h1, l1;
+            split2(__uint_as_float(r.a[i][0]), __uint_as_float(r.a[i][1]), h0, l0);
+            split2(__uint_as_float(r.a[i][2]), __uint_as_float(r.a[i][3]), h1, l1);
+            *reinterpret_cast<v2u*>(ah + row * RS + 4 * kq) = v2u{h0, h1};
+            *reinterpret_cast<v2u*>(al + row * RS + 4 * kq) = v2u{l0, l1};
+        }
+#pragma unroll
+        for (int i = 0; i < B_ITEMS; ++i) {
+            const int idx = tid + NT * i, kp = idx % (KT / 2), cu = idx / (KT / 2);
+#pragma unroll
+            for (int c = 0; c < UC; ++c) {
+                const int off = (UC * cu + c) * RS + 2 * kp;      // column-major plane
+                if constexpr (WK == W_I8) {
+                    const float q0 = (float)(int)(int8_t)(r.w[i].q[0] >> (8 * c));
+                    const float q1 = (float)(int)(int8_t)(r.w[i].q[1] >> (8 * c));
+                    *reinterpret_cast<uint32_t*>(bh + off) = bits2(to_bf2(q0, q1));   // exact
+                } else {
+                    float w0, w1;
+                    if constexpr (WK == W_I4) {
+                        // blas.c:834-840: fl((float)q * s), byte j = columns 2j (low), 2j+1
+                        w0 = __fmul_rn((float)q_i4(r.w[i].q[0] >> (8 * (c >> 1)), c & 1), r.w[i].s[0]);
+                        w1 = __fmul_rn((float)q_i4(r.w[i].q[1] >> (8 * (c >> 1)), c & 1), r.w[i].s[1]);
+                    } else {
+                        w0 = __uint_as_float(r.w[i].w[0][c]);
+                        w1 = __uint_as_float(r.w[i].w[1][c]);
+                    }
+                    uint32_t hi, lo;
+                    split2(w0, w1, hi, lo);
+                    *reinterpret_cast<uint32_t*>(bh + off) = hi;
+                    *reinterpret_cast<uint32_t*>(bl + off) = lo;
+                }
+            }
+        }
+    }
+
+    // One wave's 64 x 64 block at rows [r0, r0 + 64), columns [c0, c0 + 64)
+    // of the tile, as 2 x 2 MFMA blocks: lane (l & 31) is a row of A and a
+    // column of W, k = 8 (l >> 5) .. +7 of each 16-deep step.
+    __device__ static void multiply(const __bf16* base, v16f (&acc)[2][2], int lane, int r0, int c0)
+    {
+        const __bf16* ah = base;
+        const __bf16* al = ah + A_PLANE;
+        const __bf16* bh = al + A_PLANE;
+        const __bf16* bl = bh + B_PLANE;
+        const int r_lane = lane & 31, k_lane = 8 * (lane >> 5);
+#pragma unroll
+        for (int ks = 0; ks < KT / 16; ++ks) {
+            v8bf a_hi[2], a_lo[2], b_hi[2], b_lo[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int o = (r0 + 32 * r + r_lane) * RS + 16 * ks + k_lane;
+                a_hi[r] = *reinterpret_cast<const v8bf*>(ah + o);
+                a_lo[r] = *reinterpret_cast<const v8bf*>(al + o);
+            }
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int o = (c0 + 32 * c + r_lane) * RS + 16 * ks + k_lane;
+                b_hi[c] = *reinterpret_cast<const v8bf*>(bh + o);
+                if constexpr (WK != W_I8) b_lo[c] = *reinterpret_cast<const v8bf*>(bl + o);
+            }
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_hi[r], b_hi[c], acc[r][c], 0, 0, 0);
+                    acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_lo[r], b_hi[c], acc[r][c], 0, 0, 0);
+                    if constexpr (WK != W_I8)
+                        acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_hi[r], b_lo[c], acc[r][c], 0, 0, 0);
+                }
+        }
+    }
+};
+
+// The output step for one element of C: alpha, beta, bias and the epilogue
+// (encoder.c:193-216, 410-424, 473-475).
+__device__ inline void put(const SpArgs& p, int m, int n, float sum)
+{
+    float* cp = p.C + (size_t)m * p.ldc + n;
+    float v = __fmul_rn(p.alpha, sum);
+    if (p.beta != 0.0f) v = __fadd_rn(p.beta == 1.0f ? *cp : __fmul_rn(p.beta, *cp), v);
+    if (p.bias) v = __fadd_rn(v, p.bias[n]);
+    switch (p.epi) {
+    case EPI_SWISH:         v = swish_f(v); break;
+    case EPI_HALF_RESIDUAL: v = __fmaf_rn(v, 0.5f, *cp); break;
+    case EPI_RESIDUAL:      v = __fadd_rn(*cp, v); break;
+    case EPI_RELU:          v = v > 0.0f ? v : 0.0f; break;
+    default:                break;
+    }
+    *cp = v;
+}
+
+// Tile t of the launch, in XCD-sized runs along rows of tiles (workgroups
+// reach the 8 XCDs round-robin): an XCD's workgroups share A rows in its L2.
+// -1 for the padding workgroups of the last run.
+__device__ inline int tile_of(const SpArgs& p)
+{
+    const int per = gridDim.x / kXcd;
+    const int t = (blockIdx.x % kXcd) * per + blockIdx.x / kXcd;
+    return t < p.tiles ? t : -1;
+}
+
+__device__ inline void zero(v16f (&acc)[2][2])
+{
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[r][c][e] = 0.0f;
+}
+
+// Workgroups of WM x WN waves own (64 WM) x (64 WN) tiles of C; two LDS
+// buffers, loads PD chunks ahead.
+// Two waves per SIMD where the registers allow it without spills (the
+// others are held to one by their LDS anyway).
+template <int WK, int WM, int WN, int PD>
+__global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) void split_gemm(SpArgs p)
+{
+    typedef Pipe<WK, 64 * WM, 64 * WN, 64 * WM * WN> L;
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2 * L::BUF];
+
+    const int t = tile_of(p);
+    if (t < 0) return;                               // padding workgroup (uniform)
+    const int m0 = (t / p.tiles_n) * (64 * WM), n0 = (t % p.tiles_n) * (64 * WN);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const auto rA = rsrc(p.A, p.a_bytes), rB = rsrc(p.B, p.b_bytes), rS = rsrc(p.scales, p.s_bytes);
+
+    typename L::Raw raw[PD];                         // chunk x in slot x % PD
+    v16f acc[2][2];
+    zero(acc);
+
+    // Loads run PD chunks ahead: before chunk c multiplies, the slots hold
+    // chunks c + 1 .. c + PD.  The loop is unrolled by PD so that every slot
+    // index is a compile-time constant.
+    const int nc = p.K / KT;
+#pragma unroll
+    for (int j = 0; j < PD; ++j)
+        if (j < nc) L::load(raw[j], p, rA, rB, rS, tid, m0, n0, KT * j);
+    L::store(raw[0], smem, tid);
+    if (PD < nc) L::load(raw[0], p, rA, rB, rS, tid, m0, n0, KT * PD);
+    __syncthreads();
+    for (int c0 = 0; c0 < nc; c0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; ++j) {
+            const int c = c0 + j;
+            if (c >= nc) break;
+            L::multiply(smem + (c & 1) * L::BUF, acc, lane, 64 * wm, 64 * wn);
+            if (c + 1 < nc) {
+                const int s = (j + 1) % PD;                  // constant once unrolled
+                // the other buffer: its last reader was chunk c - 1, before the barrier
+                L::store(raw[s], smem + ((c + 1) & 1) * L::BUF, tid);
+                if (c + 1 + PD < nc) L::load(raw[s], p, rA, rB, rS, tid, m0, n0, KT * (c + 1 + PD));
+            }
+            __syncthreads();
+        }
+    }
+
+    // C[m][n]: lane (l & 31) is the column, register e the row
+    // 8 (e >> 2) + 4 (l >> 5) + (e & 3) of each 32 x 32 block
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int n = n0 + 64 * wn + 32 * c + (lane & 31);
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + 64 * wm + 32 * r + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (m < p.M) put(p, m, n, acc[r][c][e]);
+            }
+        }
+}
+
+// Workgroups of KS waves own 64 x 64 tiles, wave w the chunks
+// [w nc / KS, (w + 1) nc / KS) of K with an LDS slab of its own (no barrier
+// until the end), loads PD chunks ahead; the KS partial tiles are then
+// summed in LDS in wave order.  For shapes with too few tiles to give every
+// CU a workgroup otherwise (N = 1024 at 1656 rows).
+template <int WK, int KS, int PD>
+__global__ __launch_bounds__(64 * KS, 2) void split_gemm_k(SpArgs p)
+{
+    typedef Pipe<WK, 64, 64, 64> L;
+    constexpr int STAGE = KS * L::BUF * 2, RED = KS * 4 * 16 * 64 * 4;   // bytes
+    __shared__ __attribute__((aligned(16))) unsigned char smem[STAGE > RED ? STAGE : RED];
+
+    const int t = tile_of(p);
+    if (t < 0) return;                               // padding workgroup (uniform)
+    const int m0 = (t / p.tiles_n) * 64, n0 = (t % p.tiles_n) * 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const auto rA = rsrc(p.A, p.a_bytes), rB = rsrc(p.B, p.b_bytes), rS = rsrc(p.scales, p.s_bytes);
+    __bf16* slab = reinterpret_cast<__bf16*>(smem) + wave * L::BUF;
+
+    typename L::Raw raw[PD];
+    v16f acc[2][2];
+    zero(acc);
+    const int nc = p.K / KT, s0 = wave * nc / KS, s1 = (wave + 1) * nc / KS;
+#pragma unroll
+    for (int j = 0; j < PD; ++j)
+        if (s0 + j < s1) L::load(raw[j], p, rA, rB, rS, lane, m0, n0, KT * (s0 + j));
+    for (int c0 = s0; c0 < s1; c0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; ++j) {
+            const int c = c0 + j;
+            if (c >= s1) break;
+            // the slab's previous reads came first: LDS keeps a wave's order
+            L::store(raw[j], slab, lane);
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (c + PD < s1) L::load(raw[j], p, rA, rB, rS, lane, m0, n0, KT * (c + PD));
+            L::multiply(slab, acc, lane, 0, 0);
+        }
+    }
+
+    // fixed-order sum over the waves: red[w][block][e][lane]
+    __syncthreads();                                 // every slab read done: reuse as red
+    float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) red[((wave * 4 + 2 * r + c) * 16 + e) * 64 + lane] = acc[r][c][e];
+    __syncthreads();
+    for (int o = threadIdx.x; o < 4 * 16 * 64; o += 64 * KS) {
+        const int blk = o >> 10, e = (o >> 6) & 15, l = o & 63;
+        float sum = red[o];
+#pragma unroll
+        for (int w = 1; w < KS; ++w) sum = __fadd_rn(sum, red[w * 4096 + o]);
+        const int m = m0 + 32 * (blk >> 1) + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
+        const int n = n0 + 32 * (blk & 1) + (l & 31);
+        if (m < p.M && n < p.N) put(p, m, n, sum);
+    }
+}
+
+// Launch shape: the largest workgroup tile (128 x 128, 128 x 64) whose tile
+// count still gives every CU a workgroup; else 64 x 64 tiles with K split
+// over 4 waves (when each wave gets at least two chunks), else 64 x 64 tiles
+// of one wave.
+enum SplitShape { SP_2x2, SP_2x1, SP_K4, SP_1x1 };
+constexpr int kKSplit = 4;
+
+SplitShape split_shape(int M, int N, int K)
+{
+    auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    if (tiles(128, 128) >= 256) return SP_2x2;
+    if (tiles(128, 64) >= 256) return SP_2x1;
+    if (K / KT >= 2 * kKSplit) return SP_K4;
+    return SP_1x1;
+}
+
+unsigned padded_grid(SpArgs& a, int bm, int bn)
+{
+    a.tiles_n = (a.N + bn - 1) / bn;
+    a.tiles = ((a.M + bm - 1) / bm) * a.tiles_n;
+    return (unsigned)(((a.tiles + kXcd - 1) / kXcd) * kXcd);
+}
+
+template <int WK>
+hipError_t launch_kind(SpArgs a, SplitShape s, hipStream_t st)
+{
+    // Chunks of loads in flight, as many as fit two waves per SIMD without
+    // spills: a lane holds 16 A bytes per 64 rows of the tile and chunk, plus
+    // its weight units (fp32's take 4 times int8's registers).
+    constexpr int PD22 = WK == W_F32 ? 2 : 3, PD21 = 2, PDK = WK == W_F32 ? 1 : 2;
+    switch (s) {
+    case SP_2x2:
+        hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22>), dim3(padded_grid(a, 128, 128)), dim3(256), 0, st, a);
+        break;
+    case SP_2x1:
+        hipLaunchKernelGGL((split_gemm<WK, 2, 1, PD21>), dim3(padded_grid(a, 128, 64)), dim3(128), 0, st, a);
+        break;
+    case SP_K4:
+        hipLaunchKernelGGL((split_gemm_k<WK, kKSplit, PDK>), dim3(padded_grid(a, 64, 64)), dim3(64 * kKSplit),
+                           0, st, a);
+        break;
+    default:
+        hipLaunchKernelGGL((split_gemm<WK, 1, 1, 2>), dim3(padded_grid(a, 64, 64)), dim3(64), 0, st, a);
+        break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool split_supports(const GemmProblem& p)
+{
+    if (p.M < 1 || p.N < 1 || p.K < KT || p.K % KT) return false;
+    if (p.chain_bias) return false;
+    if (p.alpha == 0.0f || (p.kind == W_I8 && p.scale == 0.0f)) return false;   // beta-only step
+    if (p.N % 32) return false;
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(p.A), pb = reinterpret_cast<uintptr_t>(p.B);
+    if (p.lda % 4 || pa % 16) return false;
+    switch (p.kind) {
+    case W_I8:  return p.ldb % 4 == 0 && pb % 4 == 0;
+    case W_I4:  return p.ldb % 4 == 0 && pb % 4 == 0 && reinterpret_cast<uintptr_t>(p.scales) % 4 == 0;
+    default:    return p.ldb % 4 == 0 && pb % 16 == 0;
+    }
+}
+
+hipError_t launch_split(const GemmProblem& p, hipStream_t st)
+{
+    if (!split_supports(p)) return hipErrorNotSupported;
+    SpArgs a = {};
+    a.M = p.M; a.N = p.N; a.K = p.K;
+    a.alpha = p.kind == W_I8 ? p.alpha * p.scale : p.alpha;
+    a.beta = p.beta;
+    a.A = p.A; a.lda = p.lda;
+    a.B = p.B; a.ldb = p.ldb;
+    a.scales = p.scales; a.n_groups = p.N / 32;
+    a.C = p.C; a.ldc = p.ldc;
+    a.bias = p.bias; a.epi = p.epi;
+    const size_t b_row = p.kind == W_I4 ? (size_t)p.N / 2 : (size_t)p.N;
+    const size_t a_ext = ((size_t)(p.M - 1) * p.lda + p.K) * 4;
+    const size_t b_ext = ((size_t)(p.K - 1) * p.ldb + b_row) * (p.kind == W_F32 ? 4 : 1);
+    const size_t s_ext = p.kind == W_I4 ? (size_t)p.K * (p.N / 32) * 4 : 0;
+    const size_t lim = (size_t)1 << 31;
+    if (a_ext >= lim || b_ext >= lim || s_ext >= lim) return hipErrorNotSupported;
+    a.a_bytes = (uint32_t)a_ext;
+    a.b_bytes = (uint32_t)b_ext;
+    a.s_bytes = (uint32_t)s_ext;
+    const SplitShape s = split_shape(p.M, p.N, p.K);
+    switch (p.kind) {
+    case W_I8: return launch_kind<W_I8>(a, s, st);
+    case W_I4: return launch_kind<W_I4>(a, s, st);
+    default:   return launch_kind<W_F32>(a, s, st);
+    }
+}
+
+}  // namespace pkgpu

@@ -62,14 +62,16 @@ class Dev:
         self.torch.cuda.synchronize(self.dev)
 
     def gemm(self, kind, A, W, C0, alpha=1.0, beta=0.0, scale=None, scales=None, cfg=-1,
-             bias=None, epi=None, exact=True):
+             bias=None, epi=None, exact=True, numerics=None):
         """Run C = beta*C0 + alpha*A*W through the *_dev entry points (the *_ex_dev
         ones when a bias or an epilogue is given); returns numpy C.  exact: with
         PK_GPU_NUMERICS_EXACT on this thread (bit-identical chains for every
-        shape); otherwise the default numerics (the small-M kernels for M <= 64)."""
+        shape); otherwise the default numerics (the small-M kernels for M <= 64).
+        numerics, when given, is the PK_GPU_NUMERICS_* mode instead."""
         lib = pk.load()
         prev = lib.pk_gpu_get_numerics()
-        pk.call("pk_gpu_set_numerics", pk.NUMERICS_EXACT if exact else pk.NUMERICS_DEFAULT)
+        mode = numerics if numerics is not None else (pk.NUMERICS_EXACT if exact else pk.NUMERICS_DEFAULT)
+        pk.call("pk_gpu_set_numerics", mode)
         try:
             return self._gemm(kind, A, W, C0, alpha, beta, scale, scales, cfg, bias, epi)
         finally:

@@ -4,7 +4,9 @@ Under PK_GPU_NUMERICS_EXACT (the default) every operation is the
 reference's, and the output equals the oracle's whole encoder
 (pk_oracle_encoder.c) bit for bit.  Under PK_GPU_NUMERICS_DEFAULT the weight
 GEMMs of a row group of at most 64 rows (a 2.56 s clip's 33 frames) take the
-small-M kernels, each within 1e-3 of the reference GEMM (about 1e-5); over
+small-M kernels, and under PK_GPU_NUMERICS_FAST every weight GEMM takes the
+small-M or the split kernels, each within 1e-3 of the reference GEMM (about
+1e-5); over
 24 blocks the deviations compound, so the model here has trained-like
 attention weights (the int8 attention projections' scales x 0.05, as
 oracle/ref_encode_main.c's PK_SYNTH_ATTN_GAIN does for the end-to-end token
@@ -41,7 +43,7 @@ def model():
     return m
 
 
-def run(m, x, chunk, mode):
+def run(m, x, chunk, mode, overlap=8):
     import torch
     enc = ctypes.c_void_p()
     pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(m.blocks, ctypes.c_void_p),
@@ -54,7 +56,7 @@ def run(m, x, chunk, mode):
         dout = torch.full_like(dx, float("nan"))
         outs = []
         for _ in range(2):               # capture, then replay
-            pk.call("pk_gpu_encoder_run_dev", enc, dx.data_ptr(), x.shape[0], chunk, 8,
+            pk.call("pk_gpu_encoder_run_dev", enc, dx.data_ptr(), x.shape[0], chunk, overlap,
                     dout.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
             torch.cuda.synchronize(dev)
             outs.append(dout.cpu().numpy())
@@ -81,6 +83,23 @@ def test_short_clip_small_m_within_tolerance(model, T):
         assert bits_equal(got, want), describe_mismatch(got, want)
 
 
+@pytest.mark.parametrize("T,chunk", [(200, 0), (300, 140)])
+def test_fast_mode_within_tolerance(model, T, chunk):
+    """PK_GPU_NUMERICS_FAST: every weight GEMM of every length on the
+    tolerance kernels (the split kernels above 64 rows per group; 300 frames
+    in chunks of 140 run as two row groups).  Over 24 blocks the output stays
+    within 1e-3 of the oracle's exact encoder, and replays repeat the first
+    run bit for bit."""
+    x = bench.enc_rng(0xFEA7, T + 1).standard_normal((T, bench.D)).astype(np.float32)
+    ov = 8 if chunk else 0
+    want = po.encoder(model.blocks, bench.N_BLOCKS, model.pe, bench.PE_CENTER, x, chunk, ov)
+    got = run(model, x, chunk, pk.NUMERICS_FAST, overlap=ov)
+    e = rel_dev(got[0], want)
+    print(f"T {T} chunk {chunk}: fast max |out - oracle| / max |oracle| = {e:.3g}", flush=True)
+    assert e <= TOL, e
+    assert bits_equal(got[1], got[0]), "fast replay differs from its capture run"
+
+
 def test_long_input_unaffected(model):
     """200 frames unchunked (one group of 200 rows): the setting changes nothing."""
     x = bench.enc_rng(0xFEA7, 200).standard_normal((200, bench.D)).astype(np.float32)
@@ -99,5 +118,6 @@ def test_numerics_argument_checks(model):
     try:
         assert lib.pk_gpu_encoder_get_numerics(enc) == pk.NUMERICS_EXACT
         assert lib.pk_gpu_encoder_set_numerics(enc, 5) == -1
+        assert lib.pk_gpu_encoder_set_numerics(enc, pk.NUMERICS_FAST) == 0
     finally:
         lib.pk_gpu_encoder_destroy(enc)

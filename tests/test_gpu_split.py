@@ -1,0 +1,143 @@
+"""GPU: the split kernels (pk_split.hip), which GEMMs with M > 64 take under
+PK_GPU_NUMERICS_FAST (pk_gpu_set_numerics).
+
+The reference computes every output as one fp32 fma chain over k
+(blas.c:187-218, 759-771, 950-963).  These kernels take the same products
+(activations split into two bf16 halves; int8 and int4 codes exact, int4
+weights dequantised exactly as blas.c:834-840 does and then split, fp32
+weights split) through v_mfma_f32_32x32x16_bf16 with fp32 accumulators, in
+another, fixed order.  The contract is max |C - R| / max |R| <= 1e-3 against
+the oracle R (bit-identical to the reference, test_oracle.py); the tests
+also hold the measured error below 1e-4, so a lost term, a wrong scale
+group, nibble or output position fails them.  Each of the four launch shapes
+(workgroup tiles of 128 x 128 and 128 x 64; 64 x 64 with K split over 4
+waves and summed in LDS, also with chunk counts that do not divide by 4;
+64 x 64 on one wave) is taken by some of the shapes below; rows and columns
+past M and N, alpha, beta and the fused epilogues are covered, and results
+are deterministic."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+from pkgpu import Dev, bits_equal, gpu_available, pk
+from test_gpu_gemm import make, oracle
+
+pytestmark = pytest.mark.gpu
+
+CONTRACT, MEASURED = 1e-3, 1e-4
+#                      launch shape the shape takes (tiles of 128 x 128 >= 256,
+#                      else of 128 x 64 >= 256, else 64 x 64 with K over 4 waves
+#                      when K >= 256, else 64 x 64 on one wave)
+SHAPES = [("i8", 1024, 4096, 256),    # 128 x 128: 8 x 32 tiles
+          ("i4", 1024, 4096, 256),
+          ("f32", 1024, 4096, 128),
+          ("i8", 1024, 2048, 128),    # 128 x 64: 8 x 32 tiles
+          ("i4", 1000, 2048, 160),    # partial last row tile
+          ("f32", 1024, 2048, 96),
+          ("i8", 416, 3072, 1024),    # K over 4 waves: the QKV of one 416-row chunk
+          ("i4", 416, 4096, 1024),    # feed-forward up and down of one chunk
+          ("i4", 375, 1024, 4096),
+          ("f32", 416, 2048, 1024),   # pointwise 1
+          ("i8", 300, 512, 1056),     # 33 chunks: waves take 8, 8, 8 and 9
+          ("f32", 130, 256, 320),     # 10 chunks: 2, 3, 2, 3
+          ("i4", 97, 96, 288),
+          ("i8", 65, 96, 64), ("i4", 130, 160, 224), ("f32", 77, 32, 32), ("i8", 200, 1056, 32)]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not gpu_available():
+        pytest.skip("no GPU")
+    return Dev()
+
+
+def bits_of(kind):
+    return {"i4": 4, "i8": 8, "f32": 32}[kind]
+
+
+def rel_err(got, want):
+    return float(np.abs(got.astype(np.float64) - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+def fast(dev, kind, A, W, extra, C0, alpha=1.0, beta=0.0, bias=None, epi=None):
+    kw = {"scales": extra} if kind == "i4" else {"scale": extra} if kind == "i8" else {}
+    return dev.gemm(kind, A, W, C0, alpha, beta, bias=bias, epi=epi, numerics=pk.NUMERICS_FAST, **kw)
+
+
+def uses_split(M, N, K, bits):
+    lib = pk.load()
+    prev = lib.pk_gpu_get_numerics()
+    pk.call("pk_gpu_set_numerics", pk.NUMERICS_FAST)
+    try:
+        return lib.pk_gpu_uses_split(M, N, K, bits)
+    finally:
+        pk.call("pk_gpu_set_numerics", prev)
+
+
+@pytest.mark.parametrize("kind,M,N,K", SHAPES)
+def test_split_within_tolerance(dev, kind, M, N, K):
+    assert uses_split(M, N, K, bits_of(kind)) == 1
+    A, W, extra, _ = make(kind, M, N, K, f"sp.{kind}.{M}.{N}.{K}")
+    Z = np.zeros((M, N), np.float32)
+    want = oracle(kind, A, W, extra, Z)
+    got = fast(dev, kind, A, W, extra, Z)
+    e = rel_err(got, want)
+    print(f"{kind} {M}x{N}x{K}: max|C - R| / max|R| = {e:.3g}", flush=True)
+    assert e <= CONTRACT and e <= MEASURED, e
+    assert bits_equal(fast(dev, kind, A, W, extra, Z), got), "not deterministic"
+
+
+@pytest.mark.parametrize("kind", ["i8", "i4", "f32"])
+def test_split_alpha_beta_and_epilogues(dev, kind):
+    M, N, K = 200, 256, 512
+    A, W, extra, C0 = make(kind, M, N, K, f"spepi.{kind}")
+    bias = po.normal((N,), 0.0, 0.02, po.seed(0x5EED3000, f"spepi.{kind}.b"))
+    Z = np.zeros((M, N), np.float32)
+    plain = oracle(kind, A, W, extra, Z)
+    for alpha, beta in [(0.75, 0.5), (1.0, 1.0), (-2.0, 0.0)]:
+        want = oracle(kind, A, W, extra, C0, alpha, beta)
+        assert rel_err(fast(dev, kind, A, W, extra, C0, alpha, beta), want) <= MEASURED, (alpha, beta)
+    biased = (plain + bias[None, :]).astype(np.float32)
+    cases = {
+        pk.EPI_NONE: biased,
+        pk.EPI_SWISH: po.swish(biased),
+        pk.EPI_HALF_RESIDUAL: (C0 + np.float32(0.5) * biased).astype(np.float32),
+        pk.EPI_RESIDUAL: (C0 + biased).astype(np.float32),
+        4: np.maximum(biased, 0.0),                                   # EPI_RELU
+    }
+    for epi, want in cases.items():
+        C_in = C0 if epi in (pk.EPI_HALF_RESIDUAL, pk.EPI_RESIDUAL) else Z
+        got = fast(dev, kind, A, W, extra, C_in, 1.0, 0.0, bias=bias, epi=epi)
+        assert rel_err(got, want) <= MEASURED, f"epilogue {epi}"
+
+
+def test_split_dispatch_rules(dev):
+    """FAST sends M <= 64 to the small-M kernels and other suitable shapes
+    here; DEFAULT and EXACT never take these kernels, a forced tile
+    configuration means exact chains, and shapes outside the rules (N or K
+    not a multiple of 32) stay exact."""
+    lib = pk.load()
+    assert uses_split(33, 3072, 1024, 8) == 0 and uses_split(65, 3072, 1024, 8) == 1
+    assert uses_split(1656, 1000, 1024, 8) == 0          # N % 32
+    assert uses_split(1656, 1024, 1000, 32) == 0          # K % 32
+    for mode in (pk.NUMERICS_DEFAULT, pk.NUMERICS_EXACT):
+        prev = lib.pk_gpu_get_numerics()
+        pk.call("pk_gpu_set_numerics", mode)
+        try:
+            assert lib.pk_gpu_uses_split(1656, 4096, 1024, 4) == 0
+        finally:
+            pk.call("pk_gpu_set_numerics", prev)
+    pk.call("pk_gpu_force_config", 20)
+    try:
+        assert uses_split(1656, 4096, 1024, 4) == 0
+    finally:
+        pk.call("pk_gpu_force_config", -1)
+    assert lib.pk_gpu_set_numerics(3) == -1
+
+
+def test_split_shapes_outside_rules_stay_exact(dev):
+    """N not a multiple of 32 under FAST: the exact chains, bit for bit."""
+    M, N, K = 200, 1000, 256
+    A, W, extra, _ = make("i8", M, N, K, "spx")
+    Z = np.zeros((M, N), np.float32)
+    assert bits_equal(fast(dev, "i8", A, W, extra, Z), oracle("i8", A, W, extra, Z))
