@@ -434,8 +434,8 @@ int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
  *       max |C - R| / max |R| <= 1e-3 of the reference (about 1e-5),
  *       deterministic, no memory beyond the operands.  Shapes outside those
  *       rules stay bit-identical.
- * The environment variable PK_GPU_NUMERICS=exact makes EXACT every thread's
- * default.  A forced configuration (pk_gpu_force_config) implies exact
+ * The environment variable PK_GPU_NUMERICS=exact (or =fast) makes EXACT (or
+ * FAST) every thread's default.  A forced configuration (pk_gpu_force_config) implies exact
  * chains.  The device-resident encoder (pk_gpu_encoder_*) has a setting of
  * its own (pk_gpu_encoder_set_numerics), exact by default.
  * No counterpart in the reference. */

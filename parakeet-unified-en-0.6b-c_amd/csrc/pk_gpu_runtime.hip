@@ -67,12 +67,15 @@ size_t g_resident_bytes = 0;
 
 thread_local std::string t_err;
 thread_local int t_force_cfg = -1;
-// PK_GPU_NUMERICS_DEFAULT or _EXACT for this thread's later calls; the
-// environment's PK_GPU_NUMERICS=exact sets every thread's default.
+// PK_GPU_NUMERICS_DEFAULT, _EXACT or _FAST for this thread's later calls;
+// the environment's PK_GPU_NUMERICS=exact or =fast sets every thread's
+// default.
 int default_numerics()
 {
     const char* e = getenv("PK_GPU_NUMERICS");
-    return (e && strcmp(e, "exact") == 0) ? PK_GPU_NUMERICS_EXACT : PK_GPU_NUMERICS_DEFAULT;
+    if (e && strcmp(e, "exact") == 0) return PK_GPU_NUMERICS_EXACT;
+    if (e && strcmp(e, "fast") == 0) return PK_GPU_NUMERICS_FAST;
+    return PK_GPU_NUMERICS_DEFAULT;
 }
 thread_local int t_numerics = default_numerics();
 

@@ -18,17 +18,23 @@
 // The dropped A_lo W_lo term and the operands' residues r are below 2^-16 of
 // each product; the measured error is about 1e-5.
 //
-// Tiles.  A workgroup of WM x WN waves computes a (64 WM) x (64 WN) tile of
-// C, each wave 64 x 64 as 2 x 2 MFMA blocks of 32 x 32, over the whole of K
-// in 32-deep chunks.  Per chunk, every thread loads its share of the A rows
-// (16-byte loads) and of the weight rows (4 or 16 bytes per unit and two
-// consecutive k rows per unit), splits them, and writes them to LDS as
-// planes [row or column][k] of bf16 with a padded stride of 40, so the
-// MFMA operands (8 consecutive k of one row or column per lane) are single
-// 16-byte LDS reads.  Two LDS buffers: the next chunk's global loads are in
-// flight while the current chunk multiplies, and are split into the other
-// buffer after it.  Every workgroup sums its own tile over all of K in a
-// fixed order, so results are deterministic.
+// Staging (Pipe).  K goes in 32-deep chunks.  Per chunk, every thread loads
+// its share of the A rows (16-byte loads) and of the weight rows (4 or 16
+// bytes per unit, two consecutive k rows per unit), splits them, and writes
+// them to LDS as planes [row or column][k] of bf16 with a padded stride of
+// 40, so the MFMA operands (8 consecutive k of one row or column per lane)
+// are single 16-byte LDS reads.  Loads run 1-3 chunks ahead in registers.
+// Each wave computes a 64 x 64 block of C as 2 x 2 MFMA blocks of 32 x 32.
+//
+// Launch shapes (split_shape):
+//   split_gemm    workgroups of WM x WN waves own (64 WM) x (64 WN) tiles
+//                 (128 x 128 or 128 x 64 where that still gives every CU a
+//                 workgroup, else 64 x 64) over all of K, two LDS buffers;
+//   split_gemm_k  for shapes with too few such tiles (N = 1024 at 1656 rows):
+//                 64 x 64 tiles, K split over 4 waves with an LDS slab each,
+//                 the 4 partial tiles summed in LDS in wave order.
+// Every workgroup sums its own tile in a fixed order, so results are
+// deterministic, and no memory beyond the operands is used.
 #include "pk_gemm_kernels.h"
 #include "pk_device_math.h"
 

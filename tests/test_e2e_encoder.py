@@ -117,6 +117,30 @@ def test_gpu_dropin_short_clip_small_m(attn_gain, tmp_path):
         assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"]
 
 
+@pytest.mark.gpu
+@pytest.mark.timeout(600)
+def test_gpu_dropin_fast_numerics(tmp_path):
+    """600 frames (two chunks of about 316 rows) through the GEMM drop-in with
+    PK_GPU_NUMERICS=fast: every weight GEMM of the reference's encoder.c takes
+    the split kernels (rows > 64), each within 1e-3 of the reference GEMM.
+    With trained-like attention weights the encoder output stays within 1e-3
+    of the reference's and the greedy token ids are equal."""
+    import numpy as np
+    frames = 600
+    gpu = run("pk_encode_gpu", frames, tmp_path, dump=tmp_path / "gpu.f32", attn_gain=0.05,
+              extra_env={"PK_GPU_NUMERICS": "fast"})
+    ref = run("pk_encode_ref", frames, tmp_path, dump=tmp_path / "ref.f32", attn_gain=0.05)
+    a = np.fromfile(tmp_path / "gpu.f32", dtype=np.float32)
+    b = np.fromfile(tmp_path / "ref.f32", dtype=np.float32)
+    dev = float(np.abs(a - b).max() / np.abs(b).max())
+    print(json.dumps({"frames": frames, "max_rel_deviation_fast": dev, "tokens_fast": gpu["n_tokens"],
+                      "tokens_reference": ref["n_tokens"],
+                      "tokens_equal": gpu["tokens_fnv"] == ref["tokens_fnv"]}), flush=True)
+    assert gpu["finite"] == 1 and gpu["chunked"] == ref["chunked"]
+    assert dev <= 1e-3
+    assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"]
+
+
 def resident_vs_reference(frames, tmp_path, attn_gain, from_mel=False):
     import numpy as np
     gres = run("pk_encode_gpures", frames, tmp_path, dump=tmp_path / "gpures.f32", attn_gain=attn_gain,
