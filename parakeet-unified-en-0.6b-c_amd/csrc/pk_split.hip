@@ -484,6 +484,8 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     a.a_bytes = (uint32_t)a_ext;
     a.b_bytes = (uint32_t)b_ext;
     a.s_bytes = (uint32_t)s_ext;
+    // 64 x 64 tiles at most: their count must fit the launch's int arithmetic
+    if ((long long)((p.M + 63) / 64) * ((p.N + 63) / 64) > (1LL << 30)) return hipErrorNotSupported;
     const SplitShape s = split_shape(p.M, p.N, p.K);
     switch (p.kind) {
     case W_I8: return launch_kind<W_I8>(a, s, st);
