@@ -945,7 +945,10 @@ def encoder_mode(args):
         if name == "gemm_i4":
             i4_flops, i4_sec, i4_launches = fl.value, sec, n.value
     pk.call("pk_gpu_encoder_profile", enc, 0)
-    fast = fast_mode_rates(pk, lib, enc, step, timed, K, KP, args.warmup)
+    try:
+        fast = fast_mode_rates(pk, lib, enc, step, timed, K, KP, args.warmup)
+    except Exception as e:        # reported in the line; the exact figures stand
+        fast = {"error": repr(e)}
     rows = chunk_rows()
     groups = args.groups or 2
     group_rows = plan_group_rows(rows, groups)
