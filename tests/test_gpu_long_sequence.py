@@ -94,6 +94,49 @@ def test_long_then_short_and_chunked(model):
         enc.close()
 
 
+@pytest.fixture(scope="module")
+def trained_like():
+    """The model with the int8 attention projections' scales x 0.05 (as the
+    numerics tests and oracle/ref_encode_main.c's PK_SYNTH_ATTN_GAIN do): at
+    the workloads' statistics one block's softmax amplifies a 1e-5 GEMM
+    difference to about 2e-3."""
+    if not gpu_available():
+        pytest.skip("no GPU")
+    import torch
+    pk.call("pk_gpu_init", 0)
+    torch.cuda.set_device(0)
+    m = bench.EncoderModel(pk, n_blocks=2)
+    for b in range(2):
+        w = m.blocks[b]
+        for name in ("linear_qkv_w", "linear_pos_w", "linear_out_w"):
+            wt = getattr(w, name)
+            wt.scale = wt.scale * 0.05
+            setattr(w, name, wt)
+    return m
+
+
+@pytest.mark.parametrize("T,n_blocks", [(1100, 1), (640, 2)])
+def test_unchunked_long_sequence_fast_numerics(trained_like, T, n_blocks):
+    """PK_GPU_NUMERICS_FAST on sequences past the LDS attention limit: the
+    weight GEMMs (M = T) take the split kernels, attention keeps its exact
+    workspace path.  With trained-like attention weights the output stays
+    within 1e-3 of the oracle's exact encoder (the split GEMMs are within
+    about 1e-5 each), and a replay repeats the first run bit for bit."""
+    model = trained_like
+    x = features(T, 11)
+    want = po.encoder(model.blocks, n_blocks, model.pe, bench.PE_CENTER, x, 0, 0)
+    enc = Encoder(model, n_blocks)
+    try:
+        pk.call("pk_gpu_encoder_set_numerics", enc.enc, pk.NUMERICS_FAST)
+        got = enc.run(x, 0, 0)
+    finally:
+        enc.close()
+    e = float(np.abs(got[0].astype(np.float64) - want).max() / np.abs(want).max())
+    print(f"T {T}, {n_blocks} block(s): fast max |out - oracle| / max |oracle| = {e:.3g}", flush=True)
+    assert e <= 1e-3, e
+    assert bits_equal(got[1], got[0]), "fast replay differs from its capture run"
+
+
 def test_longer_than_the_table_is_refused(model):
     enc = Encoder(model, 1)
     try:
