@@ -40,6 +40,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 namespace pkgpu {
 namespace {
@@ -113,8 +114,10 @@ struct Pipe {
     static constexpr int A_ITEMS = BM * (KT / 4) / NT;
     // weight units of two consecutive k rows: 4 columns (int8, fp32) or 8 (int4)
     static constexpr int UC = WK == W_I4 ? 8 : 4;
-    static constexpr int B_ITEMS = (KT / 2) * (BN / UC) / NT;
-    static_assert(A_ITEMS * NT == BM * (KT / 4) && B_ITEMS * NT == (KT / 2) * (BN / UC), "even split");
+    static constexpr int B_TOTAL = (KT / 2) * (BN / UC);
+    static constexpr int B_ITEMS = (B_TOTAL + NT - 1) / NT;     // the last one partial if NT > B_TOTAL
+    static_assert(A_ITEMS * NT == BM * (KT / 4) && (B_TOTAL % NT == 0 || B_TOTAL < NT), "even split");
+    static_assert(B_TOTAL % 64 == 0, "whole waves per weight item");
 
     struct Raw {
         v4u a[A_ITEMS];
@@ -137,6 +140,7 @@ struct Pipe {
 #pragma unroll
         for (int i = 0; i < B_ITEMS; ++i) {
             const int idx = tid + NT * i, kp = idx % (KT / 2), cu = idx / (KT / 2);
+            if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
             const int n = n0 + UC * cu;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -173,6 +177,7 @@ struct Pipe {
 #pragma unroll
         for (int i = 0; i < B_ITEMS; ++i) {
             const int idx = tid + NT * i, kp = idx % (KT / 2), cu = idx / (KT / 2);
+            if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
 #pragma unroll
             for (int c = 0; c < UC; ++c) {
                 const int off = (UC * cu + c) * RS + 2 * kp;      // column-major plane
@@ -398,16 +403,20 @@ __global__ __launch_bounds__(64 * KS, 2) void split_gemm_k(SpArgs p)
     }
 }
 
-// Launch shape: the largest workgroup tile (128 x 128, 128 x 64) whose tile
-// count still gives every CU a workgroup; else 64 x 64 tiles with K split
-// over 4 waves (when each wave gets at least two chunks), else 64 x 64 tiles
-// of one wave.
-enum SplitShape { SP_2x2, SP_2x1, SP_K4, SP_1x1 };
+// Launch shape.  Where 128 x 128 tiles outnumber the CUs, 256 x 128 tiles
+// (8 waves, one workgroup per CU by its LDS) give no CU more rows x columns
+// than two 128 x 128 workgroups would, and split each weight for twice the
+// rows: the int4 up projection at 1656 rows took 66.7 against 71.7 us.
+// Otherwise the largest tile (128 x 128, 128 x 64) whose count still gives
+// every CU a workgroup; else 64 x 64 tiles with K split over 4 waves (when
+// each wave gets at least two chunks), else 64 x 64 tiles of one wave.
+enum SplitShape { SP_4x2, SP_2x2, SP_2x1, SP_K4, SP_1x1 };
 constexpr int kKSplit = 4;
 
 SplitShape split_shape(int M, int N, int K)
 {
     auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    if (tiles(128, 128) > 256) return SP_4x2;
     if (tiles(128, 128) >= 256) return SP_2x2;
     if (tiles(128, 64) >= 256) return SP_2x1;
     if (K / KT >= 2 * kKSplit) return SP_K4;
@@ -427,8 +436,11 @@ hipError_t launch_kind(SpArgs a, SplitShape s, hipStream_t st)
     // Chunks of loads in flight, as many as fit two waves per SIMD without
     // spills: a lane holds 16 A bytes per 64 rows of the tile and chunk, plus
     // its weight units (fp32's take 4 times int8's registers).
-    constexpr int PD22 = WK == W_F32 ? 2 : 3, PD21 = 2, PDK = WK == W_F32 ? 1 : 2;
+    constexpr int PD22 = WK == W_F32 ? 2 : 3, PD21 = 2, PDK = WK == W_F32 ? 1 : 2, PD42 = 2;
     switch (s) {
+    case SP_4x2:
+        hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42>), dim3(padded_grid(a, 256, 128)), dim3(512), 0, st, a);
+        break;
     case SP_2x2:
         hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22>), dim3(padded_grid(a, 128, 128)), dim3(256), 0, st, a);
         break;

@@ -9,8 +9,8 @@ weights split) through v_mfma_f32_32x32x16_bf16 with fp32 accumulators, in
 another, fixed order.  The contract is max |C - R| / max |R| <= 1e-3 against
 the oracle R (bit-identical to the reference, test_oracle.py); the tests
 also hold the measured error below 1e-4, so a lost term, a wrong scale
-group, nibble or output position fails them.  Each of the four launch shapes
-(workgroup tiles of 128 x 128 and 128 x 64; 64 x 64 with K split over 4
+group, nibble or output position fails them.  Each of the five launch shapes
+(workgroup tiles of 256 x 128, 128 x 128 and 128 x 64; 64 x 64 with K split over 4
 waves and summed in LDS, also with chunk counts that do not divide by 4;
 64 x 64 on one wave) is taken by some of the shapes below; rows and columns
 past M and N, alpha, beta and the fused epilogues are covered, and results
@@ -25,10 +25,14 @@ from test_gpu_gemm import make, oracle
 pytestmark = pytest.mark.gpu
 
 CONTRACT, MEASURED = 1e-3, 1e-4
-#                      launch shape the shape takes (tiles of 128 x 128 >= 256,
-#                      else of 128 x 64 >= 256, else 64 x 64 with K over 4 waves
+#                      launch shape the shape takes (256 x 128 when tiles of
+#                      128 x 128 > 256; 128 x 128 at exactly 256; else 128 x 64
+#                      when >= 256 of them; else 64 x 64 with K over 4 waves
 #                      when K >= 256, else 64 x 64 on one wave)
-SHAPES = [("i8", 1024, 4096, 256),    # 128 x 128: 8 x 32 tiles
+SHAPES = [("i4", 1656, 4096, 96),     # 256 x 128 (more than 256 tiles of 128 x 128)
+          ("i8", 1600, 3072, 64),     # partial last row tile
+          ("f32", 1100, 4160, 64),    # partial last column tile
+          ("i8", 1024, 4096, 256),    # 128 x 128: 8 x 32 tiles
           ("i4", 1024, 4096, 256),
           ("f32", 1024, 4096, 128),
           ("i8", 1024, 2048, 128),    # 128 x 64: 8 x 32 tiles
