@@ -1062,8 +1062,8 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU only (single-GPU hot path; "
-              "multi-GPU sharding is a design note, not built)", file=sys.stderr)
+        print("bench.py: runs on one GPU only (the single-GPU hot path; multi-GPU "
+              "sharding is a design note, not built)", file=sys.stderr)
         sys.exit(2)
     if args.gemm:
         gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup,
