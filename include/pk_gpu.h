@@ -381,6 +381,11 @@ int pk_gpu_encoder_profile_read(pk_gpu_encoder *enc, int stage, double *ms, long
  * one after another. */
 #define PK_GPU_MAX_GROUPS 4
 int pk_gpu_encoder_set_groups(pk_gpu_encoder *enc, int n_groups);
+/* Modules of block 0 (0..3: none, feed-forward 1, + self-attention,
+ * + convolution) that group 0 runs before the other groups start; -1 (the
+ * initial setting) takes PK_GPU_GROUP_LAG from the environment, else 1.
+ * The results do not depend on it.  No counterpart in the reference. */
+int pk_gpu_encoder_set_group_lag(pk_gpu_encoder *enc, int modules);
 /* Numerics of this encoder's weight GEMMs.  PK_GPU_NUMERICS_EXACT (the
  * default): every GEMM is the reference's fma chain, and the whole encoder
  * is bit-identical to the reference's arithmetic.  PK_GPU_NUMERICS_DEFAULT:

@@ -130,6 +130,7 @@ struct pk_gpu_encoder {
     // Row groups replayed concurrently: group 0 on the caller's stream, group
     // g > 0 on side[g - 1], joined through events around the replay.
     int n_groups = 2;
+    int lag = -1;                  // pk_gpu_encoder_set_group_lag (-1: group_lag())
     std::vector<hipStream_t> side;
     std::vector<hipEvent_t> side_done;
     hipEvent_t inputs_ready = nullptr;
@@ -726,7 +727,7 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
         // The other groups start when group 0 has run the first `lag` modules
         // of block 0 (its lead graph), so that the groups' GEMMs and their
         // row kernels fall at different times.
-        const int lag = groups.size() > 1 ? group_lag() : 0;
+        const int lag = groups.size() < 2 ? 0 : e->lag >= 0 ? e->lag : group_lag();
         if (e->graphs.size() + groups.size() + (lag > 0) > kMaxGraphs &&
             !e->graphs.count(std::make_tuple(T, chunk, ov, lag > 0 ? 100 + lag : 0, forced,
                                              e->numerics))) {
@@ -1076,6 +1077,14 @@ int pk_gpu_encoder_set_numerics(pk_gpu_encoder* enc, int mode)
 int pk_gpu_encoder_get_numerics(pk_gpu_encoder* enc)
 {
     return enc ? enc->numerics : -1;
+}
+
+int pk_gpu_encoder_set_group_lag(pk_gpu_encoder* enc, int modules)
+{
+    if (!enc) return error(PK_GPU_EINVAL, "encoder is NULL");
+    if (modules < -1 || modules > 3) return error(PK_GPU_EINVAL, "group lag %d (-1..3)", modules);
+    enc->lag = modules;            // graphs are kept per lead
+    return PK_GPU_OK;
 }
 
 int pk_gpu_encoder_set_groups(pk_gpu_encoder* enc, int n_groups)

@@ -64,6 +64,7 @@ _PROTOS = {
     "pk_gpu_encoder_destroy": (None, [_p]),
     "pk_gpu_encoder_profile": (_i, [_p, _i]),
     "pk_gpu_encoder_set_groups": (_i, [_p, _i]),
+    "pk_gpu_encoder_set_group_lag": (_i, [_p, _i]),
     "pk_gpu_encoder_set_numerics": (_i, [_p, _i]),
     "pk_gpu_encoder_get_numerics": (_i, [_p]),
     "pk_gpu_encoder_set_pre_encode": (_i, [_p, _p]),

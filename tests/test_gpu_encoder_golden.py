@@ -48,7 +48,7 @@ def model():
     return m
 
 
-def resident(m, n_blocks, x, chunk, overlap, groups=None):
+def resident(m, n_blocks, x, chunk, overlap, groups=None, lag=None):
     """pk_gpu_encoder_run_dev over device copies of x, as bench.py calls it."""
     import torch
     enc = ctypes.c_void_p()
@@ -57,6 +57,8 @@ def resident(m, n_blocks, x, chunk, overlap, groups=None):
     try:
         if groups:
             pk.call("pk_gpu_encoder_set_groups", enc, groups)
+        if lag is not None:
+            pk.call("pk_gpu_encoder_set_group_lag", enc, lag)
         dev = torch.device("cuda:0")
         dx = torch.from_numpy(x).to(dev)
         dout = torch.full_like(dx, float("nan"))
@@ -110,6 +112,19 @@ def test_resident_encoder_digest_any_grouping(model, groups):
     x = bench.encoder_features(wl["frames"])
     for got in resident(model, bench.N_BLOCKS, x, wl["chunk"], wl["overlap"], groups):
         assert sha(got) == wl["output_sha256"]
+
+
+@pytest.mark.parametrize("groups,lag", [(2, 0), (2, 2), (2, 3), (3, 3)])
+def test_resident_encoder_digest_any_group_lead(model, groups, lag):
+    """The 900-frame workload with the other row groups starting after 0, 2 or
+    3 modules of group 0's block 0 (the default is 1): the order in which the
+    groups' kernels run changes, the digest does not."""
+    wl = GOLD["workloads"][1]
+    x = bench.encoder_features(wl["frames"])
+    for got in resident(model, bench.N_BLOCKS, x, wl["chunk"], wl["overlap"], groups, lag):
+        assert sha(got) == wl["output_sha256"]
+    lib = pk.load()
+    assert lib.pk_gpu_encoder_set_group_lag(None, 1) == -1
 
 
 @pytest.mark.parametrize("T,chunk,n_blocks", [(300, 0, 3), (132, 64, 2)])
