@@ -159,6 +159,7 @@ def fast_mode_rates(pk, lib, enc, step, timed, K, KP, warmup):
             "ms_per_step": round(ms / K, 4),
             "gemm_ms_per_step": {n: round(stages[n][0] * 1e3 / KP, 3)
                                  for n in ("gemm_i4", "gemm_i8", "gemm_f32")},
+            "attention_ms_per_step": round(stages["attention"][0] * 1e3 / KP, 3),
             "int4_gemm": {"tflops": round(useful, 2),
                           "mfma_tflops": round(3 * useful, 2),
                           "frac_bf16_mfma": round(3 * useful / PEAK_BF16_MFMA_TFLOPS, 4),
