@@ -204,12 +204,13 @@ def alg_bytes(kind, m, n, k):
 
 
 def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, force_config=-1,
-              numerics="default"):
+              numerics="default", split_k=True):
     """One JSON line per GEMM shape ("kind:MxNxK"): resident inputs, weights
     rotating over enough replicas to exceed the Infinity Cache, average launch
     time from HIP events around a graph replay of `steps` launches (eager: the
     same launches from a host loop, for profilers that trace kernels one by
-    one; its average includes the host's launch gaps)."""
+    one; its average includes the host's launch gaps).  split_k: the calls
+    have a split-K workspace (pk_gpu_set_workspace), which fast numerics use."""
     import torch
     pk = load_binding()
     pk.call("pk_gpu_init", 0)
@@ -220,6 +221,9 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
     dev = torch.device("cuda:0")
     cur = lambda: torch.cuda.current_stream(dev).cuda_stream   # the capture stream inside a graph
     g = torch.Generator(device=dev)
+    work = torch.empty(pk.SPLIT_WORKSPACE_BYTES // 4, device=dev) if split_k else None
+    pk.call("pk_gpu_set_workspace", work.data_ptr() if split_k else None,
+            pk.SPLIT_WORKSPACE_BYTES if split_k else 0)
     for spec in specs:
         kind, dims = spec.split(":")
         m, n, k = (int(v) for v in dims.lower().split("x"))
@@ -280,6 +284,7 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
                                     "split (bf16 split, tolerance path)" if split else
                                     "exact chains",
                           "numerics": numerics,
+                          "k_segments": lib.pk_gpu_split_k_segments(m, n, k, bits) if split else None,
                           "config": None if small_m or split else
                                     (force_config if force_config >= 0 else
                                      lib.pk_gpu_pick_config_bits(m, n, k, bits)),
@@ -591,6 +596,19 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
             return None, 0
         return cpu_seconds_per_call(fn, cpu_budget_s)
 
+    work = torch.empty(pk.SPLIT_WORKSPACE_BYTES // 4, device=dev)
+
+    def fast_us(fn, iters, warm):
+        # the same replay with this thread's numerics set to PK_GPU_NUMERICS_FAST
+        # and a split-K workspace
+        pk.call("pk_gpu_set_numerics", pk.NUMERICS_FAST)
+        pk.call("pk_gpu_set_workspace", work.data_ptr(), pk.SPLIT_WORKSPACE_BYTES)
+        try:
+            return graph_us(torch, dev, fn, iters, warm)
+        finally:
+            pk.call("pk_gpu_set_workspace", None, 0)
+            pk.call("pk_gpu_set_numerics", pk.NUMERICS_DEFAULT)
+
     # 0: int8 fused QKV of a 2.56 s clip, M = 32 (cblas_sgemm_qb)
     m, n, k = 32, 3072, 1024
     r0 = np.random.Generator(np.random.PCG64([0x5EED0000, 0]))
@@ -648,12 +666,14 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         pk.check("down", lib.pk_gpu_gemm_i4_dev(M, D, FF, 1.0, dH.data_ptr(), FF, P2d.data_ptr(),
                                                 S2d.data_ptr(), D // 2, 0.0, dO.data_ptr(), D, cur()))
     us1 = graph_us(torch, dev, pair, 100, 5)
+    us1f = fast_us(pair, 100, 5)
     cpu1 = None if not have_ref else cpu_baseline(X1, P1, S1, P2, S2, cpu_budget_s)
     fl1 = 4.0 * M * D * FF
     out["1_int4_ffn_pair_m375"] = {
         "gemm": "int4 375x4096x1024 (+ Swish) then 375x1024x4096, 32-column fp32 scales",
         "gpu_us": round(us1, 2), "tflops": round(fl1 / us1 / 1e6, 2),
         "frac_mfma_fp32": round(fl1 / us1 / 1e6 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "fast_us": round(us1f, 2), "fast_tflops": round(fl1 / us1f / 1e6, 2),
         "cpu_ref_us": cpu1["ms_per_step"] * 1e3 if cpu1 else None,
         "note": "the reference's x86 AVX2 int4 unpack decodes nibbles differently from its "
                 "portable path (the format definition, which the GPU follows), so only its time "
@@ -680,6 +700,7 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         pk.check("sgemm", lib.pk_gpu_sgemm_dev(m2, D, FF, 1.0, dH2.data_ptr(), FF, b.data_ptr(), D, 0.0,
                                                dO2.data_ptr(), D, cur()))
     us2 = graph_us(torch, dev, fp32_pair, 50, 3)
+    us2f = fast_us(fp32_pair, 50, 3)
     fp32_pair(0)
     torch.cuda.synchronize(dev)
     got2 = dO2.cpu().numpy()
@@ -694,6 +715,7 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         "gemm": "fp32 500x4096x1024 then 500x1024x4096", "gpu_us": round(us2, 2),
         "tflops": round(fl2 / us2 / 1e6, 2),
         "frac_mfma_fp32": round(fl2 / us2 / 1e6 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "fast_us": round(us2f, 2), "fast_tflops": round(fl2 / us2f / 1e6, 2),
         "cpu_ref_us": round(cpu2 * 1e6, 1) if cpu2 else None, "cpu_ref_calls": n2,
         "bit_identical_to_ref": bool(np.array_equal(got2.view(np.uint32), O2.view(np.uint32)))
         if have_ref else None}
@@ -1055,6 +1077,8 @@ def main():
                     help="with --gemm: force this tile configuration (exact chains)")
     ap.add_argument("--numerics", choices=["default", "exact", "fast"], default="default",
                     help="with --gemm: the PK_GPU_NUMERICS_* mode of the timed calls")
+    ap.add_argument("--no-split-k", action="store_true",
+                    help="with --gemm: no split-K workspace for fast numerics")
     ap.add_argument("--eager", action="store_true",
                     help="with --gemm: launch from a host loop instead of a graph replay "
                          "(for kernel tracers)")
@@ -1068,7 +1092,8 @@ def main():
         sys.exit(2)
     if args.gemm:
         gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup,
-                  eager=args.eager, force_config=args.force_config, numerics=args.numerics)
+                  eager=args.eager, force_config=args.force_config, numerics=args.numerics,
+                  split_k=not args.no_split_k)
         return
     if args.ffn:
         args.steps = args.steps or 200

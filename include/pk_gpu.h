@@ -395,7 +395,9 @@ int pk_gpu_encoder_set_group_lag(pk_gpu_encoder *enc, int modules);
  * longer inputs are unaffected.  PK_GPU_NUMERICS_FAST: every weight GEMM
  * takes the small-M or the split kernels (see pk_gpu_set_numerics), each
  * within the same bound; over 24 blocks the deviations compound, so the
- * output is not bit-identical at any length.  Captured graphs are kept per
+ * output is not bit-identical at any length.  In this mode a run also holds
+ * PK_GPU_SPLIT_WORKSPACE_BYTES per row group for the split kernels' partial
+ * tiles (counted by pk_gpu_encoder_bytes).  Captured graphs are kept per
  * mode.  No counterpart in the reference.  get returns the mode, -1 for
  * NULL. */
 int pk_gpu_encoder_set_numerics(pk_gpu_encoder *enc, int mode);
@@ -437,8 +439,9 @@ int pk_gpu_pick_config_bits(int M, int N, int K, int bits);
  *       into two bf16 halves (the int8 codes and int4 codes exactly; int4
  *       weights dequantised exactly first), fp32 accumulators, within
  *       max |C - R| / max |R| <= 1e-3 of the reference (about 1e-5),
- *       deterministic, no memory beyond the operands.  Shapes outside those
- *       rules stay bit-identical.
+ *       deterministic, no memory beyond the operands unless the thread gives
+ *       a workspace (pk_gpu_set_workspace).  Shapes outside those rules stay
+ *       bit-identical.
  * The environment variable PK_GPU_NUMERICS=exact (or =fast) makes EXACT (or
  * FAST) every thread's default.  A forced configuration (pk_gpu_force_config) implies exact
  * chains.  The device-resident encoder (pk_gpu_encoder_*) has a setting of
@@ -455,6 +458,22 @@ int pk_gpu_uses_small_m(int M, int N, int K, int bits);
 /* Whether such a GEMM would take the split kernels on this thread
  * (PK_GPU_NUMERICS_FAST and a shape the small-M kernels do not take). */
 int pk_gpu_uses_split(int M, int N, int K, int bits);
+/* Device memory that this thread's later split-kernel GEMMs
+ * (PK_GPU_NUMERICS_FAST) may use for partial tiles.  With at least
+ * PK_GPU_SPLIT_WORKSPACE_BYTES, a shape with fewer 128 x 128 tiles than the
+ * 256 CUs splits K over workgroups: each stores its raw partial tile, and a
+ * second launch sums a tile's partials in segment order before alpha, beta,
+ * bias and the epilogue, so results stay deterministic.  NULL (the default)
+ * or fewer bytes: no workspace is used.  The memory stays the caller's and
+ * must outlive the calls; GEMMs that may overlap on the device (different
+ * streams or threads) must not share it.  The reference's counterpart is
+ * the per-thread pack buffer of its sgemm (blas.c:477-505). */
+#define PK_GPU_SPLIT_WORKSPACE_BYTES 33554432
+int pk_gpu_set_workspace(void *dwork, size_t bytes);
+/* Segments of K over workgroups that a split-kernel GEMM of this shape and
+ * weight format (bits 4, 8 or 32) takes with this thread's workspace (1: K
+ * is not split over workgroups). */
+int pk_gpu_split_k_segments(int M, int N, int K, int bits);
 /* Debug: the weights the GEMM kernels multiply, written to dout [K][N] on
  * `stream` through the kernels' own weight loads and conversions: int8
  * (bits 8) fl(q * scale), int4 (bits 4) fl(q * dscales[k][n/32]) with the

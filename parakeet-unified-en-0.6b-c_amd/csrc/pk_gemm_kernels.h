@@ -41,7 +41,16 @@ struct GemmProblem {
     // Chains start from chain_bias[j] instead of beta*C (beta must be 0 and
     // bias null): a convolution whose sum starts from its bias (pk_conv2d).
     const float* chain_bias = nullptr;
+    // Device memory of kSplitWorkBytes or more that the split kernels may
+    // use for partial tiles (K split over workgroups), or null.  Calls that
+    // overlap on the device must not share it.
+    float* work = nullptr;
+    size_t work_bytes = 0;
 };
+
+// Partial tiles of one split-K launch: at most 256 workgroups of at most
+// 256 x 128 fp32 outputs each (32 MiB).
+constexpr size_t kSplitWorkBytes = (size_t)256 * 256 * 128 * 4;
 
 // Kernel tile configuration chosen for a shape (see choose_config_index).
 //   family 'R': rows on MFMA lanes, one MFMA = 64 rows x mfma columns,
@@ -91,7 +100,12 @@ hipError_t launch_smallm(const GemmProblem& p, hipStream_t stream);
 // weight rows (16-byte for fp32), no chain_bias.
 bool split_supports(const GemmProblem& p);
 // Launch on `stream`; hipErrorNotSupported if the shape is not handled.
+// With p.work, shapes with too few tiles to fill the CUs split K over
+// workgroups and sum the partial tiles in a second launch.
 hipError_t launch_split(const GemmProblem& p, hipStream_t stream);
+// Segments of K over workgroups that launch_split takes for a shape given
+// work_bytes of workspace (1: K is not split over workgroups).
+int split_k_segments(WeightKind kind, int M, int N, int K, size_t work_bytes);
 
 // Which shapes may leave the exact chains for a kernel within the 1e-3
 // contract: none; those the small-M kernels take (M <= 64); or those and

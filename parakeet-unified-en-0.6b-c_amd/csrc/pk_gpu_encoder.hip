@@ -70,6 +70,7 @@ struct RowGroup {
     int r0 = 0, R = 0, Tmax = 0, tab = 0, n = 0;
     std::map<int, std::pair<int, int>> by_len;
     size_t scores_off = 0;      // its attention's score rows (Tmax > kAttnMaxT) in e->scores
+    float* part = nullptr;      // its split-K partial tiles (fast numerics), or null
 };
 
 constexpr int kMels = 128;        // PK_N_MELS
@@ -145,6 +146,10 @@ struct pk_gpu_encoder {
     DevPreEncode pre;
     float *pre_a = nullptr, *pre_b = nullptr, *pre_x = nullptr;
     size_t pre_a_n = 0, pre_b_n = 0, pre_x_n = 0;
+    // fast numerics: kSplitWorkBytes of split-K partial tiles per row group
+    // (groups replay concurrently, so each has its own), grown on demand
+    float* part = nullptr;
+    size_t part_groups = 0;
 };
 
 namespace {
@@ -323,7 +328,8 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, size_t scores_n, 
 }
 
 int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float* bias,
-                Epilogue epi, hipStream_t s, pkgpu::Tolerance tol = pkgpu::TOL_NONE)
+                Epilogue epi, hipStream_t s, pkgpu::Tolerance tol = pkgpu::TOL_NONE,
+                float* work = nullptr)
 {
     GemmProblem p{};
     p.kind = w.kind;
@@ -342,6 +348,10 @@ int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float
     p.ldc = w.N;
     p.bias = bias;
     p.epi = epi;
+    if (work) {
+        p.work = work;
+        p.work_bytes = pkgpu::kSplitWorkBytes;
+    }
     return pkgpu::rt::gemm(p, s, tol);
 }
 
@@ -457,9 +467,10 @@ std::vector<Chunk> plan_chunks(int T, int C, int ov)
     return v;
 }
 
-// A weight GEMM of the block: M rows of A through w, with its epilogue.
+// A weight GEMM of the block: M rows of A through w, with its epilogue;
+// `work`: the row group's split-K partial tiles, or null.
 int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
-         const float* bias, Epilogue epi, hipStream_t s)
+         const float* bias, Epilogue epi, hipStream_t s, float* work = nullptr)
 {
     const double flops = 2.0 * M * w.N * w.K;
     double bytes = weight_bytes_of(w) + 4.0 * M * w.K + 4.0 * M * w.N;
@@ -467,7 +478,7 @@ int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
     if (epi == pkgpu::EPI_HALF_RESIDUAL || epi == pkgpu::EPI_RESIDUAL) bytes += 4.0 * M * w.N;
     const pkgpu::Tolerance tol = pkgpu::rt::tolerance_of(e->numerics);
     return timed(e, stage_of(w), flops, bytes, s,
-                 [&] { return gemm_launch(w, A, M, C, bias, epi, s, tol); });
+                 [&] { return gemm_launch(w, A, M, C, bias, epi, s, tol, work); });
 }
 
 int layer_norm(pk_gpu_encoder* e, const float* x, const float* g, const float* b, float* out, int R,
@@ -496,14 +507,14 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     auto ffn = [&](const float* gm, const float* be, const DevWeight& w1, const float* b1,
                    const DevWeight& w2, const float* b2) {
         int r = layer_norm(e, x, gm, be, ln, R, s);
-        if (!r) r = gemm(e, w1, ln, R, h, b1, pkgpu::EPI_SWISH, s);            // encoder.c:193-196
-        if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s);     // encoder.c:198-216
+        if (!r) r = gemm(e, w1, ln, R, h, b1, pkgpu::EPI_SWISH, s, g.part);            // encoder.c:193-196
+        if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s, g.part);     // encoder.c:198-216
         return r;
     };
     // self-attention (encoder.c:300-424)
     auto self_attention = [&]() {
         int rc = layer_norm(e, x, b.ln_sa_w, b.ln_sa_b, ln, R, s);
-        if (!rc) rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s);
+        if (!rc) rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s, g.part);
         if (rc) return rc;
         // every chunk of the group in one launch, each with its own length
         double flops = 0.0, bytes = 4.0 * (2 * Tmax - 1) * kD;   // the P rows read
@@ -524,13 +535,13 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         rc = timed(e, PK_GPU_STAGE_ATTENTION, flops, bytes, s, [&] {
             return check(pkgpu::launch_attention(a, g.n, s), "attention");
         });
-        if (!rc) rc = gemm(e, b.out, att, R, x, b.out_b, pkgpu::EPI_RESIDUAL, s);
+        if (!rc) rc = gemm(e, b.out, att, R, x, b.out_b, pkgpu::EPI_RESIDUAL, s, g.part);
         return rc;
     };
     // convolution module (encoder.c:430-476), time-major throughout
     auto convolution = [&]() {
         int rc = layer_norm(e, x, b.ln_conv_w, b.ln_conv_b, ln, R, s);
-        if (!rc) rc = gemm(e, b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s);
+        if (!rc) rc = gemm(e, b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s, g.part);
         if (!rc)
             rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 12.0 * R * kD, s, [&] {
                 return check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu");
@@ -547,7 +558,7 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 8.0 * R * kD, s, [&] {
             return check(pkgpu::launch_depthwise(d, g.n, s), "depthwise conv");
         });
-        if (!rc) rc = gemm(e, b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s);
+        if (!rc) rc = gemm(e, b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s, g.part);
         return rc;
     };
     for (int m = from; m < to; ++m) {
@@ -689,6 +700,25 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
     }
     int rc = workspace(e, (size_t)R, table.size(), scores_n, s);
     if (rc) return rc;
+    if (e->numerics == PK_GPU_NUMERICS_FAST) {
+        if (groups.size() > e->part_groups) {
+            // the graphs hold the old partial-tile pointers
+            wait_all(e);
+            drop_graphs(e);
+            if (e->part) (void)hipFree(e->part);
+            e->part = nullptr;
+            e->part_groups = 0;
+            if (hipMalloc(reinterpret_cast<void**>(&e->part), groups.size() * pkgpu::kSplitWorkBytes) !=
+                hipSuccess) {
+                e->part = nullptr;
+                return error(PK_GPU_ENOMEM, "split-K workspace of %zu bytes failed",
+                             groups.size() * pkgpu::kSplitWorkBytes);
+            }
+            e->part_groups = groups.size();
+        }
+        for (size_t gi = 0; gi < groups.size(); ++gi)
+            groups[gi].part = e->part + gi * (pkgpu::kSplitWorkBytes / sizeof(float));
+    }
     std::vector<int> want(2 * e->rows_cap, 0);
     std::copy(table.begin(), table.end(), want.begin());
     std::copy(lens.begin(), lens.end(), want.begin() + e->rows_cap);
@@ -1016,7 +1046,7 @@ int pk_gpu_encoder_run_dev(pk_gpu_encoder* enc, const float* dx, int T, int chun
 
 size_t pk_gpu_encoder_bytes(const pk_gpu_encoder* enc)
 {
-    return enc ? enc->weight_bytes + enc->ws_bytes : 0;
+    return enc ? enc->weight_bytes + enc->ws_bytes + enc->part_groups * pkgpu::kSplitWorkBytes : 0;
 }
 
 int pk_gpu_encoder_profile(pk_gpu_encoder* enc, int enable)
@@ -1054,6 +1084,7 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
     for (hipEvent_t ev : enc->event_pool) (void)hipEventDestroy(ev);
     free_workspace(enc);
     free_pre(enc);
+    if (enc->part) (void)hipFree(enc->part);
     for (void* p : enc->allocs) (void)hipFree(p);
     for (void* p : enc->pos_allocs) (void)hipFree(p);
     for (hipEvent_t ev : enc->side_done) (void)hipEventDestroy(ev);

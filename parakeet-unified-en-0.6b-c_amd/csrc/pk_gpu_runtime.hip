@@ -78,6 +78,9 @@ int default_numerics()
     return PK_GPU_NUMERICS_DEFAULT;
 }
 thread_local int t_numerics = default_numerics();
+// pk_gpu_set_workspace: partial tiles of this thread's split-K GEMMs
+thread_local float* t_work = nullptr;
+thread_local size_t t_work_bytes = 0;
 
 // Per-thread stream and staging buffers (slot 0: A, 1: B, 2: C, 3: scales).
 struct ThreadCtx {
@@ -273,7 +276,12 @@ int launch(const GemmProblem& p, hipStream_t s, bool tol_ok)
 {
     const pkgpu::Tolerance tol =
         tol_ok && t_force_cfg < 0 ? pkgpu::rt::tolerance_of(t_numerics) : pkgpu::TOL_NONE;
-    const hipError_t e = pkgpu::launch_gemm(p, s, t_force_cfg, tol);
+    GemmProblem q = p;
+    if (tol == pkgpu::TOL_ALL) {
+        q.work = t_work;
+        q.work_bytes = t_work_bytes;
+    }
+    const hipError_t e = pkgpu::launch_gemm(q, s, t_force_cfg, tol);
     if (e == hipErrorInvalidValue)
         return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
                     p.M, p.N, p.K);
@@ -722,6 +730,21 @@ int pk_gpu_set_numerics(int mode)
 }
 
 int pk_gpu_get_numerics(void) { return t_numerics; }
+
+int pk_gpu_set_workspace(void* dwork, size_t bytes)
+{
+    if (dwork && reinterpret_cast<uintptr_t>(dwork) % 16)
+        return fail(PK_GPU_EINVAL, "workspace %p is not 16-byte aligned", dwork);
+    t_work = dwork ? static_cast<float*>(dwork) : nullptr;
+    t_work_bytes = dwork ? bytes : 0;
+    return PK_GPU_OK;
+}
+
+int pk_gpu_split_k_segments(int M, int N, int K, int bits)
+{
+    const pkgpu::WeightKind kind = bits == 4 ? pkgpu::W_I4 : bits == 8 ? pkgpu::W_I8 : pkgpu::W_F32;
+    return pkgpu::split_k_segments(kind, M, N, K, t_work ? t_work_bytes : 0);
+}
 
 int pk_gpu_dequant_dev(int bits, int K, int N, const void* dB, int ldb, float scale,
                        const float* dscales, int unit_path, float* dout, void* stream)

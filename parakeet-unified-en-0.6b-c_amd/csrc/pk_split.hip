@@ -66,7 +66,11 @@ struct SpArgs {
     float* C; int ldc;
     const float* bias; int epi;
     uint32_t a_bytes, b_bytes, s_bytes;   // buffer extents (reads past them return 0)
-    int tiles_n, tiles;           // column tiles, all tiles
+    int tiles_n, tiles;           // column tiles, workgroups (tiles x segments)
+    // K split over workgroups: n_seg segments of the n_tiles tiles, partial
+    // tiles in work (n_seg = 1: none)
+    int n_seg, n_tiles;
+    float* work;
 };
 
 __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
@@ -284,14 +288,18 @@ __device__ inline void zero(v16f (&acc)[2][2])
 // buffers, loads PD chunks ahead.
 // Two waves per SIMD where the registers allow it without spills (the
 // others are held to one by their LDS anyway).
-template <int WK, int WM, int WN, int PD>
+// SK: workgroup u takes segment u / n_tiles of K (a contiguous run of its
+// chunks) for tile u % n_tiles and stores its raw sums to the tile's slot
+// of that segment in work, in register order (split_reduce finishes).
+template <int WK, int WM, int WN, int PD, bool SK>
 __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) void split_gemm(SpArgs p)
 {
     typedef Pipe<WK, 64 * WM, 64 * WN, 64 * WM * WN> L;
     __shared__ __attribute__((aligned(16))) __bf16 smem[2 * L::BUF];
 
-    const int t = tile_of(p);
-    if (t < 0) return;                               // padding workgroup (uniform)
+    const int u = tile_of(p);
+    if (u < 0) return;                               // padding workgroup (uniform)
+    const int t = SK ? u % p.n_tiles : u, seg = SK ? u / p.n_tiles : 0;
     const int m0 = (t / p.tiles_n) * (64 * WM), n0 = (t % p.tiles_n) * (64 * WN);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -303,13 +311,14 @@ __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) v
 
     // Loads run PD chunks ahead: before chunk c multiplies, the slots hold
     // chunks c + 1 .. c + PD.  The loop is unrolled by PD so that every slot
-    // index is a compile-time constant.
-    const int nc = p.K / KT;
+    // index is a compile-time constant.  Chunks [kc, kc + nc) of K.
+    const int kc = SK ? seg * (p.K / KT) / p.n_seg : 0;
+    const int nc = SK ? (seg + 1) * (p.K / KT) / p.n_seg - kc : p.K / KT;
 #pragma unroll
     for (int j = 0; j < PD; ++j)
-        if (j < nc) L::load(raw[j], p, rA, rB, rS, tid, m0, n0, KT * j);
+        if (j < nc) L::load(raw[j], p, rA, rB, rS, tid, m0, n0, KT * (kc + j));
     L::store(raw[0], smem, tid);
-    if (PD < nc) L::load(raw[0], p, rA, rB, rS, tid, m0, n0, KT * PD);
+    if (PD < nc) L::load(raw[0], p, rA, rB, rS, tid, m0, n0, KT * (kc + PD));
     __syncthreads();
     for (int c0 = 0; c0 < nc; c0 += PD) {
 #pragma unroll
@@ -321,10 +330,23 @@ __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) v
                 const int s = (j + 1) % PD;                  // constant once unrolled
                 // the other buffer: its last reader was chunk c - 1, before the barrier
                 L::store(raw[s], smem + ((c + 1) & 1) * L::BUF, tid);
-                if (c + 1 + PD < nc) L::load(raw[s], p, rA, rB, rS, tid, m0, n0, KT * (c + 1 + PD));
+                if (c + 1 + PD < nc) L::load(raw[s], p, rA, rB, rS, tid, m0, n0, KT * (kc + c + 1 + PD));
             }
             __syncthreads();
         }
+    }
+
+    if constexpr (SK) {
+        // slot (seg, t): wave-major, then block, register, lane (each store
+        // instruction writes 256 contiguous bytes)
+        float* w = p.work + ((size_t)seg * p.n_tiles + t) * (WM * WN * 4096) + (size_t)wave * 4096;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) w[((2 * r + c) * 16 + e) * 64 + lane] = acc[r][c][e];
+        return;
     }
 
     // C[m][n]: lane (l & 31) is the column, register e the row
@@ -341,6 +363,37 @@ __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) v
                 if (m < p.M) put(p, m, n, acc[r][c][e]);
             }
         }
+}
+
+// The second launch of a split-K GEMM: output i of tile t is the sum of
+// its n_seg partials in segment order, then alpha, beta, bias and the
+// epilogue (put).  Each thread takes outputs i .. i + 3 of a tile: four
+// lanes of one register, so four consecutive columns of one row (N is a
+// multiple of 32, so all four are in range or none).
+template <int WM, int WN>
+__global__ __launch_bounds__(256) void split_reduce(SpArgs p)
+{
+    constexpr int TS = WM * WN * 4096;               // floats per tile
+    constexpr int PER = TS / 1024;                   // workgroups per tile
+    const int t = blockIdx.x / PER, i = ((blockIdx.x % PER) * 256 + threadIdx.x) * 4;
+    const int wave = i >> 12, blk = (i >> 10) & 3, e = (i >> 6) & 15, l = i & 63;
+    const int m = (t / p.tiles_n) * (64 * WM) + 64 * (wave / WN) + 32 * (blk >> 1) + 8 * (e >> 2) +
+                  4 * (l >> 5) + (e & 3);
+    const int n = (t % p.tiles_n) * (64 * WN) + 64 * (wave % WN) + 32 * (blk & 1) + (l & 31);
+    if (m >= p.M || n >= p.N) return;
+    const float* w = p.work + (size_t)t * TS + i;
+    float4 sum = *reinterpret_cast<const float4*>(w);
+    for (int s = 1; s < p.n_seg; ++s) {
+        const float4 v = *reinterpret_cast<const float4*>(w + (size_t)s * p.n_tiles * TS);
+        sum.x = __fadd_rn(sum.x, v.x);
+        sum.y = __fadd_rn(sum.y, v.y);
+        sum.z = __fadd_rn(sum.z, v.z);
+        sum.w = __fadd_rn(sum.w, v.w);
+    }
+    put(p, m, n, sum.x);
+    put(p, m, n + 1, sum.y);
+    put(p, m, n + 2, sum.z);
+    put(p, m, n + 3, sum.w);
 }
 
 // Workgroups of KS waves own 64 x 64 tiles, wave w the chunks
@@ -423,36 +476,101 @@ SplitShape split_shape(int M, int N, int K)
     return SP_1x1;
 }
 
-unsigned padded_grid(SpArgs& a, int bm, int bn)
+// K split over workgroups, for shapes with too few 128 x 128 tiles to give
+// every CU one (split_shape's SP_2x1, SP_K4, SP_1x1): 256 x 128 tiles, or
+// 128 x 128 where 256-row tiles would pad more than 10% more rows, and as
+// many segments of at least kMinSegChunks chunks as keep the workgroups
+// within one per CU.  The partial tiles then take n_seg x tiles x tile
+// floats <= 256 x 256 x 128 x 4 bytes = kSplitWorkBytes.
+// The second launch moves every partial through memory (5-10 us at 1656
+// rows), so int8 and int4 weights split K only from K = 2048: at 1656 x
+// 1024 x 1024 (int8) and 375 x 4096 x 1024 (int4) their 64 x 64 tiles with K
+// over 4 waves were faster (26.0 and 30.1 us against 29.9 and 33.4), while
+// fp32's, with a third of their loads in flight, lost to split-K at every
+// measured shape (46.9 against 31.1 us at 500 x 4096 x 1024).
+constexpr int kMinSegChunks = 4;
+
+struct SplitPlan {
+    SplitShape shape;
+    int n_seg;
+};
+
+// PK_GPU_SPLIT_K: 0 never splits K over workgroups, 2 splits every shape the
+// plan allows regardless of weight format and K, anything else (the
+// default, 1) follows the rule above.  A tuning switch, read once.
+int split_k_mode()
+{
+    static const int mode = [] {
+        const char* v = getenv("PK_GPU_SPLIT_K");
+        const int m = v ? atoi(v) : 1;
+        return m >= 0 && m <= 2 ? m : 1;
+    }();
+    return mode;
+}
+
+SplitPlan split_plan(WeightKind kind, int M, int N, int K, size_t work_bytes)
+{
+    const SplitShape s = split_shape(M, N, K);
+    const int mode = split_k_mode();
+    if (s == SP_4x2 || s == SP_2x2 || work_bytes < kSplitWorkBytes || mode == 0) return {s, 1};
+    if (mode == 1 && kind != W_F32 && K < 2048) return {s, 1};
+    const long long rows256 = (M + 255LL) / 256 * 256, rows128 = (M + 127LL) / 128 * 128;
+    const bool wide = rows256 * 10 <= rows128 * 11;
+    const int bm = wide ? 256 : 128;
+    const long long tiles = (long long)((M + bm - 1) / bm) * ((N + 127) / 128);
+    const long long seg = std::min<long long>(256 / tiles, (K / KT) / kMinSegChunks);
+    if (seg < 2) return {s, 1};
+    return {wide ? SP_4x2 : SP_2x2, (int)seg};
+}
+
+unsigned padded_grid(SpArgs& a, int bm, int bn, int n_seg = 1)
 {
     a.tiles_n = (a.N + bn - 1) / bn;
-    a.tiles = ((a.M + bm - 1) / bm) * a.tiles_n;
+    a.n_tiles = ((a.M + bm - 1) / bm) * a.tiles_n;
+    a.n_seg = n_seg;
+    a.tiles = a.n_tiles * n_seg;
     return (unsigned)(((a.tiles + kXcd - 1) / kXcd) * kXcd);
 }
 
 template <int WK>
-hipError_t launch_kind(SpArgs a, SplitShape s, hipStream_t st)
+hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
 {
     // Chunks of loads in flight, as many as fit two waves per SIMD without
     // spills: a lane holds 16 A bytes per 64 rows of the tile and chunk, plus
     // its weight units (fp32's take 4 times int8's registers).
     constexpr int PD22 = WK == W_F32 ? 2 : 3, PD21 = 2, PDK = WK == W_F32 ? 1 : 2, PD42 = 2;
-    switch (s) {
+    if (plan.n_seg > 1) {
+        const bool wide = plan.shape == SP_4x2;
+        const unsigned grid = padded_grid(a, wide ? 256 : 128, 128, plan.n_seg);
+        if (wide)
+            hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, true>), dim3(grid), dim3(512), 0, st, a);
+        else
+            hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22, true>), dim3(grid), dim3(256), 0, st, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const unsigned blocks = (unsigned)a.n_tiles * (wide ? 8 * 4096 / 1024 : 4 * 4096 / 1024);
+        if (wide)
+            hipLaunchKernelGGL((split_reduce<4, 2>), dim3(blocks), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((split_reduce<2, 2>), dim3(blocks), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
+    switch (plan.shape) {
     case SP_4x2:
-        hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42>), dim3(padded_grid(a, 256, 128)), dim3(512), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, false>), dim3(padded_grid(a, 256, 128)), dim3(512), 0, st, a);
         break;
     case SP_2x2:
-        hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22>), dim3(padded_grid(a, 128, 128)), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22, false>), dim3(padded_grid(a, 128, 128)), dim3(256), 0, st, a);
         break;
     case SP_2x1:
-        hipLaunchKernelGGL((split_gemm<WK, 2, 1, PD21>), dim3(padded_grid(a, 128, 64)), dim3(128), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 2, 1, PD21, false>), dim3(padded_grid(a, 128, 64)), dim3(128), 0, st, a);
         break;
     case SP_K4:
         hipLaunchKernelGGL((split_gemm_k<WK, kKSplit, PDK>), dim3(padded_grid(a, 64, 64)), dim3(64 * kKSplit),
                            0, st, a);
         break;
     default:
-        hipLaunchKernelGGL((split_gemm<WK, 1, 1, 2>), dim3(padded_grid(a, 64, 64)), dim3(64), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 1, 1, 2, false>), dim3(padded_grid(a, 64, 64)), dim3(64), 0, st, a);
         break;
     }
     return hipGetLastError();
@@ -498,12 +616,19 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     a.s_bytes = (uint32_t)s_ext;
     // 64 x 64 tiles at most: their count must fit the launch's int arithmetic
     if ((long long)((p.M + 63) / 64) * ((p.N + 63) / 64) > (1LL << 30)) return hipErrorNotSupported;
-    const SplitShape s = split_shape(p.M, p.N, p.K);
+    const SplitPlan plan = split_plan(p.kind, p.M, p.N, p.K, p.work ? p.work_bytes : 0);
+    a.work = p.work;
     switch (p.kind) {
-    case W_I8: return launch_kind<W_I8>(a, s, st);
-    case W_I4: return launch_kind<W_I4>(a, s, st);
-    default:   return launch_kind<W_F32>(a, s, st);
+    case W_I8: return launch_kind<W_I8>(a, plan, st);
+    case W_I4: return launch_kind<W_I4>(a, plan, st);
+    default:   return launch_kind<W_F32>(a, plan, st);
     }
+}
+
+int split_k_segments(WeightKind kind, int M, int N, int K, size_t work_bytes)
+{
+    if (M < 1 || N < 1 || K < KT) return 1;
+    return split_plan(kind, M, N, K, work_bytes).n_seg;
 }
 
 }  // namespace pkgpu

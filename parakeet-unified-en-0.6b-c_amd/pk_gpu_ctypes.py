@@ -49,6 +49,8 @@ _PROTOS = {
     "pk_gpu_get_numerics": (_i, []),
     "pk_gpu_uses_small_m": (_i, [_i, _i, _i, _i]),
     "pk_gpu_uses_split": (_i, [_i, _i, _i, _i]),
+    "pk_gpu_set_workspace": (_i, [_p, _sz]),
+    "pk_gpu_split_k_segments": (_i, [_i, _i, _i, _i]),
     "pk_gpu_force_small_tile": (_i, [_i, _i]),
     "pk_gpu_dequant_dev": (_i, [_i, _i, _i, _p, _i, _f, _p, _i, _p, _p]),
     "pk_gpu_layer_norm_dev": (_i, [_p, _p, _p, _p, _i, _i, _p]),
@@ -77,6 +79,7 @@ _PROTOS = {
 EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL, EPI_RESIDUAL = 0, 1, 2, 3
 NUMERICS_DEFAULT, NUMERICS_EXACT, NUMERICS_FAST = 0, 1, 2
 NOALLOC_BYTES = 64 << 20          # PK_GPU_NOALLOC_BYTES
+SPLIT_WORKSPACE_BYTES = 32 << 20  # PK_GPU_SPLIT_WORKSPACE_BYTES
 
 
 class Weight(ctypes.Structure):

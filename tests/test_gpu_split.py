@@ -14,7 +14,13 @@ group, nibble or output position fails them.  Each of the five launch shapes
 waves and summed in LDS, also with chunk counts that do not divide by 4;
 64 x 64 on one wave) is taken by some of the shapes below; rows and columns
 past M and N, alpha, beta and the fused epilogues are covered, and results
-are deterministic."""
+are deterministic.
+
+With a workspace (pk_gpu_set_workspace), shapes with fewer 128 x 128 tiles
+than CUs split K over workgroups: 256 x 128 or 128 x 128 tiles, partial tiles
+summed in segment order by a second launch.  The same bounds hold there, on
+shapes with 2 to 16 segments, with chunk counts that do not divide evenly, and
+with partial row and column tiles."""
 import numpy as np
 import pytest
 
@@ -145,3 +151,99 @@ def test_split_shapes_outside_rules_stay_exact(dev):
     A, W, extra, _ = make("i8", M, N, K, "spx")
     Z = np.zeros((M, N), np.float32)
     assert bits_equal(fast(dev, "i8", A, W, extra, Z), oracle("i8", A, W, extra, Z))
+
+
+#                          segments of K with a 32 MiB workspace
+SPLIT_K = [("i4", 1656, 1024, 4096, 4),    # feed-forward down of a 1656-row group
+           ("i8", 1656, 1024, 2048, 4),
+           ("f32", 1656, 2048, 1024, 2),   # pointwise 1
+           ("f32", 1656, 1024, 1024, 4),   # pointwise 2
+           ("i4", 375, 1024, 4096, 10),    # 128 x 128 tiles (256-row tiles pad too much)
+           ("i4", 300, 2048, 2048, 5),
+           ("f32", 500, 1024, 4096, 16),
+           ("f32", 500, 4096, 1024, 4),
+           ("i8", 300, 512, 2080, 16),     # 65 chunks over 16 segments
+           ("i4", 97, 96, 2336, 18),       # one partial tile, 73 chunks
+           ("f32", 130, 256, 320, 2)]
+
+
+class Workspace:
+    """pk_gpu_set_workspace on this thread for the duration of a with-block."""
+
+    def __init__(self, dev, nbytes=pk.SPLIT_WORKSPACE_BYTES):
+        import torch
+        self.buf = torch.empty(nbytes // 4, dtype=torch.float32, device=dev.dev)
+        self.nbytes = nbytes
+
+    def __enter__(self):
+        pk.call("pk_gpu_set_workspace", self.buf.data_ptr(), self.nbytes)
+        return self
+
+    def __exit__(self, *exc):
+        pk.call("pk_gpu_set_workspace", None, 0)
+
+
+@pytest.mark.parametrize("kind,M,N,K,segs", SPLIT_K)
+def test_split_k_within_tolerance(dev, kind, M, N, K, segs):
+    lib = pk.load()
+    A, W, extra, _ = make(kind, M, N, K, f"spk.{kind}.{M}.{N}.{K}")
+    Z = np.zeros((M, N), np.float32)
+    want = oracle(kind, A, W, extra, Z)
+    assert lib.pk_gpu_split_k_segments(M, N, K, bits_of(kind)) == 1
+    with Workspace(dev):
+        assert lib.pk_gpu_split_k_segments(M, N, K, bits_of(kind)) == segs
+        got = fast(dev, kind, A, W, extra, Z)
+        again = fast(dev, kind, A, W, extra, Z)
+    e = rel_err(got, want)
+    print(f"{kind} {M}x{N}x{K}, {segs} segments: max|C - R| / max|R| = {e:.3g}", flush=True)
+    assert e <= CONTRACT and e <= MEASURED, e
+    assert bits_equal(again, got), "not deterministic"
+
+
+@pytest.mark.parametrize("kind", ["i8", "i4", "f32"])
+def test_split_k_alpha_beta_and_epilogues(dev, kind):
+    """alpha, beta, bias and every epilogue are applied once, after the
+    partial tiles are summed (16 segments of 256 x 128 tiles here)."""
+    lib = pk.load()
+    M, N, K = 200, 256, 2048
+    A, W, extra, C0 = make(kind, M, N, K, f"spkepi.{kind}")
+    bias = po.normal((N,), 0.0, 0.02, po.seed(0x5EED3000, f"spkepi.{kind}.b"))
+    Z = np.zeros((M, N), np.float32)
+    plain = oracle(kind, A, W, extra, Z)
+    biased = (plain + bias[None, :]).astype(np.float32)
+    cases = {
+        pk.EPI_NONE: biased,
+        pk.EPI_SWISH: po.swish(biased),
+        pk.EPI_HALF_RESIDUAL: (C0 + np.float32(0.5) * biased).astype(np.float32),
+        pk.EPI_RESIDUAL: (C0 + biased).astype(np.float32),
+        4: np.maximum(biased, 0.0),                                   # EPI_RELU
+    }
+    with Workspace(dev):
+        assert lib.pk_gpu_split_k_segments(M, N, K, bits_of(kind)) == 16
+        for alpha, beta in [(0.75, 0.5), (1.0, 1.0), (-2.0, 0.0)]:
+            want = oracle(kind, A, W, extra, C0, alpha, beta)
+            assert rel_err(fast(dev, kind, A, W, extra, C0, alpha, beta), want) <= MEASURED, (alpha, beta)
+        for epi, want in cases.items():
+            C_in = C0 if epi in (pk.EPI_HALF_RESIDUAL, pk.EPI_RESIDUAL) else Z
+            got = fast(dev, kind, A, W, extra, C_in, 1.0, 0.0, bias=bias, epi=epi)
+            assert rel_err(got, want) <= MEASURED, f"epilogue {epi}"
+
+
+def test_split_k_workspace_rules(dev):
+    """A workspace smaller than PK_GPU_SPLIT_WORKSPACE_BYTES is not used (the
+    GEMM still runs, without split-K), a misaligned one is refused, and
+    DEFAULT numerics never touch it."""
+    lib = pk.load()
+    M, N, K = 375, 1024, 4096
+    A, W, extra, _ = make("i4", M, N, K, "spkrule")
+    Z = np.zeros((M, N), np.float32)
+    want = oracle("i4", A, W, extra, Z)
+    with Workspace(dev, pk.SPLIT_WORKSPACE_BYTES - 4096) as ws:
+        assert lib.pk_gpu_split_k_segments(M, N, K, 4) == 1
+        assert rel_err(fast(dev, "i4", A, W, extra, Z), want) <= MEASURED
+        assert lib.pk_gpu_set_workspace(ws.buf.data_ptr() + 4, pk.SPLIT_WORKSPACE_BYTES) == -1
+    with Workspace(dev) as ws:
+        ws.buf.fill_(float("nan"))
+        got = dev.gemm("i4", A, W, Z, scales=extra, exact=False)
+        assert bits_equal(got, want)                 # M > 64: exact chains
+        assert bool(ws.buf.isnan().all())            # untouched

@@ -130,3 +130,42 @@ def test_null_device_operands_are_rejected():
     assert lib.pk_gpu_gemm_i4_dev(4, 32, 8, 1.0, C.ctypes.data, 8, C.ctypes.data, None, 16, 0.0,
                                   C.ctypes.data, 32, None) == -1
     assert b"NULL" in lib.pk_gpu_last_error()
+
+
+# K segments over workgroups that the split kernels take (fast numerics) with
+# a PK_GPU_SPLIT_WORKSPACE_BYTES workspace: shapes with fewer 128 x 128 tiles
+# than the 256 CUs, int8 and int4 weights from K = 2048 only, 256 x 128 tiles
+# unless 256-row tiles pad more than 10% more rows, as many segments of at
+# least 4 chunks as keep the workgroups within 256.
+SPLIT_K_PLANS = [
+    (4, 1656, 1024, 4096, 4),      # 7 x 8 tiles of 256 x 128
+    (8, 1656, 1024, 1024, 1),      # int8 below K = 2048
+    (8, 1656, 1024, 2048, 4),
+    (32, 1656, 1024, 1024, 4),     # fp32 at any K
+    (32, 1656, 2048, 1024, 2),     # 7 x 16
+    (8, 1656, 3072, 4096, 1),      # 13 x 24 tiles of 128 x 128: no split
+    (4, 1656, 4096, 4096, 1),
+    (4, 375, 1024, 4096, 10),      # 3 x 8 tiles of 128 x 128
+    (4, 375, 4096, 1024, 1),       # int4 below K = 2048
+    (32, 375, 4096, 1024, 2),      # 3 x 32 tiles of 128 x 128 (256-row tiles would pad 36%)
+    (32, 500, 1024, 4096, 16),     # 2 x 8 tiles of 256 x 128
+    (4, 3312, 1024, 4096, 2),      # 26 x 8 = 208 tiles of 128 x 128; 13 x 8 of 256 x 128
+    (32, 200, 256, 2048, 16),
+    (32, 97, 96, 96, 1),           # 3 chunks: fewer than two segments of 4
+]
+
+
+@pytest.mark.parametrize("bits,M,N,K,segs", SPLIT_K_PLANS)
+def test_split_k_plans(bits, M, N, K, segs):
+    """Host-side planning only: the pointer is never dereferenced."""
+    lib = pk.load()
+    assert lib.pk_gpu_split_k_segments(M, N, K, bits) == 1     # no workspace yet
+    fake = 1 << 20
+    assert lib.pk_gpu_set_workspace(fake, pk.SPLIT_WORKSPACE_BYTES) == 0
+    try:
+        assert lib.pk_gpu_split_k_segments(M, N, K, bits) == segs
+        assert lib.pk_gpu_set_workspace(fake, pk.SPLIT_WORKSPACE_BYTES - 1) == 0
+        assert lib.pk_gpu_split_k_segments(M, N, K, bits) == 1     # too small: unused
+        assert lib.pk_gpu_set_workspace(fake + 4, pk.SPLIT_WORKSPACE_BYTES) == -1
+    finally:
+        assert lib.pk_gpu_set_workspace(None, 0) == 0
