@@ -32,9 +32,14 @@
 //                 workgroup, else 64 x 64) over all of K, two LDS buffers;
 //   split_gemm_k  for shapes with too few such tiles (N = 1024 at 1656 rows):
 //                 64 x 64 tiles, K split over 4 waves with an LDS slab each,
-//                 the 4 partial tiles summed in LDS in wave order.
-// Every workgroup sums its own tile in a fixed order, so results are
-// deterministic, and no memory beyond the operands is used.
+//                 the 4 partial tiles summed in LDS in wave order;
+//   split-K       where the caller gives a workspace (GemmProblem::work),
+//                 those shapes instead run 256 x 128 or 128 x 128 tiles with
+//                 K split over workgroups (split_gemm<..., SK = true>), each
+//                 storing its raw partial tile, and split_reduce sums each
+//                 tile's partials in segment order before the epilogue.
+// Every sum has a fixed order, so results are deterministic; without a
+// workspace no memory beyond the operands is used.
 #include "pk_gemm_kernels.h"
 #include "pk_device_math.h"
 
@@ -320,21 +325,28 @@ __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) v
     L::store(raw[0], smem, tid);
     if (PD < nc) L::load(raw[0], p, rA, rB, rS, tid, m0, n0, KT * (kc + PD));
     __syncthreads();
-    for (int c0 = 0; c0 < nc; c0 += PD) {
-#pragma unroll
-        for (int j = 0; j < PD; ++j) {
-            const int c = c0 + j;
-            if (c >= nc) break;
-            L::multiply(smem + (c & 1) * L::BUF, acc, lane, 64 * wm, 64 * wn);
-            if (c + 1 < nc) {
-                const int s = (j + 1) % PD;                  // constant once unrolled
-                // the other buffer: its last reader was chunk c - 1, before the barrier
-                L::store(raw[s], smem + ((c + 1) & 1) * L::BUF, tid);
-                if (c + 1 + PD < nc) L::load(raw[s], p, rA, rB, rS, tid, m0, n0, KT * (kc + c + 1 + PD));
-            }
-            __syncthreads();
+    // chunk c, whose loads sit in slot j % PD (j constant once unrolled)
+    auto step = [&](int c, int j) {
+        L::multiply(smem + (c & 1) * L::BUF, acc, lane, 64 * wm, 64 * wn);
+        if (c + 1 < nc) {
+            const int s = (j + 1) % PD;
+            // the other buffer: its last reader was chunk c - 1, before the barrier
+            L::store(raw[s], smem + ((c + 1) & 1) * L::BUF, tid);
+            if (c + 1 + PD < nc) L::load(raw[s], p, rA, rB, rS, tid, m0, n0, KT * (kc + c + 1 + PD));
         }
+        __syncthreads();
+    };
+    // Whole rounds of PD chunks without an exit inside: an exit between the
+    // multiplies made the compiler copy every accumulator at the end of each
+    // round, after waiting for the matrix cores.
+    int c0 = 0;
+    for (; c0 + PD <= nc; c0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; ++j) step(c0 + j, j);
     }
+#pragma unroll
+    for (int j = 0; j < PD - 1; ++j)
+        if (c0 + j < nc) step(c0 + j, j);
 
     if constexpr (SK) {
         // slot (seg, t): wave-major, then block, register, lane (each store
@@ -422,6 +434,8 @@ __global__ __launch_bounds__(64 * KS, 2) void split_gemm_k(SpArgs p)
 #pragma unroll
     for (int j = 0; j < PD; ++j)
         if (s0 + j < s1) L::load(raw[j], p, rA, rB, rS, lane, m0, n0, KT * (s0 + j));
+    // (here the exit inside a round costs no accumulator copies, and the
+    // split_gemm form of the loop spills)
     for (int c0 = s0; c0 < s1; c0 += PD) {
 #pragma unroll
         for (int j = 0; j < PD; ++j) {
@@ -570,7 +584,8 @@ hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
                            0, st, a);
         break;
     default:
-        hipLaunchKernelGGL((split_gemm<WK, 1, 1, 2, false>), dim3(padded_grid(a, 64, 64)), dim3(64), 0, st, a);
+        // K < 256 here: one chunk ahead is enough, and int4 spills with two
+        hipLaunchKernelGGL((split_gemm<WK, 1, 1, 1, false>), dim3(padded_grid(a, 64, 64)), dim3(64), 0, st, a);
         break;
     }
     return hipGetLastError();
