@@ -832,37 +832,42 @@ void chain_gemm_xs(KArgs p)
     // lane BS*t + i reads A[row i][k + t]
     const int a_off = (lane / BS) * AS + wrow + (lane % BS);
     const int b_off = wn * 64 + bpos<WK, BN>(lane);
-    const int nchunks = (p.K + KT - 1) / KT;
-    for (int c = 0; c < nchunks; ++c) {
+    // Whole chunks, then the partial last one (if any) after the loop: a
+    // partial-chunk branch inside the loop made the compiler keep the
+    // accumulators in two register sets and copy them on every chunk.
+    // The MFMAs and their order are the same either way.
+    const int nfull = p.K / KT;
+    for (int c = 0; c < nfull; ++c) {
         const float* as = &As[c & 1][a_off];
         const float* bs = &Bs[c & 1][b_off];
-        const int kn = min(KT, p.K - c * KT);
-        if (kn == KT) {
-            float a[2][R], b[2][NB];
+        float a[2][R], b[2][NB];
 #pragma unroll
-            for (int g = 0; g < R; ++g) a[0][g] = as[g * BS];
+        for (int g = 0; g < R; ++g) a[0][g] = as[g * BS];
 #pragma unroll
-            for (int t = 0; t < NB; ++t) b[0][t] = bs[t * BN];
+        for (int t = 0; t < NB; ++t) b[0][t] = bs[t * BN];
 #pragma unroll
-            for (int kb = 0; kb < NBLK; ++kb) {
-                const int cur = kb & 1;
-                if (kb + 1 < NBLK) {
+        for (int kb = 0; kb < NBLK; ++kb) {
+            const int cur = kb & 1;
+            if (kb + 1 < NBLK) {
 #pragma unroll
-                    for (int g = 0; g < R; ++g) a[cur ^ 1][g] = as[(kb + 1) * NB * AS + g * BS];
+                for (int g = 0; g < R; ++g) a[cur ^ 1][g] = as[(kb + 1) * NB * AS + g * BS];
 #pragma unroll
-                    for (int t = 0; t < NB; ++t) b[cur ^ 1][t] = bs[((kb + 1) * NB + t) * BN];
-                }
-                x_steps<T, R, 0>(a[cur], b[cur], acc);
+                for (int t = 0; t < NB; ++t) b[cur ^ 1][t] = bs[((kb + 1) * NB + t) * BN];
             }
-        } else {
-            for (int kb = 0; kb < kn; kb += NB) {
-                float a[R], b[NB];
+            x_steps<T, R, 0>(a[cur], b[cur], acc);
+        }
+        __syncthreads();
+    }
+    if (const int kn = p.K - nfull * KT; kn > 0) {
+        const float* as = &As[nfull & 1][a_off];
+        const float* bs = &Bs[nfull & 1][b_off];
+        for (int kb = 0; kb < kn; kb += NB) {
+            float a[R], b[NB];
 #pragma unroll
-                for (int g = 0; g < R; ++g) a[g] = as[kb * AS + g * BS];
+            for (int g = 0; g < R; ++g) a[g] = as[kb * AS + g * BS];
 #pragma unroll
-                for (int t = 0; t < NB; ++t) b[t] = bs[(kb + t) * BN];
-                x_steps_n<T, R, 0>(a, b, acc, kn - kb);
-            }
+            for (int t = 0; t < NB; ++t) b[t] = bs[(kb + t) * BN];
+            x_steps_n<T, R, 0>(a, b, acc, kn - kb);
         }
         __syncthreads();
     }
