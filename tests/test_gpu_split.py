@@ -247,3 +247,24 @@ def test_split_k_workspace_rules(dev):
         got = dev.gemm("i4", A, W, Z, scales=extra, exact=False)
         assert bits_equal(got, want)                 # M > 64: exact chains
         assert bool(ws.buf.isnan().all())            # untouched
+
+
+def test_split_swish_epilogue_against_its_input(dev):
+    """The split kernels' Swish epilogue against the oracle's pk_swish
+    applied to the same GEMM's un-activated output (the same sums, so the
+    difference is the epilogue's alone).  The kernels use the reference's
+    own form (its exp polynomial and the IEEE division), so the two agree to
+    rounding; the bound would still hold for any Swish within 5e-6 relative
+    (a hardware exp2 / reciprocal form measured about 3e-7), and a wrong sign
+    or scale in the exponent fails it by orders of magnitude."""
+    M, N, K = 300, 512, 256
+    A, W, extra, _ = make("i4", M, N, K, "spswish")
+    A = (A * np.float32(4.0)).astype(np.float32)                 # outputs over about +-30
+    bias = po.normal((N,), 0.0, 0.5, po.seed(0x5EED3000, "spswish.b"))
+    Z = np.zeros((M, N), np.float32)
+    plain = fast(dev, "i4", A, W, extra, Z, 1.0, 0.0, bias=bias, epi=pk.EPI_NONE)
+    act = fast(dev, "i4", A, W, extra, Z, 1.0, 0.0, bias=bias, epi=pk.EPI_SWISH)
+    want = po.swish(plain).astype(np.float64)
+    err = np.abs(act.astype(np.float64) - want)
+    assert float(np.abs(plain).max()) > 8.0                      # both tails exercised
+    assert float((err / np.maximum(np.abs(want), 1e-30)).max()) <= 5e-6, float(err.max())
