@@ -121,3 +121,40 @@ def test_numerics_argument_checks(model):
         assert lib.pk_gpu_encoder_set_numerics(enc, pk.NUMERICS_FAST) == 0
     finally:
         lib.pk_gpu_encoder_destroy(enc)
+
+
+def test_fast_mode_row_group_changes(model):
+    """PK_GPU_NUMERICS_FAST with split-K: the encoder holds a partial-tile
+    workspace per row group.  Going from two groups to three grows it (the
+    captured graphs, which hold its addresses, are dropped and recaptured)
+    and going back reuses it: every run stays within 1e-3 of the oracle, and
+    the two-group runs before and after are bit-identical."""
+    import torch
+    T, chunk, ov = 300, 64, 8                     # 5 chunks of up to 80 rows
+    x = bench.enc_rng(0xFEA7, 301).standard_normal((T, bench.D)).astype(np.float32)
+    want = po.encoder(model.blocks, bench.N_BLOCKS, model.pe, bench.PE_CENTER, x, chunk, ov)
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(model.blocks, ctypes.c_void_p),
+            bench.N_BLOCKS, model.pe.ctypes.data, bench.PE_ROWS, bench.PE_CENTER)
+    try:
+        lib = pk.load()
+        pk.call("pk_gpu_encoder_set_numerics", enc, pk.NUMERICS_FAST)
+        dev = torch.device("cuda:0")
+        dx = torch.from_numpy(x).to(dev)
+        outs = {}
+        for step, groups in enumerate((2, 3, 2)):
+            pk.call("pk_gpu_encoder_set_groups", enc, groups)
+            dout = torch.full_like(dx, float("nan"))
+            for _ in range(2):                    # capture, then replay
+                pk.call("pk_gpu_encoder_run_dev", enc, dx.data_ptr(), T, chunk, ov, dout.data_ptr(),
+                        torch.cuda.current_stream(dev).cuda_stream)
+            torch.cuda.synchronize(dev)
+            got = dout.cpu().numpy()
+            e = rel_dev(got, want)
+            print(f"groups {groups}: fast max |out - oracle| / max |oracle| = {e:.3g}, "
+                  f"device bytes {lib.pk_gpu_encoder_bytes(enc)}", flush=True)
+            assert e <= TOL, (groups, e)
+            outs[step] = got
+        assert bits_equal(outs[2], outs[0]), describe_mismatch(outs[2], outs[0])
+    finally:
+        pk.load().pk_gpu_encoder_destroy(enc)
