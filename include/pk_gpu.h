@@ -397,8 +397,11 @@ int pk_gpu_encoder_set_group_lag(pk_gpu_encoder *enc, int modules);
  * within the same bound; over 24 blocks the deviations compound, so the
  * output is not bit-identical at any length.  In this mode a run also holds
  * PK_GPU_SPLIT_WORKSPACE_BYTES per row group for the split kernels' partial
- * tiles (counted by pk_gpu_encoder_bytes).  Captured graphs are kept per
- * mode.  No counterpart in the reference.  get returns the mode, -1 for
+ * tiles (counted by pk_gpu_encoder_bytes), and the LayerNorms that feed a
+ * GEMM write their output already split into the bf16 halves those kernels
+ * multiply (the same bits as splitting it in the GEMM; PK_GPU_PRESPLIT=0 in
+ * the environment when the encoder is created turns that off).  Captured
+ * graphs are kept per mode.  No counterpart in the reference.  get returns the mode, -1 for
  * NULL. */
 int pk_gpu_encoder_set_numerics(pk_gpu_encoder *enc, int mode);
 int pk_gpu_encoder_get_numerics(pk_gpu_encoder *enc);

@@ -70,6 +70,11 @@ struct DwArgs {
 
 hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const float* beta,
                              float* out, int ldo, int rows, int D, hipStream_t s);
+// The same LayerNorm with its output pre-split for the split GEMM kernels
+// (GemmProblem::a_presplit): the fp32 row's bytes hold, per group of 8
+// columns, the 8 bf16 hi then the 8 bf16 lo halves.
+hipError_t launch_layer_norm_split(const float* x, int ldx, const float* gamma, const float* beta,
+                                   float* out, int ldo, int rows, int D, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s);
 hipError_t launch_glu(const float* in, int ldi, float* out, int ldo, int rows, int D, hipStream_t s);
 hipError_t launch_depthwise(const DwArgs& a, int n_chunks, hipStream_t s);

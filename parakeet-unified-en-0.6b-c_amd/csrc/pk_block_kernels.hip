@@ -58,8 +58,12 @@ __device__ inline float hsum8(const float (&p)[8])
 // 16-byte group: each lane then needs 4 of gamma's and beta's groups
 // (loaded first, with the rows) instead of 2 x NPL scattered values.
 // In place (out == x) is safe: every row is read before any is written.
+// SPLIT: each output o goes out split as the split GEMM kernels multiply it
+// (hi = bf16(o), lo = bf16(o - hi), both to nearest: the split those kernels
+// would make of the fp32 output), in their pre-split layout: per row and
+// group of 8 columns, the 8 hi then the 8 lo, in the fp32 row's bytes.
 
-template <int NPL>
+template <int NPL, bool SPLIT>
 __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta,
@@ -127,7 +131,19 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
             o.y = __fmaf_rn(__fmul_rn(d.y, s), g4[j].y, b4[j].y);
             o.z = __fmaf_rn(__fmul_rn(d.z, s), g4[j].z, b4[j].z);
             o.w = __fmaf_rn(__fmul_rn(d.w, s), g4[j].w, b4[j].w);
-            *reinterpret_cast<float4*>(out + (size_t)(row0 + rr) * ldo + 4 * c4) = o;
+            if constexpr (SPLIT) {
+                uint32_t h0, l0, h1, l1;
+                split_bf16x2(o.x, o.y, h0, l0);
+                split_bf16x2(o.z, o.w, h1, l1);
+                // columns 4 c4 .. +3: half (c4 & 1) of group c4 / 2, whose 16
+                // bf16 values occupy the group's 8 floats
+                unsigned short* g8 = reinterpret_cast<unsigned short*>(
+                    out + (size_t)(row0 + rr) * ldo + 8 * (c4 >> 1));
+                *reinterpret_cast<uint2*>(g8 + 4 * (c4 & 1)) = make_uint2(h0, h1);
+                *reinterpret_cast<uint2*>(g8 + 8 + 4 * (c4 & 1)) = make_uint2(l0, l1);
+            } else {
+                *reinterpret_cast<float4*>(out + (size_t)(row0 + rr) * ldo + 4 * c4) = o;
+            }
         }
     }
 }
@@ -731,8 +747,23 @@ hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const 
          reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 ||
         ldx % 4 || ldo % 4)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(layer_norm_rows<128>, dim3((rows + 7) / 8), dim3(64), 0, s, x, ldx, gamma,
-                       beta, out, ldo, rows);
+    hipLaunchKernelGGL((layer_norm_rows<128, false>), dim3((rows + 7) / 8), dim3(64), 0, s, x, ldx,
+                       gamma, beta, out, ldo, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_layer_norm_split(const float* x, int ldx, const float* gamma, const float* beta,
+                                   float* out, int ldo, int rows, int D, hipStream_t s)
+{
+    if (rows <= 0) return hipSuccess;
+    if (D != 1024) return hipErrorInvalidValue;   // d_model (PK_D_MODEL)
+    // 16-byte loads of x, gamma and beta; 8-byte stores into 32-byte groups
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+         reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 ||
+        ldx % 4 || ldo % 8)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((layer_norm_rows<128, true>), dim3((rows + 7) / 8), dim3(64), 0, s, x, ldx,
+                       gamma, beta, out, ldo, rows);
     return hipGetLastError();
 }
 

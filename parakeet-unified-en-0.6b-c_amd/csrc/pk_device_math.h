@@ -37,6 +37,30 @@
 
 namespace pkgpu {
 
+// The operand split of the bf16 tolerance kernels: x = hi + lo + r with
+// hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest (x - hi is
+// exact in fp32), for two values packed as bf16 pairs.  The split GEMM
+// kernels and the producers that hand them pre-split activations share it,
+// so both give the same bits.  The bf16 value is read back through a
+// by-value function: a bit cast applied directly to an element of a bf16
+// vector gave wrong bits with this compiler.
+typedef float split_v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 split_v2bf __attribute__((ext_vector_type(2)));
+
+__device__ inline float bf16_value(__bf16 h)
+{
+    return __uint_as_float((uint32_t)__builtin_bit_cast(unsigned short, h) << 16);
+}
+
+__device__ inline void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo)
+{
+    const split_v2bf h = __builtin_convertvector((split_v2f){x0, x1}, split_v2bf);
+    hi = __builtin_bit_cast(uint32_t, h);
+    const split_v2bf l = __builtin_convertvector(
+        (split_v2f){__fsub_rn(x0, bf16_value(h[0])), __fsub_rn(x1, bf16_value(h[1]))}, split_v2bf);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
 __device__ inline float exp_poly(float x)
 {
     x = fminf(fmaxf(x, -87.0f), 87.0f);

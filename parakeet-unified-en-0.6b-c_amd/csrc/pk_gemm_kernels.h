@@ -46,6 +46,12 @@ struct GemmProblem {
     // overlap on the device must not share it.
     float* work = nullptr;
     size_t work_bytes = 0;
+    // A given pre-split (split kernels only, TOL_ALL): per row and group of
+    // 8 consecutive k, the 8 values hi = bf16(a) then the 8 lo = bf16(a - hi)
+    // (split_bf16x2), so a row keeps the bytes and the pitch lda (in floats)
+    // of the fp32 row.  launch_gemm refuses the problem if the split kernels
+    // do not take it.
+    bool a_presplit = false;
 };
 
 // Partial tiles of one split-K launch: at most 256 workgroups of at most

@@ -144,6 +144,11 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
         return hipGetLastError();
     }
 
+    if (p.a_presplit) {
+        // A comes pre-split: only the split kernels read it
+        if (tol != TOL_ALL || cfg_index >= 0 || !split_supports(p)) return hipErrorInvalidValue;
+        return launch_split(p, stream);
+    }
     if (tol != TOL_NONE && cfg_index < 0) {
         if (smallm_supports(p)) {
             const hipError_t e = launch_smallm(p, stream);

@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <tuple>
 #include <vector>
@@ -132,6 +133,9 @@ struct pk_gpu_encoder {
     // g > 0 on side[g - 1], joined through events around the replay.
     int n_groups = 2;
     int lag = -1;                  // pk_gpu_encoder_set_group_lag (-1: group_lag())
+    // fast numerics: LayerNorms feeding a GEMM write pre-split output
+    // (PK_GPU_PRESPLIT=0 at creation turns it off; the results are the same)
+    bool presplit = true;
     std::vector<hipStream_t> side;
     std::vector<hipEvent_t> side_done;
     hipEvent_t inputs_ready = nullptr;
@@ -327,9 +331,11 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, size_t scores_n, 
     return PK_GPU_OK;
 }
 
+// presplit: A holds a split-output LayerNorm's rows (GemmProblem::a_presplit),
+// for the split kernels only.
 int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float* bias,
                 Epilogue epi, hipStream_t s, pkgpu::Tolerance tol = pkgpu::TOL_NONE,
-                float* work = nullptr)
+                float* work = nullptr, bool presplit = false)
 {
     GemmProblem p{};
     p.kind = w.kind;
@@ -352,6 +358,7 @@ int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float
         p.work = work;
         p.work_bytes = pkgpu::kSplitWorkBytes;
     }
+    p.a_presplit = presplit;
     return pkgpu::rt::gemm(p, s, tol);
 }
 
@@ -468,9 +475,11 @@ std::vector<Chunk> plan_chunks(int T, int C, int ov)
 }
 
 // A weight GEMM of the block: M rows of A through w, with its epilogue;
-// `work`: the row group's split-K partial tiles, or null.
+// `work`: the row group's split-K partial tiles, or null; `presplit`: A holds
+// a split-output LayerNorm's rows (layer_norm with split).
 int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
-         const float* bias, Epilogue epi, hipStream_t s, float* work = nullptr)
+         const float* bias, Epilogue epi, hipStream_t s, float* work = nullptr,
+         bool presplit = false)
 {
     const double flops = 2.0 * M * w.N * w.K;
     double bytes = weight_bytes_of(w) + 4.0 * M * w.K + 4.0 * M * w.N;
@@ -478,13 +487,19 @@ int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
     if (epi == pkgpu::EPI_HALF_RESIDUAL || epi == pkgpu::EPI_RESIDUAL) bytes += 4.0 * M * w.N;
     const pkgpu::Tolerance tol = pkgpu::rt::tolerance_of(e->numerics);
     return timed(e, stage_of(w), flops, bytes, s,
-                 [&] { return gemm_launch(w, A, M, C, bias, epi, s, tol, work); });
+                 [&] {
+                     return gemm_launch(w, A, M, C, bias, epi, s, tol, work, presplit);
+                 });
 }
 
+// split: the output pre-split for the split GEMM kernels, for a GEMM that
+// then reads it with presplit.
 int layer_norm(pk_gpu_encoder* e, const float* x, const float* g, const float* b, float* out, int R,
-               hipStream_t s)
+               hipStream_t s, bool split = false)
 {
     return timed(e, PK_GPU_STAGE_LAYER_NORM, 0.0, 8.0 * R * kD + 8.0 * kD, s, [&] {
+        if (split)
+            return check(pkgpu::launch_layer_norm_split(x, kD, g, b, out, kD, R, kD, s), "layer norm");
         return check(pkgpu::launch_layer_norm(x, kD, g, b, out, kD, R, kD, s), "layer norm");
     });
 }
@@ -504,17 +519,26 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     float* att = e->att + (size_t)g.r0 * kD;
     const int* rows = e->rows_tab + g.tab;
     const int* lens = e->rows_tab + e->rows_cap + g.tab;
+    // Fast numerics beyond the small-M rows: the LayerNorms that feed a GEMM
+    // (feed-forward up, QKV, pointwise 1) write their outputs pre-split, so
+    // those GEMMs stage A without splitting it again per column tile (fast
+    // pass +0.8-1.8%).  The GEMMs' inputs, and so every result, are the same
+    // bits.  The up projection's Swish output pre-split for the down
+    // projection measured no faster: its scattered 2-byte stores cost what
+    // the down projection saved.
+    const bool ps = e->presplit && e->numerics == PK_GPU_NUMERICS_FAST &&
+                    pkgpu::rt::forced_config() < 0 && R > 64;
     auto ffn = [&](const float* gm, const float* be, const DevWeight& w1, const float* b1,
                    const DevWeight& w2, const float* b2) {
-        int r = layer_norm(e, x, gm, be, ln, R, s);
-        if (!r) r = gemm(e, w1, ln, R, h, b1, pkgpu::EPI_SWISH, s, g.part);            // encoder.c:193-196
+        int r = layer_norm(e, x, gm, be, ln, R, s, ps);
+        if (!r) r = gemm(e, w1, ln, R, h, b1, pkgpu::EPI_SWISH, s, g.part, ps);        // encoder.c:193-196
         if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s, g.part);     // encoder.c:198-216
         return r;
     };
     // self-attention (encoder.c:300-424)
     auto self_attention = [&]() {
-        int rc = layer_norm(e, x, b.ln_sa_w, b.ln_sa_b, ln, R, s);
-        if (!rc) rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s, g.part);
+        int rc = layer_norm(e, x, b.ln_sa_w, b.ln_sa_b, ln, R, s, ps);
+        if (!rc) rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s, g.part, ps);
         if (rc) return rc;
         // every chunk of the group in one launch, each with its own length
         double flops = 0.0, bytes = 4.0 * (2 * Tmax - 1) * kD;   // the P rows read
@@ -540,8 +564,8 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     };
     // convolution module (encoder.c:430-476), time-major throughout
     auto convolution = [&]() {
-        int rc = layer_norm(e, x, b.ln_conv_w, b.ln_conv_b, ln, R, s);
-        if (!rc) rc = gemm(e, b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s, g.part);
+        int rc = layer_norm(e, x, b.ln_conv_w, b.ln_conv_b, ln, R, s, ps);
+        if (!rc) rc = gemm(e, b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s, g.part, ps);
         if (!rc)
             rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 12.0 * R * kD, s, [&] {
                 return check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu");
@@ -1002,6 +1026,7 @@ int pk_gpu_encoder_create(pk_gpu_encoder** out, const pk_gpu_block_weights* bloc
     int rc = pkgpu::rt::bind(nullptr);
     if (rc) return rc;
     pk_gpu_encoder* e = new pk_gpu_encoder;
+    if (const char* v = getenv("PK_GPU_PRESPLIT")) e->presplit = strcmp(v, "0") != 0;
     hipError_t r = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
     if (r != hipSuccess) {
         delete e;

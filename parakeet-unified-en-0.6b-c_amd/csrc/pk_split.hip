@@ -86,19 +86,12 @@ __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
 
 __device__ inline v2bf to_bf2(float a, float b) { return __builtin_convertvector((v2f){a, b}, v2bf); }
 
-__device__ inline float bf_to_f(__bf16 h)
-{
-    return __uint_as_float((uint32_t)__builtin_bit_cast(unsigned short, h) << 16);
-}
-
 __device__ inline uint32_t bits2(v2bf v) { return __builtin_bit_cast(uint32_t, v); }
 
 // (x0, x1) -> hi = bf16 pair, lo = bf16 pair of the residues
 __device__ inline void split2(float x0, float x1, uint32_t& hi, uint32_t& lo)
 {
-    const v2bf h = to_bf2(x0, x1);
-    hi = bits2(h);
-    lo = bits2(to_bf2(__fsub_rn(x0, bf_to_f(h[0])), __fsub_rn(x1, bf_to_f(h[1]))));
+    split_bf16x2(x0, x1, hi, lo);
 }
 
 // Signed nibble j (0: low, 1: high) of byte b.
@@ -114,7 +107,10 @@ template <> struct WUnit<W_F32> { v4u w[2]; };
 
 // Staging and multiplying one chunk of a BM x BN tile by NT threads.
 // A chunk's LDS planes: A_hi, A_lo [BM][RS], then W_hi (and W_lo) [BN][RS].
-template <int WK, int BM, int BN, int NT>
+// AS: A comes pre-split by its producer (GemmProblem::a_presplit: per row and
+// 8 consecutive k, the 8 bf16 hi then the 8 bf16 lo, so a row takes the bytes
+// and the pitch of the fp32 row), and staging it is a copy.
+template <int WK, int BM, int BN, int NT, bool AS>
 struct Pipe {
     static constexpr int NBP = WK == W_I8 ? 1 : 2;             // weight planes
     static constexpr int A_PLANE = BM * RS, B_PLANE = BN * RS;   // bf16 elements
@@ -135,6 +131,8 @@ struct Pipe {
 
     // the global loads of the chunk at k0 (rows past M, columns past the
     // operands' extents read 0; columns past N only feed unstored outputs)
+    // (the same 16-byte loads with or without AS: 4 k of fp32, or the hi or
+    // the lo half of 8 pre-split k)
     __device__ static void load(Raw& r, const SpArgs& p, __amdgpu_buffer_rsrc_t rA,
                                 __amdgpu_buffer_rsrc_t rB, __amdgpu_buffer_rsrc_t rS, int tid,
                                 int m0, int n0, int k0)
@@ -174,14 +172,23 @@ struct Pipe {
         __bf16* al = ah + A_PLANE;
         __bf16* bh = al + A_PLANE;
         __bf16* bl = bh + B_PLANE;                   // int4, fp32 only
+        if constexpr (AS) {
+            // part kq: the hi (even) or lo (odd) half of k group kq / 2
 #pragma unroll
-        for (int i = 0; i < A_ITEMS; ++i) {
-            const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
-            uint32_t h0, l0, h1, l1;
-            split2(__uint_as_float(r.a[i][0]), __uint_as_float(r.a[i][1]), h0, l0);
-            split2(__uint_as_float(r.a[i][2]), __uint_as_float(r.a[i][3]), h1, l1);
-            *reinterpret_cast<v2u*>(ah + row * RS + 4 * kq) = v2u{h0, h1};
-            *reinterpret_cast<v2u*>(al + row * RS + 4 * kq) = v2u{l0, l1};
+            for (int i = 0; i < A_ITEMS; ++i) {
+                const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
+                *reinterpret_cast<v4u*>(ah + (kq & 1) * A_PLANE + row * RS + 8 * (kq >> 1)) = r.a[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_ITEMS; ++i) {
+                const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
+                uint32_t h0, l0, h1, l1;
+                split2(__uint_as_float(r.a[i][0]), __uint_as_float(r.a[i][1]), h0, l0);
+                split2(__uint_as_float(r.a[i][2]), __uint_as_float(r.a[i][3]), h1, l1);
+                *reinterpret_cast<v2u*>(ah + row * RS + 4 * kq) = v2u{h0, h1};
+                *reinterpret_cast<v2u*>(al + row * RS + 4 * kq) = v2u{l0, l1};
+            }
         }
 #pragma unroll
         for (int i = 0; i < B_ITEMS; ++i) {
@@ -296,10 +303,10 @@ __device__ inline void zero(v16f (&acc)[2][2])
 // SK: workgroup u takes segment u / n_tiles of K (a contiguous run of its
 // chunks) for tile u % n_tiles and stores its raw sums to the tile's slot
 // of that segment in work, in register order (split_reduce finishes).
-template <int WK, int WM, int WN, int PD, bool SK>
+template <int WK, int WM, int WN, int PD, bool SK, bool AS>
 __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) void split_gemm(SpArgs p)
 {
-    typedef Pipe<WK, 64 * WM, 64 * WN, 64 * WM * WN> L;
+    typedef Pipe<WK, 64 * WM, 64 * WN, 64 * WM * WN, AS> L;
     __shared__ __attribute__((aligned(16))) __bf16 smem[2 * L::BUF];
 
     const int u = tile_of(p);
@@ -308,7 +315,8 @@ __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) v
     const int m0 = (t / p.tiles_n) * (64 * WM), n0 = (t % p.tiles_n) * (64 * WN);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    const auto rA = rsrc(p.A, p.a_bytes), rB = rsrc(p.B, p.b_bytes), rS = rsrc(p.scales, p.s_bytes);
+    const auto rA = rsrc(p.A, p.a_bytes);
+    const auto rB = rsrc(p.B, p.b_bytes), rS = rsrc(p.scales, p.s_bytes);
 
     typename L::Raw raw[PD];                         // chunk x in slot x % PD
     v16f acc[2][2];
@@ -418,10 +426,10 @@ __global__ __launch_bounds__(256) void split_reduce(SpArgs p)
 // until the end), loads PD chunks ahead; the KS partial tiles are then
 // summed in LDS in wave order.  For shapes with too few tiles to give every
 // CU a workgroup otherwise (N = 1024 at 1656 rows).
-template <int WK, int KS, int PD>
+template <int WK, int KS, int PD, bool AS>
 __global__ __launch_bounds__(64 * KS, 2) void split_gemm_k(SpArgs p)
 {
-    typedef Pipe<WK, 64, 64, 64> L;
+    typedef Pipe<WK, 64, 64, 64, AS> L;
     constexpr int STAGE = KS * L::BUF * 2, RED = KS * 4 * 16 * 64 * 4;   // bytes
     __shared__ __attribute__((aligned(16))) unsigned char smem[STAGE > RED ? STAGE : RED];
 
@@ -429,7 +437,8 @@ __global__ __launch_bounds__(64 * KS, 2) void split_gemm_k(SpArgs p)
     if (t < 0) return;                               // padding workgroup (uniform)
     const int m0 = (t / p.tiles_n) * 64, n0 = (t % p.tiles_n) * 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const auto rA = rsrc(p.A, p.a_bytes), rB = rsrc(p.B, p.b_bytes), rS = rsrc(p.scales, p.s_bytes);
+    const auto rA = rsrc(p.A, p.a_bytes);
+    const auto rB = rsrc(p.B, p.b_bytes), rS = rsrc(p.scales, p.s_bytes);
     __bf16* slab = reinterpret_cast<__bf16*>(smem) + wave * L::BUF;
 
     typename L::Raw raw[PD];
@@ -551,7 +560,7 @@ unsigned padded_grid(SpArgs& a, int bm, int bn, int n_seg = 1)
     return (unsigned)(((a.tiles + kXcd - 1) / kXcd) * kXcd);
 }
 
-template <int WK>
+template <int WK, bool AS>
 hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
 {
     // Chunks of loads in flight, as many as fit two waves per SIMD without
@@ -562,9 +571,9 @@ hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
         const bool wide = plan.shape == SP_4x2;
         const unsigned grid = padded_grid(a, wide ? 256 : 128, 128, plan.n_seg);
         if (wide)
-            hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, true>), dim3(grid), dim3(512), 0, st, a);
+            hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, true, AS>), dim3(grid), dim3(512), 0, st, a);
         else
-            hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22, true>), dim3(grid), dim3(256), 0, st, a);
+            hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22, true, AS>), dim3(grid), dim3(256), 0, st, a);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const unsigned blocks = (unsigned)a.n_tiles * (wide ? 8 * 4096 / 1024 : 4 * 4096 / 1024);
@@ -576,21 +585,21 @@ hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
     }
     switch (plan.shape) {
     case SP_4x2:
-        hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, false>), dim3(padded_grid(a, 256, 128)), dim3(512), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, false, AS>), dim3(padded_grid(a, 256, 128)), dim3(512), 0, st, a);
         break;
     case SP_2x2:
-        hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22, false>), dim3(padded_grid(a, 128, 128)), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22, false, AS>), dim3(padded_grid(a, 128, 128)), dim3(256), 0, st, a);
         break;
     case SP_2x1:
-        hipLaunchKernelGGL((split_gemm<WK, 2, 1, PD21, false>), dim3(padded_grid(a, 128, 64)), dim3(128), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 2, 1, PD21, false, AS>), dim3(padded_grid(a, 128, 64)), dim3(128), 0, st, a);
         break;
     case SP_K4:
-        hipLaunchKernelGGL((split_gemm_k<WK, kKSplit, PDK>), dim3(padded_grid(a, 64, 64)), dim3(64 * kKSplit),
+        hipLaunchKernelGGL((split_gemm_k<WK, kKSplit, PDK, AS>), dim3(padded_grid(a, 64, 64)), dim3(64 * kKSplit),
                            0, st, a);
         break;
     default:
         // K < 256 here: one or two chunks ahead, as many as fit without spills
-        hipLaunchKernelGGL((split_gemm<WK, 1, 1, WK == W_I4 ? 1 : 2, false>), dim3(padded_grid(a, 64, 64)), dim3(64), 0, st, a);
+        hipLaunchKernelGGL((split_gemm<WK, 1, 1, WK == W_I4 ? 1 : 2, false, AS>), dim3(padded_grid(a, 64, 64)), dim3(64), 0, st, a);
         break;
     }
     return hipGetLastError();
@@ -638,10 +647,17 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     if ((long long)((p.M + 63) / 64) * ((p.N + 63) / 64) > (1LL << 30)) return hipErrorNotSupported;
     const SplitPlan plan = split_plan(p.kind, p.M, p.N, p.K, p.work ? p.work_bytes : 0);
     a.work = p.work;
+    if (p.a_presplit) {
+        switch (p.kind) {
+        case W_I8: return launch_kind<W_I8, true>(a, plan, st);
+        case W_I4: return launch_kind<W_I4, true>(a, plan, st);
+        default:   return launch_kind<W_F32, true>(a, plan, st);
+        }
+    }
     switch (p.kind) {
-    case W_I8: return launch_kind<W_I8>(a, plan, st);
-    case W_I4: return launch_kind<W_I4>(a, plan, st);
-    default:   return launch_kind<W_F32>(a, plan, st);
+    case W_I8: return launch_kind<W_I8, false>(a, plan, st);
+    case W_I4: return launch_kind<W_I4, false>(a, plan, st);
+    default:   return launch_kind<W_F32, false>(a, plan, st);
     }
 }
 

@@ -158,3 +158,19 @@ def test_fast_mode_row_group_changes(model):
         assert bits_equal(outs[2], outs[0]), describe_mismatch(outs[2], outs[0])
     finally:
         pk.load().pk_gpu_encoder_destroy(enc)
+
+
+def test_fast_mode_presplit_layer_norm_is_bit_identical(model, monkeypatch):
+    """Under PK_GPU_NUMERICS_FAST the LayerNorms that feed a GEMM write their
+    output already split into the bf16 halves the split kernels multiply.
+    That moves the split, not the arithmetic: an encoder created with
+    PK_GPU_PRESPLIT=0 (the GEMMs split the fp32 LayerNorm output themselves)
+    gives the same bits, over two row groups and 24 blocks."""
+    T, chunk, ov = 300, 140, 8
+    x = bench.enc_rng(0xFEA7, 302).standard_normal((T, bench.D)).astype(np.float32)
+    monkeypatch.delenv("PK_GPU_PRESPLIT", raising=False)
+    pre = run(model, x, chunk, pk.NUMERICS_FAST, overlap=ov)
+    monkeypatch.setenv("PK_GPU_PRESPLIT", "0")
+    plain = run(model, x, chunk, pk.NUMERICS_FAST, overlap=ov)
+    for a, b in zip(pre, plain):
+        assert bits_equal(a, b), describe_mismatch(a, b)
