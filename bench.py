@@ -52,7 +52,7 @@ PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_BF16_MFMA_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 CPU_THREADS = 16            # the reference clamps PK_THREADS to 16 (threadpool.c:10)
-SEED = 0x5EED0001           # workload 1
+SEED = 0x5EED0001           # the int4 FFN pair at M = 375
 
 
 def int4_bytes(K, N):
@@ -407,9 +407,9 @@ def ffn_mode(args):
 
 
 
-# ---- the 24-block encoder (workload 4) -----------------------------------
+# ---- the 24-block encoder over 3200 frames ---------------------------------
 
-ENC_SEED = 0x5EED0004          # workload 4
+ENC_SEED = 0x5EED0004          # the 3200-frame encoder
 ENC_FRAMES, ENC_CHUNK, ENC_OVERLAP = 3200, 400, 8
 N_BLOCKS = 24
 PE_ROWS, PE_CENTER = 9999, 4999
@@ -543,7 +543,7 @@ def encoder_cpu_baseline(model, x, budget_s):
             "s_per_pass": round(el / passes, 3)}
 
 
-# ---- the per-GEMM workloads (0-3), timed beside the encoder ----------------
+# ---- the per-GEMM workloads, timed beside the encoder ----------------------
 
 def graph_us(torch, dev, call, steps, warmup):
     """Average microseconds of call(i): HIP events around a graph replay of
@@ -580,7 +580,8 @@ def cpu_seconds_per_call(fn, budget_s, max_calls=10000):
 
 
 def workload_timings(pk, lib, torch, dev, cpu_budget_s):
-    """Workloads 0-3 of the benchmark definition, each on the GPU (inputs
+    """The smaller workloads (int8 QKV at M = 32, int4 FFN pair at M = 375,
+    fp32 pair at M = 500, one block at 416 rows, a 33-frame clip), each on the GPU (inputs
     resident, weights rotating over replicas that exceed the 256 MB Infinity
     Cache, graph replays) and through the reference's own x86 build
     (oracle/_ref, PK_THREADS = 16) on the same inputs for ~cpu_budget_s."""
@@ -1062,7 +1063,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-workloads", action="store_true",
-                    help="skip the workloads 0-4 timings (profiler runs of the encoder)")
+                    help="skip the smaller workloads' timings (profiler runs of the encoder)")
     ap.add_argument("--ffn", action="store_true",
                     help="time the int4 feed-forward pair at M = 375 instead of the encoder")
     ap.add_argument("--copy-calibration", action="store_true",
