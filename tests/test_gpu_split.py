@@ -268,3 +268,57 @@ def test_split_swish_epilogue_against_its_input(dev):
     err = np.abs(act.astype(np.float64) - want)
     assert float(np.abs(plain).max()) > 8.0                      # both tails exercised
     assert float((err / np.maximum(np.abs(want), 1e-30)).max()) <= 5e-6, float(err.max())
+
+
+def test_split_k_workspaces_per_thread(dev):
+    """Four threads at once, each with its own workspace (thread-local, as
+    pk_gpu_set_workspace documents) and its own stream, run split-K GEMMs of
+    two shapes twice: every result equals the single-thread run bit for bit
+    (the sums have a fixed order)."""
+    import threading
+    import torch
+    lib = pk.load()
+    shapes = [("i4", 375, 1024, 4096), ("f32", 500, 1024, 2048)]
+    cases = [make(kind, M, N, K, f"spkthr.{kind}.{M}") for kind, M, N, K in shapes]
+    with Workspace(dev):
+        want = [fast(dev, kind, A, W, extra, np.zeros((M, N), np.float32))
+                for (kind, M, N, K), (A, W, extra, _) in zip(shapes, cases)]
+        assert all(lib.pk_gpu_split_k_segments(M, N, K, bits_of(kind)) > 1 for kind, M, N, K in shapes)
+    n_thr = 4
+    spaces = [torch.empty(pk.SPLIT_WORKSPACE_BYTES // 4, device=dev.dev) for _ in range(n_thr)]
+    streams = [torch.cuda.Stream(device=dev.dev) for _ in range(n_thr)]
+    dev_in = []
+    for (kind, M, N, K), (A, W, extra, _) in zip(shapes, cases):
+        dev_in.append((dev.put(A), dev.put(W), dev.put(extra) if kind == "i4" else None))
+    outs = [[torch.empty((M, N), device=dev.dev) for kind, M, N, K in shapes] for _ in range(n_thr)]
+    torch.cuda.synchronize(dev.dev)
+    errs = []
+
+    def work(t):
+        try:
+            pk.call("pk_gpu_set_numerics", pk.NUMERICS_FAST)
+            pk.call("pk_gpu_set_workspace", spaces[t].data_ptr(), pk.SPLIT_WORKSPACE_BYTES)
+            st = streams[t].cuda_stream
+            for _ in range(2):
+                for s, ((kind, M, N, K), (dA, dW, dS)) in enumerate(zip(shapes, dev_in)):
+                    C = outs[t][s]
+                    if kind == "i4":
+                        pk.call("pk_gpu_gemm_i4_dev", M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(),
+                                dS.data_ptr(), N // 2, 0.0, C.data_ptr(), N, st)
+                    else:
+                        pk.call("pk_gpu_sgemm_dev", M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(), N,
+                                0.0, C.data_ptr(), N, st)
+            streams[t].synchronize()
+            pk.call("pk_gpu_set_workspace", None, 0)
+        except Exception as e:                       # reported on the main thread
+            errs.append(f"thread {t}: {e}")
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(n_thr)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errs, errs
+    for t in range(n_thr):
+        for s in range(len(shapes)):
+            assert bits_equal(outs[t][s].cpu().numpy(), want[s]), (t, shapes[s])
