@@ -76,6 +76,7 @@ struct SpArgs {
     // tiles in work (n_seg = 1: none)
     int n_seg, n_tiles;
     float* work;
+    int c_vec4;                   // C rows and the bias allow 16-byte accesses (split_reduce)
 };
 
 __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
@@ -415,6 +416,37 @@ __global__ __launch_bounds__(256) void split_reduce(SpArgs p)
         sum.z = __fadd_rn(sum.z, v.z);
         sum.w = __fadd_rn(sum.w, v.w);
     }
+    if (p.c_vec4) {
+        // the same steps as put, on 16-byte accesses of C and the bias
+        float4* cp = reinterpret_cast<float4*>(p.C + (size_t)m * p.ldc + n);
+        float v[4] = {__fmul_rn(p.alpha, sum.x), __fmul_rn(p.alpha, sum.y), __fmul_rn(p.alpha, sum.z),
+                      __fmul_rn(p.alpha, sum.w)};
+        const bool reads_c = p.beta != 0.0f || p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL;
+        float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (reads_c) {
+            const float4 c4 = *cp;
+            c[0] = c4.x; c[1] = c4.y; c[2] = c4.z; c[3] = c4.w;
+        }
+        float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p.bias) {
+            const float4 b4 = *reinterpret_cast<const float4*>(p.bias + n);
+            b[0] = b4.x; b[1] = b4.y; b[2] = b4.z; b[3] = b4.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (p.beta != 0.0f) v[i] = __fadd_rn(p.beta == 1.0f ? c[i] : __fmul_rn(p.beta, c[i]), v[i]);
+            if (p.bias) v[i] = __fadd_rn(v[i], b[i]);
+            switch (p.epi) {
+            case EPI_SWISH:         v[i] = swish_f(v[i]); break;
+            case EPI_HALF_RESIDUAL: v[i] = __fmaf_rn(v[i], 0.5f, c[i]); break;
+            case EPI_RESIDUAL:      v[i] = __fadd_rn(c[i], v[i]); break;
+            case EPI_RELU:          v[i] = v[i] > 0.0f ? v[i] : 0.0f; break;
+            default:                break;
+            }
+        }
+        *cp = make_float4(v[0], v[1], v[2], v[3]);
+        return;
+    }
     put(p, m, n, sum.x);
     put(p, m, n + 1, sum.y);
     put(p, m, n + 2, sum.z);
@@ -647,6 +679,8 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     if ((long long)((p.M + 63) / 64) * ((p.N + 63) / 64) > (1LL << 30)) return hipErrorNotSupported;
     const SplitPlan plan = split_plan(p.kind, p.M, p.N, p.K, p.work ? p.work_bytes : 0);
     a.work = p.work;
+    a.c_vec4 = p.ldc % 4 == 0 && reinterpret_cast<uintptr_t>(p.C) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(p.bias) % 16 == 0;
     if (p.a_presplit) {
         switch (p.kind) {
         case W_I8: return launch_kind<W_I8, true>(a, plan, st);

@@ -322,3 +322,30 @@ def test_split_k_workspaces_per_thread(dev):
     for t in range(n_thr):
         for s in range(len(shapes)):
             assert bits_equal(outs[t][s].cpu().numpy(), want[s]), (t, shapes[s])
+
+
+def test_split_k_unaligned_output_rows(dev):
+    """The split-K reduce writes C with 16-byte accesses where its rows allow
+    it; with ldc = N + 1 it takes the per-element path: the same sums, the
+    column past N untouched."""
+    import torch
+    M, N, K = 500, 1024, 2048
+    A, W, _, C0 = make("f32", M, N, K, "spkldc")
+    want = oracle("f32", A, W, None, C0, 1.0, 1.0)
+    lib = pk.load()
+    with Workspace(dev):
+        assert lib.pk_gpu_split_k_segments(M, N, K, 32) > 1
+        big = np.full((M, N + 1), 7.0, np.float32)
+        big[:, :N] = C0
+        dA, dW, dC = dev.put(A), dev.put(W), dev.put(big)
+        prev = lib.pk_gpu_get_numerics()
+        pk.call("pk_gpu_set_numerics", pk.NUMERICS_FAST)
+        try:
+            pk.call("pk_gpu_sgemm_dev", M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(), N, 1.0,
+                    dC.data_ptr(), N + 1, dev.stream())
+        finally:
+            pk.call("pk_gpu_set_numerics", prev)
+        dev.sync()
+        got = dC.cpu().numpy()
+    assert rel_err(got[:, :N], want) <= MEASURED
+    assert bool((got[:, N] == 7.0).all())
