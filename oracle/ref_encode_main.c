@@ -33,7 +33,9 @@
 
 #include "pk_oracle.h"
 
+#include <errno.h>
 #include <stdint.h>
+#include <sys/stat.h>
 #include <time.h>
 #include <unistd.h>
 #include <xmmintrin.h>
@@ -140,11 +142,56 @@ static void g_int4(Writer *w, const char *name, int K, int N)
     free(p);
 }
 
-/* A mixed-mode model at the statistics of the benchmark workloads:
- * int4 FF linears, int8 attention and pre-encode projections (Q/K/V with
- * different scales, so the fused-QKV requantisation runs), fp32 elsewhere. */
+/* PK_SYNTH_MODE picks which of the reference's three weight directories
+ * (c_weights_{fp32,int8,mixed}, download_weights.py:20) the synthetic model
+ * imitates:
+ *   mixed (default)  int4 FF linears, int8 attention and pre-encode
+ *                    projections (extract_weights.py:726-840);
+ *   int8             every matmul weight int8 with one scale, FF linears
+ *                    included (extract_weights.py:376-391);
+ *   fp32             every weight fp32 (extract_weights.py:88-200), so the
+ *                    fused QKV is the fp32 interleave (weights.c:421-436).
+ * The pointwise convolutions are fp32 in all three, as extracted. */
+enum { MODE_MIXED, MODE_INT8, MODE_FP32 };
+
+static int synth_mode(void)
+{
+    const char *m = getenv("PK_SYNTH_MODE");
+    if (!m || !strcmp(m, "mixed")) return MODE_MIXED;
+    if (!strcmp(m, "int8")) return MODE_INT8;
+    if (!strcmp(m, "fp32")) return MODE_FP32;
+    fprintf(stderr, "PK_SYNTH_MODE=%s: expected mixed, int8 or fp32\n", m);
+    exit(2);
+}
+
+/* Codes uniform in [-127, 127] have standard deviation 127/sqrt(3). */
+#define I8_CODE_STD 73.32f
+
+/* One int8 projection of the mixed and int8 models with scale `scale`; in
+ * the fp32 model, N(0, scale * 127/sqrt(3)) weights of the same spread. */
+static void g_proj(Writer *w, int mode, const char *name, size_t n, float scale)
+{
+    if (mode == MODE_FP32) g_normal(w, name, n, scale * I8_CODE_STD);
+    else g_int8(w, name, n, scale);
+}
+
+/* One feed-forward linear [K][N]: GPTQ int4 in the mixed model; int8 with
+ * scale 0.0008 or N(0, 0.06) in the others, about the int4 weights' spread
+ * (codes -8..7 times scales ~U(0.005, 0.02)). */
+static void g_ff(Writer *w, int mode, const char *name, int K, int N)
+{
+    if (mode == MODE_MIXED) g_int4(w, name, K, N);
+    else if (mode == MODE_INT8) g_int8(w, name, (size_t)K * N, 0.0008f);
+    else g_normal(w, name, (size_t)K * N, 0.06f);
+}
+
+/* The model at the statistics of the benchmark workloads: in the mixed
+ * mode int4 FF linears, int8 attention and pre-encode projections (Q/K/V
+ * with different scales, so the fused-QKV requantisation runs), fp32
+ * elsewhere; the other modes as synth_mode() describes. */
 static int write_model(const char *dir)
 {
+    const int mode = synth_mode();
     /* PK_SYNTH_ATTN_GAIN scales the int8 attention projections' scales.
      * At the default 1 (codes uniform in [-127, 127], scale ~0.01) the
      * attention logits reach several hundred and the encoder amplifies a
@@ -167,7 +214,7 @@ static int write_model(const char *dir)
         snprintf(nm, sizeof nm, "pre_encode.conv.%s.bias", convs[c]);
         g_normal(&w, nm, 256, 0.02f);
     }
-    g_int8(&w, "pre_encode.out.weight", (size_t)4096 * 1024, 0.01f);
+    g_proj(&w, mode, "pre_encode.out.weight", (size_t)4096 * 1024, 0.01f);
     g_normal(&w, "pre_encode.out.bias", 1024, 0.02f);
 
     {   /* sinusoidal relative-position table centred at PK_PE_CENTER */
@@ -195,11 +242,11 @@ static int write_model(const char *dir)
         }
         for (int f = 1; f <= 2; f++) {
             snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear1.weight", b, f);
-            g_int4(&w, nm, 1024, 4096);
+            g_ff(&w, mode, nm, 1024, 4096);
             snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear1.bias", b, f);
             g_normal(&w, nm, 4096, 0.02f);
             snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear2.weight", b, f);
-            g_int4(&w, nm, 4096, 1024);
+            g_ff(&w, mode, nm, 4096, 1024);
             snprintf(nm, sizeof nm, "layers.%d.feed_forward%d.linear2.bias", b, f);
             g_normal(&w, nm, 1024, 0.02f);
         }
@@ -207,7 +254,7 @@ static int write_model(const char *dir)
         const float pscale[] = {0.0100f, 0.0110f, 0.0090f, 0.0100f, 0.0100f};
         for (int k = 0; k < 5; k++) {
             snprintf(nm, sizeof nm, "layers.%d.self_attn.%s.weight", b, proj[k]);
-            g_int8(&w, nm, (size_t)1024 * 1024, pscale[k] * attn_gain);
+            g_proj(&w, mode, nm, (size_t)1024 * 1024, pscale[k] * attn_gain);
             if (k != 3) {
                 snprintf(nm, sizeof nm, "layers.%d.self_attn.%s.bias", b, proj[k]);
                 g_normal(&w, nm, 1024, 0.02f);
@@ -376,9 +423,14 @@ int main(int argc, char **argv)
         return 2;
     }
     const int T = atoi(argv[1]);
+    /* PK_MODEL_DIR=<dir>: keep the model there and reuse it on later runs
+     * whose PK_SYNTH_MODE / PK_SYNTH_ATTN_GAIN match (model.tag records
+     * them); otherwise a fresh temporary directory, removed at the end. */
+    const char *keep = getenv("PK_MODEL_DIR");
     char dir[512];
-    snprintf(dir, sizeof dir, "%s/pk_encode_XXXXXX", argc > 2 ? argv[2] : "/tmp");
-    if (T <= 0 || !mkdtemp(dir)) {
+    if (keep) snprintf(dir, sizeof dir, "%s", keep);
+    else snprintf(dir, sizeof dir, "%s/pk_encode_XXXXXX", argc > 2 ? argv[2] : "/tmp");
+    if (T <= 0 || (keep ? (mkdir(dir, 0700) && errno != EEXIST) : !mkdtemp(dir))) {
         fprintf(stderr, "bad frame count or workdir\n");
         return 2;
     }
@@ -386,10 +438,27 @@ int main(int argc, char **argv)
 
     fpenv("start");
     double t0 = now_s();
-    if (write_model(dir)) { fprintf(stderr, "writing the model failed\n"); return 1; }
-    char bin[600], json[600];
+    char bin[600], json[600], tagp[600], tag[256], old_tag[256] = "";
     snprintf(bin, sizeof bin, "%s/weights.bin", dir);
     snprintf(json, sizeof json, "%s/weights.json", dir);
+    snprintf(tagp, sizeof tagp, "%s/model.tag", dir);
+    snprintf(tag, sizeof tag, "mode=%s gain=%s\n", getenv("PK_SYNTH_MODE") ? getenv("PK_SYNTH_MODE") : "mixed",
+             getenv("PK_SYNTH_ATTN_GAIN") ? getenv("PK_SYNTH_ATTN_GAIN") : "1");
+    if (keep) {
+        FILE *f = fopen(tagp, "r");
+        if (f) {
+            if (!fgets(old_tag, sizeof old_tag, f)) old_tag[0] = 0;
+            fclose(f);
+        }
+    }
+    if (!keep || strcmp(tag, old_tag)) {
+        unlink(tagp);
+        if (write_model(dir)) { fprintf(stderr, "writing the model failed\n"); return 1; }
+        if (keep) {
+            FILE *f = fopen(tagp, "w");
+            if (!f || fputs(tag, f) < 0 || fclose(f)) { fprintf(stderr, "writing %s failed\n", tagp); return 1; }
+        }
+    }
     PkModel m;
     memset(&m, 0, sizeof m);
     if (pk_load_weights(&m, bin, json)) { fprintf(stderr, "pk_load_weights failed\n"); return 1; }
@@ -507,7 +576,13 @@ int main(int argc, char **argv)
            T, from_mel, should_chunk(T), (unsigned long long)fnv1a(enc, (size_t)T * PK_D_MODEL * 4), amax,
            finite, n_tok, (unsigned long long)fnv1a(tokens, (size_t)n_tok * sizeof(int)));
     for (int i = 0; i < n_tok && i < 16; i++) printf("%s%d", i ? ", " : "", tokens[i]);
-    printf("], \"threads\": %d, \"load_s\": %.3f, \"encoder_s\": %.4f, \"encoder_first_s\": %.4f, "
+    /* the formats pk_load_weights produced: 32, 8 or 4 bits per weight */
+    const ConformerBlock *b0 = &m.enc.blocks[0];
+    printf("], \"bits\": {\"ff_linear1\": %d, \"ff_linear2\": %d, \"qkv\": %d, \"pos\": %d, "
+           "\"out\": %d, \"pre_encode_out\": %d}",
+           b0->ff1.linear1_w.bits, b0->ff1.linear2_w.bits, b0->mha.linear_qkv_w.bits,
+           b0->mha.linear_pos_w.bits, b0->mha.linear_out_w.bits, m.enc.pre_encode.out_w.bits);
+    printf(", \"threads\": %d, \"load_s\": %.3f, \"encoder_s\": %.4f, \"encoder_first_s\": %.4f, "
            "\"decoder_s\": %.4f}\n",
            pk_pool_nthreads(pk_pool()), t_load, t_enc, t_first, t_dec);
 
@@ -523,8 +598,10 @@ int main(int argc, char **argv)
     pk_gpu_shutdown();
 #endif
     pk_free_weights(&m);
-    unlink(bin);
-    unlink(json);
-    rmdir(dir);
+    if (!keep) {
+        unlink(bin);
+        unlink(json);
+        rmdir(dir);
+    }
     return 0;
 }

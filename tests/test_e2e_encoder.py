@@ -4,7 +4,10 @@ the weight GEMMs taken from the GPU drop-in, against the same host code
 with blas.c's portable weight GEMMs.  Both load the same synthetic mixed
 int4/int8/fp32 model through pk_load_weights (fused-QKV requantisation
 included); every other object is shared, so equal encoder-output and
-token hashes mean the GPU GEMMs changed nothing.
+token hashes mean the GPU GEMMs changed nothing.  The reference's other two
+weight directories (c_weights_int8: every matmul weight int8; c_weights_fp32:
+every weight fp32) are imitated the same way (PK_SYNTH_MODE) and checked by
+the *_weight_directories tests.
 
 The x86 AVX2 build of the reference decodes int4 weights wrongly
 (blas.c:815-833, see test_oracle.test_x86_int4_unpack_defect); its output
@@ -30,11 +33,21 @@ REF = os.path.join(os.path.dirname(HERE), "oracle", "_ref")
 THREADS = str(min(os.cpu_count() or 1, 16))
 
 
-def run(binary, frames, tmp_path, dump=None, attn_gain=None, from_mel=False, extra_env=None):
+def run(binary, frames, tmp_path, dump=None, attn_gain=None, from_mel=False, extra_env=None,
+        mode=None, model_dir=None):
+    """mode: the weight directory the synthetic model imitates (mixed, int8,
+    fp32; PK_SYNTH_MODE); model_dir: where the model is kept and reused by
+    later runs of the same mode and gain (PK_MODEL_DIR)."""
     path = os.path.join(REF, binary)
     if not os.path.exists(path):
         pytest.skip(f"{binary} not built (oracle/Makefile ref)")
     env = dict(os.environ, PK_THREADS=THREADS, MALLOC_PERTURB_="192")  # 0x3f3f3f3f fill
+    env.pop("PK_SYNTH_MODE", None)
+    env.pop("PK_MODEL_DIR", None)
+    if mode:
+        env["PK_SYNTH_MODE"] = mode
+    if model_dir:
+        env["PK_MODEL_DIR"] = str(model_dir)
     if dump:
         env["PK_DUMP_ENC"] = str(dump)
     if attn_gain is not None:
@@ -58,6 +71,54 @@ def test_reference_drivers_cpu(tmp_path):
     x86 = run("pk_encode_ref_x86", 48, tmp_path)
     assert ref["finite"] == 1 and x86["finite"] == 1 and ref["frames"] == 48
     assert ref["enc_fnv"] != x86["enc_fnv"]
+
+
+# the formats pk_load_weights builds from each weight directory
+MODE_BITS = {
+    "mixed": {"ff_linear1": 4, "ff_linear2": 4, "qkv": 8, "pos": 8, "out": 8, "pre_encode_out": 8},
+    "int8": {"ff_linear1": 8, "ff_linear2": 8, "qkv": 8, "pos": 8, "out": 8, "pre_encode_out": 8},
+    "fp32": {"ff_linear1": 32, "ff_linear2": 32, "qkv": 32, "pos": 32, "out": 32, "pre_encode_out": 32},
+}
+
+
+def test_reference_driver_int8_model_cpu(tmp_path):
+    """CPU only: the int8 weight directory's model (every matmul weight int8,
+    FF linears included) loads through pk_load_weights with the formats the
+    reference builds, and the portable and x86 builds agree bit for bit (the
+    x86 build differs only in its int4 unpack, which this model does not
+    use)."""
+    ref = run("pk_encode_ref", 48, tmp_path, mode="int8", model_dir=tmp_path / "m")
+    x86 = run("pk_encode_ref_x86", 48, tmp_path, mode="int8", model_dir=tmp_path / "m")
+    assert ref["bits"] == MODE_BITS["int8"] and x86["bits"] == MODE_BITS["int8"]
+    assert ref["finite"] == 1 and ref["enc_fnv"] == x86["enc_fnv"]
+    assert ref["tokens_fnv"] == x86["tokens_fnv"]
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("mode", ["int8", "fp32"])
+def test_gpu_dropin_weight_directories(mode, tmp_path):
+    """The reference's other two weight directories through the GEMM drop-in,
+    900 frames (chunks of 408/416/108 rows): int8 (every matmul weight int8,
+    so the FF linears take cblas_sgemm_qb at K = 1024 and 4096) and fp32
+    (every matmul cblas_sgemm, the fused QKV the fp32 interleave of
+    weights.c:421-436).  Neither uses int4, so the reference exactly as its
+    Makefile builds it on x86 (AVX2 weight GEMMs) must agree bit for bit
+    too: encoder output and greedy token ids."""
+    frames = 900
+    mdir = tmp_path / "model"
+    gpu = run("pk_encode_gpu", frames, tmp_path, mode=mode, model_dir=mdir)
+    ref = run("pk_encode_ref", frames, tmp_path, mode=mode, model_dir=mdir)
+    x86 = run("pk_encode_ref_x86", frames, tmp_path, mode=mode, model_dir=mdir)
+    assert gpu["bits"] == ref["bits"] == MODE_BITS[mode]
+    assert gpu["finite"] == 1 and gpu["chunked"] == ref["chunked"] == 1
+    assert gpu["enc_fnv"] == ref["enc_fnv"] == x86["enc_fnv"], "encoder outputs differ"
+    assert gpu["n_tokens"] == ref["n_tokens"] == x86["n_tokens"]
+    assert gpu["tokens_fnv"] == ref["tokens_fnv"] == x86["tokens_fnv"]
+    print(json.dumps({"mode": mode, "frames": frames, "threads": THREADS,
+                      "encoder_frames_per_s_gpu_dropin": round(frames / gpu["encoder_s"], 1),
+                      "encoder_frames_per_s_cpu_reference_x86": round(frames / x86["encoder_s"], 1)}),
+          flush=True)
 
 
 @pytest.mark.gpu
@@ -141,16 +202,19 @@ def test_gpu_dropin_fast_numerics(tmp_path):
     assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"]
 
 
-def resident_vs_reference(frames, tmp_path, attn_gain, from_mel=False):
+def resident_vs_reference(frames, tmp_path, attn_gain, from_mel=False, mode=None):
     import numpy as np
+    mdir = tmp_path / "model"
     gres = run("pk_encode_gpures", frames, tmp_path, dump=tmp_path / "gpures.f32", attn_gain=attn_gain,
-               from_mel=from_mel)
+               from_mel=from_mel, mode=mode, model_dir=mdir)
     ref = run("pk_encode_ref", frames, tmp_path, dump=tmp_path / "ref.f32", attn_gain=attn_gain,
-              from_mel=from_mel)
+              from_mel=from_mel, mode=mode, model_dir=mdir)
+    assert gres["bits"] == ref["bits"] == MODE_BITS[mode or "mixed"]
     a = np.fromfile(tmp_path / "gpures.f32", dtype=np.float32).reshape(frames, 1024)
     b = np.fromfile(tmp_path / "ref.f32", dtype=np.float32).reshape(frames, 1024)
     dev = float(np.abs(a - b).max() / np.abs(b).max())
-    print(json.dumps({"frames": frames, "from_mel": from_mel, "attn_gain": attn_gain, "threads": THREADS,
+    print(json.dumps({"frames": frames, "mode": mode or "mixed", "from_mel": from_mel, "attn_gain": attn_gain,
+                      "threads": THREADS,
                       "max_rel_deviation": dev, "identical_fraction": float(np.mean(a == b)),
                       "tokens_gpu_resident": gres["n_tokens"], "tokens_reference": ref["n_tokens"],
                       "tokens_equal": gres["tokens_fnv"] == ref["tokens_fnv"],
@@ -211,5 +275,20 @@ def test_gpu_resident_encoder_from_mel(frames, tmp_path):
     pk_gpu_encoder_run_mel (pre-encode on the device, bit-identical, then the
     resident blocks), trained-like attention weights; token ids equal."""
     gres, ref, dev = resident_vs_reference(frames, tmp_path, 0.05, from_mel=True)
+    assert dev <= 1e-3
+    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"]
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("mode", ["int8", "fp32"])
+def test_gpu_resident_encoder_weight_directories(mode, tmp_path):
+    """The device-resident encoder on the int8 and fp32 weight directories'
+    models (every block linear int8, or every one fp32, including the fused
+    QKV and the position projection), 900 frames from mel, trained-like
+    attention weights: pre-encode's int8 or fp32 output projection, then the
+    blocks; within 1e-3 of the reference and token ids equal, as for the
+    mixed model."""
+    gres, ref, dev = resident_vs_reference(900, tmp_path, 0.05, from_mel=True, mode=mode)
     assert dev <= 1e-3
     assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"]
