@@ -73,6 +73,16 @@ def test_reference_drivers_cpu(tmp_path):
     assert ref["enc_fnv"] != x86["enc_fnv"]
 
 
+@pytest.fixture
+def model_dir(tmp_path):
+    """A directory that keeps one written model for the runs of a test (the
+    fp32 model is 2.3 GB), removed when the test ends."""
+    import shutil
+    d = tmp_path / "model"
+    yield d
+    shutil.rmtree(d, ignore_errors=True)
+
+
 # the formats pk_load_weights builds from each weight directory
 MODE_BITS = {
     "mixed": {"ff_linear1": 4, "ff_linear2": 4, "qkv": 8, "pos": 8, "out": 8, "pre_encode_out": 8},
@@ -81,14 +91,14 @@ MODE_BITS = {
 }
 
 
-def test_reference_driver_int8_model_cpu(tmp_path):
+def test_reference_driver_int8_model_cpu(tmp_path, model_dir):
     """CPU only: the int8 weight directory's model (every matmul weight int8,
     FF linears included) loads through pk_load_weights with the formats the
     reference builds, and the portable and x86 builds agree bit for bit (the
     x86 build differs only in its int4 unpack, which this model does not
     use)."""
-    ref = run("pk_encode_ref", 48, tmp_path, mode="int8", model_dir=tmp_path / "m")
-    x86 = run("pk_encode_ref_x86", 48, tmp_path, mode="int8", model_dir=tmp_path / "m")
+    ref = run("pk_encode_ref", 48, tmp_path, mode="int8", model_dir=model_dir)
+    x86 = run("pk_encode_ref_x86", 48, tmp_path, mode="int8", model_dir=model_dir)
     assert ref["bits"] == MODE_BITS["int8"] and x86["bits"] == MODE_BITS["int8"]
     assert ref["finite"] == 1 and ref["enc_fnv"] == x86["enc_fnv"]
     assert ref["tokens_fnv"] == x86["tokens_fnv"]
@@ -97,7 +107,7 @@ def test_reference_driver_int8_model_cpu(tmp_path):
 @pytest.mark.gpu
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("mode", ["int8", "fp32"])
-def test_gpu_dropin_weight_directories(mode, tmp_path):
+def test_gpu_dropin_weight_directories(mode, tmp_path, model_dir):
     """The reference's other two weight directories through the GEMM drop-in,
     900 frames (chunks of 408/416/108 rows): int8 (every matmul weight int8,
     so the FF linears take cblas_sgemm_qb at K = 1024 and 4096) and fp32
@@ -106,10 +116,9 @@ def test_gpu_dropin_weight_directories(mode, tmp_path):
     Makefile builds it on x86 (AVX2 weight GEMMs) must agree bit for bit
     too: encoder output and greedy token ids."""
     frames = 900
-    mdir = tmp_path / "model"
-    gpu = run("pk_encode_gpu", frames, tmp_path, mode=mode, model_dir=mdir)
-    ref = run("pk_encode_ref", frames, tmp_path, mode=mode, model_dir=mdir)
-    x86 = run("pk_encode_ref_x86", frames, tmp_path, mode=mode, model_dir=mdir)
+    gpu = run("pk_encode_gpu", frames, tmp_path, mode=mode, model_dir=model_dir)
+    ref = run("pk_encode_ref", frames, tmp_path, mode=mode, model_dir=model_dir)
+    x86 = run("pk_encode_ref_x86", frames, tmp_path, mode=mode, model_dir=model_dir)
     assert gpu["bits"] == ref["bits"] == MODE_BITS[mode]
     assert gpu["finite"] == 1 and gpu["chunked"] == ref["chunked"] == 1
     assert gpu["enc_fnv"] == ref["enc_fnv"] == x86["enc_fnv"], "encoder outputs differ"
@@ -203,8 +212,17 @@ def test_gpu_dropin_fast_numerics(tmp_path):
 
 
 def resident_vs_reference(frames, tmp_path, attn_gain, from_mel=False, mode=None):
-    import numpy as np
+    import shutil
+
     mdir = tmp_path / "model"
+    try:
+        return _resident_vs_reference(frames, tmp_path, attn_gain, from_mel, mode, mdir)
+    finally:
+        shutil.rmtree(mdir, ignore_errors=True)
+
+
+def _resident_vs_reference(frames, tmp_path, attn_gain, from_mel, mode, mdir):
+    import numpy as np
     gres = run("pk_encode_gpures", frames, tmp_path, dump=tmp_path / "gpures.f32", attn_gain=attn_gain,
                from_mel=from_mel, mode=mode, model_dir=mdir)
     ref = run("pk_encode_ref", frames, tmp_path, dump=tmp_path / "ref.f32", attn_gain=attn_gain,
