@@ -26,13 +26,35 @@ def _ptr(a):
     return ctypes.c_void_p(a.ctypes.data)
 
 
+# int8 codes uniform in [-127, 127] have standard deviation 127/sqrt(3)
+I8_CODE_STD = 73.32
+
+
 class Block:
-    def __init__(self, seed, qkv_bits=8, attn_scale=0.01):
+    """One conformer block's parameters with random values.  mode picks the
+    weight directory whose formats the linears take (download_weights.py:20):
+    "mixed" (int4 FF linears, int8 attention projections), "int8" (every
+    linear int8, FF scale 0.0008) or "fp32" (every linear fp32, with the
+    int8 weights' spread).  The mixed model's values do not depend on the
+    other modes' code paths (same draws in the same order)."""
+
+    def __init__(self, seed, qkv_bits=8, attn_scale=0.01, mode="mixed"):
+        assert mode in ("mixed", "int8", "fp32")
         rng = np.random.default_rng(seed)
         self.keep = []
         f32 = lambda a: self._keep(np.ascontiguousarray(a, dtype=np.float32))
         normal = lambda shape, s: f32(rng.standard_normal(shape) * s)
         w = pk.BlockWeights()
+
+        def ff(K, N):
+            if mode == "int8":
+                return i8(K, N, 0.0008)
+            if mode == "fp32":
+                return fp(K, N, 0.06)
+            return i4(K, N)
+
+        def proj(K, N, scale):
+            return fp(K, N, scale * I8_CODE_STD) if mode == "fp32" else i8(K, N, scale)
 
         def i4(K, N):
             data = self._keep(rng.integers(0, 256, (K, N // 2), dtype=np.uint8))
@@ -51,21 +73,21 @@ class Block:
             return f32(1.0 + rng.standard_normal(D) * 0.1).ctypes.data, normal(D, 0.1).ctypes.data
 
         w.norm_ff1_w, w.norm_ff1_b = ln()
-        w.ff1_linear1_w, w.ff1_linear1_b = i4(D, FF), normal(FF, 0.02).ctypes.data
-        w.ff1_linear2_w, w.ff1_linear2_b = i4(FF, D), normal(D, 0.02).ctypes.data
+        w.ff1_linear1_w, w.ff1_linear1_b = ff(D, FF), normal(FF, 0.02).ctypes.data
+        w.ff1_linear2_w, w.ff1_linear2_b = ff(FF, D), normal(D, 0.02).ctypes.data
         w.norm_sa_w, w.norm_sa_b = ln()
-        w.linear_qkv_w = i8(D, 3 * D, attn_scale) if qkv_bits == 8 else fp(D, 3 * D)
+        w.linear_qkv_w = proj(D, 3 * D, attn_scale) if qkv_bits == 8 else fp(D, 3 * D)
         w.linear_qkv_b = normal(3 * D, 0.02).ctypes.data
-        w.linear_pos_w = i8(D, D, attn_scale)
-        w.linear_out_w, w.linear_out_b = i8(D, D, attn_scale), normal(D, 0.02).ctypes.data
+        w.linear_pos_w = proj(D, D, attn_scale)
+        w.linear_out_w, w.linear_out_b = proj(D, D, attn_scale), normal(D, 0.02).ctypes.data
         w.pos_bias_u, w.pos_bias_v = normal(D, 0.02).ctypes.data, normal(D, 0.02).ctypes.data
         w.norm_conv_w, w.norm_conv_b = ln()
         w.conv_pw1_w, w.conv_pw1_b = normal((2 * D, D), 0.02).ctypes.data, normal(2 * D, 0.02).ctypes.data
         w.conv_dw_w, w.conv_dw_b = normal((D, KCONV), 1.0 / 3.0).ctypes.data, normal(D, 0.02).ctypes.data
         w.conv_pw2_w, w.conv_pw2_b = normal((D, D), 0.02).ctypes.data, normal(D, 0.02).ctypes.data
         w.norm_ff2_w, w.norm_ff2_b = ln()
-        w.ff2_linear1_w, w.ff2_linear1_b = i4(D, FF), normal(FF, 0.02).ctypes.data
-        w.ff2_linear2_w, w.ff2_linear2_b = i4(FF, D), normal(D, 0.02).ctypes.data
+        w.ff2_linear1_w, w.ff2_linear1_b = ff(D, FF), normal(FF, 0.02).ctypes.data
+        w.ff2_linear2_w, w.ff2_linear2_b = ff(FF, D), normal(D, 0.02).ctypes.data
         w.norm_out_w, w.norm_out_b = ln()
         self.w = w
 

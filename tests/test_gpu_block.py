@@ -224,6 +224,28 @@ def test_encoder_block_workload_stats_within_tolerance(dev):
         e.close()
 
 
+@pytest.mark.parametrize("mode", ["int8", "fp32"])
+@pytest.mark.parametrize("T,chunk", [(300, 0), (132, 64)])
+def test_encoder_weight_directories_bit_exact_to_oracle(dev, mode, T, chunk):
+    """The resident encoder with the int8 weight directory's formats (every
+    linear int8, the FF linears included) and the fp32 one's (every linear
+    fp32: QKV, position and output projections on the fp32 chains), two
+    blocks, bit for bit against the oracle's encoder on the same blocks: an
+    unchunked 300-frame sequence (softmax's scalar tail) and 64-frame chunks
+    of 72, 76 and 12 rows."""
+    blocks = [bg.Block(0xD1500 + i, attn_scale=0.0005, mode=mode) for i in range(2)]
+    assert {blocks[0].w.ff1_linear1_w.bits, blocks[0].w.linear_out_w.bits} == \
+        {8 if mode == "int8" else 32}
+    e = Encoder(dev, blocks, bg.pe_table())
+    try:
+        x = rows(T, 1024)
+        want = po.encoder(e.arr, 2, e.pe, 4999, x, chunk, 8)
+        got = e.run(x, chunk=chunk)
+        assert bits_equal(got, want), describe_mismatch(got, want)
+    finally:
+        e.close()
+
+
 def test_encoder_chunk_batch_equals_chunks_alone(dev, enc2):
     """Chunked mode runs all chunks as one batch (GEMMs over every chunk's
     rows, attention and depthwise per chunk length); each chunk's rows must
