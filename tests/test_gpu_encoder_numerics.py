@@ -44,10 +44,16 @@ def model():
 
 
 def run(m, x, chunk, mode, overlap=8):
+    return run_blocks(m.blocks, bench.N_BLOCKS, m.pe, x, chunk, mode, overlap)
+
+
+def run_blocks(blocks, n_blocks, pe, x, chunk, mode, overlap=8):
+    """Two runs (graph capture, then replay) of an encoder over n_blocks of
+    the ctypes block array `blocks` under numerics `mode`."""
     import torch
     enc = ctypes.c_void_p()
-    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(m.blocks, ctypes.c_void_p),
-            bench.N_BLOCKS, m.pe.ctypes.data, bench.PE_ROWS, bench.PE_CENTER)
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(blocks, ctypes.c_void_p),
+            n_blocks, pe.ctypes.data, pe.shape[0], bench.PE_CENTER)
     try:
         pk.call("pk_gpu_encoder_set_numerics", enc, mode)
         assert pk.load().pk_gpu_encoder_get_numerics(enc) == mode
@@ -98,6 +104,29 @@ def test_fast_mode_within_tolerance(model, T, chunk):
     print(f"T {T} chunk {chunk}: fast max |out - oracle| / max |oracle| = {e:.3g}", flush=True)
     assert e <= TOL, e
     assert bits_equal(got[1], got[0]), "fast replay differs from its capture run"
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp32"])
+@pytest.mark.parametrize("T,chunk,mode", [(33, 0, "default"), (300, 140, "fast")])
+def test_weight_directories_tolerance_modes(model, fmt, T, chunk, mode):
+    """Four blocks in the int8 weight directory's formats (every linear int8,
+    the FF linears included) or the fp32 one's (every linear fp32), trained-
+    like attention weights: a 33-frame clip under the default setting (small-M
+    kernels) and 300 frames in chunks of 140 under the fast one (split
+    kernels, two row groups), within 1e-3 of the oracle's exact encoder;
+    replays repeat the first run bit for bit."""
+    import blockgen as bg
+    blocks = [bg.Block(0xD1600 + i, attn_scale=0.0005, mode=fmt) for i in range(4)]
+    arr, pe = bg.block_array(blocks), bg.pe_table()
+    numerics = pk.NUMERICS_DEFAULT if mode == "default" else pk.NUMERICS_FAST
+    x = bench.enc_rng(0xFEA8, T).standard_normal((T, bench.D)).astype(np.float32)
+    ov = 8 if chunk else 0
+    want = po.encoder(arr, 4, pe, bench.PE_CENTER, x, chunk, ov)
+    got = run_blocks(arr, 4, pe, x, chunk, numerics, ov)
+    e = rel_dev(got[0], want)
+    print(f"{fmt} T {T} chunk {chunk} {mode}: max |out - oracle| / max |oracle| = {e:.3g}", flush=True)
+    assert e <= TOL, e
+    assert bits_equal(got[1], got[0]), "replay differs from its capture run"
 
 
 def test_long_input_unaffected(model):
