@@ -229,11 +229,14 @@ def _host_call(kind, M, N, K, A, lda, W, extra, C, ldc, alpha, beta):
 
 @pytest.mark.parametrize("kind", ["f32", "i8", "i4"])
 @pytest.mark.parametrize("resident", [False, True])
-def test_host_pointer_dropin_strided(dev, kind, resident):
-    """pk_gpu_gemm_* on host memory with lda > K and ldc > N, beta != 0;
-    with the weight staged per call or resident after registration."""
-    M, N, K = 45, 96, 130
-    lda, ldc = K + 7, N + 5
+@pytest.mark.parametrize("M,pad", [(45, True), (45, False), (1, True)])
+def test_host_pointer_dropin_strided(dev, kind, resident, M, pad):
+    """pk_gpu_gemm_* on host memory, beta != 0, with the weight staged per
+    call or resident after registration: lda > K and ldc > N (rows copied
+    with their pitches), contiguous rows (one linear copy per operand), and a
+    single strided row (one linear copy of the row)."""
+    N, K = 96, 130
+    lda, ldc = (K + 7, N + 5) if pad else (K, N)
     A, W, extra, C0 = make(kind, M, N, K, f"host.{kind}")
     Apad = np.zeros((M, lda), np.float32)
     Apad[:, :K] = A
