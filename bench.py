@@ -204,13 +204,16 @@ def alg_bytes(kind, m, n, k):
 
 
 def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, force_config=-1,
-              numerics="default", split_k=True):
+              numerics="default", split_k=True, panel=True):
     """One JSON line per GEMM shape ("kind:MxNxK"): resident inputs, weights
     rotating over enough replicas to exceed the Infinity Cache, average launch
     time from HIP events around a graph replay of `steps` launches (eager: the
     same launches from a host loop, for profilers that trace kernels one by
     one; its average includes the host's launch gaps).  split_k: the calls
-    have a split-K workspace (pk_gpu_set_workspace), which fast numerics use."""
+    have a split-K workspace (pk_gpu_set_workspace), which fast numerics and
+    the panel kernels use.  panel: every replica of a small-M shape (M <= 64)
+    gets its panel (pk_gpu_pack_weight_dev, a one-time repack outside the
+    timed region, as registration makes it), so the panel kernels run."""
     import torch
     pk = load_binding()
     pk.call("pk_gpu_init", 0)
@@ -248,6 +251,16 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
             W = [torch.randn((k, n), device=dev, generator=g) * 0.02 for _ in range(reps)]
             call = lambda i: lib.pk_gpu_sgemm_dev(m, n, k, 1.0, A.data_ptr(), k, W[i % reps].data_ptr(),
                                                   n, 0.0, C.data_ptr(), n, cur())
+        bits = {"i4": 4, "i8": 8}.get(kind, 32)
+        ldb = n // 2 if kind == "i4" else n
+        packed = []
+        if panel and m <= 64 and k % 32 == 0 and numerics != "exact":
+            for r in range(reps):
+                pk.call("pk_gpu_pack_weight_dev", bits, k, n, W[r].data_ptr(), ldb,
+                        S[r].data_ptr() if kind == "i4" else None, cur())
+                packed.append(W[r].data_ptr())
+        uses_panel = bool(lib.pk_gpu_uses_panel(m, n, k, bits, W[0].data_ptr(), ldb,
+                                                S[0].data_ptr() if kind == "i4" else None))
         for i in range(warmup):
             assert call(i) == 0, lib.pk_gpu_last_error()
         torch.cuda.synchronize(dev)
@@ -276,15 +289,16 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
         us = e0.elapsed_time(e1) / steps * 1e3
         tf = 2.0 * m * n * k / us / 1e6
         gbs = alg_bytes(kind, m, n, k) / us / 1e3
-        bits = {"i4": 4, "i8": 8}.get(kind, 32)
         small_m = bool(lib.pk_gpu_uses_small_m(m, n, k, bits))
         split = bool(lib.pk_gpu_uses_split(m, n, k, bits))
         print(json.dumps({"gemm": f"{kind} {m}x{n}x{k}",
-                          "kernel": "small-M (bf16 split, tolerance path)" if small_m else
+                          "kernel": "panel (small-M on repacked weights, tolerance path)" if uses_panel else
+                                    "small-M (bf16 split, tolerance path)" if small_m else
                                     "split (bf16 split, tolerance path)" if split else
                                     "exact chains",
                           "numerics": numerics,
-                          "k_segments": lib.pk_gpu_split_k_segments(m, n, k, bits) if split else None,
+                          "k_segments": lib.pk_gpu_panel_segments(m, n, k) if uses_panel else
+                                        lib.pk_gpu_split_k_segments(m, n, k, bits) if split else None,
                           "config": None if small_m or split else
                                     (force_config if force_config >= 0 else
                                      lib.pk_gpu_pick_config_bits(m, n, k, bits)),
@@ -293,6 +307,8 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
                           "frac_mfma_fp32": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_replicas": reps,
                           "steps": steps}), flush=True)
+        for ptr in packed:
+            pk.call("pk_gpu_unpack_weight_dev", ptr)
         del W, A, C
         torch.cuda.empty_cache()
 
@@ -1079,7 +1095,9 @@ def main():
     ap.add_argument("--numerics", choices=["default", "exact", "fast"], default="default",
                     help="with --gemm: the PK_GPU_NUMERICS_* mode of the timed calls")
     ap.add_argument("--no-split-k", action="store_true",
-                    help="with --gemm: no split-K workspace for fast numerics")
+                    help="with --gemm: no split-K workspace (fast numerics and panel kernels)")
+    ap.add_argument("--no-panel", action="store_true",
+                    help="with --gemm: no panel copies of the weights (the small-M narrow kernels)")
     ap.add_argument("--eager", action="store_true",
                     help="with --gemm: launch from a host loop instead of a graph replay "
                          "(for kernel tracers)")
@@ -1094,7 +1112,7 @@ def main():
     if args.gemm:
         gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup,
                   eager=args.eager, force_config=args.force_config, numerics=args.numerics,
-                  split_k=not args.no_split_k)
+                  split_k=not args.no_split_k, panel=not args.no_panel)
         return
     if args.ffn:
         args.steps = args.steps or 200

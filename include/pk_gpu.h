@@ -45,7 +45,8 @@ typedef enum {
     PK_GPU_ENOTSUP  = -2,   /* form the reference call sites never use       */
     PK_GPU_ENOMEM   = -3,   /* device or pinned allocation failed            */
     PK_GPU_EHIP     = -4,   /* HIP runtime or launch error                   */
-    PK_GPU_ENODEV   = -5    /* no gfx950 device                              */
+    PK_GPU_ENODEV   = -5,   /* no gfx950 device                              */
+    PK_GPU_EBUSY    = -6    /* a call on another thread is using the weight  */
 } pk_gpu_status;
 
 /* Select the device (-1: $PK_GPU_DEVICE or 0) and check it is gfx950.
@@ -67,11 +68,12 @@ const char *pk_gpu_last_error(void);
  * read-only mmap'd or load-time buffers, weights.c:294-302, 404-546).
  * Registering an overlapping range is PK_GPU_EINVAL. */
 int pk_gpu_register_weight(const void *host, size_t bytes);
-/* Later calls no longer find the range; the device copy is freed after the
- * work queued on the device (a host-pointer GEMM that already found it keeps
- * it until that call returns).  Unregister only while no thread is in a
- * GEMM call that reads the weight: unregistering during such calls is not
- * supported. */
+/* Later calls no longer find the range; the device copy (and any panel
+ * made from it, pk_gpu_pack_weight_dev) is freed on the calling thread after
+ * the work queued on the device.  While a host-pointer GEMM on another thread
+ * is reading the weight it returns PK_GPU_EBUSY and changes nothing: try
+ * again after that call.  Device-pointer work that reads the copy through
+ * pk_gpu_device_ptr must be queued before the unregister. */
 int pk_gpu_unregister_weight(const void *host);
 /* Device address of a registered host pointer (or NULL), valid until the
  * weight is unregistered. */
@@ -493,6 +495,49 @@ int pk_gpu_dequant_dev(int bits, int K, int N, const void *dB, int ldb, float sc
  * hook with no counterpart in the reference.  Returns PK_GPU_EINVAL for
  * other values. */
 int pk_gpu_force_small_tile(int rb, int nct);
+/* ---- panels: weights repacked for the small-M kernels ------------------
+ * No counterpart in the reference (its weights stay in their on-disk
+ * layout, weights.c:240-266).  A panel is a copy of one weight re-laid out
+ * once in the matrix cores' operand order (int8 / int4 codes, int4 scales
+ * transposed to [N/32][K], fp32 weights as bf16 hi and lo halves), which the
+ * small-M kernels (M <= 64, PK_GPU_NUMERICS_DEFAULT or _FAST) read instead
+ * of the [K][ldb] weight: same products, same tolerance, faster.  A
+ * host-pointer GEMM makes the panel of a registered weight (and, for int4,
+ * registered scales) on its first small-M use; device callers ask for one
+ * here.  Panels cost panel bytes of device memory: int8 about K*N, int4
+ * K*N/2 + K*N/8, fp32 4*K*N. */
+
+/* Make the panel of device weight dB (bits 4, 8 or 32; K a multiple of 32;
+ * int4: N a multiple of 32 and its scales dscales [K][N/32]) for later
+ * *_dev / *_ex_dev GEMMs whose B is dB with the same bits, K, N, ldb (and
+ * dscales).  Runs on `stream` and waits for it; not during stream capture.
+ * Idempotent for the same parameters; PK_GPU_EINVAL if dB already has a
+ * panel of another shape.  The weight's bytes must not change afterwards. */
+int pk_gpu_pack_weight_dev(int bits, int K, int N, const void *dB, int ldb,
+                           const float *dscales, void *stream);
+/* Free the panel made for dB by pk_gpu_pack_weight_dev (after the device's
+ * queued work); PK_GPU_EBUSY while a host-pointer call reads it. */
+int pk_gpu_unpack_weight_dev(const void *dB);
+/* Device bytes held by panels. */
+size_t pk_gpu_panel_bytes(void);
+/* Whether a GEMM on this thread with this shape, format and weight (and, for
+ * int4, scales) would take the panel kernels, given aligned A rows. */
+int pk_gpu_uses_panel(int M, int N, int K, int bits, const void *dB, int ldb,
+                      const float *dscales);
+/* Segments of K over workgroups that a panel GEMM of this shape takes with
+ * this thread's workspace (pk_gpu_set_workspace): above one, each workgroup
+ * stores its partial tile there and a second launch sums them in segment
+ * order before alpha, beta, bias and the epilogue (deterministic). */
+int pk_gpu_panel_segments(int M, int N, int K);
+/* Test hook: the weights as the panel kernels multiply them, to dout [K][N]
+ * on `stream`: int8 fl(q * B_scale), int4 fl(q * s[k][n/32]), fp32 hi + lo. */
+int pk_gpu_panel_decode_dev(int bits, int K, int N, const void *dB, int ldb,
+                            const float *dscales, float B_scale, float *dout, void *stream);
+/* Tuning and test hook: the panel workgroup tile for later calls on this
+ * thread, mb 16-row blocks (1..4; more rows than mb * 16 go to more
+ * workgroups) and nct 16-column tiles (1..2); (0, 0) = the default choice. */
+int pk_gpu_force_panel_tile(int mb, int nct);
+
 /* Force a configuration for later calls on this thread (-1 = automatic),
  * encoder runs included: an encoder keeps its captured graphs per forced
  * configuration, so a change takes effect on the next run. */

@@ -52,6 +52,9 @@ struct GemmProblem {
     // of the fp32 row.  launch_gemm refuses the problem if the split kernels
     // do not take it.
     bool a_presplit = false;
+    // The weight's panel copy (launch_pack of this B, scales, K and N), or
+    // null.  With it, the small-M path takes the panel kernels.
+    const void* panel = nullptr;
 };
 
 // Partial tiles of one split-K launch: at most 256 workgroups of at most
@@ -100,6 +103,35 @@ bool smallm_force_tile(int rb, int nct);
 // Launch on `stream`; hipErrorNotSupported if the shape is not handled (the
 // caller then takes the exact kernels).
 hipError_t launch_smallm(const GemmProblem& p, hipStream_t stream);
+
+// ---- panel kernels (pk_panel.hip): small-M GEMMs on repacked weights ------
+// Bytes of a weight's panel copy (0 if K is not a multiple of 32): int8
+// ceil(N/16)*16*K, int4 half that plus the scales [N/32][K], fp32 4*that
+// (bf16 hi and lo halves).
+size_t panel_bytes(WeightKind kind, int K, int N);
+// Write the panel copy of B [K][ldb] (int4: and its scales [K][N/32]) to
+// `panel` (panel_bytes of device memory) on `stream`.
+hipError_t launch_pack(WeightKind kind, int K, int N, const void* B, int ldb, const float* scales,
+                       void* panel, hipStream_t stream);
+// The weights as the panel kernels multiply them, to out [K][N] (int8 with
+// `scale`): for tests of the repack.
+hipError_t launch_panel_decode(WeightKind kind, int K, int N, const void* panel, float scale, float* out,
+                               hipStream_t stream);
+// Whether the panel kernels take a problem (p.panel set, M <= 64, K % 32 ==
+// 0, 16-byte aligned A rows, int4 N % 32 == 0, alpha and scale nonzero, no
+// chain bias).
+bool panel_supports(const GemmProblem& p);
+// K segments over workgroups a problem takes (> 1 only with p.work: the
+// partial tiles are summed by a second launch).
+int panel_segments(const GemmProblem& p);
+// k of one LDS phase for a workgroup of `rows` rows.
+int panel_phase_k(int rows);
+// The workgroup tile a problem takes: mb 16-row blocks, nct 16-column tiles.
+void panel_tile(const GemmProblem& p, int* mb, int* nct);
+// Force the workgroup tile (mb 1..4, nct 1..2) on the calling thread ((0,
+// 0): the default); false if out of range.
+bool panel_force_tiles(int mb, int nct);
+hipError_t launch_panel(const GemmProblem& p, hipStream_t stream);
 
 // Whether a shape and its operands suit the split kernels (pk_split.hip):
 // any M, K % 32 == 0, N % 32 == 0, 16-byte aligned A rows, dword-aligned

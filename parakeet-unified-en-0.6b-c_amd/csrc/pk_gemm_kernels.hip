@@ -150,6 +150,10 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
         return launch_split(p, stream);
     }
     if (tol != TOL_NONE && cfg_index < 0) {
+        if (panel_supports(p)) {
+            const hipError_t e = launch_panel(p, stream);
+            if (e != hipErrorNotSupported) return e;
+        }
         if (smallm_supports(p)) {
             const hipError_t e = launch_smallm(p, stream);
             if (e != hipErrorNotSupported) return e;

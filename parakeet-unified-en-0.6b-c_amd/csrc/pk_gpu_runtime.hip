@@ -44,9 +44,10 @@ void* g_noalloc_base[kMaxDevices] = {};  // written at initialisation, under g_m
 std::mutex g_noalloc_mu;
 
 // A registered weight's device copy.  Host-pointer GEMMs hold a reference
-// from the lookup until their stream has finished, so an unregister on
-// another thread only removes the entry; the copy is freed (after the
-// device's queued work) when the last holder lets go.
+// from the lookup (taken under g_mu) until their stream has finished; while
+// one does, pk_gpu_unregister_weight refuses (PK_GPU_EBUSY), so the copy is
+// freed on the unregistering thread (or at shutdown), after the device's
+// queued work.
 struct Resident {
     size_t bytes = 0;
     void* dev = nullptr;
@@ -64,6 +65,28 @@ struct Resident {
 std::map<uintptr_t, std::shared_ptr<Resident>>& g_weights =
     *new std::map<uintptr_t, std::shared_ptr<Resident>>;
 size_t g_resident_bytes = 0;
+
+// A weight's panel copy (pk_panel.hip): the layout the small-M kernels read,
+// made once from the weight at a device address with the shape and format it
+// is multiplied with.  Made by pk_gpu_pack_weight_dev, or by a host-pointer
+// GEMM from a registered weight's resident copy (owner: that copy's base;
+// unregistering the weight frees its panels).
+struct Panel {
+    pkgpu::WeightKind kind = pkgpu::W_F32;
+    int K = 0, N = 0, ldb = 0;
+    const void* scales = nullptr;   // int4: the device scales it was made from
+    uintptr_t owner = 0;            // resident copy it was made from (0: a device weight)
+    void* dev = nullptr;
+    size_t bytes = 0;
+    Panel() = default;
+    Panel(const Panel&) = delete;
+    Panel& operator=(const Panel&) = delete;
+    ~Panel() { (void)hipFree(dev); }   // hipFree waits for the device's queued work
+};
+// weight device address -> its panel; never destroyed (see g_weights)
+std::map<uintptr_t, std::shared_ptr<Panel>>& g_panels = *new std::map<uintptr_t, std::shared_ptr<Panel>>;
+size_t g_panel_bytes = 0;
+std::mutex g_pack_mu;           // one panel made at a time (host-pointer GEMMs)
 
 thread_local std::string t_err;
 thread_local int t_force_cfg = -1;
@@ -283,23 +306,96 @@ bool does_multiply(const GemmProblem& p)
            !(p.kind == pkgpu::W_I8 && p.scale == 0.0f);
 }
 
+// The panel made from weight p.B with p's format and shape, or null; *hold
+// (if given) keeps it alive.
+const void* panel_for(const GemmProblem& p, std::shared_ptr<Panel>* hold = nullptr)
+{
+    if (!p.B) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_panels.find(reinterpret_cast<uintptr_t>(p.B));
+    if (it == g_panels.end()) return nullptr;
+    const Panel& q = *it->second;
+    if (q.kind != p.kind || q.K != p.K || q.N != p.N || q.ldb != p.ldb ||
+        (p.kind == pkgpu::W_I4 && q.scales != p.scales))
+        return nullptr;
+    if (hold) *hold = it->second;
+    return q.dev;
+}
+
+// Whether a call may leave the exact chains (this thread's numerics, no
+// forced tile) and has the small-M kernels' shape.
+bool small_m_call(const GemmProblem& p, bool tol_ok)
+{
+    return tol_ok && t_force_cfg < 0 && t_numerics != PK_GPU_NUMERICS_EXACT &&
+           p.M > 0 && p.M <= pkgpu::kSmallMaxM;
+}
+
 // tol_ok: the call may leave the exact chains as this thread's numerics
-// allow (the public GEMM entry points, unless a tile is forced).
-int launch(const GemmProblem& p, hipStream_t s, bool tol_ok)
+// allow (the public GEMM entry points, unless a tile is forced).  The small-M
+// kernels read the weight's panel when one was made for it.
+int launch(const GemmProblem& p, hipStream_t s, bool tol_ok, std::shared_ptr<Panel>* hold = nullptr)
 {
     const pkgpu::Tolerance tol =
         tol_ok && t_force_cfg < 0 ? pkgpu::rt::tolerance_of(t_numerics) : pkgpu::TOL_NONE;
     GemmProblem q = p;
-    if (tol == pkgpu::TOL_ALL) {
+    if (tol != pkgpu::TOL_NONE) {
         q.work = t_work;
         q.work_bytes = t_work_bytes;
     }
+    if (small_m_call(p, tol_ok)) q.panel = panel_for(p, hold);
     const hipError_t e = pkgpu::launch_gemm(q, s, t_force_cfg, tol);
     if (e == hipErrorInvalidValue)
         return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
                     p.M, p.N, p.K);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return PK_GPU_OK;
+}
+
+// Make the panel of device weight p.B (format, K, N, ldb, scales of p) on
+// stream s and register it; owner: the resident copy it lies in (0: none).
+// A panel already made for p.B with the same parameters is kept.  The panel
+// is complete when this returns (the stream is synchronised).
+int make_panel(const GemmProblem& p, uintptr_t owner, hipStream_t s)
+{
+    const size_t bytes = pkgpu::panel_bytes(p.kind, p.K, p.N);
+    if (!bytes) return fail(PK_GPU_EINVAL, "panel: K = %d is not a multiple of 32", p.K);
+    auto pn = std::make_shared<Panel>();
+    pn->kind = p.kind;
+    pn->K = p.K;
+    pn->N = p.N;
+    pn->ldb = p.ldb;
+    pn->scales = p.kind == pkgpu::W_I4 ? p.scales : nullptr;
+    pn->owner = owner;
+    pn->bytes = bytes;
+    hipError_t e = hipMalloc(&pn->dev, bytes);
+    if (e != hipSuccess) {
+        pn->dev = nullptr;
+        return fail(PK_GPU_ENOMEM, "panel: device alloc of %zu bytes failed", bytes);
+    }
+    e = pkgpu::launch_pack(p.kind, p.K, p.N, p.B, p.ldb, p.scales, pn->dev, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "panel: repack");
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto& slot = g_panels[reinterpret_cast<uintptr_t>(p.B)];
+    if (slot) return fail(PK_GPU_EINVAL, "panel: weight %p already has a panel of another shape", p.B);
+    slot = pn;
+    g_panel_bytes += bytes;
+    return PK_GPU_OK;
+}
+
+// The panel of a resident weight, made on first use by a small-M call.
+int make_resident_panel(const GemmProblem& p, uintptr_t owner, hipStream_t s)
+{
+    if (panel_for(p) || !pkgpu::panel_bytes(p.kind, p.K, p.N) || (p.kind == pkgpu::W_I4 && p.N % 32))
+        return PK_GPU_OK;
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    if (panel_for(p)) return PK_GPU_OK;             // another thread made it meanwhile
+    {
+        std::lock_guard<std::mutex> lk2(g_mu);
+        if (g_panels.count(reinterpret_cast<uintptr_t>(p.B)))
+            return PK_GPU_OK;                       // made for another shape: keep the narrow kernels
+    }
+    return make_panel(p, owner, s);
 }
 
 // Host-pointer GEMM: stage what is not resident, run, copy C back, wait.
@@ -354,7 +450,14 @@ int host_gemm(GemmProblem p, const float* hA, const void* hB, const float* hScal
     const int ldc_host = p.ldc;
     p.C = static_cast<float*>(dC);
     p.ldc = p.N;
-    rc = launch(p, c->stream, true);
+    // a registered weight (and, for int4, registered scales) that the small-M
+    // kernels will read gets its panel on first use
+    if (mul && hold[1] && (p.kind != pkgpu::W_I4 || hold[2]) && small_m_call(p, true)) {
+        rc = make_resident_panel(p, reinterpret_cast<uintptr_t>(hold[1]->dev), c->stream);
+        if (rc) return rc;
+    }
+    std::shared_ptr<Panel> panel_hold;
+    rc = launch(p, c->stream, true, &panel_hold);
     if (rc) return rc;
     e = copy_rows(hC, (size_t)ldc_host * 4, dC, (size_t)p.N * 4, (size_t)p.N * 4, p.M,
                   hipMemcpyDeviceToHost, c->stream);
@@ -412,7 +515,10 @@ int noalloc_gemm(GemmProblem p, const float* hA, const void* hB, float* hC, size
         } else {
             e = copy_rows(dA, (size_t)p.K * 4, hA, (size_t)p.lda * 4, (size_t)p.K * 4, p.M,
                           hipMemcpyHostToDevice, s);
-            if (e != hipSuccess) return hip_fail(e, "A upload");
+            if (e != hipSuccess) {
+                (void)hipStreamSynchronize(s);      // the array is free again when the lock is
+                return hip_fail(e, "A upload");
+            }
             p.A = reinterpret_cast<const float*>(dA);
             p.lda = p.K;
         }
@@ -421,7 +527,10 @@ int noalloc_gemm(GemmProblem p, const float* hA, const void* hB, float* hC, size
         } else {
             e = copy_rows(dB, (size_t)b_cols * b_elem, hB, (size_t)p.ldb * b_elem,
                           (size_t)b_cols * b_elem, p.K, hipMemcpyHostToDevice, s);
-            if (e != hipSuccess) return hip_fail(e, "B upload");
+            if (e != hipSuccess) {
+                (void)hipStreamSynchronize(s);
+                return hip_fail(e, "B upload");
+            }
             p.B = dB;
             p.ldb = b_cols;
         }
@@ -429,7 +538,10 @@ int noalloc_gemm(GemmProblem p, const float* hA, const void* hB, float* hC, size
     if (p.beta != 0.0f) {
         e = copy_rows(dC, (size_t)p.N * 4, hC, (size_t)p.ldc * 4, (size_t)p.N * 4, p.M,
                       hipMemcpyHostToDevice, s);
-        if (e != hipSuccess) return hip_fail(e, "C upload");
+        if (e != hipSuccess) {
+            (void)hipStreamSynchronize(s);
+            return hip_fail(e, "C upload");
+        }
     }
     const int ldc_host = p.ldc;
     p.C = dC;
@@ -475,13 +587,17 @@ void pk_gpu_shutdown(void)
 {
     std::vector<ThreadCtx*> idle;
     std::map<uintptr_t, std::shared_ptr<Resident>> weights;
+    std::map<uintptr_t, std::shared_ptr<Panel>> panels;
     {
         std::lock_guard<std::mutex> lk(g_mu);
         weights.swap(g_weights);
         g_resident_bytes = 0;
+        panels.swap(g_panels);
+        g_panel_bytes = 0;
         idle.swap(g_free_ctx);
     }
-    weights.clear();          // each copy freed after queued work, or by its last holder
+    panels.clear();           // each freed after queued work, or by its last holder
+    weights.clear();
     for (ThreadCtx* c : idle) free_ctx(c);
     if (t_holder.c) {
         free_ctx(t_holder.c);
@@ -540,17 +656,31 @@ int pk_gpu_register_weight(const void* host, size_t bytes)
 int pk_gpu_unregister_weight(const void* host)
 {
     std::shared_ptr<Resident> r;
+    std::vector<std::shared_ptr<Panel>> panels;
     {
         std::lock_guard<std::mutex> lk(g_mu);
         auto it = g_weights.find(reinterpret_cast<uintptr_t>(host));
         if (it == g_weights.end()) return fail(PK_GPU_EINVAL, "unregister: not registered");
+        // Lookups take their references under g_mu, so no call can start
+        // holding it after this test.
+        if (it->second.use_count() > 1)
+            return fail(PK_GPU_EBUSY, "unregister: a GEMM call on another thread is reading the weight");
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(it->second->dev), hi = lo + it->second->bytes;
+        for (auto pit = g_panels.lower_bound(lo); pit != g_panels.end() && pit->first < hi;) {
+            if (pit->second->owner == lo) {
+                g_panel_bytes -= pit->second->bytes;
+                panels.push_back(std::move(pit->second));
+                pit = g_panels.erase(pit);
+            } else {
+                ++pit;
+            }
+        }
         r = std::move(it->second);
         g_resident_bytes -= r->bytes;
         g_weights.erase(it);
     }
-    // Later lookups miss it.  A host-pointer GEMM that found it holds it until
-    // its stream is done; otherwise it is freed here, after the device's
-    // queued work.
+    // freed here, after the device's queued work
+    panels.clear();
     r.reset();
     return PK_GPU_OK;
 }
@@ -697,6 +827,108 @@ int pk_gpu_swish_dev(const float* dx, float* dy, long long n, void* stream)
     if (rc) return rc;
     hipError_t e = pkgpu::launch_swish(dx, dy, n, s);
     return e == hipSuccess ? PK_GPU_OK : hip_fail(e, "swish launch");
+}
+
+static pkgpu::WeightKind kind_of_bits(int bits)
+{
+    return bits == 4 ? pkgpu::W_I4 : bits == 8 ? pkgpu::W_I8 : pkgpu::W_F32;
+}
+
+int pk_gpu_pack_weight_dev(int bits, int K, int N, const void* dB, int ldb, const float* dscales,
+                           void* stream)
+{
+    if (bits != 4 && bits != 8 && bits != 32) return fail(PK_GPU_EINVAL, "pack: bits = %d (4, 8 or 32)", bits);
+    if (K <= 0 || N <= 0 || K % 32) return fail(PK_GPU_EINVAL, "pack: K = %d (a positive multiple of 32), N = %d", K, N);
+    if (bits == 4 && N % 32) return fail(PK_GPU_EINVAL, "pack: int4 N = %d is not a multiple of 32", N);
+    if (ldb < (bits == 4 ? N / 2 : N)) return fail(PK_GPU_EINVAL, "pack: ldb = %d too small for N = %d", ldb, N);
+    if (!dB || (bits == 4 && !dscales)) return fail(PK_GPU_EINVAL, "pack: NULL operand");
+    int rc = 0;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+        return fail(PK_GPU_EINVAL, "pack: not during stream capture (it allocates and waits)");
+    GemmProblem p{};
+    p.kind = kind_of_bits(bits);
+    p.K = K; p.N = N; p.B = dB; p.ldb = ldb;
+    p.scales = bits == 4 ? dscales : nullptr;
+    if (panel_for(p)) return PK_GPU_OK;              // already made with these parameters
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    return make_panel(p, 0, s);
+}
+
+int pk_gpu_unpack_weight_dev(const void* dB)
+{
+    std::shared_ptr<Panel> pn;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_panels.find(reinterpret_cast<uintptr_t>(dB));
+        if (it == g_panels.end()) return fail(PK_GPU_EINVAL, "unpack: no panel for %p", dB);
+        if (it->second->owner)
+            return fail(PK_GPU_EINVAL, "unpack: the panel of a registered weight goes with pk_gpu_unregister_weight");
+        if (it->second.use_count() > 1)
+            return fail(PK_GPU_EBUSY, "unpack: a GEMM call on another thread is reading the panel");
+        pn = std::move(it->second);
+        g_panel_bytes -= pn->bytes;
+        g_panels.erase(it);
+    }
+    pn.reset();                                      // freed after the device's queued work
+    return PK_GPU_OK;
+}
+
+size_t pk_gpu_panel_bytes(void)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    return g_panel_bytes;
+}
+
+int pk_gpu_uses_panel(int M, int N, int K, int bits, const void* dB, int ldb, const float* dscales)
+{
+    GemmProblem p{};
+    p.kind = kind_of_bits(bits);
+    p.M = M; p.N = N; p.K = K;
+    p.alpha = 1.0f; p.scale = 1.0f;
+    p.A = reinterpret_cast<const float*>(uintptr_t(256));
+    p.lda = K;
+    p.B = dB; p.ldb = ldb;
+    p.scales = dscales;
+    p.ldc = N;
+    if (!small_m_call(p, true)) return 0;
+    p.panel = panel_for(p);
+    return pkgpu::panel_supports(p);
+}
+
+int pk_gpu_panel_segments(int M, int N, int K)
+{
+    GemmProblem p{};
+    p.M = M; p.N = N; p.K = K;
+    p.work = t_work;
+    p.work_bytes = t_work_bytes;
+    return pkgpu::panel_segments(p);
+}
+
+int pk_gpu_panel_decode_dev(int bits, int K, int N, const void* dB, int ldb, const float* dscales,
+                            float B_scale, float* dout, void* stream)
+{
+    GemmProblem p{};
+    p.kind = kind_of_bits(bits);
+    p.K = K; p.N = N; p.B = dB; p.ldb = ldb;
+    p.scales = bits == 4 ? dscales : nullptr;
+    const void* pn = panel_for(p);
+    if (!pn) return fail(PK_GPU_EINVAL, "decode: no panel for %p with these parameters", dB);
+    if (!dout) return fail(PK_GPU_EINVAL, "decode: NULL output");
+    int rc = 0;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    const hipError_t e = pkgpu::launch_panel_decode(p.kind, K, N, pn, B_scale, dout, s);
+    return e == hipSuccess ? PK_GPU_OK : hip_fail(e, "panel decode launch");
+}
+
+int pk_gpu_force_panel_tile(int mb, int nct)
+{
+    if (!pkgpu::panel_force_tiles(mb, nct))
+        return fail(PK_GPU_EINVAL, "panel tile mb = %d, nct = %d (mb 1..4, nct 1..2; (0, 0) = default)", mb, nct);
+    return PK_GPU_OK;
 }
 
 int pk_gpu_num_configs(void) { return pkgpu::num_configs(); }

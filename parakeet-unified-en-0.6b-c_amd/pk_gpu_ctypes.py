@@ -52,6 +52,13 @@ _PROTOS = {
     "pk_gpu_set_workspace": (_i, [_p, _sz]),
     "pk_gpu_split_k_segments": (_i, [_i, _i, _i, _i]),
     "pk_gpu_force_small_tile": (_i, [_i, _i]),
+    "pk_gpu_pack_weight_dev": (_i, [_i, _i, _i, _p, _i, _p, _p]),
+    "pk_gpu_unpack_weight_dev": (_i, [_p]),
+    "pk_gpu_panel_bytes": (_sz, []),
+    "pk_gpu_uses_panel": (_i, [_i, _i, _i, _i, _p, _i, _p]),
+    "pk_gpu_panel_segments": (_i, [_i, _i, _i]),
+    "pk_gpu_panel_decode_dev": (_i, [_i, _i, _i, _p, _i, _p, _f, _p, _p]),
+    "pk_gpu_force_panel_tile": (_i, [_i, _i]),
     "pk_gpu_dequant_dev": (_i, [_i, _i, _i, _p, _i, _f, _p, _i, _p, _p]),
     "pk_gpu_layer_norm_dev": (_i, [_p, _p, _p, _p, _i, _i, _p]),
     "pk_gpu_attention_dev": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p]),
@@ -118,7 +125,7 @@ class PreEncodeWeights(ctypes.Structure):
                 ("conv3_w", _p), ("conv3_b", _p), ("conv5_w", _p), ("conv5_b", _p),
                 ("conv6_w", _p), ("conv6_b", _p), ("out_w", Weight), ("out_b", _p)]
 
-STATUS = {0: "OK", -1: "EINVAL", -2: "ENOTSUP", -3: "ENOMEM", -4: "EHIP", -5: "ENODEV"}
+STATUS = {0: "OK", -1: "EINVAL", -2: "ENOTSUP", -3: "ENOMEM", -4: "EHIP", -5: "ENODEV", -6: "EBUSY"}
 
 
 class PkGpuError(RuntimeError):
