@@ -66,6 +66,10 @@ struct DwArgs {
     const int* chunk_T;        // device, n entries, each in [1, T] (null: all T)
     int T, C, K;
     int swish;
+    // x holds the pointwise convolution's 2C-wide rows and each input value
+    // is their GLU, gated = x[t][c] * (1 / (1 + exp(-x[t][C + c]))), formed
+    // as the GLU kernel forms it (the GLU fused: the same bits)
+    int glu;
 };
 
 hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const float* beta,

@@ -30,17 +30,6 @@ namespace {
 
 using tiles::v4f;
 
-// ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)) across the 8 lanes of an aligned
-// lane group (pk_hsum_avx2, tensor_ops.c:126-134); every lane of the group
-// gets the sum.  fl(a+b) == fl(b+a), so the xor partners give the same
-// association on every lane.
-__device__ inline float hsum8_lanes(float p)
-{
-    const float a = __fadd_rn(p, __shfl_xor(p, 4));
-    const float b = __fadd_rn(a, __shfl_xor(a, 2));
-    return __fadd_rn(b, __shfl_xor(b, 1));
-}
-
 __device__ inline float hsum8(const float (&p)[8])
 {
     return __fadd_rn(__fadd_rn(__fadd_rn(p[0], p[4]), __fadd_rn(p[2], p[6])),
@@ -556,14 +545,17 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
 
 // ---- GLU (encoder.c:453-461) -------------------------------------------------
 // gated[r][d] = va * (1 / (1 + exp(-vb))), va = in[r][d], vb = in[r][D + d].
+__device__ inline float glu_value(float va, float vb)
+{
+    return __fmul_rn(va, __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ieee(-vb))));
+}
+
 __global__ void glu_rows(const float* __restrict__ in, int ldi, float* out, int ldo, int rows, int D)
 {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long long)rows * D) return;
     const int r = (int)(idx / D), d = (int)(idx % D);
-    const float va = in[(size_t)r * ldi + d], vb = in[(size_t)r * ldi + D + d];
-    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_ieee(-vb)));
-    out[(size_t)r * ldo + d] = __fmul_rn(va, s);
+    out[(size_t)r * ldo + d] = glu_value(in[(size_t)r * ldi + d], in[(size_t)r * ldi + D + d]);
 }
 
 // ---- depthwise convolution + Swish (tensor_ops.c:476-548, encoder.c:467-469)
@@ -584,6 +576,11 @@ __global__ void depthwise_swish(DwArgs p)
     const int t = (int)(idx / p.C), c = (int)(idx % p.C);
     const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.y] : 0;
     const float* x = p.x + (size_t)row0 * p.ldx + c;
+    // input value at time u (GLU'd on the fly when p.glu)
+    auto in = [&](int u) {
+        const float* xr = x + (size_t)u * p.ldx;
+        return p.glu ? glu_value(xr[0], xr[p.C]) : xr[0];
+    };
     const int K = KK ? KK : p.K;
     const float* wc = p.w + (size_t)c * K;
     const int pad = (K - 1) / 2;
@@ -595,13 +592,13 @@ __global__ void depthwise_swish(DwArgs p)
             float xv[KK], wv[KK];
 #pragma unroll
             for (int k = 0; k < KK; ++k) {
-                xv[k] = x[(size_t)(t - pad + k) * p.ldx];
+                xv[k] = in(t - pad + k);
                 wv[k] = wc[k];
             }
 #pragma unroll
             for (int k = 0; k < KK; ++k) val = __fmaf_rn(xv[k], wv[k], val);
         } else {
-            for (int k = 0; k < K; ++k) val = __fmaf_rn(x[(size_t)(t - pad + k) * p.ldx], wc[k], val);
+            for (int k = 0; k < K; ++k) val = __fmaf_rn(in(t - pad + k), wc[k], val);
         }
     } else {
         const int K8 = K & ~7;
@@ -610,13 +607,13 @@ __global__ void depthwise_swish(DwArgs p)
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
                 const int src = t - pad + k0 + l;
-                pr[l] = (src >= 0 && src < T) ? __fmul_rn(x[(size_t)src * p.ldx], wc[k0 + l]) : 0.0f;
+                pr[l] = (src >= 0 && src < T) ? __fmul_rn(in(src), wc[k0 + l]) : 0.0f;
             }
             val = __fadd_rn(val, hsum8(pr));
         }
         for (int k = K8; k < K; ++k) {
             const int src = t - pad + k;
-            if (src >= 0 && src < T) val = __fmaf_rn(x[(size_t)src * p.ldx], wc[k], val);
+            if (src >= 0 && src < T) val = __fmaf_rn(in(src), wc[k], val);
         }
     }
     p.out[(size_t)(row0 + t) * p.ldo + c] = p.swish ? swish_f(val) : val;

@@ -61,6 +61,54 @@ __device__ inline void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& 
     lo = __builtin_bit_cast(uint32_t, l);
 }
 
+// ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)) across the 8 lanes of an aligned
+// lane group (pk_hsum_avx2, tensor_ops.c:126-134); every lane of the group
+// gets the sum.  fl(a+b) == fl(b+a), so the xor partners give the same
+// association on every lane.
+__device__ inline float hsum8_lanes(float p)
+{
+    const float a = __fadd_rn(p, __shfl_xor(p, 4));
+    const float b = __fadd_rn(a, __shfl_xor(a, 2));
+    return __fadd_rn(b, __shfl_xor(b, 1));
+}
+
+// LayerNorm's statistics of one row of D floats (tensor_ops.c:150-185 as
+// the x86 build computes them), for lane l (0..7) of an aligned 8-lane
+// group: lane l sums the elements l, l+8, ... in order (one AVX2 lane), the
+// partials are added as hsum8_lanes, mean = sum / D; then the squared
+// deviations fl(x - mean) the same way through an fma chain, var = sum / D,
+// inv = 1 / sqrtf(var + 1e-5) (correctly rounded '/' and sqrtf).  The
+// normalised value is then fl(fl(fl(x - mean) * inv) * gamma + beta) (one
+// fma).  row may be LDS or global memory.  D must be a multiple of 8 * CH:
+// the lane's elements are read CH at a time into registers ahead of their
+// chain of additions, so the reads do not wait one by one.
+template <int CH>
+__device__ inline void ln_row_stats(const float* row, int D, int l, float& mean, float& inv)
+{
+    float p = 0.0f;
+    for (int i0 = 0; i0 < D; i0 += 8 * CH) {
+        float v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[c] = row[i0 + 8 * c + l];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) p = __fadd_rn(p, v[c]);
+    }
+    mean = __fdiv_rn(hsum8_lanes(p), (float)D);
+    float q = 0.0f;
+    for (int i0 = 0; i0 < D; i0 += 8 * CH) {
+        float v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[c] = row[i0 + 8 * c + l];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const float d = __fsub_rn(v[c], mean);
+            q = __fmaf_rn(d, d, q);
+        }
+    }
+    const float var = __fdiv_rn(hsum8_lanes(q), (float)D);
+    inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
+}
+
 __device__ inline float exp_poly(float x)
 {
     x = fminf(fmaxf(x, -87.0f), 87.0f);

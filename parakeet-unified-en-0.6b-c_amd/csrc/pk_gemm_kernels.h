@@ -55,6 +55,16 @@ struct GemmProblem {
     // The weight's panel copy (launch_pack of this B, scales, K and N), or
     // null.  With it, the small-M path takes the panel kernels.
     const void* panel = nullptr;
+    // Panel kernels only (panel_supports): A is x, and the GEMM multiplies
+    // LayerNorm(x) over its K columns with these gamma, beta [K] (the
+    // LayerNorm kernel's arithmetic, bit for bit; K <= 1024).
+    const float* ln_gamma = nullptr;
+    const float* ln_beta = nullptr;
+    // Panel kernels with K split over workgroups only (panel_fuses_out_ln):
+    // after the output step, each output row is replaced by its LayerNorm
+    // with these gamma, beta [N].
+    const float* out_ln_gamma = nullptr;
+    const float* out_ln_beta = nullptr;
 };
 
 // Partial tiles of one split-K launch: at most 256 workgroups of at most
@@ -126,6 +136,9 @@ bool panel_supports(const GemmProblem& p);
 int panel_segments(const GemmProblem& p);
 // k of one LDS phase for a workgroup of `rows` rows.
 int panel_phase_k(int rows);
+// Whether the panel kernels can fuse an output LayerNorm (p.out_ln_gamma)
+// into a problem: panel_supports(p) with K split over workgroups.
+bool panel_fuses_out_ln(const GemmProblem& p);
 // The workgroup tile a problem takes: mb 16-row blocks, nct 16-column tiles.
 void panel_tile(const GemmProblem& p, int* mb, int* nct);
 // Force the workgroup tile (mb 1..4, nct 1..2) on the calling thread ((0,

@@ -137,6 +137,7 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
 
     const bool fused = p.bias != nullptr || p.epi != EPI_NONE;
     const bool early = (p.alpha == 0.0f) || (p.kind == W_I8 && p.scale == 0.0f) || p.K <= 0;
+    if (p.out_ln_gamma && early) return hipErrorInvalidValue;   // the output LayerNorm rides on the panel reduce
     if (early) {   // blas.c:764-765, 955-956, 1063-1064: only the beta step runs
         if (p.beta == 1.0f && !fused) return hipSuccess;
         const long long n = (long long)p.M * p.N;
@@ -144,6 +145,11 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
         return hipGetLastError();
     }
 
+    if (p.ln_gamma || p.out_ln_gamma) {
+        // fused LayerNorms: only the panel kernels apply them
+        if (tol == TOL_NONE || cfg_index >= 0 || !panel_supports(p)) return hipErrorInvalidValue;
+        return launch_panel(p, stream);
+    }
     if (p.a_presplit) {
         // A comes pre-split: only the split kernels read it
         if (tol != TOL_ALL || cfg_index >= 0 || !split_supports(p)) return hipErrorInvalidValue;

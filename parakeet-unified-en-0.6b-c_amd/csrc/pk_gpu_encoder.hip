@@ -45,6 +45,9 @@ struct DevWeight {
     float scale = 0.0f;
     const float* scales = nullptr;
     int K = 0, N = 0;
+    // its panel copy for the small-M kernels (pk_panel.hip), made on the
+    // first run with a row group of at most 64 rows outside exact numerics
+    const void* panel = nullptr;
 };
 
 struct DevBlock {
@@ -136,6 +139,9 @@ struct pk_gpu_encoder {
     // fast numerics: LayerNorms feeding a GEMM write pre-split output
     // (PK_GPU_PRESPLIT=0 at creation turns it off; the results are the same)
     bool presplit = true;
+    // small row groups on the panel kernels: LayerNorms fused into the GEMMs
+    // (PK_GPU_FUSE_LN=0 at creation turns it off; the results are the same)
+    bool fuse_ln = true;
     std::vector<hipStream_t> side;
     std::vector<hipEvent_t> side_done;
     hipEvent_t inputs_ready = nullptr;
@@ -154,6 +160,9 @@ struct pk_gpu_encoder {
     // (groups replay concurrently, so each has its own), grown on demand
     float* part = nullptr;
     size_t part_groups = 0;
+    // the block weights' panels (made once, see DevWeight::panel)
+    std::vector<void*> panel_allocs;
+    size_t panel_bytes = 0;
 };
 
 namespace {
@@ -331,11 +340,17 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, size_t scores_n, 
     return PK_GPU_OK;
 }
 
-// presplit: A holds a split-output LayerNorm's rows (GemmProblem::a_presplit),
-// for the split kernels only.
-int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float* bias,
-                Epilogue epi, hipStream_t s, pkgpu::Tolerance tol = pkgpu::TOL_NONE,
-                float* work = nullptr, bool presplit = false)
+// LayerNorms fused into a small-M GEMM (panel kernels only): `in` normalises
+// its input rows, `out` its output rows after the epilogue.
+struct FusedLn {
+    const float *in_g = nullptr, *in_b = nullptr, *out_g = nullptr, *out_b = nullptr;
+};
+
+// The GEMM problem of a block weight; presplit: A holds a split-output
+// LayerNorm's rows (GemmProblem::a_presplit), for the split kernels only.
+GemmProblem block_problem(const DevWeight& w, const float* A, int M, float* C, const float* bias,
+                          Epilogue epi, pkgpu::Tolerance tol, float* work, bool presplit,
+                          const FusedLn& ln)
 {
     GemmProblem p{};
     p.kind = w.kind;
@@ -359,7 +374,19 @@ int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float
         p.work_bytes = pkgpu::kSplitWorkBytes;
     }
     p.a_presplit = presplit;
-    return pkgpu::rt::gemm(p, s, tol);
+    if (tol != pkgpu::TOL_NONE) p.panel = w.panel;      // read only where the small-M path may run
+    p.ln_gamma = ln.in_g;
+    p.ln_beta = ln.in_b;
+    p.out_ln_gamma = ln.out_g;
+    p.out_ln_beta = ln.out_b;
+    return p;
+}
+
+int gemm_launch(const DevWeight& w, const float* A, int M, float* C, const float* bias,
+                Epilogue epi, hipStream_t s, pkgpu::Tolerance tol = pkgpu::TOL_NONE,
+                float* work = nullptr, bool presplit = false, const FusedLn& ln = FusedLn())
+{
+    return pkgpu::rt::gemm(block_problem(w, A, M, C, bias, epi, tol, work, presplit, ln), s, tol);
 }
 
 int check(hipError_t r, const char* what) { return r == hipSuccess ? PK_GPU_OK : hip_error(r, what); }
@@ -476,20 +503,37 @@ std::vector<Chunk> plan_chunks(int T, int C, int ov)
 
 // A weight GEMM of the block: M rows of A through w, with its epilogue;
 // `work`: the row group's split-K partial tiles, or null; `presplit`: A holds
-// a split-output LayerNorm's rows (layer_norm with split).
+// a split-output LayerNorm's rows (layer_norm with split); `exact`: the
+// exact chains whatever the encoder's numerics; `ln`: LayerNorms fused into
+// it (fusable() said the panel kernels take them).
 int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
          const float* bias, Epilogue epi, hipStream_t s, float* work = nullptr,
-         bool presplit = false)
+         bool presplit = false, bool exact = false, const FusedLn& ln = FusedLn())
 {
     const double flops = 2.0 * M * w.N * w.K;
     double bytes = weight_bytes_of(w) + 4.0 * M * w.K + 4.0 * M * w.N;
     if (bias) bytes += 4.0 * w.N;
     if (epi == pkgpu::EPI_HALF_RESIDUAL || epi == pkgpu::EPI_RESIDUAL) bytes += 4.0 * M * w.N;
-    const pkgpu::Tolerance tol = pkgpu::rt::tolerance_of(e->numerics);
+    if (ln.in_g) bytes += 8.0 * w.K;
+    if (ln.out_g) bytes += 8.0 * w.N;
+    const pkgpu::Tolerance tol = exact ? pkgpu::TOL_NONE : pkgpu::rt::tolerance_of(e->numerics);
     return timed(e, stage_of(w), flops, bytes, s,
                  [&] {
-                     return gemm_launch(w, A, M, C, bias, epi, s, tol, work, presplit);
+                     return gemm_launch(w, A, M, C, bias, epi, s, tol, work, presplit, ln);
                  });
+}
+
+// Whether the panel kernels take this block GEMM with these LayerNorms
+// fused (the encoder's numerics allow the small-M path, no forced tile, the
+// weight has its panel, and the shape and LDS allow it).
+bool fusable(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C, const float* bias,
+             Epilogue epi, float* work, const FusedLn& ln)
+{
+    if (!e->fuse_ln || e->numerics == PK_GPU_NUMERICS_EXACT || pkgpu::rt::forced_config() >= 0 || !w.panel)
+        return false;
+    const GemmProblem p = block_problem(w, A, M, C, bias, epi, pkgpu::rt::tolerance_of(e->numerics), work,
+                                        false, ln);
+    return ln.out_g ? pkgpu::panel_fuses_out_ln(p) : pkgpu::panel_supports(p);
 }
 
 // split: the output pre-split for the split GEMM kernels, for a GEMM that
@@ -528,17 +572,46 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     // the down projection saved.
     const bool ps = e->presplit && e->numerics == PK_GPU_NUMERICS_FAST &&
                     pkgpu::rt::forced_config() < 0 && R > 64;
+    // Small row groups on the panel kernels: each LayerNorm that feeds a GEMM
+    // is fused into that GEMM (its rows normalised as they are staged), and
+    // the block's output LayerNorm into the second feed-forward's split-K
+    // reduce; the results are the same bits as the separate launches give
+    // those kernels.
+    auto fused_in = [&](const DevWeight& w, const float* gm, const float* be, float* C, const float* bias,
+                        Epilogue epi) {
+        FusedLn f;
+        f.in_g = gm;
+        f.in_b = be;
+        return fusable(e, w, x, R, C, bias, epi, g.part, f) ? f : FusedLn();
+    };
+    // the normalised input of a GEMM: fused into it, or a LayerNorm launch into `ln`
+    auto norm_in = [&](const FusedLn& f, const float* gm, const float* be, const float** A) {
+        *A = f.in_g ? x : ln;
+        return f.in_g ? PK_GPU_OK : layer_norm(e, x, gm, be, ln, R, s, ps);
+    };
+    // out_ln: fuse the block's output LayerNorm into the down projection (sets *fused)
     auto ffn = [&](const float* gm, const float* be, const DevWeight& w1, const float* b1,
-                   const DevWeight& w2, const float* b2) {
-        int r = layer_norm(e, x, gm, be, ln, R, s, ps);
-        if (!r) r = gemm(e, w1, ln, R, h, b1, pkgpu::EPI_SWISH, s, g.part, ps);        // encoder.c:193-196
-        if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s, g.part);     // encoder.c:198-216
+                   const DevWeight& w2, const float* b2, bool out_ln, bool* fused) {
+        const FusedLn f = fused_in(w1, gm, be, h, b1, pkgpu::EPI_SWISH);
+        const float* A = nullptr;
+        int r = norm_in(f, gm, be, &A);
+        if (!r) r = gemm(e, w1, A, R, h, b1, pkgpu::EPI_SWISH, s, g.part, ps && !f.in_g, false, f);   // encoder.c:193-196
+        FusedLn o;
+        if (out_ln) {
+            o.out_g = b.ln_out_w;
+            o.out_b = b.ln_out_b;
+            if (!fusable(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, g.part, o)) o = FusedLn();
+        }
+        if (fused) *fused = o.out_g != nullptr;
+        if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s, g.part, false, false, o);   // encoder.c:198-216
         return r;
     };
     // self-attention (encoder.c:300-424)
     auto self_attention = [&]() {
-        int rc = layer_norm(e, x, b.ln_sa_w, b.ln_sa_b, ln, R, s, ps);
-        if (!rc) rc = gemm(e, b.qkv, ln, R, h, b.qkv_b, pkgpu::EPI_NONE, s, g.part, ps);
+        const FusedLn f = fused_in(b.qkv, b.ln_sa_w, b.ln_sa_b, h, b.qkv_b, pkgpu::EPI_NONE);
+        const float* A = nullptr;
+        int rc = norm_in(f, b.ln_sa_w, b.ln_sa_b, &A);
+        if (!rc) rc = gemm(e, b.qkv, A, R, h, b.qkv_b, pkgpu::EPI_NONE, s, g.part, ps && !f.in_g, false, f);
         if (rc) return rc;
         // every chunk of the group in one launch, each with its own length
         double flops = 0.0, bytes = 4.0 * (2 * Tmax - 1) * kD;   // the P rows read
@@ -564,16 +637,24 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     };
     // convolution module (encoder.c:430-476), time-major throughout
     auto convolution = [&]() {
-        int rc = layer_norm(e, x, b.ln_conv_w, b.ln_conv_b, ln, R, s, ps);
-        if (!rc) rc = gemm(e, b.pw1t, ln, R, h, b.pw1_b, pkgpu::EPI_NONE, s, g.part, ps);
-        if (!rc)
+        const FusedLn f = fused_in(b.pw1t, b.ln_conv_w, b.ln_conv_b, h, b.pw1_b, pkgpu::EPI_NONE);
+        const float* A = nullptr;
+        int rc = norm_in(f, b.ln_conv_w, b.ln_conv_b, &A);
+        if (!rc) rc = gemm(e, b.pw1t, A, R, h, b.pw1_b, pkgpu::EPI_NONE, s, g.part, ps && !f.in_g, false, f);
+        // Small row groups (fused LayerNorms on) take the GLU inside the
+        // depthwise convolution: each input value is gated where it is read
+        // (9 times, a few thousand rows' worth of work), one launch fewer.
+        const bool glu_in_dw = f.in_g != nullptr;
+        if (!rc && !glu_in_dw)
             rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 12.0 * R * kD, s, [&] {
                 return check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu");
             });
         if (rc) return rc;
         // every chunk of the group in one launch, each with its own length
         pkgpu::DwArgs d{};
-        d.x = att; d.ldx = kD;
+        d.x = glu_in_dw ? h : att;
+        d.ldx = glu_in_dw ? 2 * kD : kD;
+        d.glu = glu_in_dw ? 1 : 0;
         d.w = b.dw_w; d.b = b.dw_b;
         d.out = ln; d.ldo = kD;
         d.chunk_rows = rows;
@@ -589,14 +670,16 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         int rc = PK_GPU_OK;
         switch (m) {
         case 0:     // feed-forward 1 (encoder.c:483)
-            rc = ffn(b.ln_ff1_w, b.ln_ff1_b, b.ff1_w1, b.ff1_b1, b.ff1_w2, b.ff1_b2);
+            rc = ffn(b.ln_ff1_w, b.ln_ff1_b, b.ff1_w1, b.ff1_b1, b.ff1_w2, b.ff1_b2, false, nullptr);
             break;
         case 1: rc = self_attention(); break;
         case 2: rc = convolution(); break;
-        default:    // feed-forward 2 and the block's output LayerNorm (encoder.c:486-487)
-            rc = ffn(b.ln_ff2_w, b.ln_ff2_b, b.ff2_w1, b.ff2_b1, b.ff2_w2, b.ff2_b2);
-            if (!rc) rc = layer_norm(e, x, b.ln_out_w, b.ln_out_b, x, R, s);
+        default: {  // feed-forward 2 and the block's output LayerNorm (encoder.c:486-487)
+            bool out_fused = false;
+            rc = ffn(b.ln_ff2_w, b.ln_ff2_b, b.ff2_w1, b.ff2_b1, b.ff2_w2, b.ff2_b2, true, &out_fused);
+            if (!rc && !out_fused) rc = layer_norm(e, x, b.ln_out_w, b.ln_out_b, x, R, s);
             break;
+        }
         }
         if (rc) return rc;
     }
@@ -669,6 +752,49 @@ int group_lag()
     return lag;
 }
 
+// The panels of every block weight the small-M kernels read (pk_panel.hip),
+// made once on the encoder's stream and waited for (never under capture).
+int make_panels(pk_gpu_encoder* e)
+{
+    if (!e->panel_allocs.empty()) return PK_GPU_OK;
+    std::vector<void*> fresh;
+    size_t total = 0;
+    int rc = PK_GPU_OK;
+    for (DevBlock& b : e->blocks) {
+        for (DevWeight* w : {&b.ff1_w1, &b.ff1_w2, &b.ff2_w1, &b.ff2_w2, &b.qkv, &b.out, &b.pw1t, &b.pw2t}) {
+            const size_t bytes = pkgpu::panel_bytes(w->kind, w->K, w->N);
+            void* d = nullptr;
+            if (!bytes || hipMalloc(&d, bytes) != hipSuccess) {
+                rc = error(PK_GPU_ENOMEM, "weight panels: device allocation of %zu bytes failed", bytes);
+                break;
+            }
+            fresh.push_back(d);
+            total += bytes;
+            const hipError_t r = pkgpu::launch_pack(w->kind, w->K, w->N, w->data,
+                                                    w->kind == pkgpu::W_I4 ? w->N / 2 : w->N, w->scales, d,
+                                                    e->stream);
+            if (r != hipSuccess) {
+                rc = hip_error(r, "weight panels");
+                break;
+            }
+        }
+        if (rc) break;
+    }
+    if (!rc) rc = check(hipStreamSynchronize(e->stream), "weight panels");
+    if (rc) {
+        (void)hipStreamSynchronize(e->stream);
+        for (void* d : fresh) (void)hipFree(d);
+        return rc;
+    }
+    size_t i = 0;
+    for (DevBlock& b : e->blocks)
+        for (DevWeight* w : {&b.ff1_w1, &b.ff1_w2, &b.ff2_w1, &b.ff2_w2, &b.qkv, &b.out, &b.pw1t, &b.pw2t})
+            w->panel = fresh[i++];
+    e->panel_allocs.swap(fresh);
+    e->panel_bytes = total;
+    return PK_GPU_OK;
+}
+
 int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
                hipStream_t s, hipMemcpyKind in_kind, hipMemcpyKind out_kind)
 {
@@ -724,7 +850,17 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
     }
     int rc = workspace(e, (size_t)R, table.size(), scores_n, s);
     if (rc) return rc;
-    if (e->numerics == PK_GPU_NUMERICS_FAST) {
+    // Row groups of at most 64 rows take the small-M kernels outside exact
+    // numerics: they read the weights' panels, and split K over workgroups
+    // in their group's partial tiles.
+    bool small = false;
+    for (const RowGroup& g : groups) small = small || g.R <= pkgpu::kSmallMaxM;
+    small = small && e->numerics != PK_GPU_NUMERICS_EXACT;
+    if (small && e->panel_allocs.empty()) {
+        if ((rc = check(hipStreamSynchronize(s), "encoder stream"))) return rc;
+        if ((rc = make_panels(e))) return rc;
+    }
+    if (e->numerics == PK_GPU_NUMERICS_FAST || small) {
         if (groups.size() > e->part_groups) {
             // the graphs hold the old partial-tile pointers
             wait_all(e);
@@ -993,7 +1129,10 @@ int project_positions(pk_gpu_encoder* e, int T)
             break;
         }
         fresh.push_back(d);
-        rc = gemm(e, b.pos, slice, L, static_cast<float*>(d), nullptr, pkgpu::EPI_NONE, e->stream);
+        // exact chains in every numerics mode: the projections are constants
+        // that later runs in any mode read (encoder.c:319-338)
+        rc = gemm(e, b.pos, slice, L, static_cast<float*>(d), nullptr, pkgpu::EPI_NONE, e->stream,
+                  nullptr, false, true);
         if (rc) break;
     }
     if (!rc) rc = check(hipStreamSynchronize(e->stream), "position projections");
@@ -1027,6 +1166,7 @@ int pk_gpu_encoder_create(pk_gpu_encoder** out, const pk_gpu_block_weights* bloc
     if (rc) return rc;
     pk_gpu_encoder* e = new pk_gpu_encoder;
     if (const char* v = getenv("PK_GPU_PRESPLIT")) e->presplit = strcmp(v, "0") != 0;
+    if (const char* v = getenv("PK_GPU_FUSE_LN")) e->fuse_ln = strcmp(v, "0") != 0;
     hipError_t r = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
     if (r != hipSuccess) {
         delete e;
@@ -1071,7 +1211,9 @@ int pk_gpu_encoder_run_dev(pk_gpu_encoder* enc, const float* dx, int T, int chun
 
 size_t pk_gpu_encoder_bytes(const pk_gpu_encoder* enc)
 {
-    return enc ? enc->weight_bytes + enc->ws_bytes + enc->part_groups * pkgpu::kSplitWorkBytes : 0;
+    return enc ? enc->weight_bytes + enc->ws_bytes + enc->part_groups * pkgpu::kSplitWorkBytes +
+                     enc->panel_bytes
+               : 0;
 }
 
 int pk_gpu_encoder_profile(pk_gpu_encoder* enc, int enable)
@@ -1112,6 +1254,7 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
     if (enc->part) (void)hipFree(enc->part);
     for (void* p : enc->allocs) (void)hipFree(p);
     for (void* p : enc->pos_allocs) (void)hipFree(p);
+    for (void* p : enc->panel_allocs) (void)hipFree(p);
     for (hipEvent_t ev : enc->side_done) (void)hipEventDestroy(ev);
     if (enc->inputs_ready) (void)hipEventDestroy(enc->inputs_ready);
     if (enc->last_done) (void)hipEventDestroy(enc->last_done);

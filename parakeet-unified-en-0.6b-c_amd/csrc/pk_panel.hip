@@ -66,6 +66,7 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 constexpr int kXcd = 8;
 constexpr int kPW = 8;                  // waves per workgroup
 constexpr int kLds = 147456;            // LDS bytes of a workgroup
+constexpr int kLnChunk = 64;            // fused LayerNorms: rows of a multiple of 8 * 64
 
 // Panel bytes per lane per (tile, step).
 constexpr int unit_bytes(int wk) { return wk == W_I8 ? 8 : wk == W_I4 ? 4 : 32; }
@@ -82,6 +83,8 @@ struct PanelArgs {
     float* work;               // grid.z > 1: partial tiles [grid.z][M][N]
     int kseg, kph;             // k per segment (grid.z) and per LDS phase, multiples of 32
     uint32_t a_bytes, p_bytes, s_bytes;
+    const float* ln_g;         // LN kernels: A is x and the products take LayerNorm(x) with
+    const float* ln_b;         //   these gamma, beta [K] (one phase holds all of K)
 };
 
 __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
@@ -149,7 +152,14 @@ template <int MB> struct PanelShape {
     static constexpr int SPW = CPR * 8 / kPW;            // steps per wave per phase
 };
 
-template <int WK, int MB, int NCT>
+// LN: the activations are normalised on the way in (the LayerNorm that feeds
+// the GEMM, fused): after the rows are in LDS, 8 lanes per row compute its
+// mean and 1/sqrt(var + eps) exactly as the LayerNorm kernel does
+// (ln_row_stats), and each fragment read forms fl(fl(fl(x - mean) * inv) *
+// gamma + beta), the LayerNorm output bit for bit, before the int4 scale
+// fold and the split.  LDS past the rows: 32 zero bytes, the rows' (mean,
+// inv) pairs (64 rows' worth), gamma and beta [K], int4 scales [K].
+template <int WK, int MB, int NCT, bool LN>
 __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
 {
     typedef PanelShape<MB> L;
@@ -171,6 +181,8 @@ __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
 
     // rows >= M read their fragments from 32 zero bytes past the last row
     if (threadIdx.x < 2) *reinterpret_cast<v4u*>(smem + M * pitch + 16 * threadIdx.x) = v4u{0, 0, 0, 0};
+    float* ln_st = reinterpret_cast<float*>(smem + M * pitch + 32);      // [64][mean, inv]
+    float* ln_gb = ln_st + 128;                                           // gamma [K], beta [K], scales [K]
 
     v4f acc[MB][NCT];
 #pragma unroll
@@ -194,11 +206,25 @@ __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
                     rA, (int)(((uint32_t)(m0 + wave + kPW * q) * (uint32_t)p.lda +
                                (uint32_t)(k0 + 256 * c + 4 * lane)) * 4u), 0, 0);
         v4u sreg[L::CPR];
-        if constexpr (WK == W_I4) {
+        if constexpr (WK == W_I4 && !LN) {
 #pragma unroll
             for (int c = 0; c < L::CPR; ++c)
                 sreg[c] = __builtin_amdgcn_raw_buffer_load_b128(
                     rS, (int)((grp * (uint32_t)p.K + (uint32_t)(k0 + 256 * c + 4 * lane)) * 4u), 0, 0);
+        }
+        // LN: gamma, beta (and the int4 group's scales), 4 k per unit, K <= 1024
+        constexpr int GBU = WK == W_I4 ? 3 : 2;
+        v4f gbreg[2];
+        const int q4 = p.K / 4;
+        if constexpr (LN) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int u = threadIdx.x + 64 * kPW * h, which = u / q4, j = u % q4;
+                if (u < GBU * q4)
+                    gbreg[h] = which == 0 ? *reinterpret_cast<const v4f*>(p.ln_g + 4 * j)
+                             : which == 1 ? *reinterpret_cast<const v4f*>(p.ln_b + 4 * j)
+                                          : *reinterpret_cast<const v4f*>(p.ST + (size_t)grp * p.K + 4 * j);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         typename WUnit<WK>::T wreg[L::SPW][NCT];
@@ -227,7 +253,7 @@ __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
             for (int c = 0; c < L::CPR; ++c) {
                 const int kk = 256 * c + 4 * lane;
                 v4u v = areg[q][c];
-                if constexpr (WK == W_I4) {
+                if constexpr (WK == W_I4 && !LN) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         v[e] = __float_as_uint(__fmul_rn(__uint_as_float(v[e]), __uint_as_float(sreg[c][e])));
@@ -236,13 +262,44 @@ __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
                     *static_cast<v4u*>(__builtin_assume_aligned(smem + r * pitch + kk * 4, 16)) = v;
             }
         }
+        if constexpr (LN) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int u = threadIdx.x + 64 * kPW * h;
+                if (u < GBU * q4) *reinterpret_cast<v4f*>(ln_gb + 4 * u) = gbreg[h];
+            }
+        }
         __syncthreads();
+        if constexpr (LN) {
+            // every row's mean and 1 / sqrt(var + eps): 8 lanes a row, one pass for 64 rows
+            const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
+            if (r < M) {
+                float mean, inv;
+                ln_row_stats<kLnChunk>(reinterpret_cast<const float*>(smem + r * pitch), p.K, l, mean, inv);
+                if (l == 0) {
+                    ln_st[2 * r] = mean;
+                    ln_st[2 * r + 1] = inv;
+                }
+            }
+            __syncthreads();
+        }
         // this wave's steps: fragments read and split, then the weights
 #pragma unroll
         for (int q = 0; q < L::SPW; ++q) {
             const int st = wave + kPW * q;
             if (st >= sph) break;                         // uniform per wave
             v8bf ahi[MB], alo[MB];
+            // LN: this step's 8 gammas, betas (and int4 scales) of k = 32 st + 8 g ..
+            v4f lg[2], lb[2], ls[2];
+            if constexpr (LN) {
+                const int k = 32 * st + 8 * g;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    lg[h] = *reinterpret_cast<const v4f*>(ln_gb + k + 4 * h);
+                    lb[h] = *reinterpret_cast<const v4f*>(ln_gb + p.K + k + 4 * h);
+                    if constexpr (WK == W_I4) ls[h] = *reinterpret_cast<const v4f*>(ln_gb + 2 * p.K + k + 4 * h);
+                }
+            }
 #pragma unroll
             for (int rb = 0; rb < MB; ++rb) {
                 const int r = 16 * rb + i;
@@ -250,9 +307,18 @@ __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
                     r < M ? smem + r * pitch + (32 * st + 8 * g) * 4 : smem + M * pitch, 16));
                 const v4u a0 = *reinterpret_cast<const v4u*>(f);
                 const v4u a1 = *reinterpret_cast<const v4u*>(f + 16);
-                const float xa[8] = {__uint_as_float(a0[0]), __uint_as_float(a0[1]), __uint_as_float(a0[2]),
-                                     __uint_as_float(a0[3]), __uint_as_float(a1[0]), __uint_as_float(a1[1]),
-                                     __uint_as_float(a1[2]), __uint_as_float(a1[3])};
+                float xa[8] = {__uint_as_float(a0[0]), __uint_as_float(a0[1]), __uint_as_float(a0[2]),
+                               __uint_as_float(a0[3]), __uint_as_float(a1[0]), __uint_as_float(a1[1]),
+                               __uint_as_float(a1[2]), __uint_as_float(a1[3])};
+                if constexpr (LN) {
+                    // rows >= M (zeros, whatever they become) reach only output rows >= M
+                    const float mean = r < M ? ln_st[2 * r] : 0.0f, inv = r < M ? ln_st[2 * r + 1] : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        xa[e] = __fmaf_rn(__fmul_rn(__fsub_rn(xa[e], mean), inv), lg[e >> 2][e & 3], lb[e >> 2][e & 3]);
+                        if constexpr (WK == W_I4) xa[e] = __fmul_rn(xa[e], ls[e >> 2][e & 3]);
+                    }
+                }
                 split8(xa, ahi[rb], alo[rb]);
             }
             v8bf bhi[NCT], blo[NCT];
@@ -306,15 +372,72 @@ __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
     }
 }
 
+// The partials of output o over segs <= kMaxSegs segments, added in segment
+// order; every load is issued before the first addition (the extra loads of
+// absent segments read segment 0 and are not added).
+constexpr int kMaxSegs = 16;
+__device__ inline float sum_segments(const float* work, size_t o, size_t mn, int segs)
+{
+    float v[kMaxSegs];
+#pragma unroll
+    for (int z = 0; z < kMaxSegs; ++z) v[z] = work[(z < segs ? (size_t)z * mn : 0) + o];
+    float sum = v[0];
+#pragma unroll
+    for (int z = 1; z < kMaxSegs; ++z) sum = z < segs ? __fadd_rn(sum, v[z]) : sum;
+    return sum;
+}
+
+// Segment partials summed in segment order, then the output step, then,
+// over each whole output row, LayerNorm with gamma, beta [N] (the block's
+// LayerNorm that follows the residual add, fused): one workgroup per row,
+// the row in LDS, its statistics by the first 8 lanes (ln_row_stats), then
+// C = fl(fl(fl(v - mean) * inv) * gamma + beta).  N <= kReduceLnMaxN.
+constexpr int kReduceLnMaxN = 4096;
+__global__ __launch_bounds__(256) void panel_reduce_ln(PanelArgs p, int segs, const float* gamma,
+                                                       const float* beta)
+{
+    __shared__ float row[kReduceLnMaxN];
+    __shared__ float st[2];
+    const int m = blockIdx.x;
+    const size_t mn = (size_t)p.M * p.N;
+    for (int n = threadIdx.x; n < p.N; n += 256) {
+        const size_t o = (size_t)m * p.N + n;
+        const float sum = sum_segments(p.work, o, mn, segs);
+        float* cp = p.C + (size_t)m * p.ldc + n;
+        float r = __fmul_rn(p.alpha, sum);
+        if (p.beta != 0.0f) r = __fadd_rn(p.beta == 1.0f ? *cp : __fmul_rn(p.beta, *cp), r);
+        if (p.bias) r = __fadd_rn(r, p.bias[n]);
+        switch (p.epi) {
+        case EPI_SWISH:         r = swish_f(r); break;
+        case EPI_HALF_RESIDUAL: r = __fmaf_rn(r, 0.5f, *cp); break;
+        case EPI_RESIDUAL:      r = __fadd_rn(*cp, r); break;
+        case EPI_RELU:          r = r > 0.0f ? r : 0.0f; break;
+        default:                break;
+        }
+        row[n] = r;
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        float mean, inv;
+        ln_row_stats<kLnChunk>(row, p.N, threadIdx.x, mean, inv);
+        if (threadIdx.x == 0) {
+            st[0] = mean;
+            st[1] = inv;
+        }
+    }
+    __syncthreads();
+    const float mean = st[0], inv = st[1];
+    for (int n = threadIdx.x; n < p.N; n += 256)
+        p.C[(size_t)m * p.ldc + n] = __fmaf_rn(__fmul_rn(__fsub_rn(row[n], mean), inv), gamma[n], beta[n]);
+}
+
 // Segment partials summed in segment order, then the output step.
 __global__ __launch_bounds__(256) void panel_reduce(PanelArgs p, int segs)
 {
     const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long mn = (long long)p.M * p.N;
     if (o >= mn) return;
-    float sum = p.work[o];
-    for (int z = 1; z < segs; ++z) sum = __fadd_rn(sum, p.work[(size_t)z * mn + o]);
-    store_out(p, (int)(o / p.N), (int)(o % p.N), sum);
+    store_out(p, (int)(o / p.N), (int)(o % p.N), sum_segments(p.work, (size_t)o, (size_t)mn, segs));
 }
 
 // ---- the repack -------------------------------------------------------------
@@ -399,10 +522,20 @@ size_t scales_offset(WeightKind kind, int K, int N)
     return kind == W_I4 ? (codes_bytes(kind, K, N) + 255) & ~(size_t)255 : 0;
 }
 
+// Tiles with a fused input LayerNorm: all but fp32 weights at 3-4 row blocks
+// and 2 column tiles, whose registers would spill (panel_tile skips them).
+constexpr bool ln_tile(int wk, int mb, int nct) { return !(wk == W_F32 && mb >= 3 && nct == 2); }
+
 template <int WK, int MB, int NCT>
 void launch_t(const PanelArgs& a, dim3 grid, hipStream_t st)
 {
-    hipLaunchKernelGGL((smallm_panel<WK, MB, NCT>), grid, dim3(64 * kPW), 0, st, a);
+    if constexpr (ln_tile(WK, MB, NCT)) {
+        if (a.ln_g) {
+            hipLaunchKernelGGL((smallm_panel<WK, MB, NCT, true>), grid, dim3(64 * kPW), 0, st, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((smallm_panel<WK, MB, NCT, false>), grid, dim3(64 * kPW), 0, st, a);
 }
 
 template <int WK>
@@ -421,6 +554,67 @@ void launch_wk(int MB, int NCT, const PanelArgs& a, dim3 grid, hipStream_t st)
 }
 
 thread_local int t_panel_mb = 0, t_panel_nct = 0;   // forced workgroup tile (0: the choice below)
+
+// LDS bytes past the rows and their zero bytes: with a fused input
+// LayerNorm, the rows' statistics (64 pairs), gamma and beta, and the int4
+// group's scales.
+size_t lds_extra(const GemmProblem& p)
+{
+    if (!p.ln_gamma) return 0;
+    return 512 + (size_t)p.K * 4 * (p.kind == W_I4 ? 3 : 2);
+}
+
+// k per LDS phase: the longest multiple of 256 (at most 1024) whose rows, at
+// a pitch of 16 bytes beyond the row, the 32 zero bytes and `extra` fit the
+// LDS (0 if not even 256 do).
+int phase_k(int rows, size_t extra)
+{
+    int kph = 1024;
+    while (kph > 0 && (long long)rows * (kph * 4 + 16) + 32 + (long long)extra > kLds) kph -= 256;
+    return std::min(kph, rows > 48 ? 512 : 1024);
+}
+
+// Whether a workgroup of `rows` rows can take a problem: a fused input
+// LayerNorm needs all of K in one phase.
+bool rows_fit(const GemmProblem& p, int rows)
+{
+    const int kph = phase_k(rows, lds_extra(p));
+    if (kph <= 0) return false;
+    return !p.ln_gamma || p.K <= kph;
+}
+
+// K segments for a workgroup of `rows` rows: one per LDS phase when the
+// caller gave a workspace big enough for the partial tiles (and there is no
+// fused input LayerNorm), else one.
+int segments_for(const GemmProblem& p, int rows)
+{
+    const int kph = phase_k(rows, lds_extra(p));
+    if (!p.work || p.ln_gamma || p.K <= kph) return 1;
+    const int segs = (p.K + kph - 1) / kph;
+    if (segs > kMaxSegs || (size_t)segs * p.M * p.N * 4 > p.work_bytes) return 1;
+    return segs;
+}
+
+// Modelled time (us) of a workgroup tile: MB 16-row blocks (grid.y = row
+// groups) and NCT 16-column tiles.  Workgroups run in rounds of 256 (one per
+// CU); a round costs the busiest workgroup's split work (every one of its
+// padded rows over its k), its matrix-core work (row blocks x column tiles
+// x k; fp32 weights take 3 products instead of 2) and a fixed part.  Fitted
+// to a sweep of every tile over the encoder's M = 33 shapes, workload 0
+// (M = 32) and M = 1, 16, 64 on MI355X: it picks the fastest tile on 10 of
+// 11 shapes and one within 1% on the other.
+double tile_cost(const GemmProblem& p, int mb, int nct)
+{
+    const int rows = std::min(p.M, 16 * mb);
+    const int segs = segments_for(p, rows);
+    const double kseg = (double)p.K / segs;
+    const double wgs = (double)((p.N + 16 * nct - 1) / (16 * nct)) * ((p.M + 16 * mb - 1) / (16 * mb)) * segs;
+    const double rounds = std::ceil(wgs / 256.0);
+    const double split = 16.0 * mb * kseg / 1024.0;
+    const double mfma = mb * nct * kseg / 1024.0 * (p.kind == W_F32 ? 1.5 : 1.0);
+    return rounds * (0.080 * split + 0.499 * mfma + 1.80) + 0.64;
+}
+
 
 }  // namespace
 
@@ -466,17 +660,6 @@ hipError_t launch_panel_decode(WeightKind kind, int K, int N, const void* panel,
     return hipGetLastError();
 }
 
-bool panel_supports(const GemmProblem& p)
-{
-    if (!p.panel) return false;
-    if (p.M < 1 || p.M > kSmallMaxM || p.N < 1 || p.K < 32 || p.K % 32) return false;
-    if (p.chain_bias || p.a_presplit) return false;
-    if (p.alpha == 0.0f || (p.kind == W_I8 && p.scale == 0.0f)) return false;   // beta-only step
-    if (p.lda % 4 || reinterpret_cast<uintptr_t>(p.A) % 16) return false;
-    if (p.kind == W_I4 && p.N % 32) return false;
-    return true;
-}
-
 bool panel_force_tiles(int mb, int nct)
 {
     if (mb == 0 && nct == 0) { t_panel_mb = t_panel_nct = 0; return true; }
@@ -486,53 +669,16 @@ bool panel_force_tiles(int mb, int nct)
     return true;
 }
 
-// k per LDS phase: the longest multiple of 256 (at most 1024) whose rows, at
-// a pitch of 16 bytes beyond the row, and the 32 zero bytes fit the LDS.
-int panel_phase_k(int rows)
-{
-    int kph = 1024;
-    while (kph > 256 && (long long)rows * (kph * 4 + 16) + 32 > kLds) kph -= 256;
-    return std::min(kph, rows > 48 ? 512 : 1024);
-}
-
-// K segments for a workgroup of `rows` rows: one per LDS phase when the
-// caller gave a workspace big enough for the partial tiles, else one.
-int segments_for(const GemmProblem& p, int rows)
-{
-    const int kph = panel_phase_k(rows);
-    if (!p.work || p.K <= kph) return 1;
-    const int segs = (p.K + kph - 1) / kph;
-    if ((size_t)segs * p.M * p.N * 4 > p.work_bytes) return 1;
-    return segs;
-}
-
-// Modelled time (us) of a workgroup tile: MB 16-row blocks (grid.y = row
-// groups) and NCT 16-column tiles.  Workgroups run in rounds of 256 (one per
-// CU); a round costs the busiest workgroup's split work (every one of its
-// padded rows over its k), its matrix-core work (row blocks x column tiles
-// x k; fp32 weights take 3 products instead of 2) and a fixed part.  Fitted
-// to a sweep of every tile over the encoder's M = 33 shapes, workload 0
-// (M = 32) and M = 1, 16, 64 on MI355X: it picks the fastest tile on 10 of
-// 11 shapes and one within 1% on the other.
-double tile_cost(const GemmProblem& p, int mb, int nct)
-{
-    const int rows = std::min(p.M, 16 * mb);
-    const int segs = segments_for(p, rows);
-    const double kseg = (double)p.K / segs;
-    const double wgs = (double)((p.N + 16 * nct - 1) / (16 * nct)) * ((p.M + 16 * mb - 1) / (16 * mb)) * segs;
-    const double rounds = std::ceil(wgs / 256.0);
-    const double split = 16.0 * mb * kseg / 1024.0;
-    const double mfma = mb * nct * kseg / 1024.0 * (p.kind == W_F32 ? 1.5 : 1.0);
-    return rounds * (0.080 * split + 0.499 * mfma + 1.80) + 0.64;
-}
-
+// The tile of a problem, or mb = 0 if no tile holds its rows.
 void panel_tile(const GemmProblem& p, int* mb, int* nct)
 {
     const int MB = (p.M + 15) / 16;
-    int b = 1, c = 1;
+    int b = 0, c = 1;
     double best = 1e300;
     for (int cc = 1; cc <= 2; ++cc)
         for (int bb = 1; bb <= MB; ++bb) {
+            if (!rows_fit(p, std::min(p.M, 16 * bb))) continue;
+            if (p.ln_gamma && !ln_tile(p.kind, bb, cc)) continue;
             const double t = tile_cost(p, bb, cc);
             if (t < best - 1e-9) { best = t; b = bb; c = cc; }
         }
@@ -544,8 +690,13 @@ void panel_tile(const GemmProblem& p, int* mb, int* nct)
             return std::make_pair(x, y);
         return std::make_pair(0, 0);
     }();
-    if (forced.first) { b = std::min(forced.first, MB); c = forced.second; }
-    if (t_panel_mb) { b = std::min(t_panel_mb, MB); c = t_panel_nct; }
+    int fb = forced.first, fc = forced.second;
+    if (t_panel_mb) { fb = t_panel_mb; fc = t_panel_nct; }
+    if (fb && rows_fit(p, std::min(p.M, 16 * std::min(fb, MB))) &&
+        (!p.ln_gamma || ln_tile(p.kind, std::min(fb, MB), fc))) {
+        b = std::min(fb, MB);
+        c = fc;
+    }
     *mb = b;
     *nct = c;
 }
@@ -554,7 +705,34 @@ int panel_segments(const GemmProblem& p)
 {
     int mb = 1, nct = 1;
     panel_tile(p, &mb, &nct);
-    return segments_for(p, std::min(p.M, 16 * mb));
+    return mb ? segments_for(p, std::min(p.M, 16 * mb)) : 1;
+}
+
+bool panel_fuses_out_ln(const GemmProblem& p)
+{
+    return panel_supports(p) && p.N <= kReduceLnMaxN && p.N % (8 * kLnChunk) == 0 && panel_segments(p) > 1;
+}
+
+int panel_phase_k(int rows) { return phase_k(rows, 0); }
+
+bool panel_supports(const GemmProblem& p)
+{
+    if (!p.panel) return false;
+    if (p.M < 1 || p.M > kSmallMaxM || p.N < 1 || p.K < 32 || p.K % 32) return false;
+    if (p.chain_bias || p.a_presplit) return false;
+    if (p.alpha == 0.0f || (p.kind == W_I8 && p.scale == 0.0f)) return false;   // beta-only step
+    if (p.lda % 4 || reinterpret_cast<uintptr_t>(p.A) % 16) return false;
+    if (p.kind == W_I4 && p.N % 32) return false;
+    if (p.ln_gamma && (!p.ln_beta || p.K > 1024 || p.K % (8 * kLnChunk) || reinterpret_cast<uintptr_t>(p.ln_gamma) % 16 ||
+                       reinterpret_cast<uintptr_t>(p.ln_beta) % 16))
+        return false;
+    int mb = 0, nct = 0;
+    panel_tile(p, &mb, &nct);
+    if (!mb) return false;
+    if (p.out_ln_gamma && !(p.N <= kReduceLnMaxN && p.N % (8 * kLnChunk) == 0 && p.out_ln_beta &&
+                            segments_for(p, std::min(p.M, 16 * mb)) > 1))
+        return false;
+    return true;
 }
 
 hipError_t launch_panel(const GemmProblem& p, hipStream_t st)
@@ -579,7 +757,9 @@ hipError_t launch_panel(const GemmProblem& p, hipStream_t st)
     a.s_bytes = (uint32_t)s_ext;
     int MB = 1, NCT = 1;
     panel_tile(p, &MB, &NCT);
-    a.kph = panel_phase_k(std::min(p.M, 16 * MB));
+    a.kph = phase_k(std::min(p.M, 16 * MB), lds_extra(p));
+    a.ln_g = p.ln_gamma;
+    a.ln_b = p.ln_beta;
     const int segs = segments_for(p, std::min(p.M, 16 * MB));
     a.kseg = segs > 1 ? ((p.K / 32 + segs - 1) / segs) * 32 : p.K;
     const int z = (p.K + a.kseg - 1) / a.kseg;
@@ -594,6 +774,11 @@ hipError_t launch_panel(const GemmProblem& p, hipStream_t st)
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || z == 1) return e;
+    if (p.out_ln_gamma) {
+        hipLaunchKernelGGL(panel_reduce_ln, dim3((unsigned)p.M), dim3(256), 0, st, a, z, p.out_ln_gamma,
+                           p.out_ln_beta);
+        return hipGetLastError();
+    }
     const long long mn = (long long)p.M * p.N;
     hipLaunchKernelGGL(panel_reduce, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, a, z);
     return hipGetLastError();

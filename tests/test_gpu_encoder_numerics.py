@@ -129,6 +129,52 @@ def test_weight_directories_tolerance_modes(model, fmt, T, chunk, mode):
     assert bits_equal(got[1], got[0]), "replay differs from its capture run"
 
 
+@pytest.mark.parametrize("T", [33, 64, 20])
+def test_fused_layer_norms_are_bit_identical(model, T, monkeypatch):
+    """Row groups of at most 64 rows on the panel kernels take each LayerNorm
+    that feeds a GEMM inside that GEMM (rows normalised as they are staged)
+    and the block's output LayerNorm inside the second feed-forward's split-K
+    reduce.  Those compute the LayerNorm kernel's arithmetic operation for
+    operation, so the encoder with them (the default) equals the encoder with
+    separate LayerNorm launches (PK_GPU_FUSE_LN=0 at creation) bit for bit."""
+    x = bench.enc_rng(0xFEAA, T).standard_normal((T, bench.D)).astype(np.float32)
+    fused = run(model, x, 0, pk.NUMERICS_DEFAULT)
+    monkeypatch.setenv("PK_GPU_FUSE_LN", "0")
+    apart = run(model, x, 0, pk.NUMERICS_DEFAULT)
+    assert bits_equal(fused[0], apart[0]), describe_mismatch(fused[0], apart[0])
+    assert bits_equal(fused[1], fused[0]), "replay differs from its capture run"
+
+
+def test_exact_after_fast_regrow(model):
+    """The blocks' position projections are constants that runs in every
+    mode read.  A fast run that first sees a sequence longer than the
+    projections cover (600 frames, one sequence) recomputes them, on the
+    exact chains, so a later exact run (300 frames) is still bit-identical to
+    the oracle's encoder."""
+    import torch
+    x6 = bench.enc_rng(0xFEA9, 600).standard_normal((600, bench.D)).astype(np.float32)
+    x3 = bench.enc_rng(0xFEA9, 300).standard_normal((300, bench.D)).astype(np.float32)
+    want = po.encoder(model.blocks, bench.N_BLOCKS, model.pe, bench.PE_CENTER, x3, 0, 0)
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(model.blocks, ctypes.c_void_p),
+            bench.N_BLOCKS, model.pe.ctypes.data, model.pe.shape[0], bench.PE_CENTER)
+    try:
+        dev = torch.device("cuda:0")
+        s = torch.cuda.current_stream(dev).cuda_stream
+        d6, d3 = torch.from_numpy(x6).to(dev), torch.from_numpy(x3).to(dev)
+        o6, o3 = torch.empty_like(d6), torch.full_like(d3, float("nan"))
+        pk.call("pk_gpu_encoder_set_numerics", enc, pk.NUMERICS_FAST)
+        pk.call("pk_gpu_encoder_run_dev", enc, d6.data_ptr(), 600, 0, 0, o6.data_ptr(), s)
+        torch.cuda.synchronize(dev)
+        pk.call("pk_gpu_encoder_set_numerics", enc, pk.NUMERICS_EXACT)
+        pk.call("pk_gpu_encoder_run_dev", enc, d3.data_ptr(), 300, 0, 0, o3.data_ptr(), s)
+        torch.cuda.synchronize(dev)
+        got = o3.cpu().numpy()
+    finally:
+        pk.load().pk_gpu_encoder_destroy(enc)
+    assert bits_equal(got, want), describe_mismatch(got, want)
+
+
 def test_long_input_unaffected(model):
     """200 frames unchunked (one group of 200 rows): the setting changes nothing."""
     x = bench.enc_rng(0xFEA7, 200).standard_normal((200, bench.D)).astype(np.float32)
