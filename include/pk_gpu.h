@@ -111,8 +111,12 @@ int pk_gpu_gemm_i8_noalloc(int M, int N, int K, float alpha,
 /* Replaces cblas_sgemm_q4b (blas.h:64-69, blas.c:950-963): packed int4
  * B [K][ldb bytes] (two's-complement nibbles, low nibble = even column,
  * extract_weights.py:589-592) with fp32 scales [K][N/32] (blas.c:794, 958).
- * N must be a multiple of 32 (the format's group size,
- * extract_weights.py:523) and ldb >= N/2. */
+ * N must be even and ldb >= N/2.  As in the reference, weight (k, n) takes
+ * scale k * (N/32) + n/32 with N/32 floored: when N is not a multiple of 32
+ * (no shipped weight, extract_weights.py:523), the columns past the last
+ * whole group of row k take row k + 1's first scale, and the last row's
+ * read one float past K * (N/32), which `scales` must then hold
+ * (K * (N/32) + 1 floats). */
 int pk_gpu_gemm_i4(int M, int N, int K, float alpha,
                    const float *A, int lda,
                    const uint8_t *B, const float *scales, int ldb,

@@ -67,6 +67,15 @@ struct GemmProblem {
     const float* out_ln_beta = nullptr;
 };
 
+// Scales an int4 GEMM reads: the reference takes scale k * (N/32) + n/32 for
+// weight (k, n) with N/32 floored (blas.c:794, 958), so when N % 32 != 0 the
+// columns past the last whole group of row k read row k + 1's first scale and
+// the last row's read one float past K * (N/32).
+inline size_t int4_scale_count(int K, int N)
+{
+    return (size_t)K * (N / 32) + (N % 32 ? 1 : 0);
+}
+
 // Partial tiles of one split-K launch: at most 256 workgroups of at most
 // 256 x 128 fp32 outputs each (32 MiB).
 constexpr size_t kSplitWorkBytes = (size_t)256 * 256 * 128 * 4;

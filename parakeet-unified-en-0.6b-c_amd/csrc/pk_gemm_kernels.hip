@@ -176,7 +176,7 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
     const size_t b_row = p.kind == W_I4 ? (size_t)p.N / 2 : (size_t)p.N;
     const size_t a_ext = ((size_t)(p.M - 1) * p.lda + p.K) * 4;
     const size_t b_ext = ((size_t)(p.K - 1) * p.ldb + b_row) * esz;
-    const size_t s_ext = p.kind == W_I4 ? (size_t)p.K * (p.N / 32) * 4 : 0;
+    const size_t s_ext = p.kind == W_I4 ? int4_scale_count(p.K, p.N) * 4 : 0;
     const size_t lim = (size_t)1 << 31;
     if (a_ext >= lim || b_ext >= lim || s_ext >= lim) return hipErrorInvalidValue;
     a.a_bytes = (uint32_t)a_ext;
@@ -255,7 +255,7 @@ hipError_t launch_dequant(WeightKind kind, int K, int N, const void* B, int ldb,
     const size_t esz = kind == W_F32 ? 4 : 1;
     const size_t b_row = kind == W_I4 ? (size_t)N / 2 : (size_t)N;
     const size_t b_ext = ((size_t)(K - 1) * ldb + b_row) * esz;
-    const size_t s_ext = kind == W_I4 ? (size_t)K * (N / 32) * 4 : 0;
+    const size_t s_ext = kind == W_I4 ? int4_scale_count(K, N) * 4 : 0;
     if (b_ext >= ((size_t)1 << 31) || s_ext >= ((size_t)1 << 31)) return hipErrorInvalidValue;
     a.b_bytes = (uint32_t)b_ext;
     a.s_bytes = (uint32_t)s_ext;

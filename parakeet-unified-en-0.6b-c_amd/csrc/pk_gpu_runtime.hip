@@ -432,8 +432,8 @@ int host_gemm(GemmProblem p, const float* hA, const void* hB, const float* hScal
         if (p.kind == pkgpu::W_I4) {
             const void* dS = nullptr;
             int lds = 0;
-            rc = operand(c, 3, hScales, p.K, p.N / 32, p.N / 32, sizeof(float), &dS, &lds,
-                         &hold[2]);
+            const int ns = (int)pkgpu::int4_scale_count(p.K, p.N);   // one flat run of floats
+            rc = operand(c, 3, hScales, 1, ns, ns, sizeof(float), &dS, &lds, &hold[2]);
             if (rc) return rc;
             p.scales = static_cast<const float*>(dS);
         }
@@ -717,7 +717,7 @@ int pk_gpu_gemm_i8_noalloc(int M, int N, int K, float alpha, const float* A, int
 int pk_gpu_gemm_i4(int M, int N, int K, float alpha, const float* A, int lda,
                    const uint8_t* B, const float* scales, int ldb, float beta, float* C, int ldc)
 {
-    if (N % 32 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is not a multiple of 32", N);
+    if (N % 2 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is odd (rows hold N/2 bytes)", N);
     int rc = check_gemm(M, N, K, lda, N / 2, ldb, ldc);
     if (rc) return rc;
     GemmProblem p{pkgpu::W_I4, M, N, K, alpha, beta, nullptr, lda, nullptr, ldb,
@@ -779,7 +779,7 @@ int pk_gpu_gemm_i4_ex_dev(int M, int N, int K, float alpha, const float* dA, int
                           const uint8_t* dB, const float* dscales, int ldb, float beta, float* dC,
                           int ldc, const float* dbias, int epilogue, void* stream)
 {
-    if (N % 32 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is not a multiple of 32", N);
+    if (N % 2 != 0) return fail(PK_GPU_EINVAL, "int4: N=%d is odd (rows hold N/2 bytes)", N);
     int rc = check_gemm(M, N, K, lda, N / 2, ldb, ldc);
     if (rc) return rc;
     GemmProblem p{pkgpu::W_I4, M, N, K, alpha, beta, dA, lda, dB, ldb, 0.0f, dscales, dC, ldc};
@@ -998,7 +998,7 @@ int pk_gpu_dequant_dev(int bits, int K, int N, const void* dB, int ldb, float sc
     if (K < 0 || N < 0) return fail(PK_GPU_EINVAL, "K = %d, N = %d", K, N);
     if (K == 0 || N == 0) return PK_GPU_OK;
     const pkgpu::WeightKind kind = bits == 4 ? pkgpu::W_I4 : bits == 8 ? pkgpu::W_I8 : pkgpu::W_F32;
-    if (bits == 4 && N % 32) return fail(PK_GPU_EINVAL, "int4: N = %d is not a multiple of 32", N);
+    if (bits == 4 && N % 2) return fail(PK_GPU_EINVAL, "int4: N = %d is odd", N);
     if (ldb < (bits == 4 ? N / 2 : N)) return fail(PK_GPU_EINVAL, "ldb = %d too small for N = %d", ldb, N);
     if (unit_path && N % pkgpu::dequant_unit_columns(kind))
         return fail(PK_GPU_EINVAL, "unit path: N = %d is not a multiple of %d", N,

@@ -89,6 +89,7 @@ def test_decode_argument_checks(dev):
     lib = pk.load()
     ok = dev.zeros(64, device="cuda")
     assert pk.STATUS[lib.pk_gpu_dequant_dev(16, 4, 4, ok.data_ptr(), 4, 1.0, None, 0, ok.data_ptr(), None)] == "EINVAL"
-    assert pk.STATUS[lib.pk_gpu_dequant_dev(4, 4, 48, ok.data_ptr(), 24, 1.0, ok.data_ptr(), 0, ok.data_ptr(), None)] == "EINVAL"
+    # int4 rows hold N/2 bytes: odd N is refused before anything is launched
+    assert pk.STATUS[lib.pk_gpu_dequant_dev(4, 4, 47, ok.data_ptr(), 24, 1.0, ok.data_ptr(), 0, ok.data_ptr(), None)] == "EINVAL"
     assert pk.STATUS[lib.pk_gpu_dequant_dev(8, 4, 6, ok.data_ptr(), 6, 1.0, None, 1, ok.data_ptr(), None)] == "EINVAL"
     assert pk.STATUS[lib.pk_gpu_dequant_dev(8, 4, 8, ok.data_ptr(), 4, 1.0, None, 0, ok.data_ptr(), None)] == "EINVAL"

@@ -334,6 +334,36 @@ def test_unregister_while_other_threads_call(dev):
     assert flips > 0
 
 
+@pytest.mark.parametrize("N", [16, 40, 48, 50, 80, 82])
+def test_int4_ragged_n(dev, N):
+    """int4 with N not a multiple of 32: the reference floors n_groups and
+    keeps its scale index (the tail columns of row k read row k + 1's first
+    scale, the last row's one float past K * (N/32)); its edge columns'
+    scalar loop is the same fma chain (test_oracle pins the oracle to the
+    compiled reference there).  Device and host-pointer calls, and the cblas
+    shim's forwarder, are bit-identical to the oracle."""
+    M, K = 33, 160
+    P = po.bytes_((K, N // 2), po.seed(SEED, f"i4r.{N}.P"))
+    S = po.uniform((K * (N // 32) + (1 if N % 32 else 0),), 0.005, 0.02, po.seed(SEED, f"i4r.{N}.S"))
+    A = po.normal((M, K), 0.0, 1.0, po.seed(SEED, f"i4r.{N}.A"))
+    C0 = po.normal((M, N), 0.0, 1.0, po.seed(SEED, f"i4r.{N}.C"))
+    want = po.sgemm_q4b(A, P, S, C0.copy(), 0.75, 0.5)
+    assert_same(dev.gemm("i4", A, P, C0, 0.75, 0.5, scales=S), want, f"dev N={N}")
+    C = C0.copy()
+    pk.call("pk_gpu_gemm_i4", M, N, K, 0.75, A.ctypes.data, K, P.ctypes.data, S.ctypes.data, N // 2,
+            0.5, C.ctypes.data, N)
+    assert_same(C, want, f"host N={N}")
+    shim = ctypes.CDLL(pk.SHIM_PATH)
+    C = C0.copy()
+    shim.cblas_sgemm_q4b(ctypes.c_int(M), ctypes.c_int(N), ctypes.c_int(K), ctypes.c_float(0.75),
+                         ctypes.c_void_p(A.ctypes.data), ctypes.c_int(K), ctypes.c_void_p(P.ctypes.data),
+                         ctypes.c_void_p(S.ctypes.data), ctypes.c_int(N // 2), ctypes.c_float(0.5),
+                         ctypes.c_void_p(C.ctypes.data), ctypes.c_int(N))
+    assert_same(C, want, f"cblas_sgemm_q4b N={N}")
+    assert pk.load().pk_gpu_gemm_i4(M, N - 1, K, 1.0, A.ctypes.data, K, P.ctypes.data, S.ctypes.data,
+                                     N // 2, 0.0, C.ctypes.data, N) == -1        # odd N
+
+
 def test_pointwise_conv_weight_as_A(dev):
     """pk_pointwise_conv1d: C[Cout][T] = W[Cout][Cin] * x[Cin][T] (tensor_ops.c:579-590),
     with the weight registered as the A operand."""

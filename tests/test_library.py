@@ -63,10 +63,10 @@ def test_argument_validation_precedes_device_use():
     C = np.zeros((2, 64), np.float32)
     P = np.zeros((4, 24), np.uint8)
     S = np.ones((4, 2), np.float32)
-    # int4 needs N % 32 == 0 (the format's group size)
-    assert lib.pk_gpu_gemm_i4(2, 48, 4, 1.0, A.ctypes.data, 4, P.ctypes.data, S.ctypes.data,
+    # int4 rows hold N/2 bytes: N must be even
+    assert lib.pk_gpu_gemm_i4(2, 47, 4, 1.0, A.ctypes.data, 4, P.ctypes.data, S.ctypes.data,
                               24, 0.0, C.ctypes.data, 64) == -1
-    assert b"multiple of 32" in lib.pk_gpu_last_error()
+    assert b"odd" in lib.pk_gpu_last_error()
     # transposed forms are not used by the reference call sites
     assert lib.pk_gpu_sgemm(112, 111, 2, 4, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 4, 0.0,
                             C.ctypes.data, 64) == -2

@@ -136,6 +136,54 @@ def test_sgemm_q4b_matches_reference(M, N, K):
         assert bits_equal(got, want), (M, N, K, alpha, beta)
 
 
+def ragged_int4_case(M, N, K, tag):
+    """Packed codes [K][N/2] and the K * floor(N/32) + 1 scales the
+    reference reads when N % 32 != 0 (blas.c:794, 958)."""
+    P = po.bytes_((K, N // 2), po.seed(SEED, f"{tag}.P"))
+    n_s = K * (N // 32) + (1 if N % 32 else 0)
+    S = po.uniform((n_s,), 0.005, 0.02, po.seed(SEED, f"{tag}.S"))
+    A, C0 = rand_case(M, N, K, tag)
+    return A, P, S, C0
+
+
+@needs_portable
+@pytest.mark.parametrize("N", [16, 40, 48, 50, 80, 82, 114])
+def test_sgemm_q4b_ragged_n_matches_portable_reference(N):
+    """int4 GEMMs whose N is not a multiple of 32 (no shipped weight): the
+    reference floors n_groups = N/32 (blas.c:958) and still indexes scale
+    k * n_groups + n/32 (blas.c:794, 896, 938), and its N % 16 edge columns
+    take the scalar loop of blas.c:925-946.  The oracle (the same dequant
+    fl(q * s) and fma chain for every column) equals the compiled portable
+    build bit for bit, edge columns included (N = 50, 82, 114)."""
+    M, K = 5, 96
+    A, P, S, C0 = ragged_int4_case(M, N, K, f"i4r.{N}")
+    for alpha, beta in AB:
+        got = po.sgemm_q4b(A, P, S, C0.copy(), alpha, beta, impl="oracle")
+        want = po.sgemm_q4b(A, P, S, C0.copy(), alpha, beta, impl="portable")
+        assert bits_equal(got, want), (N, alpha, beta)
+
+
+def test_int4_ragged_n_scale_index():
+    """Independent of the reference: at N = 48 (one whole group), a code at
+    column 40 of row k takes scale k * 1 + 40 // 32 = k + 1, row k + 1's
+    first scale; at N = 16 (no whole group) every row takes scale 0.  A
+    scale index that did not floor n_groups, or that kept rows apart, fails
+    the fp64 bound."""
+    for N, col in ((48, 40), (16, 7), (80, 70)):
+        M, K = 3, 40
+        ng = N // 32
+        P = np.zeros((K, N // 2), np.uint8)
+        P[:, col // 2] = 1 if col % 2 == 0 else 0x10          # code +1 at column `col`
+        S = (np.arange(K * ng + 1, dtype=np.float32) + 1.0) / 64.0
+        A = po.normal((M, K), 0.0, 1.0, po.seed(SEED, f"i4idx.{N}"))
+        C = po.sgemm_q4b(A, P, S, np.zeros((M, N), np.float32))
+        idx = np.arange(K) * ng + col // 32
+        exact = A.astype(np.float64) @ S[idx].astype(np.float64)
+        mag = np.abs(A.astype(np.float64)) @ np.abs(S[idx].astype(np.float64))
+        assert np.all(np.abs(C[:, col] - exact) <= (K + 2) * 2.0 ** -23 * mag), N
+        assert not np.any(np.delete(C, col, axis=1)), N
+
+
 def x86_avx2_int4_weights(P, S):
     """What blas.c:815-833 produces on x86: _mm_slli/_mm_srai_epi16 work on
     16-bit lanes, so within each 8-byte (16-column) panel, column 2w gets the
