@@ -95,6 +95,51 @@ static void w_i4(Writer *w, const char *name, const uint8_t *p, size_t nbytes,
     w->off += (long long)nbytes + (long long)ns * 4;
 }
 
+/* The greedy RNN-T decode of decoder.c:80-132 replayed through the same
+ * pk_decoder_step / pk_joint calls, recording the smallest gap between the
+ * winning logit and the best other logit over every argmax (decoder.c:107-114,
+ * first maximum wins on a tie, so a gap of 0 is a tie).  A perturbation of
+ * the encoder output can change a token only where its effect on the logits
+ * exceeds such a gap.  Returns the number of tokens; *same is 1 when they
+ * equal `tokens` (the reference decoder's own output). */
+static int greedy_margin(const PkModel *m, const float *enc, int T, const int *tokens, int n_ref,
+                         float *min_gap, int *gap_frame, long *decisions, int *same)
+{
+    LSTMState st;
+    memset(&st, 0, sizeof st);
+    float pred[PK_LSTM_HIDDEN], logits[PK_VOCAB];
+    pk_decoder_step(m, PK_BLANK, &st, pred);
+    int n = 0;
+    *min_gap = 3.0e38f;
+    *gap_frame = -1;
+    *decisions = 0;
+    *same = 1;
+    for (int t = 0; t < T; t++) {
+        const float *enc_t = enc + (size_t)t * PK_D_MODEL;
+        for (int s = 0; s < 10; s++) {
+            pk_joint(m, enc_t, pred, logits);
+            int best = 0;
+            for (int v = 1; v < PK_VOCAB; v++)
+                if (logits[v] > logits[best]) best = v;
+            float second = -3.0e38f;
+            for (int v = 0; v < PK_VOCAB; v++)
+                if (v != best && logits[v] > second) second = logits[v];
+            const float gap = logits[best] - second;
+            ++*decisions;
+            if (gap < *min_gap) {
+                *min_gap = gap;
+                *gap_frame = t;
+            }
+            if (best == PK_BLANK) break;
+            if (n >= n_ref || tokens[n] != best) *same = 0;
+            n++;
+            pk_decoder_step(m, best, &st, pred);
+        }
+    }
+    if (n != n_ref) *same = 0;
+    return n;
+}
+
 static float *scratch_f;
 static size_t scratch_n;
 static float *fbuf(size_t n)
@@ -561,6 +606,10 @@ int main(int argc, char **argv)
     t0 = now_s();
     int n_tok = pk_greedy_decode(&m, enc, T, &tokens);
     double t_dec = now_s() - t0;
+    float min_gap = 0.0f;
+    int gap_frame = -1, replay_same = 0;
+    long decisions = 0;
+    (void)greedy_margin(&m, enc, T, tokens, n_tok, &min_gap, &gap_frame, &decisions, &replay_same);
 
     /* bit test: this unit is built with -ffast-math, where isfinite() folds to 1 */
     float amax = 0.0f;
@@ -582,6 +631,8 @@ int main(int argc, char **argv)
            "\"out\": %d, \"pre_encode_out\": %d}",
            b0->ff1.linear1_w.bits, b0->ff1.linear2_w.bits, b0->mha.linear_qkv_w.bits,
            b0->mha.linear_pos_w.bits, b0->mha.linear_out_w.bits, m.enc.pre_encode.out_w.bits);
+    printf(", \"min_logit_margin\": %.9g, \"margin_frame\": %d, \"decisions\": %ld, \"margin_replay_equal\": %d",
+           min_gap, gap_frame, decisions, replay_same);
     printf(", \"threads\": %d, \"load_s\": %.3f, \"encoder_s\": %.4f, \"encoder_first_s\": %.4f, "
            "\"decoder_s\": %.4f}\n",
            pk_pool_nthreads(pk_pool()), t_load, t_enc, t_first, t_dec);

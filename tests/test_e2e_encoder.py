@@ -64,6 +64,17 @@ def run(binary, frames, tmp_path, dump=None, attn_gain=None, from_mel=False, ext
     return json.loads(line)
 
 
+def margin(ref):
+    """The reference decode's smallest gap between the winning logit and the
+    best other one over all argmax decisions (decoder.c:107-114; a token can
+    change only where a perturbation of the logits exceeds it), with the
+    frame where it occurs; the driver's replay of the decode must reproduce
+    the reference's tokens."""
+    assert ref["margin_replay_equal"] == 1, "the margin replay diverged from pk_greedy_decode"
+    return {"min_logit_margin_reference": ref["min_logit_margin"], "margin_frame": ref["margin_frame"],
+            "decisions": ref["decisions"]}
+
+
 def test_reference_drivers_cpu(tmp_path):
     """CPU only: the portable-path and x86 builds run, agree on shape and
     differ in value (the x86 int4 unpack)."""
@@ -126,7 +137,8 @@ def test_gpu_dropin_weight_directories(mode, tmp_path, model_dir):
     assert gpu["tokens_fnv"] == ref["tokens_fnv"] == x86["tokens_fnv"]
     print(json.dumps({"mode": mode, "frames": frames, "threads": THREADS,
                       "encoder_frames_per_s_gpu_dropin": round(frames / gpu["encoder_s"], 1),
-                      "encoder_frames_per_s_cpu_reference_x86": round(frames / x86["encoder_s"], 1)}),
+                      "encoder_frames_per_s_cpu_reference_x86": round(frames / x86["encoder_s"], 1),
+                      **margin(ref)}),
           flush=True)
 
 
@@ -145,9 +157,10 @@ def test_gpu_dropin_matches_reference_bit_for_bit(frames, tmp_path):
     assert gpu["enc_fnv"] == ref["enc_fnv"], "encoder outputs differ"
     assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"]
     assert gpu["first_tokens"] == ref["first_tokens"]
-    print(json.dumps({"frames": frames, "threads": THREADS,
+    print(json.dumps({"frames": frames, "threads": THREADS, **margin(ref),
                       "encoder_frames_per_s_gpu_dropin": round(frames / gpu["encoder_s"], 1),
-                      "encoder_frames_per_s_cpu_reference": round(frames / ref["encoder_s"], 1)}),
+                      "encoder_frames_per_s_cpu_reference": round(frames / ref["encoder_s"], 1),
+                      **margin(ref)}),
           flush=True)
     if frames < 3200:
         x86 = run("pk_encode_ref_x86", frames, tmp_path)
@@ -179,12 +192,13 @@ def test_gpu_dropin_short_clip_small_m(attn_gain, tmp_path):
     print(json.dumps({"frames": frames, "attn_gain": attn_gain, "max_rel_deviation_small_m": dev,
                       "tokens_small_m": gpu["n_tokens"], "tokens_reference": ref["n_tokens"],
                       "tokens_equal": gpu["tokens_fnv"] == ref["tokens_fnv"],
-                      "exact_mode_bit_identical": exact["enc_fnv"] == ref["enc_fnv"]}), flush=True)
+                      "exact_mode_bit_identical": exact["enc_fnv"] == ref["enc_fnv"], **margin(ref)}),
+          flush=True)
     assert gpu["finite"] == 1 and gpu["chunked"] == ref["chunked"] == 0
     assert exact["enc_fnv"] == ref["enc_fnv"] and exact["tokens_fnv"] == ref["tokens_fnv"]
     if attn_gain is not None:
         assert dev <= 1e-3
-        assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"]
+        assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"], margin(ref)
 
 
 @pytest.mark.gpu
@@ -205,10 +219,10 @@ def test_gpu_dropin_fast_numerics(tmp_path):
     dev = float(np.abs(a - b).max() / np.abs(b).max())
     print(json.dumps({"frames": frames, "max_rel_deviation_fast": dev, "tokens_fast": gpu["n_tokens"],
                       "tokens_reference": ref["n_tokens"],
-                      "tokens_equal": gpu["tokens_fnv"] == ref["tokens_fnv"]}), flush=True)
+                      "tokens_equal": gpu["tokens_fnv"] == ref["tokens_fnv"], **margin(ref)}), flush=True)
     assert gpu["finite"] == 1 and gpu["chunked"] == ref["chunked"]
     assert dev <= 1e-3
-    assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"]
+    assert gpu["n_tokens"] == ref["n_tokens"] and gpu["tokens_fnv"] == ref["tokens_fnv"], margin(ref)
 
 
 def resident_vs_reference(frames, tmp_path, attn_gain, from_mel=False, mode=None):
@@ -261,7 +275,7 @@ def test_gpu_resident_encoder_matches_reference(frames, tmp_path):
     exactly."""
     gres, ref, dev = resident_vs_reference(frames, tmp_path, 0.05)
     assert dev <= 1e-3
-    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"]
+    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"], margin(ref)
 
 
 @pytest.mark.gpu
@@ -294,7 +308,7 @@ def test_gpu_resident_encoder_from_mel(frames, tmp_path):
     resident blocks), trained-like attention weights; token ids equal."""
     gres, ref, dev = resident_vs_reference(frames, tmp_path, 0.05, from_mel=True)
     assert dev <= 1e-3
-    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"]
+    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"], margin(ref)
 
 
 @pytest.mark.gpu
@@ -309,4 +323,4 @@ def test_gpu_resident_encoder_weight_directories(mode, tmp_path):
     mixed model."""
     gres, ref, dev = resident_vs_reference(900, tmp_path, 0.05, from_mel=True, mode=mode)
     assert dev <= 1e-3
-    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"]
+    assert gres["n_tokens"] == ref["n_tokens"] and gres["tokens_fnv"] == ref["tokens_fnv"], margin(ref)
