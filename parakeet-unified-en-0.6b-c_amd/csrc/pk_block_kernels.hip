@@ -564,41 +564,26 @@ __global__ void glu_rows(const float* __restrict__ in, int ldi, float* out, int 
 // reference's 8-wide interior take the explicit fma chain over the taps; the
 // others take the compiled form of its scalar loops: taps 0..7 multiplied,
 // out-of-range ones as +0, reduced as hsum8 and added to the bias, then fma
-// for the remaining taps.
-// KK = 9 (PK_CONV_KERNEL) fixes the tap count at compile time so every load
-// of an output is issued before its chain; KK = 0 takes p.K at run time.
-template <int KK>
-__global__ void depthwise_swish(DwArgs p)
+// for the remaining taps.  dw_output is that arithmetic for one output, with
+// the input value at window position j given by win(j) (window position 0 is
+// input time t - pad).
+template <int KK, typename Win, typename Wt>
+__device__ inline float dw_output(const DwArgs& p, int T, int t, int k_rt, float bias, Win win, Wt wt)
 {
-    const int T = p.chunk_T ? p.chunk_T[blockIdx.y] : p.T;   // this chunk's rows
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)T * p.C) return;
-    const int t = (int)(idx / p.C), c = (int)(idx % p.C);
-    const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.y] : 0;
-    const float* x = p.x + (size_t)row0 * p.ldx + c;
-    // input value at time u (GLU'd on the fly when p.glu)
-    auto in = [&](int u) {
-        const float* xr = x + (size_t)u * p.ldx;
-        return p.glu ? glu_value(xr[0], xr[p.C]) : xr[0];
-    };
-    const int K = KK ? KK : p.K;
-    const float* wc = p.w + (size_t)c * K;
+    const int K = KK > 0 ? KK : k_rt;
     const int pad = (K - 1) / 2;
     const int t_hi = T - pad > pad ? T - pad : pad;
     const int t_vec = pad + (t_hi - pad) / 8 * 8;
-    float val = p.b ? p.b[c] : 0.0f;
+    float val = bias;
     if (t >= pad && t < t_vec) {
         if constexpr (KK > 0) {
-            float xv[KK], wv[KK];
+            float xv[KK];
 #pragma unroll
-            for (int k = 0; k < KK; ++k) {
-                xv[k] = in(t - pad + k);
-                wv[k] = wc[k];
-            }
+            for (int k = 0; k < KK; ++k) xv[k] = win(k);
 #pragma unroll
-            for (int k = 0; k < KK; ++k) val = __fmaf_rn(xv[k], wv[k], val);
+            for (int k = 0; k < KK; ++k) val = __fmaf_rn(xv[k], wt(k), val);
         } else {
-            for (int k = 0; k < K; ++k) val = __fmaf_rn(in(t - pad + k), wc[k], val);
+            for (int k = 0; k < K; ++k) val = __fmaf_rn(win(k), wt(k), val);
         }
     } else {
         const int K8 = K & ~7;
@@ -607,16 +592,85 @@ __global__ void depthwise_swish(DwArgs p)
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
                 const int src = t - pad + k0 + l;
-                pr[l] = (src >= 0 && src < T) ? __fmul_rn(in(src), wc[k0 + l]) : 0.0f;
+                pr[l] = (src >= 0 && src < T) ? __fmul_rn(win(k0 + l), wt(k0 + l)) : 0.0f;
             }
             val = __fadd_rn(val, hsum8(pr));
         }
         for (int k = K8; k < K; ++k) {
             const int src = t - pad + k;
-            if (src >= 0 && src < T) val = __fmaf_rn(in(src), wc[k], val);
+            if (src >= 0 && src < T) val = __fmaf_rn(win(k), wt(k), val);
         }
     }
-    p.out[(size_t)(row0 + t) * p.ldo + c] = p.swish ? swish_f(val) : val;
+    return p.swish ? swish_f(val) : val;
+}
+
+// Any tap count: one thread per output, each input read where it is used
+// (GLU'd on the fly when p.glu).
+__global__ void depthwise_swish(DwArgs p)
+{
+    const int T = p.chunk_T ? p.chunk_T[blockIdx.y] : p.T;   // this chunk's rows
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)T * p.C) return;
+    const int t = (int)(idx / p.C), c = (int)(idx % p.C);
+    const int row0 = p.chunk_rows ? p.chunk_rows[blockIdx.y] : 0;
+    const int pad = (p.K - 1) / 2;
+    const float* x = p.x + (size_t)row0 * p.ldx + c;
+    const float* wc = p.w + (size_t)c * p.K;
+    // window position j is input time t - pad + j, read only where in range
+    auto win = [&](int j) {
+        const float* xr = x + (size_t)(t - pad + j) * p.ldx;
+        return p.glu ? glu_value(xr[0], xr[p.C]) : xr[0];
+    };
+    p.out[(size_t)(row0 + t) * p.ldo + c] =
+        dw_output<0>(p, T, t, p.K, p.b ? p.b[c] : 0.0f, win, [&](int k) { return wc[k]; });
+}
+
+// KK taps fixed at compile time: a workgroup takes TB output times of 64
+// channels of one chunk.  Its input window (TB + KK - 1 times) is staged in
+// LDS once, gated when p.glu, so each input is read, and its GLU formed,
+// once per workgroup rather than once per tap; window times outside the
+// chunk hold 0 and are never taken (the edge path checks the range).  All of
+// a thread's window loads are issued before the first is used.
+template <int KK, int TB>
+__global__ __launch_bounds__(256) void depthwise_tiled(DwArgs p)
+{
+    constexpr int pad = (KK - 1) / 2, W = TB + KK - 1, WQ = (W + 3) / 4;
+    __shared__ float win_s[W][64];
+    const int z = blockIdx.z;
+    const int T = p.chunk_T ? p.chunk_T[z] : p.T;            // this chunk's rows
+    const int t0 = blockIdx.x * TB;
+    if (t0 >= T) return;                                     // the whole workgroup
+    const int row0 = p.chunk_rows ? p.chunk_rows[z] : 0;
+    const int lane = threadIdx.x & 63, slot = threadIdx.x >> 6;
+    const int c = blockIdx.y * 64 + lane;
+    const int cc = min(c, p.C - 1);                          // loads of columns past C: column C - 1
+    const float* x = p.x + (size_t)row0 * p.ldx + cc;
+    float va[WQ], vb[WQ];
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) {
+        const int u = min(max(t0 - pad + slot + 4 * q, 0), T - 1);
+        va[q] = x[(size_t)u * p.ldx];
+        vb[q] = p.glu ? x[(size_t)u * p.ldx + p.C] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) {
+        const int j = slot + 4 * q, u = t0 - pad + j;
+        if (j < W) win_s[j][lane] = (u >= 0 && u < T) ? (p.glu ? glu_value(va[q], vb[q]) : va[q]) : 0.0f;
+    }
+    __syncthreads();
+    if (c >= p.C) return;
+    float wc[KK];
+#pragma unroll
+    for (int k = 0; k < KK; ++k) wc[k] = p.w[(size_t)c * KK + k];
+    const float bias = p.b ? p.b[c] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < TB / 4; ++q) {
+        const int t = t0 + slot + 4 * q;
+        if (t >= T) break;                                   // uniform per wave
+        const int j0 = t - t0;                               // window position of input time t - pad
+        p.out[(size_t)(row0 + t) * p.ldo + c] = dw_output<KK>(
+            p, T, t, KK, bias, [&](int j) { return win_s[j0 + j][lane]; }, [&](int k) { return wc[k]; });
+    }
 }
 
 // ---- pre-encode subsampling (encoder.c:103-174) ------------------------------
@@ -798,11 +852,18 @@ hipError_t launch_depthwise(const DwArgs& a, int n_chunks, hipStream_t s)
 {
     const long long n = (long long)a.T * a.C;
     if (n <= 0 || n_chunks <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((n + 255) / 256), n_chunks);
-    if (a.K == 9)
-        hipLaunchKernelGGL(depthwise_swish<9>, grid, dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL(depthwise_swish<0>, grid, dim3(256), 0, s, a);
+    if (a.K == 9) {
+        // short sequences: 16-time tiles (more workgroups); else 32 (less overlap)
+        const unsigned cb = (unsigned)((a.C + 63) / 64);
+        if (a.T <= 128)
+            hipLaunchKernelGGL((depthwise_tiled<9, 16>), dim3((unsigned)((a.T + 15) / 16), cb, n_chunks), dim3(256),
+                               0, s, a);
+        else
+            hipLaunchKernelGGL((depthwise_tiled<9, 32>), dim3((unsigned)((a.T + 31) / 32), cb, n_chunks), dim3(256),
+                               0, s, a);
+    } else {
+        hipLaunchKernelGGL(depthwise_swish, dim3((unsigned)((n + 255) / 256), n_chunks), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -392,7 +392,11 @@ __device__ inline float sum_segments(const float* work, size_t o, size_t mn, int
 // LayerNorm that follows the residual add, fused): one workgroup per row,
 // the row in LDS, its statistics by the first 8 lanes (ln_row_stats), then
 // C = fl(fl(fl(v - mean) * inv) * gamma + beta).  N <= kReduceLnMaxN.
-constexpr int kReduceLnMaxN = 4096;
+constexpr int kReduceLnMaxN = 2048;
+// EPT outputs per thread (N <= 256 EPT): each thread's loads (partials,
+// C, bias, gamma, beta of all its outputs) are issued before the first is
+// used, so the row costs one memory round trip rather than EPT of them.
+template <int EPT>
 __global__ __launch_bounds__(256) void panel_reduce_ln(PanelArgs p, int segs, const float* gamma,
                                                        const float* beta)
 {
@@ -400,21 +404,37 @@ __global__ __launch_bounds__(256) void panel_reduce_ln(PanelArgs p, int segs, co
     __shared__ float st[2];
     const int m = blockIdx.x;
     const size_t mn = (size_t)p.M * p.N;
-    for (int n = threadIdx.x; n < p.N; n += 256) {
+    float* crow = p.C + (size_t)m * p.ldc;
+    float part[EPT][kMaxSegs], cv[EPT], bv[EPT], gv[EPT], be[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        // outputs past N load output N - 1's operands and are not stored
+        const int n = min((int)threadIdx.x + 256 * e, p.N - 1);
         const size_t o = (size_t)m * p.N + n;
-        const float sum = sum_segments(p.work, o, mn, segs);
-        float* cp = p.C + (size_t)m * p.ldc + n;
+#pragma unroll
+        for (int z = 0; z < kMaxSegs; ++z) part[e][z] = p.work[(z < segs ? (size_t)z * mn : 0) + o];
+        cv[e] = p.beta != 0.0f || p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL ? crow[n] : 0.0f;
+        bv[e] = p.bias ? p.bias[n] : 0.0f;
+        gv[e] = gamma[n];
+        be[e] = beta[n];
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int n = threadIdx.x + 256 * e;
+        float sum = part[e][0];
+#pragma unroll
+        for (int z = 1; z < kMaxSegs; ++z) sum = z < segs ? __fadd_rn(sum, part[e][z]) : sum;
         float r = __fmul_rn(p.alpha, sum);
-        if (p.beta != 0.0f) r = __fadd_rn(p.beta == 1.0f ? *cp : __fmul_rn(p.beta, *cp), r);
-        if (p.bias) r = __fadd_rn(r, p.bias[n]);
+        if (p.beta != 0.0f) r = __fadd_rn(p.beta == 1.0f ? cv[e] : __fmul_rn(p.beta, cv[e]), r);
+        if (p.bias) r = __fadd_rn(r, bv[e]);
         switch (p.epi) {
         case EPI_SWISH:         r = swish_f(r); break;
-        case EPI_HALF_RESIDUAL: r = __fmaf_rn(r, 0.5f, *cp); break;
-        case EPI_RESIDUAL:      r = __fadd_rn(*cp, r); break;
+        case EPI_HALF_RESIDUAL: r = __fmaf_rn(r, 0.5f, cv[e]); break;
+        case EPI_RESIDUAL:      r = __fadd_rn(cv[e], r); break;
         case EPI_RELU:          r = r > 0.0f ? r : 0.0f; break;
         default:                break;
         }
-        row[n] = r;
+        if (n < p.N) row[n] = r;
     }
     __syncthreads();
     if (threadIdx.x < 8) {
@@ -427,8 +447,11 @@ __global__ __launch_bounds__(256) void panel_reduce_ln(PanelArgs p, int segs, co
     }
     __syncthreads();
     const float mean = st[0], inv = st[1];
-    for (int n = threadIdx.x; n < p.N; n += 256)
-        p.C[(size_t)m * p.ldc + n] = __fmaf_rn(__fmul_rn(__fsub_rn(row[n], mean), inv), gamma[n], beta[n]);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int n = threadIdx.x + 256 * e;
+        if (n < p.N) crow[n] = __fmaf_rn(__fmul_rn(__fsub_rn(row[n], mean), inv), gv[e], be[e]);
+    }
 }
 
 // Segment partials summed in segment order, then the output step.
@@ -775,8 +798,12 @@ hipError_t launch_panel(const GemmProblem& p, hipStream_t st)
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || z == 1) return e;
     if (p.out_ln_gamma) {
-        hipLaunchKernelGGL(panel_reduce_ln, dim3((unsigned)p.M), dim3(256), 0, st, a, z, p.out_ln_gamma,
-                           p.out_ln_beta);
+        if (p.N <= 1024)
+            hipLaunchKernelGGL(panel_reduce_ln<4>, dim3((unsigned)p.M), dim3(256), 0, st, a, z, p.out_ln_gamma,
+                               p.out_ln_beta);
+        else
+            hipLaunchKernelGGL(panel_reduce_ln<8>, dim3((unsigned)p.M), dim3(256), 0, st, a, z, p.out_ln_gamma,
+                               p.out_ln_beta);
         return hipGetLastError();
     }
     const long long mn = (long long)p.M * p.N;

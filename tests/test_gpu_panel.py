@@ -253,6 +253,13 @@ def test_panel_split_k(dev, default_numerics, workspace, kind, M, N, K):
         biased = (oracle(kind, A, W, extra, Z) + bias[None, :]).astype(np.float32)
         want = (C0 + np.float32(0.5) * biased).astype(np.float32)
         assert rel_err(pw.run(C0, bias=bias, epi=pk.EPI_HALF_RESIDUAL), want) <= MEASURED
+        # other activations on the same workspace: each call reads back the
+        # partials it wrote, none left from the call before (caches included)
+        for t in range(2):
+            A2 = make(kind, M, N, K, f"pnsk{t}.{kind}.{M}.{K}")[0]
+            pw.dA.copy_(dev.put(A2))
+            e2 = rel_err(pw.run(Z), oracle(kind, A2, W, extra, Z))
+            assert e2 <= MEASURED, (t, e2)
     finally:
         pw.close()
 
