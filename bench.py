@@ -204,7 +204,7 @@ def alg_bytes(kind, m, n, k):
 
 
 def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, force_config=-1,
-              numerics="default", split_k=True, panel=True):
+              numerics="default", split_k=True, panel=True, presplit=True):
     """One JSON line per GEMM shape ("kind:MxNxK"): resident inputs, weights
     rotating over enough replicas to exceed the Infinity Cache, average launch
     time from HIP events around a graph replay of `steps` launches (eager: the
@@ -213,7 +213,10 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
     have a split-K workspace (pk_gpu_set_workspace), which fast numerics and
     the panel kernels use.  panel: every replica of a small-M shape (M <= 64)
     gets its panel (pk_gpu_pack_weight_dev, a one-time repack outside the
-    timed region, as registration makes it), so the panel kernels run."""
+    timed region, as registration makes it), so the panel kernels run.
+    presplit: under fast numerics every replica of an int4 or fp32 shape with
+    M > 64 gets its pre-split copy (pk_gpu_presplit_weight_dev, also outside
+    the timed region), which the split kernels then read."""
     import torch
     pk = load_binding()
     pk.call("pk_gpu_init", 0)
@@ -261,6 +264,12 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
                 packed.append(W[r].data_ptr())
         uses_panel = bool(lib.pk_gpu_uses_panel(m, n, k, bits, W[0].data_ptr(), ldb,
                                                 S[0].data_ptr() if kind == "i4" else None))
+        split_copies = []
+        if presplit and numerics == "fast" and m > 64 and kind != "i8" and k % 32 == 0 and n % 32 == 0:
+            for r in range(reps):
+                pk.call("pk_gpu_presplit_weight_dev", bits, k, n, W[r].data_ptr(), ldb,
+                        S[r].data_ptr() if kind == "i4" else None, cur())
+                split_copies.append(W[r].data_ptr())
         for i in range(warmup):
             assert call(i) == 0, lib.pk_gpu_last_error()
         torch.cuda.synchronize(dev)
@@ -306,9 +315,12 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
                           "tflops": round(tf, 2), "gbps": round(gbs, 1),
                           "frac_mfma_fp32": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_replicas": reps,
+                          "weights_presplit": bool(split_copies),
                           "steps": steps}), flush=True)
         for ptr in packed:
             pk.call("pk_gpu_unpack_weight_dev", ptr)
+        for ptr in split_copies:
+            pk.call("pk_gpu_unsplit_weight_dev", ptr)
         del W, A, C
         torch.cuda.empty_cache()
 
@@ -1098,6 +1110,9 @@ def main():
                     help="with --gemm: no split-K workspace (fast numerics and panel kernels)")
     ap.add_argument("--no-panel", action="store_true",
                     help="with --gemm: no panel copies of the weights (the small-M narrow kernels)")
+    ap.add_argument("--no-presplit", action="store_true",
+                    help="with --gemm --numerics fast: no pre-split weight copies (the split "
+                         "kernels decode and split the weights themselves)")
     ap.add_argument("--eager", action="store_true",
                     help="with --gemm: launch from a host loop instead of a graph replay "
                          "(for kernel tracers)")
@@ -1112,7 +1127,7 @@ def main():
     if args.gemm:
         gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup,
                   eager=args.eager, force_config=args.force_config, numerics=args.numerics,
-                  split_k=not args.no_split_k, panel=not args.no_panel)
+                  split_k=not args.no_split_k, panel=not args.no_panel, presplit=not args.no_presplit)
         return
     if args.ffn:
         args.steps = args.steps or 200

@@ -524,6 +524,25 @@ int pk_gpu_pack_weight_dev(int bits, int K, int N, const void *dB, int ldb,
 int pk_gpu_unpack_weight_dev(const void *dB);
 /* Device bytes held by panels. */
 size_t pk_gpu_panel_bytes(void);
+/* Make the pre-split copy of device weight dB (bits 4 or 32; K and N
+ * multiples of 32; int4: its scales dscales [K][N/32]) for later
+ * PK_GPU_NUMERICS_FAST *_dev / *_ex_dev GEMMs with M > 64 whose B is dB with
+ * the same bits, K, N, ldb (and dscales): the weights the split kernels
+ * multiply (int4: fl(q * s), blas.c:834-840), each already split into its
+ * bf16 hi and lo halves in the kernels' chunk order, so those GEMMs stage
+ * them with plain copies instead of decoding and splitting every weight per
+ * row tile.  The results are the same bits.  4*K*N bytes of device memory
+ * (int4: 8 times the packed weight).  Runs on `stream` and waits for it; not
+ * during stream capture.  Idempotent for the same parameters; PK_GPU_EINVAL
+ * if dB already has a copy of another shape.  The weight's bytes must not
+ * change afterwards.  No counterpart in the reference. */
+int pk_gpu_presplit_weight_dev(int bits, int K, int N, const void *dB, int ldb,
+                               const float *dscales, void *stream);
+/* Free the copy made for dB by pk_gpu_presplit_weight_dev (after the
+ * device's queued work; no call may be using it). */
+int pk_gpu_unsplit_weight_dev(const void *dB);
+/* Device bytes held by pre-split copies. */
+size_t pk_gpu_presplit_bytes(void);
 /* Whether a GEMM on this thread with this shape, format and weight (and, for
  * int4, scales) would take the panel kernels, given aligned A rows. */
 int pk_gpu_uses_panel(int M, int N, int K, int bits, const void *dB, int ldb,

@@ -48,6 +48,9 @@ struct DevWeight {
     // its panel copy for the small-M kernels (pk_panel.hip), made on the
     // first run with a row group of at most 64 rows outside exact numerics
     const void* panel = nullptr;
+    // int4 and fp32: its pre-split copy for the split kernels (pk_split.hip),
+    // made on the first fast-numerics run with a row group of more than 64 rows
+    const void* split = nullptr;
 };
 
 struct DevBlock {
@@ -142,6 +145,9 @@ struct pk_gpu_encoder {
     // small row groups on the panel kernels: LayerNorms fused into the GEMMs
     // (PK_GPU_FUSE_LN=0 at creation turns it off; the results are the same)
     bool fuse_ln = true;
+    // fast numerics: the int4 and fp32 block weights' pre-split copies
+    // (PK_GPU_PRESPLIT_W=0 at creation turns them off; the results are the same)
+    bool presplit_w = true;
     std::vector<hipStream_t> side;
     std::vector<hipEvent_t> side_done;
     hipEvent_t inputs_ready = nullptr;
@@ -163,6 +169,9 @@ struct pk_gpu_encoder {
     // the block weights' panels (made once, see DevWeight::panel)
     std::vector<void*> panel_allocs;
     size_t panel_bytes = 0;
+    // the block weights' pre-split copies (made once, see DevWeight::split)
+    std::vector<void*> split_allocs;
+    size_t split_bytes = 0;
 };
 
 namespace {
@@ -375,6 +384,7 @@ GemmProblem block_problem(const DevWeight& w, const float* A, int M, float* C, c
     }
     p.a_presplit = presplit;
     if (tol != pkgpu::TOL_NONE) p.panel = w.panel;      // read only where the small-M path may run
+    if (tol == pkgpu::TOL_ALL) p.b_presplit = w.split;  // read only by the split kernels
     p.ln_gamma = ln.in_g;
     p.ln_beta = ln.in_b;
     p.out_ln_gamma = ln.out_g;
@@ -795,6 +805,49 @@ int make_panels(pk_gpu_encoder* e)
     return PK_GPU_OK;
 }
 
+// The int4 and fp32 block weights' pre-split copies (DevWeight::split),
+// made once on the encoder's stream.
+int make_splits(pk_gpu_encoder* e)
+{
+    if (!e->split_allocs.empty()) return PK_GPU_OK;
+    std::vector<void*> fresh;
+    std::vector<DevWeight*> made;
+    size_t total = 0;
+    int rc = PK_GPU_OK;
+    for (DevBlock& b : e->blocks) {
+        for (DevWeight* w : {&b.ff1_w1, &b.ff1_w2, &b.ff2_w1, &b.ff2_w2, &b.pw1t, &b.pw2t}) {
+            const size_t bytes = pkgpu::split_weight_bytes(w->kind, w->K, w->N);
+            if (!bytes) continue;                    // int8: the codes enter the matrix cores exactly
+            void* d = nullptr;
+            if (hipMalloc(&d, bytes) != hipSuccess) {
+                rc = error(PK_GPU_ENOMEM, "pre-split weights: device allocation of %zu bytes failed", bytes);
+                break;
+            }
+            fresh.push_back(d);
+            made.push_back(w);
+            total += bytes;
+            const hipError_t r = pkgpu::launch_split_pack(w->kind, w->K, w->N, w->data,
+                                                          w->kind == pkgpu::W_I4 ? w->N / 2 : w->N, w->scales, d,
+                                                          e->stream);
+            if (r != hipSuccess) {
+                rc = hip_error(r, "pre-split weights");
+                break;
+            }
+        }
+        if (rc) break;
+    }
+    if (!rc) rc = check(hipStreamSynchronize(e->stream), "pre-split weights");
+    if (rc) {
+        (void)hipStreamSynchronize(e->stream);
+        for (void* d : fresh) (void)hipFree(d);
+        return rc;
+    }
+    for (size_t i = 0; i < made.size(); ++i) made[i]->split = fresh[i];
+    e->split_allocs.swap(fresh);
+    e->split_bytes = total;
+    return PK_GPU_OK;
+}
+
 int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, float* out,
                hipStream_t s, hipMemcpyKind in_kind, hipMemcpyKind out_kind)
 {
@@ -859,6 +912,14 @@ int run_queued(pk_gpu_encoder* e, const float* x, int T, int chunk, int ov, floa
     if (small && e->panel_allocs.empty()) {
         if ((rc = check(hipStreamSynchronize(s), "encoder stream"))) return rc;
         if ((rc = make_panels(e))) return rc;
+    }
+    // Fast numerics on row groups above 64 rows: the split kernels read the
+    // int4 and fp32 weights' pre-split copies.
+    bool big = false;
+    for (const RowGroup& g : groups) big = big || g.R > pkgpu::kSmallMaxM;
+    if (big && e->numerics == PK_GPU_NUMERICS_FAST && e->presplit_w && e->split_allocs.empty()) {
+        if ((rc = check(hipStreamSynchronize(s), "encoder stream"))) return rc;
+        if ((rc = make_splits(e))) return rc;
     }
     if (e->numerics == PK_GPU_NUMERICS_FAST || small) {
         if (groups.size() > e->part_groups) {
@@ -1167,6 +1228,7 @@ int pk_gpu_encoder_create(pk_gpu_encoder** out, const pk_gpu_block_weights* bloc
     pk_gpu_encoder* e = new pk_gpu_encoder;
     if (const char* v = getenv("PK_GPU_PRESPLIT")) e->presplit = strcmp(v, "0") != 0;
     if (const char* v = getenv("PK_GPU_FUSE_LN")) e->fuse_ln = strcmp(v, "0") != 0;
+    if (const char* v = getenv("PK_GPU_PRESPLIT_W")) e->presplit_w = strcmp(v, "0") != 0;
     hipError_t r = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
     if (r != hipSuccess) {
         delete e;
@@ -1212,7 +1274,7 @@ int pk_gpu_encoder_run_dev(pk_gpu_encoder* enc, const float* dx, int T, int chun
 size_t pk_gpu_encoder_bytes(const pk_gpu_encoder* enc)
 {
     return enc ? enc->weight_bytes + enc->ws_bytes + enc->part_groups * pkgpu::kSplitWorkBytes +
-                     enc->panel_bytes
+                     enc->panel_bytes + enc->split_bytes
                : 0;
 }
 
@@ -1255,6 +1317,7 @@ void pk_gpu_encoder_destroy(pk_gpu_encoder* enc)
     for (void* p : enc->allocs) (void)hipFree(p);
     for (void* p : enc->pos_allocs) (void)hipFree(p);
     for (void* p : enc->panel_allocs) (void)hipFree(p);
+    for (void* p : enc->split_allocs) (void)hipFree(p);
     for (hipEvent_t ev : enc->side_done) (void)hipEventDestroy(ev);
     if (enc->inputs_ready) (void)hipEventDestroy(enc->inputs_ready);
     if (enc->last_done) (void)hipEventDestroy(enc->last_done);

@@ -86,6 +86,10 @@ struct Panel {
 // weight device address -> its panel; never destroyed (see g_weights)
 std::map<uintptr_t, std::shared_ptr<Panel>>& g_panels = *new std::map<uintptr_t, std::shared_ptr<Panel>>;
 size_t g_panel_bytes = 0;
+// weight device address -> its pre-split copy for the split kernels
+// (pk_gpu_presplit_weight_dev; the same record, owner always 0)
+std::map<uintptr_t, std::shared_ptr<Panel>>& g_splits = *new std::map<uintptr_t, std::shared_ptr<Panel>>;
+size_t g_split_bytes = 0;
 std::mutex g_pack_mu;           // one panel made at a time (host-pointer GEMMs)
 
 thread_local std::string t_err;
@@ -322,6 +326,20 @@ const void* panel_for(const GemmProblem& p, std::shared_ptr<Panel>* hold = nullp
     return q.dev;
 }
 
+// The pre-split copy made from weight p.B with p's format and shape, or null.
+const void* split_for(const GemmProblem& p)
+{
+    if (!p.B) return nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_splits.find(reinterpret_cast<uintptr_t>(p.B));
+    if (it == g_splits.end()) return nullptr;
+    const Panel& q = *it->second;
+    if (q.kind != p.kind || q.K != p.K || q.N != p.N || q.ldb != p.ldb ||
+        (p.kind == pkgpu::W_I4 && q.scales != p.scales))
+        return nullptr;
+    return q.dev;
+}
+
 // Whether a call may leave the exact chains (this thread's numerics, no
 // forced tile) and has the small-M kernels' shape.
 bool small_m_call(const GemmProblem& p, bool tol_ok)
@@ -343,6 +361,7 @@ int launch(const GemmProblem& p, hipStream_t s, bool tol_ok, std::shared_ptr<Pan
         q.work_bytes = t_work_bytes;
     }
     if (small_m_call(p, tol_ok)) q.panel = panel_for(p, hold);
+    if (tol == pkgpu::TOL_ALL && p.M > pkgpu::kSmallMaxM) q.b_presplit = split_for(p);
     const hipError_t e = pkgpu::launch_gemm(q, s, t_force_cfg, tol);
     if (e == hipErrorInvalidValue)
         return fail(PK_GPU_EINVAL, "%dx%dx%d GEMM not launched: an operand extent exceeds 2 GiB",
@@ -587,16 +606,19 @@ void pk_gpu_shutdown(void)
 {
     std::vector<ThreadCtx*> idle;
     std::map<uintptr_t, std::shared_ptr<Resident>> weights;
-    std::map<uintptr_t, std::shared_ptr<Panel>> panels;
+    std::map<uintptr_t, std::shared_ptr<Panel>> panels, splits;
     {
         std::lock_guard<std::mutex> lk(g_mu);
         weights.swap(g_weights);
         g_resident_bytes = 0;
         panels.swap(g_panels);
         g_panel_bytes = 0;
+        splits.swap(g_splits);
+        g_split_bytes = 0;
         idle.swap(g_free_ctx);
     }
     panels.clear();           // each freed after queued work, or by its last holder
+    splits.clear();
     weights.clear();
     for (ThreadCtx* c : idle) free_ctx(c);
     if (t_holder.c) {
@@ -874,6 +896,73 @@ int pk_gpu_unpack_weight_dev(const void* dB)
     }
     pn.reset();                                      // freed after the device's queued work
     return PK_GPU_OK;
+}
+
+int pk_gpu_presplit_weight_dev(int bits, int K, int N, const void* dB, int ldb, const float* dscales,
+                               void* stream)
+{
+    if (bits != 4 && bits != 32) return fail(PK_GPU_EINVAL, "presplit: bits = %d (4 or 32)", bits);
+    if (K <= 0 || N <= 0 || K % 32 || N % 32)
+        return fail(PK_GPU_EINVAL, "presplit: K = %d and N = %d must be positive multiples of 32", K, N);
+    if (ldb < (bits == 4 ? N / 2 : N)) return fail(PK_GPU_EINVAL, "presplit: ldb = %d too small for N = %d", ldb, N);
+    if (!dB || (bits == 4 && !dscales)) return fail(PK_GPU_EINVAL, "presplit: NULL operand");
+    int rc = 0;
+    hipStream_t s = pick_stream(stream, &rc);
+    if (rc) return rc;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+        return fail(PK_GPU_EINVAL, "presplit: not during stream capture (it allocates and waits)");
+    GemmProblem p{};
+    p.kind = kind_of_bits(bits);
+    p.K = K; p.N = N; p.B = dB; p.ldb = ldb;
+    p.scales = bits == 4 ? dscales : nullptr;
+    if (split_for(p)) return PK_GPU_OK;              // already made with these parameters
+    std::lock_guard<std::mutex> lk(g_pack_mu);
+    if (split_for(p)) return PK_GPU_OK;
+    const size_t bytes = pkgpu::split_weight_bytes(p.kind, K, N);
+    if (bytes >= ((size_t)1 << 31)) return fail(PK_GPU_EINVAL, "presplit: %zu bytes exceed 2 GiB", bytes);
+    auto pn = std::make_shared<Panel>();
+    pn->kind = p.kind;
+    pn->K = K;
+    pn->N = N;
+    pn->ldb = ldb;
+    pn->scales = p.scales;
+    pn->bytes = bytes;
+    hipError_t e = hipMalloc(&pn->dev, bytes);
+    if (e != hipSuccess) {
+        pn->dev = nullptr;
+        return fail(PK_GPU_ENOMEM, "presplit: device alloc of %zu bytes failed", bytes);
+    }
+    e = pkgpu::launch_split_pack(p.kind, K, N, dB, ldb, p.scales, pn->dev, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "presplit: pack");
+    std::lock_guard<std::mutex> lk2(g_mu);
+    auto& slot = g_splits[reinterpret_cast<uintptr_t>(dB)];
+    if (slot) return fail(PK_GPU_EINVAL, "presplit: weight %p already has a copy of another shape", dB);
+    slot = pn;
+    g_split_bytes += bytes;
+    return PK_GPU_OK;
+}
+
+int pk_gpu_unsplit_weight_dev(const void* dB)
+{
+    std::shared_ptr<Panel> pn;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_splits.find(reinterpret_cast<uintptr_t>(dB));
+        if (it == g_splits.end()) return fail(PK_GPU_EINVAL, "unsplit: no pre-split copy of %p", dB);
+        pn = std::move(it->second);
+        g_split_bytes -= pn->bytes;
+        g_splits.erase(it);
+    }
+    pn.reset();                                      // freed after the device's queued work
+    return PK_GPU_OK;
+}
+
+size_t pk_gpu_presplit_bytes(void)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    return g_split_bytes;
 }
 
 size_t pk_gpu_panel_bytes(void)

@@ -60,6 +60,16 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 constexpr int kXcd = 8;
 constexpr int KT = 32;            // k per chunk
 constexpr int RS = KT + 8;        // LDS row stride of a plane, in bf16 (80 bytes)
+// Lo planes start GAP bf16 (64 bytes, 16 banks) past the end of their hi
+// plane, so 16-byte stores of the hi and the lo half of one row or column in
+// one access phase land on distinct banks.
+constexpr int GAP = 32;
+// Pipe's weight format for weights given pre-split (GemmProblem::b_presplit,
+// int4 and fp32): per 32-deep chunk c and column n, 128 bytes at
+// (c N + n) * 128: the 32 bf16 hi = bf16(w) of k = 32 c .. 32 c + 31, then
+// the 32 lo = bf16(w - hi), w the weight the kernels otherwise split
+// (fl(q * s) for int4), so staging a chunk is a copy.
+constexpr int W_BS = 3;
 
 struct SpArgs {
     int M, N, K;
@@ -105,6 +115,7 @@ template <int WK> struct WUnit;
 template <> struct WUnit<W_I8> { uint32_t q[2]; };
 template <> struct WUnit<W_I4> { uint32_t q[2]; float s[2]; };
 template <> struct WUnit<W_F32> { v4u w[2]; };
+template <> struct WUnit<W_BS> { v4u w; };
 
 // Staging and multiplying one chunk of a BM x BN tile by NT threads.
 // A chunk's LDS planes: A_hi, A_lo [BM][RS], then W_hi (and W_lo) [BN][RS].
@@ -115,12 +126,15 @@ template <int WK, int BM, int BN, int NT, bool AS>
 struct Pipe {
     static constexpr int NBP = WK == W_I8 ? 1 : 2;             // weight planes
     static constexpr int A_PLANE = BM * RS, B_PLANE = BN * RS;   // bf16 elements
-    static constexpr int BUF = 2 * A_PLANE + NBP * B_PLANE;      // one chunk
+    // plane offsets in one chunk's buffer (the lo planes GAP past their hi plane)
+    static constexpr int A_LO = A_PLANE + GAP, B_HI = A_LO + A_PLANE, B_LO = B_HI + B_PLANE + GAP;
+    static constexpr int BUF = B_HI + NBP * B_PLANE + (NBP - 1) * GAP;   // one chunk
     // A: BM rows x 8 float4 per chunk
     static constexpr int A_ITEMS = BM * (KT / 4) / NT;
-    // weight units of two consecutive k rows: 4 columns (int8, fp32) or 8 (int4)
+    // weight units of two consecutive k rows: 4 columns (int8, fp32) or 8
+    // (int4); pre-split weights: 16-byte pieces, 8 per column
     static constexpr int UC = WK == W_I4 ? 8 : 4;
-    static constexpr int B_TOTAL = (KT / 2) * (BN / UC);
+    static constexpr int B_TOTAL = WK == W_BS ? 8 * BN : (KT / 2) * (BN / UC);
     static constexpr int B_ITEMS = (B_TOTAL + NT - 1) / NT;     // the last one partial if NT > B_TOTAL
     static_assert(A_ITEMS * NT == BM * (KT / 4) && (B_TOTAL % NT == 0 || B_TOTAL < NT), "even split");
     static_assert(B_TOTAL % 64 == 0, "whole waves per weight item");
@@ -144,7 +158,25 @@ struct Pipe {
             r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(
                 rA, (int)(((uint32_t)(m0 + row) * (uint32_t)p.lda + (uint32_t)(k0 + 4 * kq)) * 4u), 0, 0);
         }
-        // k pairs fastest across lanes: 16 lanes write 16 consecutive LDS words
+        // pre-split: piece idx & 7 of column idx >> 3 (8 lanes read a column's 128 bytes)
+        if constexpr (WK == W_BS) {
+#pragma unroll
+            for (int i = 0; i < B_ITEMS; ++i) {
+                const int idx = tid + NT * i;
+                if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
+                const uint32_t col = (uint32_t)(k0 / KT) * (uint32_t)p.N + (uint32_t)(n0 + (idx >> 3));
+                r.w[i].w = __builtin_amdgcn_raw_buffer_load_b128(rB, (int)(col * 128u + 16u * (idx & 7)), 0, 0);
+            }
+        } else {
+            load_units(r, p, rB, rS, tid, n0, k0);
+        }
+    }
+
+    // the weight units of the other formats: k pairs fastest across lanes,
+    // so 16 lanes write 16 consecutive LDS words
+    __device__ static void load_units(Raw& r, const SpArgs& p, __amdgpu_buffer_rsrc_t rB,
+                                      __amdgpu_buffer_rsrc_t rS, int tid, int n0, int k0)
+    {
 #pragma unroll
         for (int i = 0; i < B_ITEMS; ++i) {
             const int idx = tid + NT * i, kp = idx % (KT / 2), cu = idx / (KT / 2);
@@ -170,15 +202,15 @@ struct Pipe {
     __device__ static void store(const Raw& r, __bf16* base, int tid)
     {
         __bf16* ah = base;
-        __bf16* al = ah + A_PLANE;
-        __bf16* bh = al + A_PLANE;
-        __bf16* bl = bh + B_PLANE;                   // int4, fp32 only
+        __bf16* al = base + A_LO;
+        __bf16* bh = base + B_HI;
+        __bf16* bl = base + B_LO;                    // int4, fp32 only
         if constexpr (AS) {
             // part kq: the hi (even) or lo (odd) half of k group kq / 2
 #pragma unroll
             for (int i = 0; i < A_ITEMS; ++i) {
                 const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
-                *reinterpret_cast<v4u*>(ah + (kq & 1) * A_PLANE + row * RS + 8 * (kq >> 1)) = r.a[i];
+                *reinterpret_cast<v4u*>((kq & 1 ? al : ah) + row * RS + 8 * (kq >> 1)) = r.a[i];
             }
         } else {
 #pragma unroll
@@ -191,6 +223,23 @@ struct Pipe {
                 *reinterpret_cast<v2u*>(al + row * RS + 4 * kq) = v2u{l0, l1};
             }
         }
+        if constexpr (WK == W_BS) {
+            // piece q = idx & 7: the hi (q < 4) or the lo half's k group q & 3
+#pragma unroll
+            for (int i = 0; i < B_ITEMS; ++i) {
+                const int idx = tid + NT * i, q = idx & 7;
+                if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
+                *reinterpret_cast<v4u*>((q < 4 ? bh : bl) + (idx >> 3) * RS + 8 * (q & 3)) = r.w[i].w;
+            }
+        } else {
+            store_units(r, bh, bl, tid);
+        }
+    }
+
+    // the other formats' weight units: decoded (int4: fl(q * s)), split, and
+    // written to the planes
+    __device__ static void store_units(const Raw& r, __bf16* bh, __bf16* bl, int tid)
+    {
 #pragma unroll
         for (int i = 0; i < B_ITEMS; ++i) {
             const int idx = tid + NT * i, kp = idx % (KT / 2), cu = idx / (KT / 2);
@@ -227,9 +276,9 @@ struct Pipe {
     __device__ static void multiply(const __bf16* base, v16f (&acc)[2][2], int lane, int r0, int c0)
     {
         const __bf16* ah = base;
-        const __bf16* al = ah + A_PLANE;
-        const __bf16* bh = al + A_PLANE;
-        const __bf16* bl = bh + B_PLANE;
+        const __bf16* al = base + A_LO;
+        const __bf16* bh = base + B_HI;
+        const __bf16* bl = base + B_LO;
         const int r_lane = lane & 31, k_lane = 8 * (lane >> 5);
 #pragma unroll
         for (int ks = 0; ks < KT / 16; ++ks) {
@@ -516,6 +565,42 @@ __global__ __launch_bounds__(64 * KS, 2) void split_gemm_k(SpArgs p)
     }
 }
 
+// The pre-split copy (W_BS) of an int4 or fp32 weight [K][N]: thread i
+// writes 16-byte piece i, the hi (q < 4) or lo half of k group q & 3 (q =
+// i & 7) of column n of chunk c, with the staging's own decode (int4:
+// fl(q * s[k][n/32]), blas.c:834-840) and split (split2), so the kernels
+// multiply the same bf16 values either way.
+template <int WK>
+__global__ __launch_bounds__(256) void split_pack(int K, int N, const void* B, int ldb, const float* scales,
+                                                  unsigned char* out)
+{
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)(K / KT) * N * 8) return;
+    const int q = (int)(i & 7);
+    const long long cn = i >> 3;
+    const int n = (int)(cn % N), c = (int)(cn / N);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const size_t k = (size_t)(KT * c + 8 * (q & 3) + e);
+        float w0, w1;
+        if constexpr (WK == W_I4) {
+            const unsigned char* b = static_cast<const unsigned char*>(B);
+            const size_t g = (size_t)(N / 32);
+            w0 = __fmul_rn((float)q_i4(b[k * ldb + n / 2], n & 1), scales[k * g + n / 32]);
+            w1 = __fmul_rn((float)q_i4(b[(k + 1) * ldb + n / 2], n & 1), scales[(k + 1) * g + n / 32]);
+        } else {
+            const float* b = static_cast<const float*>(B);
+            w0 = b[k * ldb + n];
+            w1 = b[(k + 1) * ldb + n];
+        }
+        uint32_t hi, lo;
+        split2(w0, w1, hi, lo);
+        w[e / 2] = q < 4 ? hi : lo;
+    }
+    *reinterpret_cast<v4u*>(out + i * 16) = v4u{w[0], w[1], w[2], w[3]};
+}
+
 // Launch shape.  Where 128 x 128 tiles outnumber the CUs, 256 x 128 tiles
 // (8 waves, one workgroup per CU by its LDS) give no CU more rows x columns
 // than two 128 x 128 workgroups would, and split each weight for twice the
@@ -598,7 +683,8 @@ hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
     // Chunks of loads in flight, as many as fit two waves per SIMD without
     // spills: a lane holds 16 A bytes per 64 rows of the tile and chunk, plus
     // its weight units (fp32's take 4 times int8's registers).
-    constexpr int PD22 = WK == W_F32 ? 2 : 3, PD21 = 2, PDK = WK == W_F32 ? 1 : 2, PD42 = 2;
+    constexpr bool WIDE = WK == W_F32 || WK == W_BS;      // 16-byte weight loads
+    constexpr int PD22 = WIDE ? 2 : 3, PD21 = 2, PDK = WIDE ? 1 : 2, PD42 = 2;
     if (plan.n_seg > 1) {
         const bool wide = plan.shape == SP_4x2;
         const unsigned grid = padded_grid(a, wide ? 256 : 128, 128, plan.n_seg);
@@ -681,6 +767,13 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     a.work = p.work;
     a.c_vec4 = p.ldc % 4 == 0 && reinterpret_cast<uintptr_t>(p.C) % 16 == 0 &&
                reinterpret_cast<uintptr_t>(p.bias) % 16 == 0;
+    if (p.b_presplit && p.kind != W_I8) {
+        // the weight's pre-split copy (split_pack), K N 4 bytes
+        if ((size_t)p.K * p.N * 4 >= lim || reinterpret_cast<uintptr_t>(p.b_presplit) % 16) return hipErrorNotSupported;
+        a.B = p.b_presplit;
+        a.b_bytes = (uint32_t)((size_t)p.K * p.N * 4);
+        return p.a_presplit ? launch_kind<W_BS, true>(a, plan, st) : launch_kind<W_BS, false>(a, plan, st);
+    }
     if (p.a_presplit) {
         switch (p.kind) {
         case W_I8: return launch_kind<W_I8, true>(a, plan, st);
@@ -693,6 +786,26 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     case W_I4: return launch_kind<W_I4, false>(a, plan, st);
     default:   return launch_kind<W_F32, false>(a, plan, st);
     }
+}
+
+size_t split_weight_bytes(WeightKind kind, int K, int N)
+{
+    if (kind == W_I8 || K < KT || K % KT || N < 32 || N % 32) return 0;
+    return (size_t)K * N * 4;
+}
+
+hipError_t launch_split_pack(WeightKind kind, int K, int N, const void* B, int ldb, const float* scales,
+                             void* out, hipStream_t st)
+{
+    if (!split_weight_bytes(kind, K, N) || (kind == W_I4 && !scales)) return hipErrorInvalidValue;
+    const long long pieces = (long long)(K / KT) * N * 8;
+    const dim3 grid((unsigned)((pieces + 255) / 256));
+    unsigned char* o = static_cast<unsigned char*>(out);
+    if (kind == W_I4)
+        hipLaunchKernelGGL(split_pack<W_I4>, grid, dim3(256), 0, st, K, N, B, ldb, scales, o);
+    else
+        hipLaunchKernelGGL(split_pack<W_F32>, grid, dim3(256), 0, st, K, N, B, ldb, scales, o);
+    return hipGetLastError();
 }
 
 int split_k_segments(WeightKind kind, int M, int N, int K, size_t work_bytes)

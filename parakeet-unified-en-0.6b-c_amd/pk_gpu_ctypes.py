@@ -55,6 +55,9 @@ _PROTOS = {
     "pk_gpu_pack_weight_dev": (_i, [_i, _i, _i, _p, _i, _p, _p]),
     "pk_gpu_unpack_weight_dev": (_i, [_p]),
     "pk_gpu_panel_bytes": (_sz, []),
+    "pk_gpu_presplit_weight_dev": (_i, [_i, _i, _i, _p, _i, _p, _p]),
+    "pk_gpu_unsplit_weight_dev": (_i, [_p]),
+    "pk_gpu_presplit_bytes": (_sz, []),
     "pk_gpu_uses_panel": (_i, [_i, _i, _i, _i, _p, _i, _p]),
     "pk_gpu_panel_segments": (_i, [_i, _i, _i]),
     "pk_gpu_panel_decode_dev": (_i, [_i, _i, _i, _p, _i, _p, _f, _p, _p]),

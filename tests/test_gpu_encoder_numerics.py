@@ -249,3 +249,20 @@ def test_fast_mode_presplit_layer_norm_is_bit_identical(model, monkeypatch):
     plain = run(model, x, chunk, pk.NUMERICS_FAST, overlap=ov)
     for a, b in zip(pre, plain):
         assert bits_equal(a, b), describe_mismatch(a, b)
+
+
+def test_fast_mode_presplit_weights_are_bit_identical(model, monkeypatch):
+    """Under PK_GPU_NUMERICS_FAST the row groups above 64 rows read the int4
+    and fp32 block weights' pre-split copies (made once, with the split
+    kernels' own decode and split).  An encoder created with
+    PK_GPU_PRESPLIT_W=0 (the kernels decode and split every weight per row
+    tile) gives the same bits, over two row groups and 24 blocks, split-K
+    GEMMs included."""
+    T, chunk, ov = 300, 140, 8
+    x = bench.enc_rng(0xFEA7, 303).standard_normal((T, bench.D)).astype(np.float32)
+    monkeypatch.delenv("PK_GPU_PRESPLIT_W", raising=False)
+    pre = run(model, x, chunk, pk.NUMERICS_FAST, overlap=ov)
+    monkeypatch.setenv("PK_GPU_PRESPLIT_W", "0")
+    plain = run(model, x, chunk, pk.NUMERICS_FAST, overlap=ov)
+    for a, b in zip(pre, plain):
+        assert bits_equal(a, b), describe_mismatch(a, b)

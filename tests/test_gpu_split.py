@@ -349,3 +349,94 @@ def test_split_k_unaligned_output_rows(dev):
         got = dC.cpu().numpy()
     assert rel_err(got[:, :N], want) <= MEASURED
     assert bool((got[:, N] == 7.0).all())
+
+
+# ---- weights pre-split once (pk_gpu_presplit_weight_dev) ---------------------
+
+def fast_dev(dev, kind, dA, dW, dS, extra, M, N, K, dC, bias=None, epi=None):
+    """One FAST GEMM on device operands (no upload), into dC."""
+    lib = pk.load()
+    ex = bias is not None or epi is not None
+    tail = (bias.data_ptr() if bias is not None else None, epi or 0) if ex else ()
+    s = dev.stream()
+    if kind == "i4":
+        rc = getattr(lib, "pk_gpu_gemm_i4_ex_dev" if ex else "pk_gpu_gemm_i4_dev")(
+            M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(), dS.data_ptr(), N // 2, 0.0, dC.data_ptr(), N, *tail, s)
+    else:
+        rc = getattr(lib, "pk_gpu_sgemm_ex_dev" if ex else "pk_gpu_sgemm_dev")(
+            M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(), N, 0.0, dC.data_ptr(), N, *tail, s)
+    assert rc == 0, lib.pk_gpu_last_error()
+    dev.sync()
+    return dC.cpu().numpy()
+
+
+# Every launch shape the pre-split copy meets, split-K included (a workspace).
+PRESPLIT_SHAPES = [("i4", 1656, 4096, 1024), ("f32", 1656, 2048, 1024), ("i4", 1024, 4096, 256),
+                   ("f32", 1024, 2048, 96), ("i4", 416, 4096, 1024), ("i4", 375, 1024, 4096),
+                   ("f32", 130, 256, 320), ("i4", 97, 96, 288), ("f32", 77, 32, 32), ("i4", 1656, 1024, 4096)]
+
+
+@pytest.mark.parametrize("kind,M,N,K", PRESPLIT_SHAPES)
+@pytest.mark.parametrize("work", [False, True])
+def test_presplit_weights_give_the_same_bits(dev, kind, M, N, K, work):
+    """The split kernels read a weight's pre-split copy (the staging's own
+    decode and split, done once) instead of the weight: the same products in
+    the same order, so the same bits, with and without split-K."""
+    torch = dev.torch
+    A, W, extra, C0 = make(kind, M, N, K, f"sps.{kind}.{M}.{N}.{K}")
+    bias = po.normal((N,), 0.0, 0.02, po.seed(0x5EED3300, f"sps.{kind}.b"))
+    dA, dW = dev.put(A), dev.put(W)
+    dS = dev.put(extra) if kind == "i4" else None
+    dC, dB = torch.zeros((M, N), device=dev.dev), dev.put(bias)
+    lib = pk.load()
+    prev = lib.pk_gpu_get_numerics()
+    pk.call("pk_gpu_set_numerics", pk.NUMERICS_FAST)
+    try:
+        with Workspace(dev, pk.SPLIT_WORKSPACE_BYTES if work else 0):
+            presplit_case(dev, kind, A, W, extra, M, N, K, dA, dW, dS, dC, dB)
+    finally:
+        pk.call("pk_gpu_set_numerics", prev)
+
+
+def presplit_case(dev, kind, A, W, extra, M, N, K, dA, dW, dS, dC, dB):
+    lib = pk.load()
+    bits = bits_of(kind)
+    assert uses_split(M, N, K, bits) == 1
+    plain = fast_dev(dev, kind, dA, dW, dS, extra, M, N, K, dC)
+    epi = fast_dev(dev, kind, dA, dW, dS, extra, M, N, K, dC, bias=dB, epi=pk.EPI_SWISH)
+    before = lib.pk_gpu_presplit_bytes()
+    pk.call("pk_gpu_presplit_weight_dev", bits, K, N, dW.data_ptr(), N // 2 if kind == "i4" else N,
+            dS.data_ptr() if dS is not None else None, dev.stream())
+    try:
+        assert lib.pk_gpu_presplit_bytes() == before + 4 * K * N
+        # idempotent for the same parameters
+        pk.call("pk_gpu_presplit_weight_dev", bits, K, N, dW.data_ptr(), N // 2 if kind == "i4" else N,
+                dS.data_ptr() if dS is not None else None, dev.stream())
+        dW_orig = dW.clone()
+        dW.zero_()                 # the kernels must not read the weight itself any more
+        got = fast_dev(dev, kind, dA, dW, dS, extra, M, N, K, dC)
+        dW.copy_(dW_orig)
+        assert bits_equal(got, plain), describe(got, plain)
+        assert bits_equal(fast_dev(dev, kind, dA, dW, dS, extra, M, N, K, dC, bias=dB, epi=pk.EPI_SWISH), epi)
+        want = oracle(kind, A, W, extra, np.zeros((M, N), np.float32))
+        assert rel_err(got, want) <= MEASURED
+    finally:
+        pk.call("pk_gpu_unsplit_weight_dev", dW.data_ptr())
+    assert lib.pk_gpu_presplit_bytes() == before
+
+
+def describe(got, want):
+    d = got.view(np.uint32) != want.view(np.uint32)
+    return f"{int(d.sum())} of {d.size} outputs differ"
+
+
+def test_presplit_argument_checks(dev):
+    lib = pk.load()
+    W = dev.torch.zeros((64, 64), device=dev.dev)
+    s = dev.stream()
+    assert lib.pk_gpu_presplit_weight_dev(8, 64, 64, W.data_ptr(), 64, None, s) == -1     # int8: nothing to split
+    assert lib.pk_gpu_presplit_weight_dev(32, 48, 64, W.data_ptr(), 64, None, s) == -1    # K % 32
+    assert lib.pk_gpu_presplit_weight_dev(32, 64, 40, W.data_ptr(), 64, None, s) == -1    # N % 32
+    assert lib.pk_gpu_presplit_weight_dev(4, 64, 64, W.data_ptr(), 32, None, s) == -1     # no scales
+    assert lib.pk_gpu_presplit_weight_dev(32, 64, 64, W.data_ptr(), 32, None, s) == -1    # ldb < N
+    assert lib.pk_gpu_unsplit_weight_dev(W.data_ptr()) == -1                             # none made
