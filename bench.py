@@ -325,6 +325,46 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
         torch.cuda.empty_cache()
 
 
+def short_clip_mode(steps, warmup, numerics):
+    """The 24-block resident encoder on one 33-frame clip (2.56 s of audio,
+    every weight GEMM at M = 33), replayed `steps` times after `warmup` runs:
+    one JSON line with the time per call (HIP events).  For kernel tracers:
+    its launches are the short-clip workload's."""
+    import ctypes
+    import torch
+    pk = load_binding()
+    pk.call("pk_gpu_init", 0)
+    lib = pk.load()
+    dev = torch.device("cuda:0")
+    full = EncoderModel(pk)
+    x = enc_rng(0xFEA7, 4).standard_normal((33, D)).astype(np.float32)
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(full.blocks, ctypes.c_void_p),
+            N_BLOCKS, full.pe.ctypes.data, PE_ROWS, PE_CENTER)
+    try:
+        pk.call("pk_gpu_encoder_set_numerics", enc, {"default": pk.NUMERICS_DEFAULT, "exact": pk.NUMERICS_EXACT,
+                                                     "fast": pk.NUMERICS_FAST}[numerics])
+        dx = torch.from_numpy(x).to(dev)
+        dy = torch.empty_like(dx)
+        s = torch.cuda.current_stream(dev)
+        run = lambda: pk.check("pk_gpu_encoder_run_dev", lib.pk_gpu_encoder_run_dev(
+            enc, dx.data_ptr(), 33, 0, ENC_OVERLAP, dy.data_ptr(), s.cuda_stream))
+        for _ in range(max(1, warmup)):
+            run()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(steps):
+            run()
+        e1.record(s)
+        torch.cuda.synchronize(dev)
+        us = e0.elapsed_time(e1) / steps * 1e3
+    finally:
+        lib.pk_gpu_encoder_destroy(enc)
+    print(json.dumps({"work": "24-block encoder, one 33-frame clip", "numerics": numerics,
+                      "us_per_call": round(us, 1), "steps": steps}), flush=True)
+
+
 def ffn_mode(args):
     """The int4 feed-forward pair at M = 375 (one FFN of 30 s of audio)."""
     import torch
@@ -661,16 +701,36 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         got_exact = dC.cpu().numpy()
     finally:
         pk.call("pk_gpu_set_numerics", pk.NUMERICS_DEFAULT)
+    # the same calls with every replica's panel made first (as a registered or
+    # resident weight has it): the panel kernels
+    for q in dQ:
+        pk.call("pk_gpu_pack_weight_dev", 8, k, n, q.data_ptr(), n, None, cur())
+    try:
+        assert lib.pk_gpu_uses_panel(m, n, k, 8, dQ[0].data_ptr(), n, None) == 1
+        us_panel = graph_us(torch, dev, call, 200, 10)
+        call(0)
+        torch.cuda.synchronize(dev)
+        got_panel = dC.cpu().numpy()
+    finally:
+        for q in dQ:
+            pk.call("pk_gpu_unpack_weight_dev", q.data_ptr())
     R = np.zeros((m, n), np.float32)
     cpu_s, cpu_n = ref_time(lambda: po.sgemm_qb(X, Q, 0.01, R, impl="ref"))
     by = alg_bytes("i8", m, n, k)
     w0 = {"gemm": f"int8 {m}x{n}x{k}, per-tensor scale 0.01",
+          "panel_us": round(us_panel, 2), "panel_gbps": round(by / us_panel / 1e3, 1),
+          "panel_frac_hbm": round(by / us_panel / 1e3 / PEAK_HBM_GBS, 4),
           "small_m_us": round(us_small, 2), "small_m_gbps": round(by / us_small / 1e3, 1),
           "small_m_frac_hbm": round(by / us_small / 1e3 / PEAK_HBM_GBS, 4),
           "exact_us": round(us_exact, 2), "exact_gbps": round(by / us_exact / 1e3, 1),
-          "cpu_ref_us": round(cpu_s * 1e6, 1) if cpu_s else None, "cpu_ref_calls": cpu_n}
+          "cpu_ref_us": round(cpu_s * 1e6, 1) if cpu_s else None, "cpu_ref_calls": cpu_n,
+          "note": "panel: the weights repacked once (pk_gpu_pack_weight_dev, as registration "
+                  "does); small_m: the narrow kernels on the on-disk layout; both the tolerance "
+                  "path (default numerics); exact: the bit-identical chains"}
     if have_ref:
-        w0["small_m_max_rel_err_vs_ref"] = float(np.abs(got.astype(np.float64) - R).max() / np.abs(R).max())
+        rel = lambda g: float(np.abs(g.astype(np.float64) - R).max() / np.abs(R).max())
+        w0["panel_max_rel_err_vs_ref"] = rel(got_panel)
+        w0["small_m_max_rel_err_vs_ref"] = rel(got)
         w0["exact_bit_identical_to_ref"] = bool(np.array_equal(got_exact.view(np.uint32), R.view(np.uint32)))
     out["0_int8_qkv_m32"] = w0
     del dQ
@@ -695,7 +755,17 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         pk.check("down", lib.pk_gpu_gemm_i4_dev(M, D, FF, 1.0, dH.data_ptr(), FF, P2d.data_ptr(),
                                                 S2d.data_ptr(), D // 2, 0.0, dO.data_ptr(), D, cur()))
     us1 = graph_us(torch, dev, pair, 100, 5)
-    us1f = fast_us(pair, 100, 5)
+    # fast numerics on the replicas' pre-split copies (made once, outside the
+    # timed region, as the resident encoder makes them)
+    for P1d, S1d, P2d, S2d in w1:
+        pk.call("pk_gpu_presplit_weight_dev", 4, D, FF, P1d.data_ptr(), FF // 2, S1d.data_ptr(), cur())
+        pk.call("pk_gpu_presplit_weight_dev", 4, FF, D, P2d.data_ptr(), D // 2, S2d.data_ptr(), cur())
+    try:
+        us1f = fast_us(pair, 100, 5)
+    finally:
+        for P1d, _, P2d, _ in w1:
+            pk.call("pk_gpu_unsplit_weight_dev", P1d.data_ptr())
+            pk.call("pk_gpu_unsplit_weight_dev", P2d.data_ptr())
     cpu1 = None if not have_ref else cpu_baseline(X1, P1, S1, P2, S2, cpu_budget_s)
     fl1 = 4.0 * M * D * FF
     out["1_int4_ffn_pair_m375"] = {
@@ -729,7 +799,15 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         pk.check("sgemm", lib.pk_gpu_sgemm_dev(m2, D, FF, 1.0, dH2.data_ptr(), FF, b.data_ptr(), D, 0.0,
                                                dO2.data_ptr(), D, cur()))
     us2 = graph_us(torch, dev, fp32_pair, 50, 3)
-    us2f = fast_us(fp32_pair, 50, 3)
+    for a, b in w2:
+        pk.call("pk_gpu_presplit_weight_dev", 32, D, FF, a.data_ptr(), FF, None, cur())
+        pk.call("pk_gpu_presplit_weight_dev", 32, FF, D, b.data_ptr(), D, None, cur())
+    try:
+        us2f = fast_us(fp32_pair, 50, 3)
+    finally:
+        for a, b in w2:
+            pk.call("pk_gpu_unsplit_weight_dev", a.data_ptr())
+            pk.call("pk_gpu_unsplit_weight_dev", b.data_ptr())
     fp32_pair(0)
     torch.cuda.synchronize(dev)
     got2 = dO2.cpu().numpy()
@@ -818,10 +896,16 @@ def workload_timings(pk, lib, torch, dev, cpu_budget_s):
         pe4 = np.ascontiguousarray(full.pe[PE_CENTER - 33 + 1:PE_CENTER + 33])
         cpu4, _ = cpu_seconds_per_call(lambda: po.ref_blocks(full.blocks, N_BLOCKS, pe4, x4, variant="x86"),
                                        cpu_budget_s, 200)
+    # weight bytes one pass streams: per block the int4 feed-forward pair x 2
+    # (codes + scales), int8 QKV and output projection, fp32 pointwise 1 and 2
+    wb = N_BLOCKS * (2 * 2 * (D * FF // 2 + 4 * D * FF // 32) + 3 * D * D + D * D + 4 * D * 2 * D + 4 * D * D)
     out["4_short_clip_33_frames"] = {
         "work": "the 24-block encoder on a 2.56 s clip (33 frames, one sequence): every weight "
                 "GEMM at M = 33; position projections computed at creation",
         "gpu_exact_us": round(us4["exact"], 1), "gpu_small_m_us": round(us4["small_m"], 1),
+        "weight_bytes_per_pass": wb,
+        "small_m_weight_stream_gbps": round(wb / us4["small_m"] / 1e3, 1),
+        "small_m_weight_stream_frac_hbm": round(wb / us4["small_m"] / 1e3 / PEAK_HBM_GBS, 4),
         "cpu_ref_us": round(cpu4 * 1e6, 1) if cpu4 else None}
     return out
 
@@ -1092,6 +1176,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-workloads", action="store_true",
                     help="skip the smaller workloads' timings (profiler runs of the encoder)")
+    ap.add_argument("--short-clip", action="store_true",
+                    help="time only the 24-block encoder on one 33-frame clip (with --numerics)")
     ap.add_argument("--ffn", action="store_true",
                     help="time the int4 feed-forward pair at M = 375 instead of the encoder")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -1128,6 +1214,9 @@ def main():
         gemm_mode(args.gemm, args.steps or 200, 20 if args.warmup is None else args.warmup,
                   eager=args.eager, force_config=args.force_config, numerics=args.numerics,
                   split_k=not args.no_split_k, panel=not args.no_panel, presplit=not args.no_presplit)
+        return
+    if args.short_clip:
+        short_clip_mode(args.steps or 20, 3 if args.warmup is None else args.warmup, args.numerics)
         return
     if args.ffn:
         args.steps = args.steps or 200
