@@ -60,10 +60,12 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 constexpr int kXcd = 8;
 constexpr int KT = 32;            // k per chunk
 constexpr int RS = KT + 8;        // LDS row stride of a plane, in bf16 (80 bytes)
-// Lo planes start GAP bf16 (64 bytes, 16 banks) past the end of their hi
+// Lo planes start kGap bf16 (64 bytes, 16 banks) past the end of their hi
 // plane, so 16-byte stores of the hi and the lo half of one row or column in
-// one access phase land on distinct banks.
-constexpr int GAP = 32;
+// one access phase land on distinct banks; not where those 128 bytes per
+// buffer would cost a workgroup per CU (Pipe::GAP).
+constexpr int kGap = 32;
+constexpr int kCuLds = 163840;    // LDS bytes per CU
 // Pipe's weight format for weights given pre-split (GemmProblem::b_presplit,
 // int4 and fp32): per 32-deep chunk c and column n, 128 bytes at
 // (c N + n) * 128: the 32 bf16 hi = bf16(w) of k = 32 c .. 32 c + 31, then
@@ -111,6 +113,15 @@ __device__ inline int q_i4(uint32_t w, int j)
     return (int)(w << (28 - 4 * j)) >> 28;
 }
 
+// The A row that 8-lane group g stages: groups 2j and 2j + 1 (one 16-lane
+// phase of an 8-byte LDS store) take rows 4 apart within each block of 8, so
+// their 64-byte runs at the 80-byte row pitch land 16 banks apart instead of
+// overlapping by 4.
+__device__ inline int a_row(int g)
+{
+    return (g & ~7) + ((g & 1) << 2) + ((g >> 1) & 3);
+}
+
 template <int WK> struct WUnit;
 template <> struct WUnit<W_I8> { uint32_t q[2]; };
 template <> struct WUnit<W_I4> { uint32_t q[2]; float s[2]; };
@@ -126,6 +137,10 @@ template <int WK, int BM, int BN, int NT, bool AS>
 struct Pipe {
     static constexpr int NBP = WK == W_I8 ? 1 : 2;             // weight planes
     static constexpr int A_PLANE = BM * RS, B_PLANE = BN * RS;   // bf16 elements
+    // two buffers per workgroup: the gaps only where they keep as many
+    // workgroups per CU (the 128 x 128 tiles fill 160 KB exactly without)
+    static constexpr int BYTES0 = 2 * 2 * (2 * A_PLANE + NBP * B_PLANE);
+    static constexpr int GAP = kCuLds / (BYTES0 + 2 * 2 * NBP * kGap) == kCuLds / BYTES0 ? kGap : 0;
     // plane offsets in one chunk's buffer (the lo planes GAP past their hi plane)
     static constexpr int A_LO = A_PLANE + GAP, B_HI = A_LO + A_PLANE, B_LO = B_HI + B_PLANE + GAP;
     static constexpr int BUF = B_HI + NBP * B_PLANE + (NBP - 1) * GAP;   // one chunk
@@ -154,7 +169,7 @@ struct Pipe {
     {
 #pragma unroll
         for (int i = 0; i < A_ITEMS; ++i) {
-            const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
+            const int idx = tid + NT * i, row = a_row(idx >> 3), kq = idx & 7;
             r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(
                 rA, (int)(((uint32_t)(m0 + row) * (uint32_t)p.lda + (uint32_t)(k0 + 4 * kq)) * 4u), 0, 0);
         }
@@ -209,13 +224,13 @@ struct Pipe {
             // part kq: the hi (even) or lo (odd) half of k group kq / 2
 #pragma unroll
             for (int i = 0; i < A_ITEMS; ++i) {
-                const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
+                const int idx = tid + NT * i, row = a_row(idx >> 3), kq = idx & 7;
                 *reinterpret_cast<v4u*>((kq & 1 ? al : ah) + row * RS + 8 * (kq >> 1)) = r.a[i];
             }
         } else {
 #pragma unroll
             for (int i = 0; i < A_ITEMS; ++i) {
-                const int idx = tid + NT * i, row = idx >> 3, kq = idx & 7;
+                const int idx = tid + NT * i, row = a_row(idx >> 3), kq = idx & 7;
                 uint32_t h0, l0, h1, l1;
                 split2(__uint_as_float(r.a[i][0]), __uint_as_float(r.a[i][1]), h0, l0);
                 split2(__uint_as_float(r.a[i][2]), __uint_as_float(r.a[i][3]), h1, l1);
