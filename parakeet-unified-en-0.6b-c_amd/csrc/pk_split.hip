@@ -46,6 +46,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 
 namespace pkgpu {
 namespace {
@@ -626,10 +627,21 @@ __global__ __launch_bounds__(256) void split_pack(int K, int N, const void* B, i
 enum SplitShape { SP_4x2, SP_2x2, SP_2x1, SP_K4, SP_1x1 };
 constexpr int kKSplit = 4;
 
+// PK_GPU_SPLIT_WIDE=0: 128 x 128 tiles (two workgroups per CU) where 256 x
+// 128 tiles would be taken.  A tuning switch, read once.
+bool split_wide()
+{
+    static const bool wide = [] {
+        const char* v = getenv("PK_GPU_SPLIT_WIDE");
+        return !(v && strcmp(v, "0") == 0);
+    }();
+    return wide;
+}
+
 SplitShape split_shape(int M, int N, int K)
 {
     auto tiles = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (tiles(128, 128) > 256) return SP_4x2;
+    if (tiles(128, 128) > 256) return split_wide() ? SP_4x2 : SP_2x2;
     if (tiles(128, 128) >= 256) return SP_2x2;
     if (tiles(128, 64) >= 256) return SP_2x1;
     if (K / KT >= 2 * kKSplit) return SP_K4;
