@@ -293,9 +293,11 @@ def test_host_pointer_calls_from_threads(dev):
 
 @pytest.mark.skip(reason="its one GPU run (a tight unregister/register loop on the main thread "
                          "while 4 threads ran host-pointer GEMMs on the weight) wrote nothing for "
-                         "180 s and was killed; the cause is not shown, so unregistering during "
-                         "GEMM calls is documented as unsupported (pk_gpu.h) and this case stays "
-                         "off the GPU")
+                         "180 s and was killed. Unregistering now refuses (PK_GPU_EBUSY) while a "
+                         "call reads the weight, so a copy's device synchronisation and free run "
+                         "only on the unregistering thread; test_registry_cpu.py checks that "
+                         "protocol on the CPU under ThreadSanitizer. The hang's cause inside the "
+                         "runtime is not shown, so this case stays off the GPU")
 def test_unregister_while_other_threads_call(dev):
     """pk_gpu_unregister_weight may run while other threads' host-pointer
     GEMMs read that weight: a call that found the resident copy keeps it
