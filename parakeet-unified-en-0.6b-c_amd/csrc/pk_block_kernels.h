@@ -26,6 +26,19 @@ __host__ __device__ constexpr unsigned attn_lds_bytes(int T)
     return 4u * (unsigned)(kAttnRows * attn_sld(T) + 64 * 68);
 }
 
+// Sequences of at most kAttnShortT rows take rel_pos_attention_short:
+// kAttnShortRows query rows per workgroup, and every key, position and value
+// row it reads staged in LDS at once (the score rows, then 64 key rows, one
+// or two blocks of 64 position rows and the value rows, T rounded up to 16,
+// each kTileLd = 132 floats apart).
+constexpr int kAttnShortT = 64;
+constexpr int kAttnShortRows = 16;
+__host__ __device__ constexpr unsigned attn_short_lds_bytes(int T)
+{
+    return 4u * (unsigned)(kAttnShortRows * attn_sld(T) +
+                           (64 + 64 * ((T + kAttnShortRows - 1 + 63) / 64) + ((T + 15) & ~15)) * 132);
+}
+
 // Relative-position attention of n chunks (encoder.c:300-408); chunk z has
 // chunk_T[z] <= T rows (all T when chunk_T is null).
 //   qkv  [rows][ldq]: Q | K | V (H*128 columns each, bias added); chunk z

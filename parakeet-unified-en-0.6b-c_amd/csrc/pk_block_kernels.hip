@@ -23,6 +23,8 @@
 #include "pk_block_kernels.h"
 #include "pk_gemm_tiles.h"
 
+#include <cstdlib>
+#include <cstring>
 #include <utility>
 
 namespace pkgpu {
@@ -155,6 +157,7 @@ __global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
 constexpr int kDh = 128;                 // PK_HEAD_DIM
 constexpr int kTileLd = kDh + 4;         // padded LDS row of a value tile
 constexpr float kScoreScale = 0.0883883461356163f;   // 1/sqrtf(128) = 0x3db504f3
+static_assert(kTileLd == 132, "attn_short_lds_bytes counts staged rows of 132 floats");
 
 template <int T_>
 __device__ inline v4f mfma_bcast(float a, float b, v4f c)
@@ -340,6 +343,64 @@ __device__ inline void pv_steps(std::integer_sequence<int, Ts...>, const float (
                : 0), ...);
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin; renumber them so
+// each XCD runs a contiguous run of (row block, head, chunk) tasks, row
+// block fastest: the row blocks of one head of one chunk then share one
+// XCD's L2 for their K, P and V rows.  Returns the task number.
+__device__ inline int attn_task(int& rb, int& h, int& z)
+{
+    const int nrb = gridDim.x, nh = gridDim.y, total = nrb * nh * gridDim.z;
+    const int lin = blockIdx.x + nrb * (blockIdx.y + nh * blockIdx.z);
+    const int xcd = lin % 8, local = lin / 8;
+    const int base = total / 8, extra = total % 8;
+    const int task = xcd * base + min(xcd, extra) + local;
+    rb = task % nrb;
+    h = (task / nrb) % nh;
+    z = task / (nrb * nh);
+    return task;
+}
+
+// Softmax of one score row s[0, T) in place (tensor_ops.c:336-357), by the 8
+// lanes of an aligned group (lane q owns j = q, q+8, ...): the row maximum,
+// e = exp(s - max) with the partial sums of each lane in order, hsum8; the
+// last T % 8 entries by one lane, in order (the reference's scalar tail);
+// then s * (1 / sum).  A row past the sequence (live false) is zeroed.
+__device__ inline void softmax_row(float* s, int T, bool live)
+{
+    const int lane = threadIdx.x & 63, q = lane & 7;
+    if (live) {
+        float mx = s[0];
+#pragma unroll 8
+        for (int j = q; j < T; j += 8) mx = fmaxf(mx, s[j]);
+        mx = fmaxf(mx, __shfl_xor(mx, 4));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        const int T8 = T & ~7;
+        float part = 0.0f;
+#pragma unroll 8
+        for (int j = q; j < T8; j += 8) {
+            const float e = exp_poly(__fsub_rn(s[j], mx));
+            s[j] = e;
+            part = __fadd_rn(part, e);
+        }
+        float sum = hsum8_lanes(part);
+        if (T8 < T) {                 // scalar tail, one lane, in order
+            if (q == 0)
+                for (int j = T8; j < T; ++j) {
+                    const float e = expf_ieee(__fsub_rn(s[j], mx));
+                    s[j] = e;
+                    sum = __fadd_rn(sum, e);
+                }
+            sum = __shfl(sum, lane & ~7);
+        }
+        const float inv = __fdiv_rn(1.0f, sum);
+#pragma unroll 8
+        for (int j = q; j < T; j += 8) s[j] = __fmul_rn(s[j], inv);
+    } else {
+        for (int j = q; j < T; j += 8) s[j] = 0.0f;
+    }
+}
+
 // kGlobal: the block's score rows live in its own slice of p.scores (task
 // order) instead of LDS, for sequences beyond kAttnMaxT; every operation and
 // its order are the same, and __syncthreads orders the workgroup's global
@@ -351,23 +412,10 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
     extern __shared__ float smem[];
     const int sld = attn_sld(p.T);
 
-    // Workgroups are dispatched to the 8 XCDs round-robin; renumber them so
-    // each XCD runs a contiguous run of (row block, head, chunk) tasks, row
-    // block fastest: the row blocks of one head of one chunk then share one
-    // XCD's L2 for their K, P and V tiles.
+    // (row block, head, chunk) in XCD runs
     int rb, h, z;
-    float* S;
-    {
-        const int nrb = gridDim.x, nh = gridDim.y, total = nrb * nh * gridDim.z;
-        const int lin = blockIdx.x + nrb * (blockIdx.y + nh * blockIdx.z);
-        const int xcd = lin % 8, local = lin / 8;
-        const int base = total / 8, extra = total % 8;
-        const int task = xcd * base + min(xcd, extra) + local;
-        rb = task % nrb;
-        h = (task / nrb) % nh;
-        z = task / (nrb * nh);
-        S = kGlobal ? p.scores + (size_t)task * kAttnRows * sld : smem;
-    }
+    const int task = attn_task(rb, h, z);
+    float* S = kGlobal ? p.scores + (size_t)task * kAttnRows * sld : smem;
     float* tile = kGlobal ? smem : smem + kAttnRows * sld;
     const int T = p.chunk_T ? p.chunk_T[z] : p.T;           // this chunk's rows
     const int r0 = rb * kAttnRows;
@@ -461,41 +509,10 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
     const TileSrc vs{V, p.ldq, T};
     load_vtile(pre, vs, 0);               // the first value tile, during the softmax
 
-    // Softmax of each row: 8 lanes per row, lane q owns j = q, q+8, ...
+    // Softmax of each row: 8 lanes per row
     {
-        const int rl = 8 * w + (lane >> 3), q = lane & 7, r = r0 + rl;
-        float* s = S + rl * sld;
-        if (r < T) {
-            float mx = s[0];
-#pragma unroll 8
-            for (int j = q; j < T; j += 8) mx = fmaxf(mx, s[j]);
-            mx = fmaxf(mx, __shfl_xor(mx, 4));
-            mx = fmaxf(mx, __shfl_xor(mx, 2));
-            mx = fmaxf(mx, __shfl_xor(mx, 1));
-            const int T8 = T & ~7;
-            float part = 0.0f;
-#pragma unroll 8
-            for (int j = q; j < T8; j += 8) {
-                const float e = exp_poly(__fsub_rn(s[j], mx));
-                s[j] = e;
-                part = __fadd_rn(part, e);
-            }
-            float sum = hsum8_lanes(part);
-            if (T8 < T) {                 // scalar tail, one lane, in order
-                if (q == 0)
-                    for (int j = T8; j < T; ++j) {
-                        const float e = expf_ieee(__fsub_rn(s[j], mx));
-                        s[j] = e;
-                        sum = __fadd_rn(sum, e);
-                    }
-                sum = __shfl(sum, lane & ~7);
-            }
-            const float inv = __fdiv_rn(1.0f, sum);
-#pragma unroll 8
-            for (int j = q; j < T; j += 8) s[j] = __fmul_rn(s[j], inv);
-        } else {
-            for (int j = q; j < T; j += 8) s[j] = 0.0f;
-        }
+        const int rl = 8 * w + (lane >> 3);
+        softmax_row(S + rl * sld, T, r0 + rl < T);
     }
     __syncthreads();
 
@@ -541,6 +558,218 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
                 out[(size_t)r * p.ldo + 64 + lane] = acc[g][1][ii];
             }
         }
+}
+
+// ---- short sequences (T <= kAttnShortT) -------------------------------------
+// A workgroup of 4 waves takes kAttnShortRows = 16 query rows, 4 per wave.
+// Every key, position and value row it reads is loaded into LDS at once,
+// behind one barrier: keys [0, 64), positions [m_first, m_first + 64 nb)
+// (nb 64-row blocks cover the block's shifted positions), values [0, T
+// rounded up to 16).  Rows past an operand's end read 0.  After the barrier
+// each wave runs its own rows without waiting for the others.  It performs
+// the operations of rel_pos_attention, each output through the same chain in
+// the same order, so the bits are the same:
+// - AC, and BD with the shift and the scale;
+// - the softmax;
+// - scores x V.
+// Only the work division differs: 4 rows a wave instead of 8, and one
+// staging round trip instead of one per 64-row tile.
+
+// acc[t % 8] += A(step t) * b[t] for the 16 steps of one A register.
+template <int... Ts>
+__device__ inline void score_steps1(std::integer_sequence<int, Ts...>, float a, const float (&b)[16],
+                                    v4f (&acc)[8])
+{
+    ((acc[Ts & 7] = mfma_bcast<Ts>(a, b[Ts], acc[Ts & 7])), ...);
+}
+
+// 4 rows x 64 columns of NT dot products over k = 0..127: a[kb] holds the 4
+// rows in broadcast layout for k in [16 kb, 16 kb + 16), lane j's B row is
+// brow (128 floats in LDS).  Chain t % 8 of each output takes k ascending;
+// the 8 chains are reduced as hsum8 (score_half and score_sums' order).
+__device__ inline void score_rows(const float* brow, const float (&a)[8], float (&out)[4])
+{
+    v4f acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = v4f{0.f, 0.f, 0.f, 0.f};
+    float b[2][16];
+    auto fetch = [&](float (&dst)[16], int kb) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(brow + kb * 16 + 4 * q);
+            dst[4 * q] = v.x; dst[4 * q + 1] = v.y; dst[4 * q + 2] = v.z; dst[4 * q + 3] = v.w;
+        }
+    };
+    fetch(b[0], 0);
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+        if (kb + 1 < 8) fetch(b[(kb + 1) & 1], kb + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        score_steps1(std::make_integer_sequence<int, 16>{}, a[kb], b[kb & 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float s8[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) s8[l] = acc[l][i];
+        out[i] = hsum8(s8);
+    }
+}
+
+// scores x V for 4 rows: acc[d] += S[row i][j0 + t] * V[j0 + t][64 d + lane].
+template <int... Ts>
+__device__ inline void pv_steps1_full(std::integer_sequence<int, Ts...>, float a, const float* vt,
+                                      v4f (&acc)[2])
+{
+    const int lane = threadIdx.x & 63;
+    float b0[16], b1[16];
+    ((b0[Ts] = vt[Ts * kTileLd + lane], b1[Ts] = vt[Ts * kTileLd + 64 + lane]), ...);
+    ((acc[0] = mfma_bcast<Ts>(a, b0[Ts], acc[0]), acc[1] = mfma_bcast<Ts>(a, b1[Ts], acc[1])), ...);
+}
+
+template <int... Ts>
+__device__ inline void pv_steps1(std::integer_sequence<int, Ts...>, float a, const float* vt, int n,
+                                 v4f (&acc)[2])
+{
+    const int lane = threadIdx.x & 63;
+    (((Ts < n) ? (acc[0] = mfma_bcast<Ts>(a, vt[Ts * kTileLd + lane], acc[0]),
+                  acc[1] = mfma_bcast<Ts>(a, vt[Ts * kTileLd + 64 + lane], acc[1]), 0)
+               : 0), ...);
+}
+
+__global__ __launch_bounds__(256) void rel_pos_attention_short(AttnArgs p)
+{
+    // Score rows [kAttnShortRows][sld], then the staged rows [n_rows][kTileLd].
+    extern __shared__ float smem[];
+    const int sld = attn_sld(p.T);
+    int rb, h, z;
+    attn_task(rb, h, z);
+    const int T = p.chunk_T ? p.chunk_T[z] : p.T;           // this chunk's rows
+    const int r0 = rb * kAttnShortRows;
+    if (r0 >= T) return;                                     // the whole workgroup
+    const int row0 = p.chunk_rows ? p.chunk_rows[z] : 0;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int D = p.H * kDh;
+    const float* qkv = p.qkv + (size_t)row0 * p.ldq;
+    const float* K = qkv + D + h * kDh;
+    const float* V = qkv + 2 * D + h * kDh;
+    const float* P = p.P + (size_t)(p.T - T) * p.ldp + h * kDh;
+    const int r_hi = min(r0 + kAttnShortRows, T) - 1;
+    const int L = 2 * T - 1;
+    const int m_first = T - 1 - r_hi, m_last = 2 * T - 2 - r0;
+    const int nb = (m_last - m_first + 64) / 64;             // position blocks: 1 or 2
+    const int n_rows = 64 + 64 * nb + ((T + 15) & ~15);      // keys, positions, values
+    float* S = smem;
+    float* kt = smem + kAttnShortRows * sld;                 // staged row s at kt + s kTileLd
+    float* pt = kt + 64 * kTileLd;
+    float* vt = pt + 64 * nb * kTileLd;
+
+    // This wave's Q rows in broadcast layout (lane 4t + i: row r0 + 4w + i at
+    // k = 16 kb + t), loaded with the staged rows; rows past T read row T-1
+    // and are zeroed after.
+    const int i = lane & 3, t = lane >> 2;
+    const int rq = r0 + 4 * w + i;
+    float qv[8], bu[8], bv[8];
+    {
+        const float* q = qkv + (size_t)min(rq, T - 1) * p.ldq + h * kDh;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            qv[kb] = q[16 * kb + t];
+            bu[kb] = p.pos_bias_u[h * kDh + 16 * kb + t];
+            bv[kb] = p.pos_bias_v[h * kDh + 16 * kb + t];
+        }
+    }
+    // Staged row s (32 float4 per row, 8 rows per pass of the 256 threads):
+    // key s for s < 64, position m_first + s - 64 below 64 + 64 nb, then
+    // value s - 64 - 64 nb.  Region bounds are multiples of 16 rows, so each
+    // pass reads one region and its branch is uniform.
+    {
+        constexpr int kPass = (64 + 128 + kAttnShortT) / 8;
+        const TileSrc ks{K, p.ldq, T}, ps{P, p.ldp, L}, vs{V, p.ldq, T};
+        const __amdgpu_buffer_rsrc_t rk = ks.at(0), rp = ps.at(m_first), rv = vs.at(0);
+        const int sr = threadIdx.x >> 5, c = 4 * (threadIdx.x & 31);
+        float4 st[kPass];
+#pragma unroll
+        for (int q = 0; q < kPass; ++q) {
+            const int s0 = 8 * q, s = s0 + sr;
+            if (s0 < n_rows) {
+                tiles::v4u u;
+                if (s0 < 64)
+                    u = tiles::ld_v4(rk, (uint32_t)(s * p.ldq + c) * 4u);
+                else if (s0 < 64 + 64 * nb)
+                    u = tiles::ld_v4(rp, (uint32_t)((s - 64) * p.ldp + c) * 4u);
+                else
+                    u = tiles::ld_v4(rv, (uint32_t)((s - 64 - 64 * nb) * p.ldq + c) * 4u);
+                st[q] = as_float4(u);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kPass; ++q)
+            if (8 * q < n_rows) *reinterpret_cast<float4*>(kt + (8 * q + sr) * kTileLd + c) = st[q];
+    }
+    float au[8], av[8];
+    {
+        const bool live = rq < T;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            au[kb] = live ? __fadd_rn(qv[kb], bu[kb]) : 0.0f;
+            av[kb] = live ? __fadd_rn(qv[kb], bv[kb]) : 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // From here on a wave reads and writes only its own 4 score rows (LDS
+    // accesses of one wave complete in order): no more barriers.
+    float* Sw = S + 4 * w * sld;
+    {   // AC: S[row][j] = Q_u[row] . K[j], j = lane
+        float o[4];
+        score_rows(kt + lane * kTileLd, au, o);
+        if (lane < T)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) Sw[ii * sld + lane] = o[ii];
+    }
+    // BD at the shifted positions m = T-1-row+j, combined and scaled
+    for (int b = 0; b < nb; ++b) {
+        const int m0 = m_first + 64 * b;
+        float o[4];
+        score_rows(pt + (64 * b + lane) * kTileLd, av, o);
+        const int jb = m0 + lane - (T - 1) + r0;
+        float sc[4];
+        bool ok[4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const int rl = 4 * w + ii;
+            ok[ii] = r0 + rl < T && (unsigned)(jb + rl) < (unsigned)T;
+            sc[ii] = S[ok[ii] ? jb + rl * (sld + 1) : 0];
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+            if (ok[ii])
+                S[jb + (4 * w + ii) * (sld + 1)] = __fmul_rn(__fadd_rn(sc[ii], o[ii]), kScoreScale);
+    }
+    // softmax: lanes 0..31, 8 per row
+    if (lane < 32) softmax_row(Sw + (lane >> 3) * sld, T, r0 + 4 * w + (lane >> 3) < T);
+
+    // out[row][h*128 + d] = sum over j ascending of S[row][j] * V[j][d]
+    v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    const float* srow = Sw + i * sld + t;
+    int j0 = 0;
+    for (; j0 + 16 <= T; j0 += 16)
+        pv_steps1_full(std::make_integer_sequence<int, 16>{}, srow[j0], vt + j0 * kTileLd, acc);
+    if (T & 15) {
+        const float a = j0 + t < T ? srow[j0] : 0.0f;
+        pv_steps1(std::make_integer_sequence<int, 16>{}, a, vt + j0 * kTileLd, T & 15, acc);
+    }
+    float* out = p.out + (size_t)row0 * p.ldo + h * kDh;
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+        const int r = r0 + 4 * w + ii;
+        if (r < T) {
+            out[(size_t)r * p.ldo + lane] = acc[0][ii];
+            out[(size_t)r * p.ldo + 64 + lane] = acc[1][ii];
+        }
+    }
 }
 
 // ---- GLU (encoder.c:453-461) -------------------------------------------------
@@ -818,6 +1047,17 @@ hipError_t launch_layer_norm_split(const float* x, int ldx, const float* gamma, 
     return hipGetLastError();
 }
 
+// PK_GPU_ATTN_SHORT=0 sends short sequences to rel_pos_attention too (the
+// same bits; for comparing the two).
+bool attn_short_enabled()
+{
+    static const bool on = [] {
+        const char* v = getenv("PK_GPU_ATTN_SHORT");
+        return !(v && strcmp(v, "0") == 0);
+    }();
+    return on;
+}
+
 hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s)
 {
     if (a.T <= 0 || n_chunks <= 0) return hipSuccess;
@@ -828,6 +1068,15 @@ hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s)
         if ((size_t)grid.x * grid.y * grid.z * kAttnRows * attn_sld(a.T) >= ((size_t)1 << 40))
             return hipErrorInvalidValue;
         hipLaunchKernelGGL(rel_pos_attention<true>, grid, dim3(256), 4u * kTileFloats, s, a);
+        return hipGetLastError();
+    }
+    if (a.T <= kAttnShortT && attn_short_enabled()) {
+        static const hipError_t attr_s = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&rel_pos_attention_short),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)attn_short_lds_bytes(kAttnShortT));
+        if (attr_s != hipSuccess) return attr_s;
+        const dim3 gs((a.T + kAttnShortRows - 1) / kAttnShortRows, a.H, n_chunks);
+        hipLaunchKernelGGL(rel_pos_attention_short, gs, dim3(256), attn_short_lds_bytes(a.T), s, a);
         return hipGetLastError();
     }
     // LDS above the default dynamic limit is granted once per process.

@@ -271,8 +271,11 @@ __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
         }
         __syncthreads();
         if constexpr (LN) {
-            // every row's mean and 1 / sqrt(var + eps): 8 lanes a row, one pass for 64 rows
-            const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
+            // every row's mean and 1 / sqrt(var + eps): 8 lanes a row, one pass for 64 rows.
+            // Row r starts 4 r banks into the LDS (pitch 16 mod 128 bytes): a
+            // half wave takes rows 8 wave + {0, 2, 4, 6} or {1, 3, 5, 7}, whose
+            // 8-float runs then fall in distinct banks.
+            const int r = 8 * wave + 2 * ((lane >> 3) & 3) + (lane >> 5), l = lane & 7;
             if (r < M) {
                 float mean, inv;
                 ln_row_stats<kLnChunk>(reinterpret_cast<const float*>(smem + r * pitch), p.K, l, mean, inv);

@@ -74,8 +74,10 @@ def gpu_attention(dev, qkv, P, pu, pv):
     return dout.cpu().numpy()
 
 
-@pytest.mark.parametrize("T", [416, 408, 64, 24, 8, 1, 21, 108, 300, 512])
+@pytest.mark.parametrize("T", [416, 408, 64, 24, 8, 1, 21, 108, 300, 512, 33, 17, 49, 50, 63, 65])
 def test_attention_bit_exact_to_oracle(dev, T):
+    """T <= 64 takes the short-sequence kernel (every row staged in LDS at
+    once; one or two blocks of positions: T = 49 / 50), longer T the tiled one."""
     qkv, P, pu, pv = attention_inputs(T)
     got = gpu_attention(dev, qkv, P, pu, pv)
     want = po.attention_core(qkv, P, pu, pv)
@@ -225,14 +227,15 @@ def test_encoder_block_workload_stats_within_tolerance(dev):
 
 
 @pytest.mark.parametrize("mode", ["int8", "fp32"])
-@pytest.mark.parametrize("T,chunk", [(300, 0), (132, 64)])
+@pytest.mark.parametrize("T,chunk", [(300, 0), (132, 64), (100, 40)])
 def test_encoder_weight_directories_bit_exact_to_oracle(dev, mode, T, chunk):
     """The resident encoder with the int8 weight directory's formats (every
     linear int8, the FF linears included) and the fp32 one's (every linear
     fp32: QKV, position and output projections on the fp32 chains), two
     blocks, bit for bit against the oracle's encoder on the same blocks: an
-    unchunked 300-frame sequence (softmax's scalar tail) and 64-frame chunks
-    of 72, 76 and 12 rows."""
+    unchunked 300-frame sequence (softmax's scalar tail), 64-frame chunks
+    of 72, 76 and 12 rows, and 40-frame chunks of 48, 56 and 28 rows (the
+    short-sequence attention over a batch of chunks)."""
     blocks = [bg.Block(0xD1500 + i, attn_scale=0.0005, mode=mode) for i in range(2)]
     assert {blocks[0].w.ff1_linear1_w.bits, blocks[0].w.linear_out_w.bits} == \
         {8 if mode == "int8" else 32}
