@@ -39,24 +39,113 @@ __device__ inline float hsum8(const float (&p)[8])
 }
 
 // ---- LayerNorm (tensor_ops.c:150-185) ---------------------------------------
-// One workgroup of 4 waves per 8 rows.  The rows come in with 16-byte loads
-// (8 per thread) into LDS, padded 8 floats per row.  Thread c owns columns
-// 4c .. 4c + 3 of every row (one 16-byte group of gamma and of beta).  The
-// statistics are ln_row_stats: 8 lanes per row (lanes 0-15 of each wave,
-// 2 rows a wave), lane l holding the partial sums of elements l, l+8, ...
-// in order, like one AVX2 lane.  The outputs fl(fl(fl(x - mean) * inv) *
-// gamma + beta) are independent and formed per 16-byte group.  In place
-// (out == x) is safe: a workgroup reads its rows before it writes them.
-// SPLIT: each output o goes out split as the split GEMM kernels multiply it
-// (hi = bf16(o), lo = bf16(o - hi), both to nearest: the split those kernels
-// would make of the fp32 output), in their pre-split layout: per row and
-// group of 8 columns, the 8 hi then the 8 lo, in the fp32 row's bytes.
+// One wave per 8 rows, 8 lanes per row; lane l of a row holds the partial
+// sums of elements l, l+8, l+16, ... in order, like one AVX2 lane.  The rows
+// come in with 16-byte loads into LDS (padded rows: the strided reads of the
+// 64 lanes hit distinct banks but for 2-way overlaps), each lane keeps its
+// NPL = D/8 elements in registers for the two sequential passes (sum,
+// squared deviations) and writes the deviations back.  The outputs
+// fl(fl(dev * inv) * gamma + beta) are independent, so they are formed per
+// 16-byte group: each lane then needs 4 of gamma's and beta's groups
+// (loaded first, with the rows) instead of 2 x NPL scattered values.
+// In place (out == x) is safe: every row is read before any is written.
 
-template <int NPL, bool SPLIT>
-__global__ __launch_bounds__(256) void layer_norm_rows(const float* x, int ldx,
-                                                       const float* __restrict__ gamma,
-                                                       const float* __restrict__ beta,
-                                                       float* out, int ldo, int rows)
+template <int NPL>
+__global__ __launch_bounds__(64) void layer_norm_rows(const float* x, int ldx,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta,
+                                                      float* out, int ldo, int rows)
+{
+    constexpr int D = 8 * NPL, LD = D + 8, V4 = D / 4, NQ = 8 * V4 / 64;
+    static_assert(V4 % 64 == 0, "each lane's 16-byte groups repeat every 64 lanes");
+    constexpr int NG = V4 / 64;                     // distinct column groups per lane
+    __shared__ float buf[8 * LD];
+    __shared__ float inv_row[8];
+    const int lane = threadIdx.x;
+    const int row0 = blockIdx.x * 8;
+    const int nr = min(8, rows - row0);
+    // all of a lane's row loads in flight at once (rows past the end read row
+    // 0), then its gamma and beta groups: columns 4 * (lane + 64 j)
+    float4 in[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int idx = lane + 64 * q, r = idx / V4, c4 = idx % V4;
+        in[q] = *reinterpret_cast<const float4*>(x + (size_t)(r < nr ? row0 + r : row0) * ldx + 4 * c4);
+    }
+    float4 g4[NG], b4[NG];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        g4[j] = *reinterpret_cast<const float4*>(gamma + 4 * (lane + 64 * j));
+        b4[j] = *reinterpret_cast<const float4*>(beta + 4 * (lane + 64 * j));
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int idx = lane + 64 * q;
+        *reinterpret_cast<float4*>(buf + (idx / V4) * LD + 4 * (idx % V4)) = in[q];
+    }
+    __syncthreads();
+    const int r = lane >> 3, l = lane & 7;
+    float* br = buf + r * LD + l;
+    float v[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) v[i] = br[8 * i];
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) p = __fadd_rn(p, v[i]);
+    const float mean = __fdiv_rn(hsum8_lanes(p), (float)D);
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        v[i] = __fsub_rn(v[i], mean);
+        q = __fmaf_rn(v[i], v[i], q);
+    }
+    const float var = __fdiv_rn(hsum8_lanes(q), (float)D);
+    // sqrtf and '/' are correctly rounded here (HIP's __fsqrt_rn is the
+    // native, approximate square root unless OCML_BASIC_ROUNDED_OPERATIONS).
+    const float inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) br[8 * i] = v[i];      // the deviations x - mean
+    if (l == 0) inv_row[r] = inv;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int idx = lane + 64 * q, rr = idx / V4, c4 = idx % V4, j = q % NG;
+        if (rr < nr) {
+            const float4 d = *reinterpret_cast<const float4*>(buf + rr * LD + 4 * c4);
+            const float s = inv_row[rr];
+            float4 o;
+            o.x = __fmaf_rn(__fmul_rn(d.x, s), g4[j].x, b4[j].x);
+            o.y = __fmaf_rn(__fmul_rn(d.y, s), g4[j].y, b4[j].y);
+            o.z = __fmaf_rn(__fmul_rn(d.z, s), g4[j].z, b4[j].z);
+            o.w = __fmaf_rn(__fmul_rn(d.w, s), g4[j].w, b4[j].w);
+            *reinterpret_cast<float4*>(out + (size_t)(row0 + rr) * ldo + 4 * c4) = o;
+        }
+    }
+}
+
+// LayerNorm with split outputs, the fast numerics mode's input to the split
+// GEMMs: one workgroup of 4 waves per 8 rows.  The rows come in with 16-byte
+// loads (8 per thread) into LDS, padded 8 floats per row.  Thread c owns
+// columns 4c .. 4c + 3 of every row (one 16-byte group of gamma and of
+// beta).  The statistics are ln_row_stats_rolled: 8 lanes per row (lanes
+// 0-15 of each wave, 2 rows a wave), the same chains as layer_norm_rows.  The outputs
+// fl(fl(fl(x - mean) * inv) * gamma + beta) are independent and formed per
+// 16-byte group.  In place (out == x) is safe: a workgroup reads its rows
+// before it writes them.  Each output o goes out split as the split GEMM
+// kernels multiply it (hi = bf16(o), lo = bf16(o - hi), both to nearest: the
+// split those kernels would make of the fp32 output), in their pre-split
+// layout: per row and group of 8 columns, the 8 hi then the 8 lo, in the
+// fp32 row's bytes.  The statistics loops stay rolled (82 VGPRs instead of
+// 178): these workgroups run beside the other row group's split GEMMs, on
+// the CUs those leave free, and more of them fit there.  Measured on the
+// fast encoder pass (A/B on two boxes, two runs each): +0.3% and +1.5%
+// against one wave per 8 rows.  The plain LayerNorm keeps that layout: in
+// the exact pass the four-wave form measured 0.4% slower.
+template <int NPL>
+__global__ __launch_bounds__(256) void layer_norm_split_rows(const float* x, int ldx,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta,
+                                                             float* out, int ldo, int rows)
 {
     constexpr int D = 8 * NPL, LD = D + 8, V4 = D / 4, NQ = 8 * V4 / 256;
     static_assert(V4 == 256, "one 16-byte column group per thread");
@@ -79,7 +168,7 @@ __global__ __launch_bounds__(256) void layer_norm_rows(const float* x, int ldx,
     if (lane < 16) {
         const int r = 2 * w + (lane >> 3), l = lane & 7;
         float mean, inv;
-        ln_row_stats<32>(buf + r * LD, D, l, mean, inv);
+        ln_row_stats_rolled<32>(buf + r * LD, D, l, mean, inv);
         if (l == 0) {
             st[r][0] = mean;
             st[r][1] = inv;
@@ -96,19 +185,15 @@ __global__ __launch_bounds__(256) void layer_norm_rows(const float* x, int ldx,
             o.y = __fmaf_rn(__fmul_rn(__fsub_rn(v.y, mean), s), g4.y, b4.y);
             o.z = __fmaf_rn(__fmul_rn(__fsub_rn(v.z, mean), s), g4.z, b4.z);
             o.w = __fmaf_rn(__fmul_rn(__fsub_rn(v.w, mean), s), g4.w, b4.w);
-            if constexpr (SPLIT) {
-                uint32_t h0, l0, h1, l1;
-                split_bf16x2(o.x, o.y, h0, l0);
-                split_bf16x2(o.z, o.w, h1, l1);
-                // columns 4 tid .. +3: half (tid & 1) of group tid / 2, whose
-                // 16 bf16 values occupy the group's 8 floats
-                unsigned short* g8 = reinterpret_cast<unsigned short*>(
-                    out + (size_t)(row0 + q) * ldo + 8 * (tid >> 1));
-                *reinterpret_cast<uint2*>(g8 + 4 * (tid & 1)) = make_uint2(h0, h1);
-                *reinterpret_cast<uint2*>(g8 + 8 + 4 * (tid & 1)) = make_uint2(l0, l1);
-            } else {
-                *reinterpret_cast<float4*>(out + (size_t)(row0 + q) * ldo + 4 * tid) = o;
-            }
+            uint32_t h0, l0, h1, l1;
+            split_bf16x2(o.x, o.y, h0, l0);
+            split_bf16x2(o.z, o.w, h1, l1);
+            // columns 4 tid .. +3: half (tid & 1) of group tid / 2, whose
+            // 16 bf16 values occupy the group's 8 floats
+            unsigned short* g8 = reinterpret_cast<unsigned short*>(
+                out + (size_t)(row0 + q) * ldo + 8 * (tid >> 1));
+            *reinterpret_cast<uint2*>(g8 + 4 * (tid & 1)) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(g8 + 8 + 4 * (tid & 1)) = make_uint2(l0, l1);
         }
     }
 }
@@ -1001,7 +1086,7 @@ hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const 
          reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 ||
         ldx % 4 || ldo % 4)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((layer_norm_rows<128, false>), dim3((rows + 7) / 8), dim3(256), 0, s, x, ldx,
+    hipLaunchKernelGGL((layer_norm_rows<128>), dim3((rows + 7) / 8), dim3(64), 0, s, x, ldx,
                        gamma, beta, out, ldo, rows);
     return hipGetLastError();
 }
@@ -1016,7 +1101,7 @@ hipError_t launch_layer_norm_split(const float* x, int ldx, const float* gamma, 
          reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 ||
         ldx % 4 || ldo % 8)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((layer_norm_rows<128, true>), dim3((rows + 7) / 8), dim3(256), 0, s, x, ldx,
+    hipLaunchKernelGGL((layer_norm_split_rows<128>), dim3((rows + 7) / 8), dim3(256), 0, s, x, ldx,
                        gamma, beta, out, ldo, rows);
     return hipGetLastError();
 }

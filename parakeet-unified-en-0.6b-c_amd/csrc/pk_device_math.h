@@ -109,6 +109,37 @@ __device__ inline void ln_row_stats(const float* row, int D, int l, float& mean,
     inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
 }
 
+// ln_row_stats with the loops over the row's CH-element pieces kept rolled
+// (fewer registers); the same operations in the same order.
+template <int CH>
+__device__ inline void ln_row_stats_rolled(const float* row, int D, int l, float& mean, float& inv)
+{
+    float p = 0.0f;
+#pragma unroll 1
+    for (int i0 = 0; i0 < D; i0 += 8 * CH) {
+        float v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[c] = row[i0 + 8 * c + l];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) p = __fadd_rn(p, v[c]);
+    }
+    mean = __fdiv_rn(hsum8_lanes(p), (float)D);
+    float q = 0.0f;
+#pragma unroll 1
+    for (int i0 = 0; i0 < D; i0 += 8 * CH) {
+        float v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) v[c] = row[i0 + 8 * c + l];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const float d = __fsub_rn(v[c], mean);
+            q = __fmaf_rn(d, d, q);
+        }
+    }
+    const float var = __fdiv_rn(hsum8_lanes(q), (float)D);
+    inv = 1.0f / sqrtf(__fadd_rn(var, 1e-5f));
+}
+
 __device__ inline float exp_poly(float x)
 {
     x = fminf(fmaxf(x, -87.0f), 87.0f);
