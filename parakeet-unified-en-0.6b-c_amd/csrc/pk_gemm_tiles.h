@@ -940,8 +940,12 @@ hipError_t launch_chain(int cfg, const KArgs& a, hipStream_t s)
                 hipLaunchKernelGGL((chain_gemm_x<WK, mf, c, wm, wn, kt, pd, VEC, A1>),    \
                                    grid, block, 0, s, a);                                 \
         }                                                                                 \
-        else                                                                              \
-            hipLaunchKernelGGL((chain_gemm_xs<WK, mf, c, wm, wn, kt, 2, VEC, A1>), grid, block, 0, s, a); \
+        else {                                                                            \
+            /* unaligned operands take per-element loads: 128-deep chunks of */           \
+            /* them spilled, so those tiles stage 64-deep chunks (same chains) */         \
+            constexpr int kts = (!VEC && kt == 128) ? 64 : kt;                            \
+            hipLaunchKernelGGL((chain_gemm_xs<WK, mf, c, wm, wn, kts, 2, VEC, A1>), grid, block, 0, s, a); \
+        }                                                                                 \
         break;
     switch (cfg) {
         PK_CONFIGS(PK_CFG_CASE)
