@@ -548,9 +548,11 @@ size_t pk_gpu_presplit_bytes(void);
 int pk_gpu_uses_panel(int M, int N, int K, int bits, const void *dB, int ldb,
                       const float *dscales);
 /* Segments of K over workgroups that a panel GEMM of this shape takes with
- * this thread's workspace (pk_gpu_set_workspace): above one, each workgroup
- * stores its partial tile there and a second launch sums them in segment
- * order before alpha, beta, bias and the epilogue (deterministic). */
+ * this thread's workspace (pk_gpu_set_workspace): one per LDS phase when K
+ * takes at least 4 phases (fewer phases run one after the other in one
+ * launch).  Above one, each workgroup stores its partial tile there and a
+ * second launch sums them in segment order before alpha, beta, bias and the
+ * epilogue (deterministic). */
 int pk_gpu_panel_segments(int M, int N, int K);
 /* Test hook: the weights as the panel kernels multiply them, to dout [K][N]
  * on `stream`: int8 fl(q * B_scale), int4 fl(q * s[k][n/32]), fp32 hi + lo. */

@@ -609,14 +609,22 @@ bool rows_fit(const GemmProblem& p, int rows)
     return !p.ln_gamma || p.K <= kph;
 }
 
-// K segments for a workgroup of `rows` rows: one per LDS phase when the
-// caller gave a workspace big enough for the partial tiles (and there is no
-// fused input LayerNorm), else one.
+// K segments for a workgroup of `rows` rows: one per LDS phase when K takes
+// at least kMinSegs phases and the caller gave a workspace big enough for the
+// partial tiles (and there is no fused input LayerNorm), else one.  With 2
+// or 3 phases the phases run one after the other in one launch instead:
+// measured on MI355X (graph replay, both launches of the split form), i4
+// 33x1024x3072 8.1 against 9.2 us, i8 64x1024x2048 5.9 against 7.4, i4
+// 64x4096x2048 11.4 against 16.4, f32 33x1024x2048 7.0 against 8.9; from 4
+// phases the split wins (i4 33x1024x4096 9.55 against 10.06, i4
+// 16x1024x4096 7.6 against 10.8).
+constexpr int kMinSegs = 4;
 int segments_for(const GemmProblem& p, int rows)
 {
     const int kph = phase_k(rows, lds_extra(p));
     if (!p.work || p.ln_gamma || p.K <= kph) return 1;
     const int segs = (p.K + kph - 1) / kph;
+    if (segs < kMinSegs) return 1;
     if (segs > kMaxSegs || (size_t)segs * p.M * p.N * 4 > p.work_bytes) return 1;
     return segs;
 }
