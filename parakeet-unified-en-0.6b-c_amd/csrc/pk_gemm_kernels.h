@@ -64,12 +64,23 @@ struct GemmProblem {
     // LayerNorm kernel's arithmetic, bit for bit; K <= 1024).
     const float* ln_gamma = nullptr;
     const float* ln_beta = nullptr;
-    // Panel kernels with K split over workgroups only (panel_fuses_out_ln):
-    // after the output step, each output row is replaced by its LayerNorm
-    // with these gamma, beta [N].
+    // Panel kernels with K split over workgroups (panel_fuses_out_ln), or
+    // split kernels with K split over workgroups (split_fuses_ln): after the
+    // output step, each output row is replaced by its LayerNorm with these
+    // gamma, beta [N].
     const float* out_ln_gamma = nullptr;
     const float* out_ln_beta = nullptr;
+    // Split kernels with K split over workgroups only (split_fuses_ln): the
+    // LayerNorm with these gamma, beta [N] of the rows C ends with (after
+    // out_ln_gamma's, if given) is written to next_ln_out [M][N], pre-split
+    // as a_presplit describes, for a split GEMM that reads it next.
+    const float* next_ln_gamma = nullptr;
+    const float* next_ln_beta = nullptr;
+    float* next_ln_out = nullptr;
 };
+
+// The row width (N) of a split GEMM whose reduce forms LayerNorms.
+constexpr int kSplitLnN = 1024;
 
 // Scales an int4 GEMM reads: the reference takes scale k * (N/32) + n/32 for
 // weight (k, n) with N/32 floored (blas.c:794, 958), so when N % 32 != 0 the
@@ -174,6 +185,12 @@ size_t split_weight_bytes(WeightKind kind, int K, int N);
 // Write that copy of B [K][ldb] (int4: and its scales [K][N/32]) to `out`.
 hipError_t launch_split_pack(WeightKind kind, int K, int N, const void* B, int ldb, const float* scales,
                              void* out, hipStream_t stream);
+// Whether the split kernels form the LayerNorms a problem asks for
+// (p.out_ln_gamma, p.next_ln_gamma) in its split-K reduce: split_supports(p),
+// N = kSplitLnN, K split over workgroups with p.work, 16-byte aligned C
+// rows, bias, gammas, betas and next_ln_out, and no input LayerNorm.  The
+// results are the same bits as the GEMM followed by the LayerNorm kernels.
+bool split_fuses_ln(const GemmProblem& p);
 // Segments of K over workgroups that launch_split takes for a shape given
 // work_bytes of workspace (1: K is not split over workgroups).
 int split_k_segments(WeightKind kind, int M, int N, int K, size_t work_bytes);

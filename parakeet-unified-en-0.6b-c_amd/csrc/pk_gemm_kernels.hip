@@ -137,7 +137,8 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
 
     const bool fused = p.bias != nullptr || p.epi != EPI_NONE;
     const bool early = (p.alpha == 0.0f) || (p.kind == W_I8 && p.scale == 0.0f) || p.K <= 0;
-    if (p.out_ln_gamma && early) return hipErrorInvalidValue;   // the output LayerNorm rides on the panel reduce
+    // the output LayerNorms ride on the panel or split-K reduce
+    if ((p.out_ln_gamma || p.next_ln_gamma) && early) return hipErrorInvalidValue;
     if (early) {   // blas.c:764-765, 955-956, 1063-1064: only the beta step runs
         if (p.beta == 1.0f && !fused) return hipSuccess;
         const long long n = (long long)p.M * p.N;
@@ -145,10 +146,13 @@ hipError_t launch_gemm(const GemmProblem& p, hipStream_t stream, int cfg_index, 
         return hipGetLastError();
     }
 
-    if (p.ln_gamma || p.out_ln_gamma) {
-        // fused LayerNorms: only the panel kernels apply them
-        if (tol == TOL_NONE || cfg_index >= 0 || !panel_supports(p)) return hipErrorInvalidValue;
-        return launch_panel(p, stream);
+    if (p.ln_gamma || p.out_ln_gamma || p.next_ln_gamma) {
+        // fused LayerNorms: the panel kernels apply input and output ones,
+        // the split kernels' reduce output ones and the next GEMM's input
+        if (tol == TOL_NONE || cfg_index >= 0) return hipErrorInvalidValue;
+        if (!p.next_ln_gamma && panel_supports(p)) return launch_panel(p, stream);
+        if (tol == TOL_ALL && split_fuses_ln(p)) return launch_split(p, stream);
+        return hipErrorInvalidValue;
     }
     if (p.a_presplit) {
         // A comes pre-split: only the split kernels read it

@@ -142,8 +142,10 @@ struct pk_gpu_encoder {
     // fast numerics: LayerNorms feeding a GEMM write pre-split output
     // (PK_GPU_PRESPLIT=0 at creation turns it off; the results are the same)
     bool presplit = true;
-    // small row groups on the panel kernels: LayerNorms fused into the GEMMs
-    // (PK_GPU_FUSE_LN=0 at creation turns it off; the results are the same)
+    // small row groups on the panel kernels: LayerNorms fused into the GEMMs;
+    // fast numerics in larger row groups: LayerNorms formed by the split-K
+    // reduces that finish their rows
+    // (PK_GPU_FUSE_LN=0 at creation turns both off; the results are the same)
     bool fuse_ln = true;
     // fast numerics: the int4 and fp32 block weights' pre-split copies
     // (PK_GPU_PRESPLIT_W=0 at creation turns them off; the results are the same)
@@ -353,6 +355,9 @@ int workspace(pk_gpu_encoder* e, size_t rows, size_t n_chunks, size_t scores_n, 
 // its input rows, `out` its output rows after the epilogue.
 struct FusedLn {
     const float *in_g = nullptr, *in_b = nullptr, *out_g = nullptr, *out_b = nullptr;
+    // the split-K reduce's LayerNorm of its rows into next_out, pre-split
+    const float *next_g = nullptr, *next_b = nullptr;
+    float* next_out = nullptr;
 };
 
 // The GEMM problem of a block weight; presplit: A holds a split-output
@@ -389,6 +394,9 @@ GemmProblem block_problem(const DevWeight& w, const float* A, int M, float* C, c
     p.ln_beta = ln.in_b;
     p.out_ln_gamma = ln.out_g;
     p.out_ln_beta = ln.out_b;
+    p.next_ln_gamma = ln.next_g;
+    p.next_ln_beta = ln.next_b;
+    p.next_ln_out = ln.next_out;
     return p;
 }
 
@@ -526,6 +534,7 @@ int gemm(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C,
     if (epi == pkgpu::EPI_HALF_RESIDUAL || epi == pkgpu::EPI_RESIDUAL) bytes += 4.0 * M * w.N;
     if (ln.in_g) bytes += 8.0 * w.K;
     if (ln.out_g) bytes += 8.0 * w.N;
+    if (ln.next_g) bytes += 8.0 * w.N + 4.0 * M * w.N;
     const pkgpu::Tolerance tol = exact ? pkgpu::TOL_NONE : pkgpu::rt::tolerance_of(e->numerics);
     return timed(e, stage_of(w), flops, bytes, s,
                  [&] {
@@ -544,6 +553,16 @@ bool fusable(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float
     const GemmProblem p = block_problem(w, A, M, C, bias, epi, pkgpu::rt::tolerance_of(e->numerics), work,
                                         false, ln);
     return ln.out_g ? pkgpu::panel_fuses_out_ln(p) : pkgpu::panel_supports(p);
+}
+
+// Whether the split kernels form these LayerNorms (ln.out_g, ln.next_g)
+// in this block GEMM's split-K reduce (fused LayerNorms on, fast numerics,
+// no forced tile).
+bool split_fusable(pk_gpu_encoder* e, const DevWeight& w, const float* A, int M, float* C, const float* bias,
+                   Epilogue epi, float* work, const FusedLn& ln)
+{
+    if (!e->fuse_ln || e->numerics != PK_GPU_NUMERICS_FAST || pkgpu::rt::forced_config() >= 0) return false;
+    return pkgpu::split_fuses_ln(block_problem(w, A, M, C, bias, epi, pkgpu::TOL_ALL, work, false, ln));
 }
 
 // split: the output pre-split for the split GEMM kernels, for a GEMM that
@@ -594,25 +613,59 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         f.in_b = be;
         return fusable(e, w, x, R, C, bias, epi, g.part, f) ? f : FusedLn();
     };
-    // the normalised input of a GEMM: fused into it, or a LayerNorm launch into `ln`
-    auto norm_in = [&](const FusedLn& f, const float* gm, const float* be, const float** A) {
-        *A = f.in_g ? x : ln;
-        return f.in_g ? PK_GPU_OK : layer_norm(e, x, gm, be, ln, R, s, ps);
+    // The LayerNorms that a GEMM writing x forms in its split-K reduce:
+    // `want` if the split kernels take them (pre-split row groups), else its
+    // output LayerNorm alone if the panel kernels take that, else none.  Each
+    // consumer asks the same question of its producer, so both agree.
+    auto reduce_ln = [&](const DevBlock& bb, const DevWeight& w, const float* A, const float* bias,
+                         Epilogue epi, const DevBlock* next_block) {
+        FusedLn want;
+        if (&w == &bb.ff1_w2) {              // x after feed-forward 1: self-attention's input
+            want.next_g = bb.ln_sa_w;
+            want.next_b = bb.ln_sa_b;
+        } else if (&w == &bb.pw2t) {         // after the convolution: feed-forward 2's input
+            want.next_g = bb.ln_ff2_w;
+            want.next_b = bb.ln_ff2_b;
+        } else {                             // the block's output, and the next block's input
+            want.out_g = bb.ln_out_w;
+            want.out_b = bb.ln_out_b;
+            if (next_block) {
+                want.next_g = next_block->ln_ff1_w;
+                want.next_b = next_block->ln_ff1_b;
+            }
+        }
+        if (want.next_g) want.next_out = ln;
+        if (ps && split_fusable(e, w, A, R, x, bias, epi, g.part, want)) return want;
+        FusedLn o;
+        o.out_g = want.out_g;
+        o.out_b = want.out_b;
+        if (o.out_g && fusable(e, w, A, R, x, bias, epi, g.part, o)) return o;
+        return FusedLn();
     };
-    // out_ln: fuse the block's output LayerNorm into the down projection (sets *fused)
+    const size_t bi = (size_t)(&b - e->blocks.data());
+    const DevBlock* next = bi + 1 < e->blocks.size() ? &e->blocks[bi + 1] : nullptr;
+    const FusedLn ff1_o = reduce_ln(b, b.ff1_w2, h, b.ff1_b2, pkgpu::EPI_HALF_RESIDUAL, nullptr);
+    const FusedLn pw2_o = reduce_ln(b, b.pw2t, ln, b.pw2_b, pkgpu::EPI_RESIDUAL, nullptr);
+    const FusedLn ff2_o = reduce_ln(b, b.ff2_w2, h, b.ff2_b2, pkgpu::EPI_HALF_RESIDUAL, next);
+    // whether the previous block's last reduce wrote this block's first input
+    bool ff1_ready = false;
+    if (bi > 0) {
+        const DevBlock& pb = e->blocks[bi - 1];
+        ff1_ready = reduce_ln(pb, pb.ff2_w2, h, pb.ff2_b2, pkgpu::EPI_HALF_RESIDUAL, &b).next_g != nullptr;
+    }
+    // the normalised input of a GEMM: fused into it, already in `ln` (ready:
+    // the reduce before wrote it), or a LayerNorm launch into `ln`
+    auto norm_in = [&](const FusedLn& f, const float* gm, const float* be, const float** A, bool ready) {
+        *A = f.in_g ? x : ln;
+        return f.in_g || ready ? PK_GPU_OK : layer_norm(e, x, gm, be, ln, R, s, ps);
+    };
+    // o: the LayerNorms the down projection's reduce forms
     auto ffn = [&](const float* gm, const float* be, const DevWeight& w1, const float* b1,
-                   const DevWeight& w2, const float* b2, bool out_ln, bool* fused) {
+                   const DevWeight& w2, const float* b2, bool ready, const FusedLn& o) {
         const FusedLn f = fused_in(w1, gm, be, h, b1, pkgpu::EPI_SWISH);
         const float* A = nullptr;
-        int r = norm_in(f, gm, be, &A);
+        int r = norm_in(f, gm, be, &A, ready);
         if (!r) r = gemm(e, w1, A, R, h, b1, pkgpu::EPI_SWISH, s, g.part, ps && !f.in_g, false, f);   // encoder.c:193-196
-        FusedLn o;
-        if (out_ln) {
-            o.out_g = b.ln_out_w;
-            o.out_b = b.ln_out_b;
-            if (!fusable(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, g.part, o)) o = FusedLn();
-        }
-        if (fused) *fused = o.out_g != nullptr;
         if (!r) r = gemm(e, w2, h, R, x, b2, pkgpu::EPI_HALF_RESIDUAL, s, g.part, false, false, o);   // encoder.c:198-216
         return r;
     };
@@ -620,7 +673,7 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     auto self_attention = [&]() {
         const FusedLn f = fused_in(b.qkv, b.ln_sa_w, b.ln_sa_b, h, b.qkv_b, pkgpu::EPI_NONE);
         const float* A = nullptr;
-        int rc = norm_in(f, b.ln_sa_w, b.ln_sa_b, &A);
+        int rc = norm_in(f, b.ln_sa_w, b.ln_sa_b, &A, ff1_o.next_g != nullptr);
         if (!rc) rc = gemm(e, b.qkv, A, R, h, b.qkv_b, pkgpu::EPI_NONE, s, g.part, ps && !f.in_g, false, f);
         if (rc) return rc;
         // every chunk of the group in one launch, each with its own length
@@ -649,7 +702,7 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     auto convolution = [&]() {
         const FusedLn f = fused_in(b.pw1t, b.ln_conv_w, b.ln_conv_b, h, b.pw1_b, pkgpu::EPI_NONE);
         const float* A = nullptr;
-        int rc = norm_in(f, b.ln_conv_w, b.ln_conv_b, &A);
+        int rc = norm_in(f, b.ln_conv_w, b.ln_conv_b, &A, false);
         if (!rc) rc = gemm(e, b.pw1t, A, R, h, b.pw1_b, pkgpu::EPI_NONE, s, g.part, ps && !f.in_g, false, f);
         // Small row groups (fused LayerNorms on) take the GLU inside the
         // depthwise convolution: each input value is gated where it is read
@@ -673,23 +726,22 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 8.0 * R * kD, s, [&] {
             return check(pkgpu::launch_depthwise(d, g.n, s), "depthwise conv");
         });
-        if (!rc) rc = gemm(e, b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s, g.part);
+        if (!rc) rc = gemm(e, b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s, g.part, false, false, pw2_o);
         return rc;
     };
     for (int m = from; m < to; ++m) {
         int rc = PK_GPU_OK;
         switch (m) {
         case 0:     // feed-forward 1 (encoder.c:483)
-            rc = ffn(b.ln_ff1_w, b.ln_ff1_b, b.ff1_w1, b.ff1_b1, b.ff1_w2, b.ff1_b2, false, nullptr);
+            rc = ffn(b.ln_ff1_w, b.ln_ff1_b, b.ff1_w1, b.ff1_b1, b.ff1_w2, b.ff1_b2, ff1_ready, ff1_o);
             break;
         case 1: rc = self_attention(); break;
         case 2: rc = convolution(); break;
-        default: {  // feed-forward 2 and the block's output LayerNorm (encoder.c:486-487)
-            bool out_fused = false;
-            rc = ffn(b.ln_ff2_w, b.ln_ff2_b, b.ff2_w1, b.ff2_b1, b.ff2_w2, b.ff2_b2, true, &out_fused);
-            if (!rc && !out_fused) rc = layer_norm(e, x, b.ln_out_w, b.ln_out_b, x, R, s);
+        default:    // feed-forward 2 and the block's output LayerNorm (encoder.c:486-487)
+            rc = ffn(b.ln_ff2_w, b.ln_ff2_b, b.ff2_w1, b.ff2_b1, b.ff2_w2, b.ff2_b2, pw2_o.next_g != nullptr,
+                     ff2_o);
+            if (!rc && !ff2_o.out_g) rc = layer_norm(e, x, b.ln_out_w, b.ln_out_b, x, R, s);
             break;
-        }
         }
         if (rc) return rc;
     }

@@ -90,6 +90,18 @@ struct SpArgs {
     int n_seg, n_tiles;
     float* work;
     int c_vec4;                   // C rows and the bias allow 16-byte accesses (split_reduce)
+    // > 0: the partial tiles go to work row-major instead, [n_seg][work_rows][N]
+    // (work_rows: the row tiles' rows), for split_reduce_ln
+    int work_rows;
+};
+
+// LayerNorms formed by split_reduce_ln on the finished rows: out_g, out_b
+// replace C's rows by their LayerNorm (or null); next_g, next_b write the
+// LayerNorm of the rows C ends with to next_out, pre-split (or null).
+struct SpLn {
+    const float *out_g, *out_b;
+    const float *next_g, *next_b;
+    float* next_out;
 };
 
 __device__ inline __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes)
@@ -428,6 +440,22 @@ __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) v
     L::multiply(smem + ((nc - 1) & 1) * L::BUF, acc, lane, 64 * wm, 64 * wn);
 
     if constexpr (SK) {
+        if (p.work_rows) {
+            // row-major partials: row m of segment seg at (seg work_rows + m) N
+            float* w = p.work + (size_t)seg * p.work_rows * p.N;
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const int n = n0 + 64 * wn + 32 * c + (lane & 31);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int m = m0 + 64 * wm + 32 * r + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                        w[(size_t)m * p.N + n] = acc[r][c][e];
+                    }
+                }
+            return;
+        }
         // slot (seg, t): wave-major, then block, register, lane (each store
         // instruction writes 256 contiguous bytes)
         float* w = p.work + ((size_t)seg * p.n_tiles + t) * (WM * WN * 4096) + (size_t)wave * 4096;
@@ -454,6 +482,34 @@ __global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) v
                 if (m < p.M) put(p, m, n, acc[r][c][e]);
             }
         }
+}
+
+// Whether the output step reads C (beta or a residual epilogue).
+__device__ inline bool reads_c(const SpArgs& p)
+{
+    return p.beta != 0.0f || p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL;
+}
+
+// put's steps for four outputs of one row: alpha, beta with C's values c4,
+// the bias values b4, the epilogue.
+__device__ inline float4 finish4(const SpArgs& p, float4 sum, float4 c4, float4 b4)
+{
+    float v[4] = {__fmul_rn(p.alpha, sum.x), __fmul_rn(p.alpha, sum.y), __fmul_rn(p.alpha, sum.z),
+                  __fmul_rn(p.alpha, sum.w)};
+    const float c[4] = {c4.x, c4.y, c4.z, c4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (p.beta != 0.0f) v[i] = __fadd_rn(p.beta == 1.0f ? c[i] : __fmul_rn(p.beta, c[i]), v[i]);
+        if (p.bias) v[i] = __fadd_rn(v[i], b[i]);
+        switch (p.epi) {
+        case EPI_SWISH:         v[i] = swish_f(v[i]); break;
+        case EPI_HALF_RESIDUAL: v[i] = __fmaf_rn(v[i], 0.5f, c[i]); break;
+        case EPI_RESIDUAL:      v[i] = __fadd_rn(c[i], v[i]); break;
+        case EPI_RELU:          v[i] = v[i] > 0.0f ? v[i] : 0.0f; break;
+        default:                break;
+        }
+    }
+    return make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // The second launch of a split-K GEMM: output i of tile t is the sum of
@@ -484,38 +540,156 @@ __global__ __launch_bounds__(256) void split_reduce(SpArgs p)
     if (p.c_vec4) {
         // the same steps as put, on 16-byte accesses of C and the bias
         float4* cp = reinterpret_cast<float4*>(p.C + (size_t)m * p.ldc + n);
-        float v[4] = {__fmul_rn(p.alpha, sum.x), __fmul_rn(p.alpha, sum.y), __fmul_rn(p.alpha, sum.z),
-                      __fmul_rn(p.alpha, sum.w)};
-        const bool reads_c = p.beta != 0.0f || p.epi == EPI_HALF_RESIDUAL || p.epi == EPI_RESIDUAL;
-        float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (reads_c) {
-            const float4 c4 = *cp;
-            c[0] = c4.x; c[1] = c4.y; c[2] = c4.z; c[3] = c4.w;
-        }
-        float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (p.bias) {
-            const float4 b4 = *reinterpret_cast<const float4*>(p.bias + n);
-            b[0] = b4.x; b[1] = b4.y; b[2] = b4.z; b[3] = b4.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (p.beta != 0.0f) v[i] = __fadd_rn(p.beta == 1.0f ? c[i] : __fmul_rn(p.beta, c[i]), v[i]);
-            if (p.bias) v[i] = __fadd_rn(v[i], b[i]);
-            switch (p.epi) {
-            case EPI_SWISH:         v[i] = swish_f(v[i]); break;
-            case EPI_HALF_RESIDUAL: v[i] = __fmaf_rn(v[i], 0.5f, c[i]); break;
-            case EPI_RESIDUAL:      v[i] = __fadd_rn(c[i], v[i]); break;
-            case EPI_RELU:          v[i] = v[i] > 0.0f ? v[i] : 0.0f; break;
-            default:                break;
-            }
-        }
-        *cp = make_float4(v[0], v[1], v[2], v[3]);
+        const float4 c4 = reads_c(p) ? *cp : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 b4 = p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *cp = finish4(p, sum, c4, b4);
         return;
     }
     put(p, m, n, sum.x);
     put(p, m, n + 1, sum.y);
     put(p, m, n + 2, sum.z);
     put(p, m, n + 3, sum.w);
+}
+
+// fl(fl(fl(v - mean) * inv) * g + b) per element: the LayerNorm kernels'
+// output step.
+__device__ inline float4 ln4(float4 v, float mean, float inv, float4 g, float4 b)
+{
+    return make_float4(__fmaf_rn(__fmul_rn(__fsub_rn(v.x, mean), inv), g.x, b.x),
+                       __fmaf_rn(__fmul_rn(__fsub_rn(v.y, mean), inv), g.y, b.y),
+                       __fmaf_rn(__fmul_rn(__fsub_rn(v.z, mean), inv), g.z, b.z),
+                       __fmaf_rn(__fmul_rn(__fsub_rn(v.w, mean), inv), g.w, b.w));
+}
+
+// The statistics of the workgroup's RPW rows in buf (pitch LD) into st:
+// 8 lanes per row (lanes 0-15 of the first RPW / 2 waves), with the
+// LayerNorm kernels' chains (ln_row_stats_rolled).  Between two barriers.
+template <int RPW, int D, int LD>
+__device__ inline void rows_stats(const float* buf, float (*st)[2], int w, int lane)
+{
+    __syncthreads();
+    if (lane < 16 && w < RPW / 2) {
+        const int r = 2 * w + (lane >> 3), l = lane & 7;
+        float mean, inv;
+        ln_row_stats_rolled<32>(buf + r * LD, D, l, mean, inv);
+        if (l == 0) {
+            st[r][0] = mean;
+            st[r][1] = inv;
+        }
+    }
+    __syncthreads();
+}
+
+// Rows per workgroup of split_reduce_ln: 414 workgroups at 1656 rows, 64 KB
+// of partials each in flight.  Two rows per workgroup measured 1.8% slower
+// on the fast encoder pass (A/B on one box, two runs each).
+constexpr int kReduceLnRows = 4;
+
+// The second launch of a split-K GEMM whose 1024-wide output rows feed
+// LayerNorms: a workgroup of 4 waves finishes RPW whole rows, thread t the
+// columns 4 t .. 4 t + 3 of each.  Each output is its partials summed in
+// segment order and put's steps, as split_reduce forms it.  Then, per
+// SpLn: the rows' LayerNorm replaces them in C (out_g), and/or the
+// LayerNorm of what C holds is written pre-split to next_out (next_g), in
+// the layout and with the arithmetic of layer_norm_split_rows: the same
+// bits as split_reduce followed by the LayerNorm kernels, in one launch
+// that reads the rows from memory once.
+// The partials are row-major (SpArgs::work_rows), so a row of a segment is
+// 4 KB in one piece.  The loads of 4 segments are issued at once
+// (segments past the last repeat it and are not added): RPW x 4 16-byte
+// loads per thread in flight.
+template <int RPW>
+__global__ __launch_bounds__(256) void split_reduce_ln(SpArgs p, SpLn q)
+{
+    constexpr int D = 1024, LD = D + 8;
+    static_assert(RPW % 2 == 0 && RPW <= 8, "2 rows per wave's statistics lanes");
+    __shared__ float buf[RPW * LD];
+    __shared__ float st[RPW][2];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int row0 = blockIdx.x * RPW, nr = min(RPW, p.M - row0);
+    const int n = 4 * tid;
+    const size_t seg_stride = (size_t)p.work_rows * D;
+    // rows past M repeat the workgroup's first row (computed, never stored)
+    const float* wk[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) wk[r] = p.work + (size_t)(row0 + (r < nr ? r : 0)) * D + n;
+    // C's rows and the bias first, so that they are in flight with the
+    // partials (C is read whatever the epilogue: rows < M, in bounds)
+    float4 c4[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+        c4[r] = *reinterpret_cast<const float4*>(p.C + (size_t)(row0 + (r < nr ? r : 0)) * p.ldc + n);
+    const float4 b4 = p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int last = p.n_seg - 1;
+    float4 sum[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) sum[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = 0; s0 <= last; s0 += 4) {
+        float4 v[4][RPW];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+                v[j][r] = *reinterpret_cast<const float4*>(wk[r] + min(s0 + j, last) * seg_stride);
+        // every addition is made and the ones past the last segment are
+        // dropped by a select, so no load sits inside a branch (where the
+        // compiler would issue it after the previous segment's wait); the
+        // first segment is taken as it is (fl(0 + x) would turn -0 to +0)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool first = s0 + j == 0, live = s0 + j <= last;
+            // (per component: a select of whole float4 values went to scratch)
+            auto acc = [&](float s, float x) { return live ? (first ? x : __fadd_rn(s, x)) : s; };
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                sum[r].x = acc(sum[r].x, v[j][r].x);
+                sum[r].y = acc(sum[r].y, v[j][r].y);
+                sum[r].z = acc(sum[r].z, v[j][r].z);
+                sum[r].w = acc(sum[r].w, v[j][r].w);
+            }
+        }
+    }
+    const bool rc = reads_c(p);
+    float4 v[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+        v[r] = finish4(p, sum[r], rc ? c4[r] : make_float4(0.0f, 0.0f, 0.0f, 0.0f), b4);
+
+    if (q.out_g) {
+        const float4 g = *reinterpret_cast<const float4*>(q.out_g + n);
+        const float4 b = *reinterpret_cast<const float4*>(q.out_b + n);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) *reinterpret_cast<float4*>(buf + r * LD + n) = v[r];
+        rows_stats<RPW, D, LD>(buf, st, w, lane);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) v[r] = ln4(v[r], st[r][0], st[r][1], g, b);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+        if (r < nr) *reinterpret_cast<float4*>(p.C + (size_t)(row0 + r) * p.ldc + n) = v[r];
+    if (!q.next_g) return;
+
+    const float4 g = *reinterpret_cast<const float4*>(q.next_g + n);
+    const float4 b = *reinterpret_cast<const float4*>(q.next_b + n);
+    // buf's last reads (the statistics above) are behind the barrier that
+    // ended them, and so are st's (the outputs above)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) *reinterpret_cast<float4*>(buf + r * LD + n) = v[r];
+    rows_stats<RPW, D, LD>(buf, st, w, lane);
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        if (r < nr) {
+            const float4 o = ln4(v[r], st[r][0], st[r][1], g, b);
+            uint32_t h0, l0, h1, l1;
+            split_bf16x2(o.x, o.y, h0, l0);
+            split_bf16x2(o.z, o.w, h1, l1);
+            // columns 4 t .. +3: half (t & 1) of the 8-column group t / 2,
+            // whose 8 hi then 8 lo bf16 values fill the group's 8 floats
+            unsigned short* g8 = reinterpret_cast<unsigned short*>(q.next_out + (size_t)(row0 + r) * D + 8 * (tid >> 1));
+            *reinterpret_cast<uint2*>(g8 + 4 * (tid & 1)) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(g8 + 8 + 4 * (tid & 1)) = make_uint2(l0, l1);
+        }
+    }
 }
 
 // Workgroups of KS waves own 64 x 64 tiles, wave w the chunks
@@ -704,8 +878,9 @@ unsigned padded_grid(SpArgs& a, int bm, int bn, int n_seg = 1)
     return (unsigned)(((a.tiles + kXcd - 1) / kXcd) * kXcd);
 }
 
+// ln: LayerNorms for the reduce to form (K split over workgroups only), or null.
 template <int WK, bool AS>
-hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
+hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st, const SpLn* ln)
 {
     // Chunks of loads in flight, as many as fit two waves per SIMD without
     // spills: a lane holds 16 A bytes per 64 rows of the tile and chunk, plus
@@ -715,12 +890,20 @@ hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
     if (plan.n_seg > 1) {
         const bool wide = plan.shape == SP_4x2;
         const unsigned grid = padded_grid(a, wide ? 256 : 128, 128, plan.n_seg);
+        // the fused reduce reads whole rows: partials row-major (the same
+        // bytes as the tiles: N is a whole number of column tiles)
+        if (ln) a.work_rows = (a.n_tiles / a.tiles_n) * (wide ? 256 : 128);
         if (wide)
             hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, true, AS>), dim3(grid), dim3(512), 0, st, a);
         else
             hipLaunchKernelGGL((split_gemm<WK, 2, 2, PD22, true, AS>), dim3(grid), dim3(256), 0, st, a);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        if (ln) {
+            hipLaunchKernelGGL((split_reduce_ln<kReduceLnRows>), dim3((unsigned)((a.M + kReduceLnRows - 1) / kReduceLnRows)),
+                               dim3(256), 0, st, a, *ln);
+            return hipGetLastError();
+        }
         const unsigned blocks = (unsigned)a.n_tiles * (wide ? 8 * 4096 / 1024 : 4 * 4096 / 1024);
         if (wide)
             hipLaunchKernelGGL((split_reduce<4, 2>), dim3(blocks), dim3(256), 0, st, a);
@@ -728,6 +911,7 @@ hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st)
             hipLaunchKernelGGL((split_reduce<2, 2>), dim3(blocks), dim3(256), 0, st, a);
         return hipGetLastError();
     }
+    if (ln) return hipErrorNotSupported;
     switch (plan.shape) {
     case SP_4x2:
         hipLaunchKernelGGL((split_gemm<WK, 4, 2, PD42, false, AS>), dim3(padded_grid(a, 256, 128)), dim3(512), 0, st, a);
@@ -794,25 +978,45 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     a.work = p.work;
     a.c_vec4 = p.ldc % 4 == 0 && reinterpret_cast<uintptr_t>(p.C) % 16 == 0 &&
                reinterpret_cast<uintptr_t>(p.bias) % 16 == 0;
+    SpLn lnv{p.out_ln_gamma, p.out_ln_beta, p.next_ln_gamma, p.next_ln_beta, p.next_ln_out};
+    const bool fuse = p.out_ln_gamma || p.next_ln_gamma;
+    if (fuse && (!split_fuses_ln(p) || plan.n_seg < 2)) return hipErrorNotSupported;
+    const SpLn* ln = fuse ? &lnv : nullptr;
     if (p.b_presplit && p.kind != W_I8) {
         // the weight's pre-split copy (split_pack), K N 4 bytes
         if ((size_t)p.K * p.N * 4 >= lim || reinterpret_cast<uintptr_t>(p.b_presplit) % 16) return hipErrorNotSupported;
         a.B = p.b_presplit;
         a.b_bytes = (uint32_t)((size_t)p.K * p.N * 4);
-        return p.a_presplit ? launch_kind<W_BS, true>(a, plan, st) : launch_kind<W_BS, false>(a, plan, st);
+        return p.a_presplit ? launch_kind<W_BS, true>(a, plan, st, ln) : launch_kind<W_BS, false>(a, plan, st, ln);
     }
     if (p.a_presplit) {
         switch (p.kind) {
-        case W_I8: return launch_kind<W_I8, true>(a, plan, st);
-        case W_I4: return launch_kind<W_I4, true>(a, plan, st);
-        default:   return launch_kind<W_F32, true>(a, plan, st);
+        case W_I8: return launch_kind<W_I8, true>(a, plan, st, ln);
+        case W_I4: return launch_kind<W_I4, true>(a, plan, st, ln);
+        default:   return launch_kind<W_F32, true>(a, plan, st, ln);
         }
     }
     switch (p.kind) {
-    case W_I8: return launch_kind<W_I8, false>(a, plan, st);
-    case W_I4: return launch_kind<W_I4, false>(a, plan, st);
-    default:   return launch_kind<W_F32, false>(a, plan, st);
+    case W_I8: return launch_kind<W_I8, false>(a, plan, st, ln);
+    case W_I4: return launch_kind<W_I4, false>(a, plan, st, ln);
+    default:   return launch_kind<W_F32, false>(a, plan, st, ln);
     }
+}
+
+bool split_fuses_ln(const GemmProblem& p)
+{
+    if (!p.out_ln_gamma && !p.next_ln_gamma) return false;
+    if (!split_supports(p) || p.ln_gamma || p.N != kSplitLnN || !p.work || p.work_bytes < kSplitWorkBytes)
+        return false;
+    // put's 16-byte path (split_reduce's c_vec4)
+    auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+    if (p.ldc % 4 || !a16(p.C) || !a16(p.bias)) return false;
+    if (p.out_ln_gamma && (!p.out_ln_beta || !a16(p.out_ln_gamma) || !a16(p.out_ln_beta))) return false;
+    if (p.next_ln_gamma && (!p.next_ln_beta || !p.next_ln_out || !a16(p.next_ln_gamma) ||
+                            !a16(p.next_ln_beta) || !a16(p.next_ln_out)))
+        return false;
+    if (!p.next_ln_gamma && p.next_ln_out) return false;
+    return split_plan(p.kind, p.M, p.N, p.K, p.work_bytes).n_seg > 1;
 }
 
 size_t split_weight_bytes(WeightKind kind, int K, int N)

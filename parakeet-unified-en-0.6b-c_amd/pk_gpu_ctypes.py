@@ -88,6 +88,8 @@ _PROTOS = {
 
 EPI_NONE, EPI_SWISH, EPI_HALF_RESIDUAL, EPI_RESIDUAL = 0, 1, 2, 3
 NUMERICS_DEFAULT, NUMERICS_EXACT, NUMERICS_FAST = 0, 1, 2
+# PK_GPU_STAGE_*: pk_gpu_encoder_profile_read's stages
+STAGE_GEMM_I4, STAGE_GEMM_I8, STAGE_GEMM_F32, STAGE_ATTENTION, STAGE_LAYER_NORM, STAGE_CONV, STAGE_COPY = range(7)
 NOALLOC_BYTES = 64 << 20          # PK_GPU_NOALLOC_BYTES
 SPLIT_WORKSPACE_BYTES = 32 << 20  # PK_GPU_SPLIT_WORKSPACE_BYTES
 

@@ -266,3 +266,52 @@ def test_fast_mode_presplit_weights_are_bit_identical(model, monkeypatch):
     plain = run(model, x, chunk, pk.NUMERICS_FAST, overlap=ov)
     for a, b in zip(pre, plain):
         assert bits_equal(a, b), describe_mismatch(a, b)
+
+
+def layer_norm_launches(m, x, chunk, mode):
+    """LayerNorm launches of one profiled run (eager, the replay's kernels)."""
+    import torch
+    enc = ctypes.c_void_p()
+    pk.call("pk_gpu_encoder_create", ctypes.byref(enc), ctypes.cast(m.blocks, ctypes.c_void_p),
+            bench.N_BLOCKS, m.pe.ctypes.data, m.pe.shape[0], bench.PE_CENTER)
+    try:
+        pk.call("pk_gpu_encoder_set_numerics", enc, mode)
+        dev = torch.device("cuda:0")
+        dx = torch.from_numpy(x).to(dev)
+        dout = torch.empty_like(dx)
+        pk.call("pk_gpu_encoder_profile", enc, 1)
+        pk.call("pk_gpu_encoder_run_dev", enc, dx.data_ptr(), x.shape[0], chunk, 8, dout.data_ptr(),
+                torch.cuda.current_stream(dev).cuda_stream)
+        n = ctypes.c_longlong()
+        pk.call("pk_gpu_encoder_profile_read", enc, pk.STAGE_LAYER_NORM, None, ctypes.byref(n), None, None)
+        pk.call("pk_gpu_encoder_profile", enc, 0)
+        return n.value
+    finally:
+        pk.load().pk_gpu_encoder_destroy(enc)
+
+
+@pytest.mark.parametrize("T, chunk", [(300, 140), (1000, 400)])
+def test_fast_mode_reduce_layer_norms_are_bit_identical(model, T, chunk, monkeypatch):
+    """Under PK_GPU_NUMERICS_FAST, in row groups above 64 rows, the split-K
+    reduces that finish x form the LayerNorms of the rows they write:
+    feed-forward 1's down projection self-attention's input, pointwise 2
+    feed-forward 2's input, and feed-forward 2's down projection the block's
+    output LayerNorm and the next block's input (pre-split).  They use the
+    LayerNorm kernels' arithmetic, so the encoder with them equals the
+    encoder with separate LayerNorm launches (PK_GPU_FUSE_LN=0 at creation)
+    bit for bit.  Two row groups (300 frames: about 150 rows each, 1000
+    frames: about 830 and 410, the 128- and 256-row tiles' reduces); the
+    profiled run shows the launches gone: per group the convolution
+    module's LayerNorm and the first block's input one are left."""
+    x = bench.enc_rng(0xFEAB, T).standard_normal((T, bench.D)).astype(np.float32)
+    monkeypatch.delenv("PK_GPU_FUSE_LN", raising=False)
+    fused = run(model, x, chunk, pk.NUMERICS_FAST)
+    n_fused = layer_norm_launches(model, x, chunk, pk.NUMERICS_FAST)
+    monkeypatch.setenv("PK_GPU_FUSE_LN", "0")
+    apart = run(model, x, chunk, pk.NUMERICS_FAST)
+    n_apart = layer_norm_launches(model, x, chunk, pk.NUMERICS_FAST)
+    print(f"T {T} chunk {chunk}: LayerNorm launches {n_fused} fused, {n_apart} apart", flush=True)
+    assert n_apart == 2 * 5 * bench.N_BLOCKS, n_apart
+    assert n_fused == 2 * (bench.N_BLOCKS + 1), n_fused
+    for a, b in zip(fused, apart):
+        assert bits_equal(a, b), describe_mismatch(a, b)
