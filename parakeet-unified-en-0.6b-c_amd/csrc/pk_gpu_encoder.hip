@@ -704,10 +704,12 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         const float* A = nullptr;
         int rc = norm_in(f, b.ln_conv_w, b.ln_conv_b, &A, false);
         if (!rc) rc = gemm(e, b.pw1t, A, R, h, b.pw1_b, pkgpu::EPI_NONE, s, g.part, ps && !f.in_g, false, f);
-        // Small row groups (fused LayerNorms on) take the GLU inside the
-        // depthwise convolution: each input value is gated where it is read
-        // (9 times, a few thousand rows' worth of work), one launch fewer.
-        const bool glu_in_dw = f.in_g != nullptr;
+        // The GLU is formed inside the depthwise convolution, as the kernel
+        // stages its input window (each value gated once per workgroup, the
+        // window's 8 extra times aside): one launch, and one write and read
+        // of the gated rows, fewer.  The same bits (PK_GPU_FUSE_LN=0 keeps
+        // the separate GLU launch).
+        const bool glu_in_dw = e->fuse_ln;
         if (!rc && !glu_in_dw)
             rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 12.0 * R * kD, s, [&] {
                 return check(pkgpu::launch_glu(h, 2 * kD, att, kD, R, kD, s), "glu");
@@ -723,7 +725,7 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         d.chunk_rows = rows;
         d.chunk_T = lens;
         d.T = Tmax; d.C = kD; d.K = kConvK; d.swish = 1;
-        rc = timed(e, PK_GPU_STAGE_CONV, 0.0, 8.0 * R * kD, s, [&] {
+        rc = timed(e, PK_GPU_STAGE_CONV, 0.0, (glu_in_dw ? 12.0 : 8.0) * R * kD, s, [&] {
             return check(pkgpu::launch_depthwise(d, g.n, s), "depthwise conv");
         });
         if (!rc) rc = gemm(e, b.pw2t, ln, R, x, b.pw2_b, pkgpu::EPI_RESIDUAL, s, g.part, false, false, pw2_o);
