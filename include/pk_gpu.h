@@ -550,9 +550,10 @@ int pk_gpu_uses_panel(int M, int N, int K, int bits, const void *dB, int ldb,
 /* Segments of K over workgroups that a panel GEMM of this shape takes with
  * this thread's workspace (pk_gpu_set_workspace): one per LDS phase when K
  * takes at least 4 phases (fewer phases run one after the other in one
- * launch).  Above one, each workgroup stores its partial tile there and a
- * second launch sums them in segment order before alpha, beta, bias and the
- * epilogue (deterministic). */
+ * launch), or one per half phase of 512 k where that fills more CUs.  Above
+ * one, each workgroup stores its partial tile there and a second launch sums
+ * them in segment order before alpha, beta, bias and the epilogue
+ * (deterministic). */
 int pk_gpu_panel_segments(int M, int N, int K);
 /* Test hook: the weights as the panel kernels multiply them, to dout [K][N]
  * on `stream`: int8 fl(q * B_scale), int4 fl(q * s[k][n/32]), fp32 hi + lo. */

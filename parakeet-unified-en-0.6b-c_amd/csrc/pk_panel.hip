@@ -145,10 +145,11 @@ template <> struct WUnit<W_I4> { typedef uint32_t T; };
 template <> struct WUnit<W_F32> { typedef v4u T[2]; };
 
 // Activation rows per wave and 256-k row loads per phase, as the LDS allows:
-// kph is 1024 for M <= 35, at least 512 up to M = 64.
-template <int MB> struct PanelShape {
+// kph is 1024 for M <= 35, at least 512 up to M = 64.  HALF: phases of 512
+// k at most (segments of K split over twice as many workgroups).
+template <int MB, bool HALF> struct PanelShape {
     static constexpr int RPW = (16 * MB + kPW - 1) / kPW;
-    static constexpr int CPR = MB <= 3 ? 4 : 2;
+    static constexpr int CPR = MB <= 3 && !HALF ? 4 : 2;
     static constexpr int SPW = CPR * 8 / kPW;            // steps per wave per phase
 };
 
@@ -159,10 +160,10 @@ template <int MB> struct PanelShape {
 // gamma + beta), the LayerNorm output bit for bit, before the int4 scale
 // fold and the split.  LDS past the rows: 32 zero bytes, the rows' (mean,
 // inv) pairs (64 rows' worth), gamma and beta [K], int4 scales [K].
-template <int WK, int MB, int NCT, bool LN>
+template <int WK, int MB, int NCT, bool LN, bool HALF>
 __global__ __launch_bounds__(64 * kPW) void smallm_panel(PanelArgs p)
 {
-    typedef PanelShape<MB> L;
+    typedef PanelShape<MB, HALF> L;
     constexpr int UB = unit_bytes(WK);
     __shared__ __attribute__((aligned(16))) unsigned char smem[kLds];
 
@@ -552,30 +553,37 @@ size_t scales_offset(WeightKind kind, int K, int N)
 // and 2 column tiles, whose registers would spill (panel_tile skips them).
 constexpr bool ln_tile(int wk, int mb, int nct) { return !(wk == W_F32 && mb >= 3 && nct == 2); }
 
+// half: phases of 512 k (MB <= 3, no fused input LayerNorm).
 template <int WK, int MB, int NCT>
-void launch_t(const PanelArgs& a, dim3 grid, hipStream_t st)
+void launch_t(const PanelArgs& a, dim3 grid, hipStream_t st, bool half)
 {
     if constexpr (ln_tile(WK, MB, NCT)) {
         if (a.ln_g) {
-            hipLaunchKernelGGL((smallm_panel<WK, MB, NCT, true>), grid, dim3(64 * kPW), 0, st, a);
+            hipLaunchKernelGGL((smallm_panel<WK, MB, NCT, true, false>), grid, dim3(64 * kPW), 0, st, a);
             return;
         }
     }
-    hipLaunchKernelGGL((smallm_panel<WK, MB, NCT, false>), grid, dim3(64 * kPW), 0, st, a);
+    if constexpr (MB <= 3) {
+        if (half) {
+            hipLaunchKernelGGL((smallm_panel<WK, MB, NCT, false, true>), grid, dim3(64 * kPW), 0, st, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((smallm_panel<WK, MB, NCT, false, false>), grid, dim3(64 * kPW), 0, st, a);
 }
 
 template <int WK>
-void launch_wk(int MB, int NCT, const PanelArgs& a, dim3 grid, hipStream_t st)
+void launch_wk(int MB, int NCT, bool half, const PanelArgs& a, dim3 grid, hipStream_t st)
 {
     switch (MB * 2 + NCT - 1) {
-    case 2: launch_t<WK, 1, 1>(a, grid, st); break;
-    case 3: launch_t<WK, 1, 2>(a, grid, st); break;
-    case 4: launch_t<WK, 2, 1>(a, grid, st); break;
-    case 5: launch_t<WK, 2, 2>(a, grid, st); break;
-    case 6: launch_t<WK, 3, 1>(a, grid, st); break;
-    case 7: launch_t<WK, 3, 2>(a, grid, st); break;
-    case 8: launch_t<WK, 4, 1>(a, grid, st); break;
-    default: launch_t<WK, 4, 2>(a, grid, st); break;
+    case 2: launch_t<WK, 1, 1>(a, grid, st, half); break;
+    case 3: launch_t<WK, 1, 2>(a, grid, st, half); break;
+    case 4: launch_t<WK, 2, 1>(a, grid, st, half); break;
+    case 5: launch_t<WK, 2, 2>(a, grid, st, half); break;
+    case 6: launch_t<WK, 3, 1>(a, grid, st, half); break;
+    case 7: launch_t<WK, 3, 2>(a, grid, st, half); break;
+    case 8: launch_t<WK, 4, 1>(a, grid, st, half); break;
+    default: launch_t<WK, 4, 2>(a, grid, st, half); break;
     }
 }
 
@@ -618,10 +626,16 @@ bool rows_fit(const GemmProblem& p, int rows)
 // 64x4096x2048 11.4 against 16.4, f32 33x1024x2048 7.0 against 8.9; from 4
 // phases the split wins (i4 33x1024x4096 9.55 against 10.06, i4
 // 16x1024x4096 7.6 against 10.8).
+// half: phases (and so segments) of at most 512 k.
 constexpr int kMinSegs = 4;
-int segments_for(const GemmProblem& p, int rows)
+int kph_of(const GemmProblem& p, int rows, bool half)
 {
     const int kph = phase_k(rows, lds_extra(p));
+    return half ? std::min(kph, 512) : kph;
+}
+int segments_for(const GemmProblem& p, int rows, bool half = false)
+{
+    const int kph = kph_of(p, rows, half);
     if (!p.work || p.ln_gamma || p.K <= kph) return 1;
     const int segs = (p.K + kph - 1) / kph;
     if (segs < kMinSegs) return 1;
@@ -637,10 +651,10 @@ int segments_for(const GemmProblem& p, int rows)
 // to a sweep of every tile over the encoder's M = 33 shapes, workload 0
 // (M = 32) and M = 1, 16, 64 on MI355X: it picks the fastest tile on 10 of
 // 11 shapes and one within 1% on the other.
-double tile_cost(const GemmProblem& p, int mb, int nct)
+double tile_cost(const GemmProblem& p, int mb, int nct, bool half)
 {
     const int rows = std::min(p.M, 16 * mb);
-    const int segs = segments_for(p, rows);
+    const int segs = segments_for(p, rows, half);
     const double kseg = (double)p.K / segs;
     const double wgs = (double)((p.N + 16 * nct - 1) / (16 * nct)) * ((p.M + 16 * mb - 1) / (16 * mb)) * segs;
     const double rounds = std::ceil(wgs / 256.0);
@@ -703,18 +717,35 @@ bool panel_force_tiles(int mb, int nct)
     return true;
 }
 
-// The tile of a problem, or mb = 0 if no tile holds its rows.
-void panel_tile(const GemmProblem& p, int* mb, int* nct)
+// Whether a tile may take half phases: up to 3 row blocks, no fused input
+// LayerNorm, and K already split over workgroups with whole phases (where
+// the phases run in one launch, a split form costs a second launch that
+// tile_cost does not model).
+bool half_ok(const GemmProblem& p, int mb)
+{
+    return mb <= 3 && !p.ln_gamma && segments_for(p, std::min(p.M, 16 * mb)) > 1;
+}
+
+// The tile of a problem, or mb = 0 if no tile holds its rows; *half: its
+// phases are of 512 k (K split over twice as many workgroups where whole
+// phases leave CUs idle: i4 33 x 1024 x 4096 takes 3 row blocks in one
+// row group and 8 segments, 256 workgroups, instead of 2 row groups of 2
+// blocks that stream the weights twice).
+void panel_choice(const GemmProblem& p, int* mb, int* nct, bool* half)
 {
     const int MB = (p.M + 15) / 16;
     int b = 0, c = 1;
+    bool hf = false;
     double best = 1e300;
     for (int cc = 1; cc <= 2; ++cc)
         for (int bb = 1; bb <= MB; ++bb) {
             if (!rows_fit(p, std::min(p.M, 16 * bb))) continue;
             if (p.ln_gamma && !ln_tile(p.kind, bb, cc)) continue;
-            const double t = tile_cost(p, bb, cc);
-            if (t < best - 1e-9) { best = t; b = bb; c = cc; }
+            for (int h = 0; h < 2; ++h) {
+                if (h && !half_ok(p, bb)) continue;
+                const double t = tile_cost(p, bb, cc, h != 0);
+                if (t < best - 1e-9) { best = t; b = bb; c = cc; hf = h != 0; }
+            }
         }
     // PK_GPU_PANEL_TILE="MB,NCT" overrides the choice (tuning sweeps)
     static const std::pair<int, int> forced = [] {
@@ -730,16 +761,25 @@ void panel_tile(const GemmProblem& p, int* mb, int* nct)
         (!p.ln_gamma || ln_tile(p.kind, std::min(fb, MB), fc))) {
         b = std::min(fb, MB);
         c = fc;
+        hf = half_ok(p, b) && tile_cost(p, b, c, true) < tile_cost(p, b, c, false);
     }
     *mb = b;
     *nct = c;
+    *half = hf;
+}
+
+void panel_tile(const GemmProblem& p, int* mb, int* nct)
+{
+    bool half = false;
+    panel_choice(p, mb, nct, &half);
 }
 
 int panel_segments(const GemmProblem& p)
 {
     int mb = 1, nct = 1;
-    panel_tile(p, &mb, &nct);
-    return mb ? segments_for(p, std::min(p.M, 16 * mb)) : 1;
+    bool half = false;
+    panel_choice(p, &mb, &nct, &half);
+    return mb ? segments_for(p, std::min(p.M, 16 * mb), half) : 1;
 }
 
 bool panel_fuses_out_ln(const GemmProblem& p)
@@ -761,10 +801,11 @@ bool panel_supports(const GemmProblem& p)
                        reinterpret_cast<uintptr_t>(p.ln_beta) % 16))
         return false;
     int mb = 0, nct = 0;
-    panel_tile(p, &mb, &nct);
+    bool half = false;
+    panel_choice(p, &mb, &nct, &half);
     if (!mb) return false;
     if (p.out_ln_gamma && !(p.N <= kReduceLnMaxN && p.N % (8 * kLnChunk) == 0 && p.out_ln_beta &&
-                            segments_for(p, std::min(p.M, 16 * mb)) > 1))
+                            segments_for(p, std::min(p.M, 16 * mb), half) > 1))
         return false;
     return true;
 }
@@ -790,11 +831,12 @@ hipError_t launch_panel(const GemmProblem& p, hipStream_t st)
     a.p_bytes = (uint32_t)p_ext;
     a.s_bytes = (uint32_t)s_ext;
     int MB = 1, NCT = 1;
-    panel_tile(p, &MB, &NCT);
-    a.kph = phase_k(std::min(p.M, 16 * MB), lds_extra(p));
+    bool half = false;
+    panel_choice(p, &MB, &NCT, &half);
+    a.kph = kph_of(p, std::min(p.M, 16 * MB), half);
     a.ln_g = p.ln_gamma;
     a.ln_b = p.ln_beta;
-    const int segs = segments_for(p, std::min(p.M, 16 * MB));
+    const int segs = segments_for(p, std::min(p.M, 16 * MB), half);
     a.kseg = segs > 1 ? ((p.K / 32 + segs - 1) / segs) * 32 : p.K;
     const int z = (p.K + a.kseg - 1) / a.kseg;
     a.work = z > 1 ? p.work : nullptr;
@@ -802,9 +844,9 @@ hipError_t launch_panel(const GemmProblem& p, hipStream_t st)
     const dim3 grid((unsigned)(((groups + kXcd - 1) / kXcd) * kXcd), (unsigned)((p.M + 16 * MB - 1) / (16 * MB)),
                     (unsigned)z);
     switch (p.kind) {
-    case W_I8: launch_wk<W_I8>(MB, NCT, a, grid, st); break;
-    case W_I4: launch_wk<W_I4>(MB, NCT, a, grid, st); break;
-    default:   launch_wk<W_F32>(MB, NCT, a, grid, st); break;
+    case W_I8: launch_wk<W_I8>(MB, NCT, half, a, grid, st); break;
+    case W_I4: launch_wk<W_I4>(MB, NCT, half, a, grid, st); break;
+    default:   launch_wk<W_F32>(MB, NCT, half, a, grid, st); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || z == 1) return e;
