@@ -617,42 +617,53 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
     // `want` if the split kernels take them (pre-split row groups), else its
     // output LayerNorm alone if the panel kernels take that, else none.  Each
     // consumer asks the same question of its producer, so both agree.
-    auto reduce_ln = [&](const DevBlock& bb, const DevWeight& w, const float* A, const float* bias,
-                         Epilogue epi, const DevBlock* next_block) {
+    enum XWriter { FF1_DOWN, PW2, FF2_DOWN };
+    auto reduce_ln = [&](const DevBlock& bb, XWriter which, const DevBlock* next_block) {
         FusedLn want;
-        if (&w == &bb.ff1_w2) {              // x after feed-forward 1: self-attention's input
+        const DevWeight* w = nullptr;
+        const float *A = h, *bias = nullptr;
+        Epilogue epi = pkgpu::EPI_HALF_RESIDUAL;
+        switch (which) {
+        case FF1_DOWN:          // x after feed-forward 1: self-attention's input
+            w = &bb.ff1_w2;
+            bias = bb.ff1_b2;
             want.next_g = bb.ln_sa_w;
             want.next_b = bb.ln_sa_b;
-        } else if (&w == &bb.pw2t) {         // after the convolution: feed-forward 2's input
+            break;
+        case PW2:               // after the convolution: feed-forward 2's input
+            w = &bb.pw2t;
+            A = ln;
+            bias = bb.pw2_b;
+            epi = pkgpu::EPI_RESIDUAL;
             want.next_g = bb.ln_ff2_w;
             want.next_b = bb.ln_ff2_b;
-        } else {                             // the block's output, and the next block's input
+            break;
+        case FF2_DOWN:          // the block's output, and the next block's input
+            w = &bb.ff2_w2;
+            bias = bb.ff2_b2;
             want.out_g = bb.ln_out_w;
             want.out_b = bb.ln_out_b;
             if (next_block) {
                 want.next_g = next_block->ln_ff1_w;
                 want.next_b = next_block->ln_ff1_b;
             }
+            break;
         }
         if (want.next_g) want.next_out = ln;
-        if (ps && split_fusable(e, w, A, R, x, bias, epi, g.part, want)) return want;
+        if (ps && split_fusable(e, *w, A, R, x, bias, epi, g.part, want)) return want;
         FusedLn o;
         o.out_g = want.out_g;
         o.out_b = want.out_b;
-        if (o.out_g && fusable(e, w, A, R, x, bias, epi, g.part, o)) return o;
+        if (o.out_g && fusable(e, *w, A, R, x, bias, epi, g.part, o)) return o;
         return FusedLn();
     };
     const size_t bi = (size_t)(&b - e->blocks.data());
     const DevBlock* next = bi + 1 < e->blocks.size() ? &e->blocks[bi + 1] : nullptr;
-    const FusedLn ff1_o = reduce_ln(b, b.ff1_w2, h, b.ff1_b2, pkgpu::EPI_HALF_RESIDUAL, nullptr);
-    const FusedLn pw2_o = reduce_ln(b, b.pw2t, ln, b.pw2_b, pkgpu::EPI_RESIDUAL, nullptr);
-    const FusedLn ff2_o = reduce_ln(b, b.ff2_w2, h, b.ff2_b2, pkgpu::EPI_HALF_RESIDUAL, next);
+    const FusedLn ff1_o = reduce_ln(b, FF1_DOWN, nullptr);
+    const FusedLn pw2_o = reduce_ln(b, PW2, nullptr);
+    const FusedLn ff2_o = reduce_ln(b, FF2_DOWN, next);
     // whether the previous block's last reduce wrote this block's first input
-    bool ff1_ready = false;
-    if (bi > 0) {
-        const DevBlock& pb = e->blocks[bi - 1];
-        ff1_ready = reduce_ln(pb, pb.ff2_w2, h, pb.ff2_b2, pkgpu::EPI_HALF_RESIDUAL, &b).next_g != nullptr;
-    }
+    const bool ff1_ready = bi > 0 && reduce_ln(e->blocks[bi - 1], FF2_DOWN, &b).next_g != nullptr;
     // the normalised input of a GEMM: fused into it, already in `ln` (ready:
     // the reduce before wrote it), or a LayerNorm launch into `ln`
     auto norm_in = [&](const FusedLn& f, const float* gm, const float* be, const float** A, bool ready) {
