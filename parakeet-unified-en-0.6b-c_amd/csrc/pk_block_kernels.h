@@ -93,6 +93,13 @@ hipError_t launch_layer_norm(const float* x, int ldx, const float* gamma, const 
 hipError_t launch_layer_norm_split(const float* x, int ldx, const float* gamma, const float* beta,
                                    float* out, int ldo, int rows, int D, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s);
+// The same attention on split bf16 operands (fast numerics, within about 1e-5
+// of launch_attention; not bit-identical), for T <= kAttnMaxT: a first
+// launch splits the chunks' keys and values and the launch's position rows
+// into ws, in the matrix cores' fragment order, which must hold
+// attn_fast_ws_floats(a.T, a.H, n_chunks) floats.
+size_t attn_fast_ws_floats(int T, int H, int n_chunks);
+hipError_t launch_attention_fast(const AttnArgs& a, int n_chunks, float* ws, size_t ws_floats, hipStream_t s);
 hipError_t launch_glu(const float* in, int ldi, float* out, int ldo, int rows, int D, hipStream_t s);
 hipError_t launch_depthwise(const DwArgs& a, int n_chunks, hipStream_t s);
 hipError_t launch_transpose(const float* in, float* out, int R, int C, hipStream_t s);

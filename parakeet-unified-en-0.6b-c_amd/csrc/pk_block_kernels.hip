@@ -619,6 +619,391 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
         }
 }
 
+// ---- fast numerics: attention on split bf16 operands -------------------------
+// Under PK_GPU_NUMERICS_FAST the attention of chunks of kAttnShortT < T <=
+// kAttnMaxT rows multiplies on v_mfma_f32_16x16x32_bf16 with each operand
+// split as the split GEMM kernels split theirs (x = hi + lo + r, hi =
+// bf16(x), lo = bf16(x - hi), r below 2^-16 |x|): three products hi hi +
+// lo hi + hi lo per pair, within about 1e-5 of the exact kernel.  The
+// organisation is rel_pos_attention's: 32 query rows of one head of one
+// chunk per workgroup, their score rows in LDS, the content scores, then
+// the relative-position term added at the shifted positions, softmax, then
+// scores x V.  Fragments of v_mfma_f32_16x16x32_bf16: lane l = i + 16 g
+// holds row (A) or column (B) i and k = 8 g .. 8 g + 7 of a 32-deep step;
+// the 16 x 16 result gives lane l column i and rows 4 g .. 4 g + 3.
+// attn_fast_prep writes every B operand pre-split in fragment order, each
+// fragment 2 KB: the 64 lanes' 16-byte hi parts, then their lo parts, so a
+// wave's fragment load is 1 KB contiguous:
+//   Kf [n][H][KB][4]  keys: fragment (z, h, kb, s) holds key 16 kb + i of
+//                     chunk z, columns 32 s + 8 g .. of head h (KB = T/16
+//                     rounded up; keys past the chunk's end 0)
+//   Pf [H][PB][4]     the launch's position rows: (h, pb, s) holds row
+//                     16 pb + i, columns 32 s + 8 g .. of head h
+//   Vf [n][H][8][TS]  values: (z, h, db, t) holds column 16 db + i and keys
+//                     32 t + 8 g .. of chunk z (TS = T/32 rounded up)
+typedef uint32_t fa_v4u __attribute__((ext_vector_type(4)));
+typedef __bf16 fa_v8bf __attribute__((ext_vector_type(8)));
+constexpr int kFragFloats = 512;                  // one fragment, hi and lo, 2 KB
+
+struct FaLayout {
+    int KB, PB, TS;                               // key blocks, position blocks, value steps
+    size_t kf, pf;                                // Kf, Pf offsets in floats (Vf follows Pf)
+    __host__ __device__ FaLayout(int T, int H, int n)
+    {
+        KB = (T + 15) / 16;
+        PB = (2 * T - 1 + 15) / 16;
+        TS = (T + 31) / 32;
+        kf = 0;
+        pf = (size_t)n * H * KB * 4 * kFragFloats;
+    }
+    __host__ __device__ size_t vf(int H) const { return pf + (size_t)H * PB * 4 * kFragFloats; }
+    __host__ __device__ size_t floats(int H, int n) const { return vf(H) + (size_t)n * H * 8 * TS * kFragFloats; }
+};
+
+__device__ inline __amdgpu_buffer_rsrc_t fa_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 8 floats -> their bf16 hi and lo halves, in order
+__device__ inline void fa_split8(const float (&x)[8], fa_v4u& hi, fa_v4u& lo)
+{
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t h, l;
+        split_bf16x2(x[2 * k], x[2 * k + 1], h, l);
+        hi[k] = h;
+        lo[k] = l;
+    }
+}
+
+// this lane's part of fragment f (in fragments from the buffer's start);
+// past the buffer's extent both read 0
+__device__ inline void fa_load(__amdgpu_buffer_rsrc_t r, uint32_t f, fa_v8bf& hi, fa_v8bf& lo)
+{
+    const uint32_t byte = f * (kFragFloats * 4) + (threadIdx.x & 63) * 16;
+    hi = __builtin_bit_cast(fa_v8bf, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte, 0, 0));
+    lo = __builtin_bit_cast(fa_v8bf, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(byte + 1024), 0, 0));
+}
+
+__device__ inline v4f fa_mfma3(fa_v8bf ah, fa_v8bf al, fa_v8bf bh, fa_v8bf bl, v4f c)
+{
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+}
+
+// One thread per (fragment, lane): its 8 source values, split, to the
+// fragment's hi and lo parts.  Keys, then position rows, then values.
+__global__ __launch_bounds__(256) void attn_fast_prep(AttnArgs p, int n_chunks, float* ws)
+{
+    const FaLayout L(p.T, p.H, n_chunks);
+    const int D = p.H * kDh;
+    const long long nk = (long long)n_chunks * p.H * L.KB * 4 * 64, np = (long long)p.H * L.PB * 4 * 64;
+    const long long nv = (long long)n_chunks * p.H * 8 * L.TS * 64;
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int l = (int)(idx & 63), i = l & 15, g = l >> 4;
+    const long long f = idx >> 6;                 // fragment within its operand
+    float x[8];
+    float* dst;
+    if (idx < nk) {
+        const int s = (int)(f % 4), kb = (int)(f / 4 % L.KB), h = (int)(f / 4 / L.KB % p.H), z = (int)(f / 4 / L.KB / p.H);
+        const int Tz = p.chunk_T ? p.chunk_T[z] : p.T, row0 = p.chunk_rows ? p.chunk_rows[z] : 0;
+        const int j = 16 * kb + i;
+        if (j < Tz) {
+            const float4* src = reinterpret_cast<const float4*>(p.qkv + (size_t)(row0 + j) * p.ldq + D + h * kDh + 32 * s + 8 * g);
+            const float4 a = src[0], b = src[1];
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+        }
+        dst = ws + L.kf + (size_t)f * kFragFloats;
+    } else if (idx < nk + np) {
+        const long long q = f - nk / 64;
+        const int s = (int)(q % 4), pb = (int)(q / 4 % L.PB), h = (int)(q / 4 / L.PB);
+        const int m = 16 * pb + i;
+        if (m < 2 * p.T - 1) {
+            const float4* src = reinterpret_cast<const float4*>(p.P + (size_t)m * p.ldp + h * kDh + 32 * s + 8 * g);
+            const float4 a = src[0], b = src[1];
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+        }
+        dst = ws + L.pf + (size_t)q * kFragFloats;
+    } else if (idx < nk + np + nv) {
+        const long long q = f - (nk + np) / 64;
+        const int t = (int)(q % L.TS), db = (int)(q / L.TS % 8), h = (int)(q / L.TS / 8 % p.H), z = (int)(q / L.TS / 8 / p.H);
+        const int Tz = p.chunk_T ? p.chunk_T[z] : p.T, row0 = p.chunk_rows ? p.chunk_rows[z] : 0;
+        const float* v = p.qkv + 2 * D + h * kDh + 16 * db + i;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int j = 32 * t + 8 * g + e;
+            x[e] = j < Tz ? v[(size_t)(row0 + j) * p.ldq] : 0.0f;
+        }
+        dst = ws + L.vf(p.H) + (size_t)q * kFragFloats;
+    } else {
+        return;
+    }
+    fa_v4u hi, lo;
+    fa_split8(x, hi, lo);
+    reinterpret_cast<fa_v4u*>(dst)[l] = hi;
+    reinterpret_cast<fa_v4u*>(dst + 256)[l] = lo;
+}
+
+// Q + bias of this lane's fragment rows r0 + 16 b + i (rows past T repeat
+// row T - 1: their scores are zeroed and their outputs not stored), split.
+__device__ inline void fa_qfrags(const AttnArgs& p, const float* bias, int row0, int r0, int T, int h,
+                                 fa_v8bf (&qh)[2][4], fa_v8bf (&ql)[2][4])
+{
+    const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int r = min(r0 + 16 * b + i, T - 1);
+        const float* q = p.qkv + (size_t)(row0 + r) * p.ldq + h * kDh;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int d = 32 * s + 8 * g;
+            const float4 a0 = *reinterpret_cast<const float4*>(q + d), a1 = *reinterpret_cast<const float4*>(q + d + 4);
+            const float4 u0 = *reinterpret_cast<const float4*>(bias + h * kDh + d);
+            const float4 u1 = *reinterpret_cast<const float4*>(bias + h * kDh + d + 4);
+            const float x[8] = {__fadd_rn(a0.x, u0.x), __fadd_rn(a0.y, u0.y), __fadd_rn(a0.z, u0.z),
+                                __fadd_rn(a0.w, u0.w), __fadd_rn(a1.x, u1.x), __fadd_rn(a1.y, u1.y),
+                                __fadd_rn(a1.z, u1.z), __fadd_rn(a1.w, u1.w)};
+            fa_v4u hi, lo;
+            fa_split8(x, hi, lo);
+            qh[b][s] = __builtin_bit_cast(fa_v8bf, hi);
+            ql[b][s] = __builtin_bit_cast(fa_v8bf, lo);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256, 2) void rel_pos_attention_fast(AttnArgs p, const float* ws)
+{
+    extern __shared__ float S[];                     // [kAttnRows][sld] score rows
+    const int sld = attn_sld(p.T);
+    int rb, h, z;
+    attn_task(rb, h, z);
+    const int T = p.chunk_T ? p.chunk_T[z] : p.T;
+    const int r0 = rb * kAttnRows;
+    if (r0 >= T) return;                             // the whole workgroup
+    const int row0 = p.chunk_rows ? p.chunk_rows[z] : 0;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i = lane & 15, g = lane >> 4;
+    const FaLayout L(p.T, p.H, gridDim.z);
+    const auto rK = fa_rsrc(ws + L.kf, (uint32_t)((L.pf - L.kf) * 4));
+    const auto rP = fa_rsrc(ws + L.pf, (uint32_t)((L.vf(p.H) - L.pf) * 4));
+    const auto rV = fa_rsrc(ws + L.vf(p.H), (uint32_t)((L.floats(p.H, gridDim.z) - L.vf(p.H)) * 4));
+
+    // Every operand fragment comes from L2: each phase keeps kRing tiles
+    // (steps) of loads in flight in a ring of register sets, refilled right
+    // after the set is multiplied.  Past the last tile the refill loads the
+    // last one again (never multiplied), so no load sits in a branch and the
+    // wait counts stay exact.
+    constexpr int kRing = 3, kRingV = 6;
+
+    // content scores: wave w takes keys 64 t + 16 w .. + 15 of tile t
+    {
+        fa_v8bf qh[2][4], ql[2][4];
+        fa_qfrags(p, p.pos_bias_u, row0, r0, T, h, qh, ql);
+        const int nt = (T + 63) / 64;
+        fa_v8bf kh[kRing][4], kl[kRing][4];
+        const uint32_t kf0 = (uint32_t)((z * p.H + h) * L.KB) * 4;
+        auto load = [&](fa_v8bf (&bh)[4], fa_v8bf (&bl)[4], int t) {
+            const uint32_t kb = (uint32_t)(4 * min(t, nt - 1) + w);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) fa_load(rK, kf0 + 4 * kb + s, bh[s], bl[s]);
+        };
+#pragma unroll
+        for (int k = 0; k < kRing; ++k) load(kh[k], kl[k], k);
+        for (int t0 = 0; t0 < nt; t0 += kRing) {
+#pragma unroll
+            for (int k = 0; k < kRing; ++k) {
+                const int t = t0 + k;
+                if (t < nt) {
+                    v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) acc[b] = fa_mfma3(qh[b][s], ql[b][s], kh[k][s], kl[k][s], acc[b]);
+                    const int jj = 64 * t + 16 * w + i;
+                    if (jj < T)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b)
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) S[(16 * b + 4 * g + v) * sld + jj] = acc[b][v];
+                }
+                load(kh[k], kl[k], t + kRing);
+            }
+        }
+    }
+    __syncthreads();
+
+    // position term at the shifted positions m = T - 1 - row + j (each (row,
+    // j) takes exactly one m, so no two lanes write one score); wave w takes
+    // m_first + 64 t + 16 w .. + 15 of tile t
+    {
+        fa_v8bf qh[2][4], ql[2][4];
+        fa_qfrags(p, p.pos_bias_v, row0, r0, T, h, qh, ql);
+        const int r_hi = min(r0 + kAttnRows, T) - 1;
+        const int m_first = T - 1 - r_hi, m_last = 2 * T - 2 - r0;
+        // tiles of 64 launch rows m' = pbase + m from a multiple of 16; the
+        // positions outside [m_first, m_last] give no (row, j) in range
+        const int pbase = p.T - T;                   // this chunk's rows within the launch's P
+        const int a0 = (pbase + m_first) & ~15;
+        const int nt = (pbase + m_last - a0) / 64 + 1;
+        const uint32_t pf0 = (uint32_t)(h * L.PB) * 4;
+        fa_v8bf ph[kRing][4], pl[kRing][4];
+        auto load = [&](fa_v8bf (&bh)[4], fa_v8bf (&bl)[4], int t) {
+            const uint32_t pb = (uint32_t)((a0 >> 4) + 4 * min(t, nt - 1) + w);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) fa_load(rP, pf0 + 4 * pb + s, bh[s], bl[s]);
+        };
+#pragma unroll
+        for (int k = 0; k < kRing; ++k) load(ph[k], pl[k], k);
+        for (int t0 = 0; t0 < nt; t0 += kRing) {
+#pragma unroll
+            for (int k = 0; k < kRing; ++k) {
+                const int t = t0 + k;
+                if (t < nt) {
+                    v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) acc[b] = fa_mfma3(qh[b][s], ql[b][s], ph[k][s], pl[k][s], acc[b]);
+                    const int mm = a0 + 64 * t + 16 * w + i - pbase;
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const int rl = 16 * b + 4 * g + v, j = mm - (T - 1) + r0 + rl;
+                            if (r0 + rl < T && (unsigned)j < (unsigned)T) {
+                                float* sp = S + rl * sld + j;
+                                *sp = __fmul_rn(__fadd_rn(*sp, acc[b][v]), kScoreScale);
+                            }
+                        }
+                }
+                load(ph[k], pl[k], t + kRing);
+            }
+        }
+    }
+    __syncthreads();
+
+    // softmax of each row, 8 lanes a row, lane q taking the groups of 8
+    // scores q, q + 8, ...: max, exp and sum, then each group scaled and
+    // written back split in place (its 8 hi, then its 8 lo bf16 values: the
+    // A fragment scores x V reads), groups up to T rounded to 32 (zeros past
+    // T; a row past the chunk all zeros).
+    {
+        const int rl = 8 * w + (lane >> 3), q = lane & 7;
+        float* sr = S + rl * sld;
+        const int ng = (T + 7) / 8, ngp = (T + 31) / 32 * 4;
+        const bool live = r0 + rl < T;
+        float mx = -INFINITY, sum = 0.0f;
+        if (live) {
+            for (int gi = q; gi < ng; gi += 8) {
+                const float4 a = *reinterpret_cast<const float4*>(sr + 8 * gi);
+                const float4 b = *reinterpret_cast<const float4*>(sr + 8 * gi + 4);
+                const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (8 * gi + e < T) mx = fmaxf(mx, x[e]);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 4));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        if (live) {
+            for (int gi = q; gi < ng; gi += 8) {
+                float4 a = *reinterpret_cast<const float4*>(sr + 8 * gi);
+                float4 b = *reinterpret_cast<const float4*>(sr + 8 * gi + 4);
+                float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    x[e] = 8 * gi + e < T ? __expf(x[e] - mx) : 0.0f;
+                    sum += x[e];
+                }
+                *reinterpret_cast<float4*>(sr + 8 * gi) = make_float4(x[0], x[1], x[2], x[3]);
+                *reinterpret_cast<float4*>(sr + 8 * gi + 4) = make_float4(x[4], x[5], x[6], x[7]);
+            }
+        }
+        sum += __shfl_xor(sum, 4);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 1);
+        const float inv = live ? 1.0f / sum : 0.0f;
+        for (int gi = q; gi < ngp; gi += 8) {
+            float x[8];
+            if (live && gi < ng) {
+                const float4 a = *reinterpret_cast<const float4*>(sr + 8 * gi);
+                const float4 b = *reinterpret_cast<const float4*>(sr + 8 * gi + 4);
+                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] *= inv;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+            }
+            fa_v4u hi, lo;
+            fa_split8(x, hi, lo);
+            *reinterpret_cast<fa_v4u*>(sr + 8 * gi) = hi;
+            *reinterpret_cast<fa_v4u*>(sr + 8 * gi + 4) = lo;
+        }
+    }
+
+    // scores x V: wave w takes columns 32 w .. 32 w + 31 of the head for all
+    // 32 rows (each value group read once per workgroup), 32 keys a step.
+    // The value ring is filled before the barrier.
+    v4f acc[2][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[b][0] = acc[b][1] = v4f{0.f, 0.f, 0.f, 0.f};
+    {
+        const int ns = (T + 31) / 32;
+        const uint32_t vf0 = (uint32_t)(((z * p.H + h) * 8 + 2 * w) * L.TS);
+        fa_v8bf vh[kRingV][2], vl[kRingV][2];
+        auto load = [&](fa_v8bf (&bh)[2], fa_v8bf (&bl)[2], int t) {
+            const uint32_t ts = (uint32_t)min(t, ns - 1);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) fa_load(rV, vf0 + (uint32_t)(c * L.TS) + ts, bh[c], bl[c]);
+        };
+#pragma unroll
+        for (int k = 0; k < kRingV; ++k) load(vh[k], vl[k], k);
+        __syncthreads();
+        for (int t0 = 0; t0 < ns; t0 += kRingV) {
+#pragma unroll
+            for (int k = 0; k < kRingV; ++k) {
+                const int t = t0 + k;
+                if (t < ns) {
+                    // the probabilities' split groups, as the softmax left them
+                    fa_v8bf ah[2], al[2];
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        const float* sr = S + (16 * b + i) * sld + 32 * t + 8 * g;
+                        ah[b] = __builtin_bit_cast(fa_v8bf, *reinterpret_cast<const fa_v4u*>(sr));
+                        al[b] = __builtin_bit_cast(fa_v8bf, *reinterpret_cast<const fa_v4u*>(sr + 4));
+                    }
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int c = 0; c < 2; ++c)
+                            acc[b][c] = fa_mfma3(ah[b], al[b], vh[k][c], vl[k][c], acc[b][c]);
+                }
+                load(vh[k], vl[k], t + kRingV);
+            }
+        }
+    }
+    float* out = p.out + (size_t)row0 * p.ldo + h * kDh + 32 * w + i;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int r = r0 + 16 * b + 4 * g + v;
+            if (r < T) {
+                out[(size_t)r * p.ldo] = acc[b][0][v];
+                out[(size_t)r * p.ldo + 16] = acc[b][1][v];
+            }
+        }
+}
+
 // ---- short sequences (T <= kAttnShortT) -------------------------------------
 // A workgroup of 4 waves takes kAttnShortRows = 16 query rows, 4 per wave.
 // Every key, position and value row it reads is loaded into LDS at once,
@@ -1144,6 +1529,33 @@ hipError_t launch_attention(const AttnArgs& a, int n_chunks, hipStream_t s)
         (int)attn_lds_bytes(kAttnMaxT));
     if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(rel_pos_attention<false>, grid, dim3(256), attn_lds_bytes(a.T), s, a);
+    return hipGetLastError();
+}
+
+size_t attn_fast_ws_floats(int T, int H, int n_chunks)
+{
+    return FaLayout(T, H, n_chunks).floats(H, n_chunks);
+}
+
+hipError_t launch_attention_fast(const AttnArgs& a, int n_chunks, float* ws, size_t ws_floats, hipStream_t s)
+{
+    if (a.T <= 0 || n_chunks <= 0) return hipSuccess;
+    if (a.T > kAttnMaxT || !ws || attn_fast_ws_floats(a.T, a.H, n_chunks) > ws_floats ||
+        ws_floats * 4 >= ((size_t)1 << 31) || a.ldq % 4 || a.ldp % 4)
+        return hipErrorInvalidValue;
+    const FaLayout L(a.T, a.H, n_chunks);
+    const long long items = 64LL * ((long long)n_chunks * a.H * L.KB * 4 + (long long)a.H * L.PB * 4 +
+                                    (long long)n_chunks * a.H * 8 * L.TS);
+    hipLaunchKernelGGL(attn_fast_prep, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a, n_chunks, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&rel_pos_attention_fast), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)(4u * kAttnRows * attn_sld(kAttnMaxT)));
+    if (attr != hipSuccess) return attr;
+    const dim3 grid((a.T + kAttnRows - 1) / kAttnRows, a.H, n_chunks);
+    hipLaunchKernelGGL(rel_pos_attention_fast, grid, dim3(256), 4u * kAttnRows * attn_sld(a.T), s, a,
+                       static_cast<const float*>(ws));
     return hipGetLastError();
 }
 

@@ -150,6 +150,9 @@ struct pk_gpu_encoder {
     // fast numerics: the int4 and fp32 block weights' pre-split copies
     // (PK_GPU_PRESPLIT_W=0 at creation turns them off; the results are the same)
     bool presplit_w = true;
+    // fast numerics: attention of row groups above 64 rows on split bf16
+    // operands (PK_GPU_FAST_ATTN=0 at creation keeps the exact kernel)
+    bool fast_attn = true;
     std::vector<hipStream_t> side;
     std::vector<hipEvent_t> side_done;
     hipEvent_t inputs_ready = nullptr;
@@ -703,8 +706,17 @@ int run_block(pk_gpu_encoder* e, const DevBlock& b, const RowGroup& g, hipStream
         a.chunk_T = lens;
         a.T = Tmax; a.H = kHeads;
         a.scores = Tmax > pkgpu::kAttnMaxT ? e->scores + g.scores_off : nullptr;
+        // Fast numerics: split bf16 operands, prepared in the row group's
+        // split-K workspace, which nothing holds between the QKV GEMM (K is
+        // not split for it) and the output projection.
+        const size_t ws_floats = pkgpu::kSplitWorkBytes / sizeof(float);
+        const bool fast = e->fast_attn && e->numerics == PK_GPU_NUMERICS_FAST && R > pkgpu::kSmallMaxM &&
+                          Tmax > pkgpu::kAttnShortT && Tmax <= pkgpu::kAttnMaxT && g.part &&
+                          pkgpu::attn_fast_ws_floats(Tmax, kHeads, g.n) <= ws_floats;
         rc = timed(e, PK_GPU_STAGE_ATTENTION, flops, bytes, s, [&] {
-            return check(pkgpu::launch_attention(a, g.n, s), "attention");
+            return check(fast ? pkgpu::launch_attention_fast(a, g.n, g.part, ws_floats, s)
+                              : pkgpu::launch_attention(a, g.n, s),
+                         "attention");
         });
         if (!rc) rc = gemm(e, b.out, att, R, x, b.out_b, pkgpu::EPI_RESIDUAL, s, g.part);
         return rc;
@@ -1293,6 +1305,7 @@ int pk_gpu_encoder_create(pk_gpu_encoder** out, const pk_gpu_block_weights* bloc
     pk_gpu_encoder* e = new pk_gpu_encoder;
     if (const char* v = getenv("PK_GPU_PRESPLIT")) e->presplit = strcmp(v, "0") != 0;
     if (const char* v = getenv("PK_GPU_FUSE_LN")) e->fuse_ln = strcmp(v, "0") != 0;
+    if (const char* v = getenv("PK_GPU_FAST_ATTN")) e->fast_attn = strcmp(v, "0") != 0;
     if (const char* v = getenv("PK_GPU_PRESPLIT_W")) e->presplit_w = strcmp(v, "0") != 0;
     hipError_t r = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
     if (r != hipSuccess) {

@@ -315,3 +315,24 @@ def test_fast_mode_reduce_layer_norms_are_bit_identical(model, T, chunk, monkeyp
     assert n_fused == 2 * (bench.N_BLOCKS + 1), n_fused
     for a, b in zip(fused, apart):
         assert bits_equal(a, b), describe_mismatch(a, b)
+
+
+@pytest.mark.parametrize("T, chunk", [(300, 140), (1000, 400), (200, 0)])
+def test_fast_mode_split_attention(model, T, chunk, monkeypatch):
+    """Under PK_GPU_NUMERICS_FAST, row groups above 64 rows with chunks of
+    65-512 rows take the attention on split bf16 operands
+    (rel_pos_attention_fast: three bf16 products per pair, fast softmax).
+    Over 24 blocks on trained-like weights the encoder with it stays within
+    the 1e-3 contract of the same encoder with the exact attention
+    (PK_GPU_FAST_ATTN=0 at creation); the two differ, so the split kernel
+    ran; and replays repeat the first run bit for bit."""
+    x = bench.enc_rng(0xFEAC, T).standard_normal((T, bench.D)).astype(np.float32)
+    monkeypatch.delenv("PK_GPU_FAST_ATTN", raising=False)
+    fast = run(model, x, chunk, pk.NUMERICS_FAST)
+    monkeypatch.setenv("PK_GPU_FAST_ATTN", "0")
+    exact_attn = run(model, x, chunk, pk.NUMERICS_FAST)
+    e = rel_dev(fast[0], exact_attn[0].astype(np.float64))
+    print(f"T {T} chunk {chunk}: split attention against exact attention, max rel {e:.3g}", flush=True)
+    assert np.isfinite(fast[0]).all()
+    assert 0.0 < e <= TOL, e
+    assert bits_equal(fast[1], fast[0]), "replay differs from its capture run"
