@@ -797,10 +797,16 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention_fast(AttnArgs p, con
 
     // Every operand fragment comes from L2: each phase keeps kRing tiles
     // (steps) of loads in flight in a ring of register sets, refilled right
-    // after the set is multiplied.  Past the last tile the refill loads the
-    // last one again (never multiplied), so no load sits in a branch and the
-    // wait counts stay exact.
+    // after the set is multiplied.  The loops run to their bounds at T =
+    // kAttnMaxT, unrolled, and every tile is multiplied: past the chunk's
+    // last tile the loads repeat it and only the stores are skipped (their
+    // keys or positions fall outside the chunk).  A loop back edge made the
+    // compiler wait for every load in flight at its head, and a multiply
+    // under a branch let it sink the tile's loads next to their use.
     constexpr int kRing = 3, kRingV = 6;
+    constexpr int kAcTiles = kAttnMaxT / 64;                 // content tiles
+    constexpr int kBdTiles = (kAttnMaxT + 45) / 64 + 1;      // position tiles (span T + 45 at most)
+    constexpr int kPvSteps = kAttnMaxT / 32;                 // value steps
 
     // content scores: wave w takes keys 64 t + 16 w .. + 15 of tile t
     {
@@ -816,24 +822,24 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention_fast(AttnArgs p, con
         };
 #pragma unroll
         for (int k = 0; k < kRing; ++k) load(kh[k], kl[k], k);
-        for (int t0 = 0; t0 < nt; t0 += kRing) {
+#pragma unroll
+        for (int t0 = 0; t0 < kAcTiles; t0 += kRing) {
 #pragma unroll
             for (int k = 0; k < kRing; ++k) {
                 const int t = t0 + k;
-                if (t < nt) {
-                    v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+                v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
-                        for (int b = 0; b < 2; ++b) acc[b] = fa_mfma3(qh[b][s], ql[b][s], kh[k][s], kl[k][s], acc[b]);
-                    const int jj = 64 * t + 16 * w + i;
-                    if (jj < T)
+                    for (int b = 0; b < 2; ++b) acc[b] = fa_mfma3(qh[b][s], ql[b][s], kh[k][s], kl[k][s], acc[b]);
+                const int jj = 64 * t + 16 * w + i;
+                if (jj < T)
 #pragma unroll
-                        for (int b = 0; b < 2; ++b)
+                    for (int b = 0; b < 2; ++b)
 #pragma unroll
-                            for (int v = 0; v < 4; ++v) S[(16 * b + 4 * g + v) * sld + jj] = acc[b][v];
-                }
+                        for (int v = 0; v < 4; ++v) S[(16 * b + 4 * g + v) * sld + jj] = acc[b][v];
                 load(kh[k], kl[k], t + kRing);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -861,29 +867,30 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention_fast(AttnArgs p, con
         };
 #pragma unroll
         for (int k = 0; k < kRing; ++k) load(ph[k], pl[k], k);
-        for (int t0 = 0; t0 < nt; t0 += kRing) {
+#pragma unroll
+        for (int t0 = 0; t0 < kBdTiles; t0 += kRing) {
 #pragma unroll
             for (int k = 0; k < kRing; ++k) {
                 const int t = t0 + k;
-                if (t < nt) {
-                    v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+                v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
-                        for (int b = 0; b < 2; ++b) acc[b] = fa_mfma3(qh[b][s], ql[b][s], ph[k][s], pl[k][s], acc[b]);
-                    const int mm = a0 + 64 * t + 16 * w + i - pbase;
+                    for (int b = 0; b < 2; ++b) acc[b] = fa_mfma3(qh[b][s], ql[b][s], ph[k][s], pl[k][s], acc[b]);
+                // past the last tile every j falls at or past T
+                const int mm = a0 + 64 * t + 16 * w + i - pbase;
 #pragma unroll
-                    for (int b = 0; b < 2; ++b)
+                for (int b = 0; b < 2; ++b)
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            const int rl = 16 * b + 4 * g + v, j = mm - (T - 1) + r0 + rl;
-                            if (r0 + rl < T && (unsigned)j < (unsigned)T) {
-                                float* sp = S + rl * sld + j;
-                                *sp = __fmul_rn(__fadd_rn(*sp, acc[b][v]), kScoreScale);
-                            }
+                    for (int v = 0; v < 4; ++v) {
+                        const int rl = 16 * b + 4 * g + v, j = mm - (T - 1) + r0 + rl;
+                        if (r0 + rl < T && (unsigned)j < (unsigned)T) {
+                            float* sp = S + rl * sld + j;
+                            *sp = __fmul_rn(__fadd_rn(*sp, acc[b][v]), kScoreScale);
                         }
-                }
+                    }
                 load(ph[k], pl[k], t + kRing);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -968,26 +975,29 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention_fast(AttnArgs p, con
 #pragma unroll
         for (int k = 0; k < kRingV; ++k) load(vh[k], vl[k], k);
         __syncthreads();
-        for (int t0 = 0; t0 < ns; t0 += kRingV) {
+#pragma unroll
+        for (int t0 = 0; t0 < kPvSteps; t0 += kRingV) {
 #pragma unroll
             for (int k = 0; k < kRingV; ++k) {
                 const int t = t0 + k;
-                if (t < ns) {
-                    // the probabilities' split groups, as the softmax left them
-                    fa_v8bf ah[2], al[2];
+                // the probabilities' split groups, as the softmax left them;
+                // past the last step zeros (the values repeat the last step)
+                const bool live = t < ns;
+                const int tc = min(t, ns - 1);
+                fa_v8bf ah[2], al[2];
 #pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        const float* sr = S + (16 * b + i) * sld + 32 * t + 8 * g;
-                        ah[b] = __builtin_bit_cast(fa_v8bf, *reinterpret_cast<const fa_v4u*>(sr));
-                        al[b] = __builtin_bit_cast(fa_v8bf, *reinterpret_cast<const fa_v4u*>(sr + 4));
-                    }
-#pragma unroll
-                    for (int b = 0; b < 2; ++b)
-#pragma unroll
-                        for (int c = 0; c < 2; ++c)
-                            acc[b][c] = fa_mfma3(ah[b], al[b], vh[k][c], vl[k][c], acc[b][c]);
+                for (int b = 0; b < 2; ++b) {
+                    const float* sr = S + (16 * b + i) * sld + 32 * tc + 8 * g;
+                    const fa_v4u zero = {0u, 0u, 0u, 0u};
+                    ah[b] = __builtin_bit_cast(fa_v8bf, live ? *reinterpret_cast<const fa_v4u*>(sr) : zero);
+                    al[b] = __builtin_bit_cast(fa_v8bf, live ? *reinterpret_cast<const fa_v4u*>(sr + 4) : zero);
                 }
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) acc[b][c] = fa_mfma3(ah[b], al[b], vh[k][c], vl[k][c], acc[b][c]);
                 load(vh[k], vl[k], t + kRingV);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
