@@ -644,6 +644,11 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention(AttnArgs p)
 typedef uint32_t fa_v4u __attribute__((ext_vector_type(4)));
 typedef __bf16 fa_v8bf __attribute__((ext_vector_type(8)));
 constexpr int kFragFloats = 512;                  // one fragment, hi and lo, 2 KB
+// Score-row stride of the split kernel, 4 more than a multiple of 32 floats:
+// the 4 lane groups of a result store, and the 16 rows of a fragment read,
+// start 4 or 16 banks apart (8 apart, rel_pos_attention's stride, put the
+// 4 groups of a store on the same banks).
+__host__ __device__ constexpr int fa_sld(int T) { return ((T + 31) & ~31) + 4; }
 
 struct FaLayout {
     int KB, PB, TS;                               // key blocks, position blocks, value steps
@@ -779,10 +784,12 @@ __device__ inline void fa_qfrags(const AttnArgs& p, const float* bias, int row0,
     }
 }
 
+// MAXT: the launch's T rounded up to 64 (the unrolled loops' bound)
+template <int MAXT>
 __global__ __launch_bounds__(256, 2) void rel_pos_attention_fast(AttnArgs p, const float* ws)
 {
     extern __shared__ float S[];                     // [kAttnRows][sld] score rows
-    const int sld = attn_sld(p.T);
+    const int sld = fa_sld(p.T);
     int rb, h, z;
     attn_task(rb, h, z);
     const int T = p.chunk_T ? p.chunk_T[z] : p.T;
@@ -804,9 +811,9 @@ __global__ __launch_bounds__(256, 2) void rel_pos_attention_fast(AttnArgs p, con
     // compiler wait for every load in flight at its head, and a multiply
     // under a branch let it sink the tile's loads next to their use.
     constexpr int kRing = 3, kRingV = 6;
-    constexpr int kAcTiles = kAttnMaxT / 64;                 // content tiles
-    constexpr int kBdTiles = (kAttnMaxT + 45) / 64 + 1;      // position tiles (span T + 45 at most)
-    constexpr int kPvSteps = kAttnMaxT / 32;                 // value steps
+    constexpr int kAcTiles = MAXT / 64;                      // content tiles
+    constexpr int kBdTiles = (MAXT + 45) / 64 + 1;           // position tiles (span T + 45 at most)
+    constexpr int kPvSteps = MAXT / 32;                      // value steps
 
     // content scores: wave w takes keys 64 t + 16 w .. + 15 of tile t
     {
@@ -1559,14 +1566,28 @@ hipError_t launch_attention_fast(const AttnArgs& a, int n_chunks, float* ws, siz
     hipLaunchKernelGGL(attn_fast_prep, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, a, n_chunks, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&rel_pos_attention_fast), hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)(4u * kAttnRows * attn_sld(kAttnMaxT)));
-    if (attr != hipSuccess) return attr;
     const dim3 grid((a.T + kAttnRows - 1) / kAttnRows, a.H, n_chunks);
-    hipLaunchKernelGGL(rel_pos_attention_fast, grid, dim3(256), 4u * kAttnRows * attn_sld(a.T), s, a,
-                       static_cast<const float*>(ws));
-    return hipGetLastError();
+    const unsigned lds = 4u * kAttnRows * fa_sld(a.T);
+    const float* cws = ws;
+    auto run = [&](auto kern) {
+        // LDS above the default dynamic limit is granted once per instantiation
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           (int)(4u * kAttnRows * fa_sld(kAttnMaxT)));
+        if (attr != hipSuccess) return attr;
+        hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, a, cws);
+        return hipGetLastError();
+    };
+    switch ((a.T + 63) / 64) {
+    case 1:
+    case 2: return run(rel_pos_attention_fast<128>);
+    case 3: return run(rel_pos_attention_fast<192>);
+    case 4: return run(rel_pos_attention_fast<256>);
+    case 5: return run(rel_pos_attention_fast<320>);
+    case 6: return run(rel_pos_attention_fast<384>);
+    case 7: return run(rel_pos_attention_fast<448>);
+    default: return run(rel_pos_attention_fast<512>);
+    }
 }
 
 hipError_t launch_glu(const float* in, int ldi, float* out, int ldo, int rows, int D, hipStream_t s)
