@@ -214,8 +214,8 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
     the panel kernels use.  panel: every replica of a small-M shape (M <= 64)
     gets its panel (pk_gpu_pack_weight_dev, a one-time repack outside the
     timed region, as registration makes it), so the panel kernels run.
-    presplit: under fast numerics every replica of an int4 or fp32 shape with
-    M > 64 gets its pre-split copy (pk_gpu_presplit_weight_dev, also outside
+    presplit: under fast numerics every replica of a shape with M > 64 gets
+    its pre-split copy (pk_gpu_presplit_weight_dev, also outside
     the timed region), which the split kernels then read."""
     import torch
     pk = load_binding()
@@ -265,7 +265,7 @@ def gemm_mode(specs, steps, warmup, min_weight_bytes=512 << 20, eager=False, for
         uses_panel = bool(lib.pk_gpu_uses_panel(m, n, k, bits, W[0].data_ptr(), ldb,
                                                 S[0].data_ptr() if kind == "i4" else None))
         split_copies = []
-        if presplit and numerics == "fast" and m > 64 and kind != "i8" and k % 32 == 0 and n % 32 == 0:
+        if presplit and numerics == "fast" and m > 64 and k % 32 == 0 and n % 32 == 0:
             for r in range(reps):
                 pk.call("pk_gpu_presplit_weight_dev", bits, k, n, W[r].data_ptr(), ldb,
                         S[r].data_ptr() if kind == "i4" else None, cur())

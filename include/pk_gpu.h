@@ -524,15 +524,16 @@ int pk_gpu_pack_weight_dev(int bits, int K, int N, const void *dB, int ldb,
 int pk_gpu_unpack_weight_dev(const void *dB);
 /* Device bytes held by panels. */
 size_t pk_gpu_panel_bytes(void);
-/* Make the pre-split copy of device weight dB (bits 4 or 32; K and N
+/* Make the pre-split copy of device weight dB (bits 4, 8 or 32; K and N
  * multiples of 32; int4: its scales dscales [K][N/32]) for later
  * PK_GPU_NUMERICS_FAST *_dev / *_ex_dev GEMMs with M > 64 whose B is dB with
  * the same bits, K, N, ldb (and dscales): the weights the split kernels
  * multiply (int4: fl(q * s), blas.c:834-840), each already split into its
- * bf16 hi and lo halves in the kernels' chunk order, so those GEMMs stage
- * them with plain copies instead of decoding and splitting every weight per
- * row tile.  The results are the same bits.  4*K*N bytes of device memory
- * (int4: 8 times the packed weight).  Runs on `stream` and waits for it; not
+ * bf16 hi and lo halves (int8: the codes as bf16, exact) in the kernels'
+ * chunk order, so those GEMMs stage them with plain copies instead of
+ * decoding and splitting every weight per row tile.  The results are the
+ * same bits.  4*K*N bytes of device memory (int4: 8 times the packed
+ * weight; int8: 2*K*N, twice the codes).  Runs on `stream` and waits for it; not
  * during stream capture.  Idempotent for the same parameters; PK_GPU_EINVAL
  * if dB already has a copy of another shape.  The weight's bytes must not
  * change afterwards.  No counterpart in the reference. */

@@ -56,8 +56,8 @@ struct GemmProblem {
     // null.  With it, the small-M path takes the panel kernels.
     const void* panel = nullptr;
     // The weight's pre-split copy (launch_split_pack of this B, scales, K and
-    // N; int4 and fp32), or null.  The split kernels then stage it with plain
-    // copies instead of decoding and splitting B (the same bf16 values).
+    // N), or null.  The split kernels then stage it with plain copies instead
+    // of decoding and splitting B (the same bf16 values).
     const void* b_presplit = nullptr;
     // Panel kernels only (panel_supports): A is x, and the GEMM multiplies
     // LayerNorm(x) over its K columns with these gamma, beta [K] (the
@@ -178,9 +178,10 @@ bool split_supports(const GemmProblem& p);
 // With p.work, shapes with too few tiles to fill the CUs split K over
 // workgroups and sum the partial tiles in a second launch.
 hipError_t launch_split(const GemmProblem& p, hipStream_t stream);
-// Bytes of a weight's pre-split copy for the split kernels (int4 and fp32,
-// K and N multiples of 32; else 0): K N 4, per 32-deep chunk and column the
-// 32 bf16 hi halves then the 32 lo halves.
+// Bytes of a weight's pre-split copy for the split kernels (K and N
+// multiples of 32; else 0): int4 and fp32 K N 4, per 32-deep chunk and column
+// the 32 bf16 hi halves then the 32 lo halves; int8 K N 2, per chunk and
+// column the 32 codes as bf16.
 size_t split_weight_bytes(WeightKind kind, int K, int N);
 // Write that copy of B [K][ldb] (int4: and its scales [K][N/32]) to `out`.
 hipError_t launch_split_pack(WeightKind kind, int K, int N, const void* B, int ldb, const float* scales,

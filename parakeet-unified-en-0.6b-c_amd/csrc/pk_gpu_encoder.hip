@@ -882,8 +882,8 @@ int make_panels(pk_gpu_encoder* e)
     return PK_GPU_OK;
 }
 
-// The int4 and fp32 block weights' pre-split copies (DevWeight::split),
-// made once on the encoder's stream.
+// The block weights' pre-split copies (DevWeight::split; int8: the codes as
+// bf16), made once on the encoder's stream.
 int make_splits(pk_gpu_encoder* e)
 {
     if (!e->split_allocs.empty()) return PK_GPU_OK;
@@ -892,9 +892,9 @@ int make_splits(pk_gpu_encoder* e)
     size_t total = 0;
     int rc = PK_GPU_OK;
     for (DevBlock& b : e->blocks) {
-        for (DevWeight* w : {&b.ff1_w1, &b.ff1_w2, &b.ff2_w1, &b.ff2_w2, &b.pw1t, &b.pw2t}) {
+        for (DevWeight* w : {&b.ff1_w1, &b.ff1_w2, &b.ff2_w1, &b.ff2_w2, &b.qkv, &b.out, &b.pw1t, &b.pw2t}) {
             const size_t bytes = pkgpu::split_weight_bytes(w->kind, w->K, w->N);
-            if (!bytes) continue;                    // int8: the codes enter the matrix cores exactly
+            if (!bytes) continue;
             void* d = nullptr;
             if (hipMalloc(&d, bytes) != hipSuccess) {
                 rc = error(PK_GPU_ENOMEM, "pre-split weights: device allocation of %zu bytes failed", bytes);

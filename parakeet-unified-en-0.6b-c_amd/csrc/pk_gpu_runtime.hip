@@ -901,7 +901,7 @@ int pk_gpu_unpack_weight_dev(const void* dB)
 int pk_gpu_presplit_weight_dev(int bits, int K, int N, const void* dB, int ldb, const float* dscales,
                                void* stream)
 {
-    if (bits != 4 && bits != 32) return fail(PK_GPU_EINVAL, "presplit: bits = %d (4 or 32)", bits);
+    if (bits != 4 && bits != 8 && bits != 32) return fail(PK_GPU_EINVAL, "presplit: bits = %d (4, 8 or 32)", bits);
     if (K <= 0 || N <= 0 || K % 32 || N % 32)
         return fail(PK_GPU_EINVAL, "presplit: K = %d and N = %d must be positive multiples of 32", K, N);
     if (ldb < (bits == 4 ? N / 2 : N)) return fail(PK_GPU_EINVAL, "presplit: ldb = %d too small for N = %d", ldb, N);

@@ -73,6 +73,11 @@ constexpr int kCuLds = 163840;    // LDS bytes per CU
 // the 32 lo = bf16(w - hi), w the weight the kernels otherwise split
 // (fl(q * s) for int4), so staging a chunk is a copy.
 constexpr int W_BS = 3;
+// The same for int8 weights (GemmProblem::b_presplit of an int8 B): per
+// chunk c and column n, 64 bytes at (c N + n) * 64, the 32 codes of k = 32 c
+// .. 32 c + 31 as bf16 (exact), so the int8 GEMMs stage a chunk with 16-byte
+// copies instead of 4-byte loads of 32 rows and conversions.
+constexpr int W_BS8 = 4;
 
 struct SpArgs {
     int M, N, K;
@@ -140,6 +145,7 @@ template <> struct WUnit<W_I8> { uint32_t q[2]; };
 template <> struct WUnit<W_I4> { uint32_t q[2]; float s[2]; };
 template <> struct WUnit<W_F32> { v4u w[2]; };
 template <> struct WUnit<W_BS> { v4u w; };
+template <> struct WUnit<W_BS8> { v4u w; };
 
 // Staging and multiplying one chunk of a BM x BN tile by NT threads.
 // A chunk's LDS planes: A_hi, A_lo [BM][RS], then W_hi (and W_lo) [BN][RS].
@@ -148,7 +154,7 @@ template <> struct WUnit<W_BS> { v4u w; };
 // and the pitch of the fp32 row), and staging it is a copy.
 template <int WK, int BM, int BN, int NT, bool AS>
 struct Pipe {
-    static constexpr int NBP = WK == W_I8 ? 1 : 2;             // weight planes
+    static constexpr int NBP = WK == W_I8 || WK == W_BS8 ? 1 : 2;   // weight planes
     static constexpr int A_PLANE = BM * RS, B_PLANE = BN * RS;   // bf16 elements
     // two buffers per workgroup: the gaps only where they keep as many
     // workgroups per CU (the 128 x 128 tiles fill 160 KB exactly without)
@@ -160,9 +166,9 @@ struct Pipe {
     // A: BM rows x 8 float4 per chunk
     static constexpr int A_ITEMS = BM * (KT / 4) / NT;
     // weight units of two consecutive k rows: 4 columns (int8, fp32) or 8
-    // (int4); pre-split weights: 16-byte pieces, 8 per column
+    // (int4); pre-split weights: 16-byte pieces, 8 per column (int8: 4)
     static constexpr int UC = WK == W_I4 ? 8 : 4;
-    static constexpr int B_TOTAL = WK == W_BS ? 8 * BN : (KT / 2) * (BN / UC);
+    static constexpr int B_TOTAL = WK == W_BS ? 8 * BN : WK == W_BS8 ? 4 * BN : (KT / 2) * (BN / UC);
     static constexpr int B_ITEMS = (B_TOTAL + NT - 1) / NT;     // the last one partial if NT > B_TOTAL
     static_assert(A_ITEMS * NT == BM * (KT / 4) && (B_TOTAL % NT == 0 || B_TOTAL < NT), "even split");
     static_assert(B_TOTAL % 64 == 0, "whole waves per weight item");
@@ -194,6 +200,15 @@ struct Pipe {
                 if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
                 const uint32_t col = (uint32_t)(k0 / KT) * (uint32_t)p.N + (uint32_t)(n0 + (idx >> 3));
                 r.w[i].w = __builtin_amdgcn_raw_buffer_load_b128(rB, (int)(col * 128u + 16u * (idx & 7)), 0, 0);
+            }
+        } else if constexpr (WK == W_BS8) {
+            // piece idx & 3 of column idx >> 2 (4 lanes read a column's 64 bytes)
+#pragma unroll
+            for (int i = 0; i < B_ITEMS; ++i) {
+                const int idx = tid + NT * i;
+                if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
+                const uint32_t col = (uint32_t)(k0 / KT) * (uint32_t)p.N + (uint32_t)(n0 + (idx >> 2));
+                r.w[i].w = __builtin_amdgcn_raw_buffer_load_b128(rB, (int)(col * 64u + 16u * (idx & 3)), 0, 0);
             }
         } else {
             load_units(r, p, rB, rS, tid, n0, k0);
@@ -259,6 +274,14 @@ struct Pipe {
                 if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
                 *reinterpret_cast<v4u*>((q < 4 ? bh : bl) + (idx >> 3) * RS + 8 * (q & 3)) = r.w[i].w;
             }
+        } else if constexpr (WK == W_BS8) {
+            // piece q = idx & 3: k group q of column idx >> 2
+#pragma unroll
+            for (int i = 0; i < B_ITEMS; ++i) {
+                const int idx = tid + NT * i;
+                if (B_TOTAL % NT != 0 && idx >= B_TOTAL) break;   // uniform per wave
+                *reinterpret_cast<v4u*>(bh + (idx >> 2) * RS + 8 * (idx & 3)) = r.w[i].w;
+            }
         } else {
             store_units(r, bh, bl, tid);
         }
@@ -321,7 +344,7 @@ struct Pipe {
             for (int c = 0; c < 2; ++c) {
                 const int o = (c0 + 32 * c + r_lane) * RS + 16 * ks + k_lane;
                 b_hi[c] = *reinterpret_cast<const v8bf*>(bh + o);
-                if constexpr (WK != W_I8) b_lo[c] = *reinterpret_cast<const v8bf*>(bl + o);
+                if constexpr (NBP == 2) b_lo[c] = *reinterpret_cast<const v8bf*>(bl + o);
             }
 #pragma unroll
             for (int r = 0; r < 2; ++r)
@@ -329,7 +352,7 @@ struct Pipe {
                 for (int c = 0; c < 2; ++c) {
                     acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_hi[r], b_hi[c], acc[r][c], 0, 0, 0);
                     acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_lo[r], b_hi[c], acc[r][c], 0, 0, 0);
-                    if constexpr (WK != W_I8)
+                    if constexpr (NBP == 2)
                         acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_hi[r], b_lo[c], acc[r][c], 0, 0, 0);
                 }
         }
@@ -382,7 +405,7 @@ __device__ inline void zero(v16f (&acc)[2][2])
 // chunks) for tile u % n_tiles and stores its raw sums to the tile's slot
 // of that segment in work, in register order (split_reduce finishes).
 template <int WK, int WM, int WN, int PD, bool SK, bool AS>
-__global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WM * WN == 4 ? 2 : 1) void split_gemm(SpArgs p)
+__global__ __launch_bounds__(64 * WM * WN, WK == W_I8 || WK == W_BS8 || WM * WN == 4 ? 2 : 1) void split_gemm(SpArgs p)
 {
     typedef Pipe<WK, 64 * WM, 64 * WN, 64 * WM * WN, AS> L;
     __shared__ __attribute__((aligned(16))) __bf16 smem[2 * L::BUF];
@@ -791,6 +814,26 @@ __global__ __launch_bounds__(256) void split_pack(int K, int N, const void* B, i
     *reinterpret_cast<v4u*>(out + i * 16) = v4u{w[0], w[1], w[2], w[3]};
 }
 
+// The pre-split copy (W_BS8) of an int8 weight [K][N]: thread i writes
+// 16-byte piece i, the 8 codes of k group i & 3 of column n of chunk c as
+// bf16 (exact: |q| <= 128).
+__global__ __launch_bounds__(256) void split_pack_i8(int K, int N, const signed char* B, int ldb,
+                                                     unsigned char* out)
+{
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)(K / KT) * N * 4) return;
+    const int q = (int)(i & 3);
+    const long long cn = i >> 2;
+    const int n = (int)(cn % N), c = (int)(cn / N);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const size_t k = (size_t)(KT * c + 8 * q + e);
+        w[e / 2] = bits2(to_bf2((float)B[k * ldb + n], (float)B[(k + 1) * ldb + n]));
+    }
+    *reinterpret_cast<v4u*>(out + i * 16) = v4u{w[0], w[1], w[2], w[3]};
+}
+
 // Launch shape.  Where 128 x 128 tiles outnumber the CUs, 256 x 128 tiles
 // (8 waves, one workgroup per CU by its LDS) give no CU more rows x columns
 // than two 128 x 128 workgroups would, and split each weight for twice the
@@ -885,7 +928,7 @@ hipError_t launch_kind(SpArgs a, SplitPlan plan, hipStream_t st, const SpLn* ln)
     // Chunks of loads in flight, as many as fit two waves per SIMD without
     // spills: a lane holds 16 A bytes per 64 rows of the tile and chunk, plus
     // its weight units (fp32's take 4 times int8's registers).
-    constexpr bool WIDE = WK == W_F32 || WK == W_BS;      // 16-byte weight loads
+    constexpr bool WIDE = WK == W_F32 || WK == W_BS;      // 16-byte weight loads, 2 or 4 per column
     constexpr int PD22 = WIDE ? 2 : 3, PD21 = 2, PDK = WIDE ? 1 : 2, PD42 = 2;
     if (plan.n_seg > 1) {
         const bool wide = plan.shape == SP_4x2;
@@ -982,11 +1025,14 @@ hipError_t launch_split(const GemmProblem& p, hipStream_t st)
     const bool fuse = p.out_ln_gamma || p.next_ln_gamma;
     if (fuse && (!split_fuses_ln(p) || plan.n_seg < 2)) return hipErrorNotSupported;
     const SpLn* ln = fuse ? &lnv : nullptr;
-    if (p.b_presplit && p.kind != W_I8) {
-        // the weight's pre-split copy (split_pack), K N 4 bytes
-        if ((size_t)p.K * p.N * 4 >= lim || reinterpret_cast<uintptr_t>(p.b_presplit) % 16) return hipErrorNotSupported;
+    if (p.b_presplit) {
+        // the weight's pre-split copy (split_pack), split_weight_bytes long
+        const size_t bytes = split_weight_bytes(p.kind, p.K, p.N);
+        if (!bytes || bytes >= lim || reinterpret_cast<uintptr_t>(p.b_presplit) % 16) return hipErrorNotSupported;
         a.B = p.b_presplit;
-        a.b_bytes = (uint32_t)((size_t)p.K * p.N * 4);
+        a.b_bytes = (uint32_t)bytes;
+        if (p.kind == W_I8)
+            return p.a_presplit ? launch_kind<W_BS8, true>(a, plan, st, ln) : launch_kind<W_BS8, false>(a, plan, st, ln);
         return p.a_presplit ? launch_kind<W_BS, true>(a, plan, st, ln) : launch_kind<W_BS, false>(a, plan, st, ln);
     }
     if (p.a_presplit) {
@@ -1021,18 +1067,20 @@ bool split_fuses_ln(const GemmProblem& p)
 
 size_t split_weight_bytes(WeightKind kind, int K, int N)
 {
-    if (kind == W_I8 || K < KT || K % KT || N < 32 || N % 32) return 0;
-    return (size_t)K * N * 4;
+    if (K < KT || K % KT || N < 32 || N % 32) return 0;
+    return (size_t)K * N * (kind == W_I8 ? 2 : 4);
 }
 
 hipError_t launch_split_pack(WeightKind kind, int K, int N, const void* B, int ldb, const float* scales,
                              void* out, hipStream_t st)
 {
     if (!split_weight_bytes(kind, K, N) || (kind == W_I4 && !scales)) return hipErrorInvalidValue;
-    const long long pieces = (long long)(K / KT) * N * 8;
+    const long long pieces = (long long)(K / KT) * N * (kind == W_I8 ? 4 : 8);
     const dim3 grid((unsigned)((pieces + 255) / 256));
     unsigned char* o = static_cast<unsigned char*>(out);
-    if (kind == W_I4)
+    if (kind == W_I8)
+        hipLaunchKernelGGL(split_pack_i8, grid, dim3(256), 0, st, K, N, static_cast<const signed char*>(B), ldb, o);
+    else if (kind == W_I4)
         hipLaunchKernelGGL(split_pack<W_I4>, grid, dim3(256), 0, st, K, N, B, ldb, scales, o);
     else
         hipLaunchKernelGGL(split_pack<W_F32>, grid, dim3(256), 0, st, K, N, B, ldb, scales, o);

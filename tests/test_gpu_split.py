@@ -362,6 +362,9 @@ def fast_dev(dev, kind, dA, dW, dS, extra, M, N, K, dC, bias=None, epi=None):
     if kind == "i4":
         rc = getattr(lib, "pk_gpu_gemm_i4_ex_dev" if ex else "pk_gpu_gemm_i4_dev")(
             M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(), dS.data_ptr(), N // 2, 0.0, dC.data_ptr(), N, *tail, s)
+    elif kind == "i8":
+        rc = getattr(lib, "pk_gpu_gemm_i8_ex_dev" if ex else "pk_gpu_gemm_i8_dev")(
+            M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(), extra, N, 0.0, dC.data_ptr(), N, *tail, s)
     else:
         rc = getattr(lib, "pk_gpu_sgemm_ex_dev" if ex else "pk_gpu_sgemm_dev")(
             M, N, K, 1.0, dA.data_ptr(), K, dW.data_ptr(), N, 0.0, dC.data_ptr(), N, *tail, s)
@@ -373,15 +376,18 @@ def fast_dev(dev, kind, dA, dW, dS, extra, M, N, K, dC, bias=None, epi=None):
 # Every launch shape the pre-split copy meets, split-K included (a workspace).
 PRESPLIT_SHAPES = [("i4", 1656, 4096, 1024), ("f32", 1656, 2048, 1024), ("i4", 1024, 4096, 256),
                    ("f32", 1024, 2048, 96), ("i4", 416, 4096, 1024), ("i4", 375, 1024, 4096),
-                   ("f32", 130, 256, 320), ("i4", 97, 96, 288), ("f32", 77, 32, 32), ("i4", 1656, 1024, 4096)]
+                   ("f32", 130, 256, 320), ("i4", 97, 96, 288), ("f32", 77, 32, 32), ("i4", 1656, 1024, 4096),
+                   ("i8", 1656, 3072, 1024), ("i8", 1656, 1024, 1024), ("i8", 416, 3072, 1024),
+                   ("i8", 375, 1024, 4096), ("i8", 130, 256, 320), ("i8", 97, 96, 288), ("i8", 77, 32, 32)]
 
 
 @pytest.mark.parametrize("kind,M,N,K", PRESPLIT_SHAPES)
 @pytest.mark.parametrize("work", [False, True])
 def test_presplit_weights_give_the_same_bits(dev, kind, M, N, K, work):
     """The split kernels read a weight's pre-split copy (the staging's own
-    decode and split, done once) instead of the weight: the same products in
-    the same order, so the same bits, with and without split-K."""
+    decode and split, done once; int8: the codes as bf16) instead of the
+    weight: the same products in the same order, so the same bits, with and
+    without split-K."""
     torch = dev.torch
     A, W, extra, C0 = make(kind, M, N, K, f"sps.{kind}.{M}.{N}.{K}")
     bias = po.normal((N,), 0.0, 0.02, po.seed(0x5EED3300, f"sps.{kind}.b"))
@@ -408,7 +414,7 @@ def presplit_case(dev, kind, A, W, extra, M, N, K, dA, dW, dS, dC, dB):
     pk.call("pk_gpu_presplit_weight_dev", bits, K, N, dW.data_ptr(), N // 2 if kind == "i4" else N,
             dS.data_ptr() if dS is not None else None, dev.stream())
     try:
-        assert lib.pk_gpu_presplit_bytes() == before + 4 * K * N
+        assert lib.pk_gpu_presplit_bytes() == before + (2 if kind == "i8" else 4) * K * N
         # idempotent for the same parameters
         pk.call("pk_gpu_presplit_weight_dev", bits, K, N, dW.data_ptr(), N // 2 if kind == "i4" else N,
                 dS.data_ptr() if dS is not None else None, dev.stream())
@@ -434,7 +440,7 @@ def test_presplit_argument_checks(dev):
     lib = pk.load()
     W = dev.torch.zeros((64, 64), device=dev.dev)
     s = dev.stream()
-    assert lib.pk_gpu_presplit_weight_dev(8, 64, 64, W.data_ptr(), 64, None, s) == -1     # int8: nothing to split
+    assert lib.pk_gpu_presplit_weight_dev(16, 64, 64, W.data_ptr(), 64, None, s) == -1    # no such format
     assert lib.pk_gpu_presplit_weight_dev(32, 48, 64, W.data_ptr(), 64, None, s) == -1    # K % 32
     assert lib.pk_gpu_presplit_weight_dev(32, 64, 40, W.data_ptr(), 64, None, s) == -1    # N % 32
     assert lib.pk_gpu_presplit_weight_dev(4, 64, 64, W.data_ptr(), 32, None, s) == -1     # no scales
