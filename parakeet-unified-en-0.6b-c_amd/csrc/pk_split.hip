@@ -605,7 +605,8 @@ __device__ inline void rows_stats(const float* buf, float (*st)[2], int w, int l
 
 // Rows per workgroup of split_reduce_ln: 414 workgroups at 1656 rows, 64 KB
 // of partials each in flight.  Two rows per workgroup measured 1.8% slower
-// on the fast encoder pass (A/B on one box, two runs each).
+// on the fast encoder pass and eight 3.5% slower (A/B on one box each, two
+// runs each).
 constexpr int kReduceLnRows = 4;
 
 // The second launch of a split-K GEMM whose 1024-wide output rows feed
